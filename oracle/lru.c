@@ -1,0 +1,260 @@
+/*
+ * lru.c -- plain-C restatement of the per-layer expert slot LRU of the reference's
+ * `mlx-qwen38/expert_io.c` (TEST INFRASTRUCTURE ONLY: the checker for the HIP library's
+ * host and device LRU tables; never linked into the product).
+ *
+ * Restated behaviour (file:line of `mlx-qwen38/expert_io.c`):
+ *   reset             450-468  all maps -1, free stack [cap-1 .. 0] so pops yield 0,1,2,..
+ *   list helpers      358-402  doubly linked list over slots, head = LRU, tail = MRU;
+ *                              inserting an already-resident eid only refreshes it
+ *   victim choice     404-426  free stack first, else first slot from the LRU end whose eid
+ *                              is not protected, else the LRU head
+ *   decode step       583-685  classify in id order (lru hit / prefetch hit / miss, via the
+ *                              residency snapshot a prefetch leaves), predictor counters by
+ *                              popcount, allocate misses protecting the step's ids, refresh
+ *                              every id to MRU in id order and report its slot
+ *   prefetch          527-581  snapshot residency, cap = max_fetch in (0,32) else 32, take
+ *                              non-resident predictions in rank order, insert them in reverse
+ *                              rank order protecting all predictions
+ *   state get/set     726-789  LRU->MRU export; import rebuilds the free stack descending
+ *   counters          791-852  18 per-layer u64, 6 decode totals over layers 1..n-1
+ *   coalescing        187-276  (counters only) sort misses by eid, count contiguous runs
+ * Expert bytes are a per-layer parameter here; the reference hard-codes 1,536,000.
+ *
+ * Pinned by: golden traces written by the reference's own expert_io.c compiled from source
+ * (tests/golden/make_lru_traces.py), the independent OrderedDict restatement in lru.py, and
+ * invariants / brute force in tests/test_oracle_lru.py.
+ */
+#include <stdint.h>
+#include <string.h>
+
+#define O_MAX_LAYERS 64
+#define O_NUM_EXPERTS 512
+#define O_NUM_TENSORS 9
+
+typedef struct {
+    int capacity;
+    uint64_t expert_bytes;
+    int16_t slot_of[O_NUM_EXPERTS];   /* eid -> slot or -1 */
+    int16_t eid_of[O_NUM_EXPERTS];    /* slot -> eid or -1 */
+    int16_t older[O_NUM_EXPERTS];     /* towards the LRU end */
+    int16_t newer[O_NUM_EXPERTS];     /* towards the MRU end */
+    int16_t lru_end, mru_end;
+    int16_t free_stack[O_NUM_EXPERTS];
+    int n_free;
+    int snap_valid;
+    uint64_t snap_resident[8], snap_pred[8], snap_fetched[8];
+    uint64_t st[18];
+} OLayer;
+
+static OLayer g_o[O_MAX_LAYERS];
+
+static int bm_has(const uint64_t *bm, int e) { return (int)((bm[e >> 6] >> (e & 63)) & 1ULL); }
+static void bm_set(uint64_t *bm, int e) { bm[e >> 6] |= 1ULL << (e & 63); }
+
+static void unlink_slot(OLayer *L, int s) {
+    int o = L->older[s], n = L->newer[s];
+    if (o >= 0) L->newer[o] = (int16_t)n; else L->lru_end = (int16_t)n;
+    if (n >= 0) L->older[n] = (int16_t)o; else L->mru_end = (int16_t)o;
+    L->older[s] = L->newer[s] = -1;
+}
+
+static void push_mru(OLayer *L, int s) {
+    L->older[s] = L->mru_end;
+    L->newer[s] = -1;
+    if (L->mru_end >= 0) L->newer[L->mru_end] = (int16_t)s; else L->lru_end = (int16_t)s;
+    L->mru_end = (int16_t)s;
+}
+
+static void refresh(OLayer *L, int s) {
+    if (L->mru_end != s) { unlink_slot(L, s); push_mru(L, s); }
+}
+
+static void bind(OLayer *L, int e, int s) {
+    if (L->slot_of[e] >= 0) { refresh(L, L->slot_of[e]); return; }
+    L->slot_of[e] = (int16_t)s;
+    L->eid_of[s] = (int16_t)e;
+    push_mru(L, s);
+}
+
+static int take_slot(OLayer *L, const uint64_t *protect) {
+    if (L->n_free > 0) return L->free_stack[--L->n_free];
+    int s = L->lru_end;
+    for (; s >= 0; s = L->newer[s]) {
+        int e = L->eid_of[s];
+        if (e >= 0 && !bm_has(protect, e)) break;
+    }
+    if (s < 0) s = L->lru_end;            /* every resident expert is protected */
+    int e = L->eid_of[s];
+    unlink_slot(L, s);
+    if (e >= 0) L->slot_of[e] = -1;
+    L->eid_of[s] = -1;
+    return s;
+}
+
+static void count_runs(OLayer *L, const int32_t *eids, int n) {
+    if (n <= 0) return;
+    int32_t v[O_NUM_EXPERTS];
+    memcpy(v, eids, (size_t)n * sizeof(int32_t));
+    for (int i = 1; i < n; ++i) {            /* small n: insertion sort */
+        int32_t x = v[i]; int j = i;
+        while (j > 0 && v[j - 1] > x) { v[j] = v[j - 1]; --j; }
+        v[j] = x;
+    }
+    int runs = 1;
+    for (int i = 1; i < n; ++i) runs += (v[i] != v[i - 1] + 1);
+    L->st[16] += (uint64_t)n * O_NUM_TENSORS;
+    L->st[17] += (uint64_t)runs * O_NUM_TENSORS;
+}
+
+void o_layer_reset_cache(int l) {
+    if (l < 0 || l >= O_MAX_LAYERS) return;
+    OLayer *L = &g_o[l];
+    for (int i = 0; i < O_NUM_EXPERTS; ++i) L->slot_of[i] = L->eid_of[i] = L->older[i] = L->newer[i] = -1;
+    L->lru_end = L->mru_end = -1;
+    L->n_free = L->capacity;
+    for (int i = 0; i < L->capacity; ++i) L->free_stack[i] = (int16_t)(L->capacity - 1 - i);
+    L->snap_valid = 0;
+}
+
+void o_layer_reset_stats(int l) {
+    if (l < 0 || l >= O_MAX_LAYERS) return;
+    memset(g_o[l].st, 0, sizeof(g_o[l].st));
+}
+
+void o_layer_init(int l, int capacity, uint64_t expert_bytes) {
+    if (l < 0 || l >= O_MAX_LAYERS) return;
+    memset(&g_o[l], 0, sizeof(OLayer));
+    g_o[l].capacity = capacity;
+    g_o[l].expert_bytes = expert_bytes;
+    o_layer_reset_cache(l);
+}
+
+/* Returns the number of misses; out_slots[k] gets every id's slot, miss_eids/miss_slots
+ * (<= 16 each) the demand copies in allocation order. */
+int o_layer_step_decode(int l, const uint32_t *eids, int k, uint32_t *out_slots,
+                        int32_t *miss_eids, int32_t *miss_slots) {
+    if (l < 0 || l >= O_MAX_LAYERS) return 0;
+    OLayer *L = &g_o[l];
+    uint64_t want[8] = {0};
+    int n_miss = 0;
+    L->st[0] += (uint64_t)k;
+    for (int i = 0; i < k; ++i) bm_set(want, (int)eids[i]);
+    if (L->snap_valid) {
+        for (int w = 0; w < 8; ++w) {
+            uint64_t missing_before = want[w] & ~L->snap_resident[w];
+            L->st[10] += (uint64_t)__builtin_popcountll(want[w] & L->snap_pred[w]);
+            L->st[11] += (uint64_t)__builtin_popcountll(want[w]);
+            L->st[12] += (uint64_t)__builtin_popcountll(L->snap_pred[w]);
+            L->st[13] += (uint64_t)__builtin_popcountll(missing_before & L->snap_fetched[w]);
+            L->st[14] += (uint64_t)__builtin_popcountll(missing_before);
+            L->st[15] += (uint64_t)__builtin_popcountll(L->snap_fetched[w]);
+        }
+    }
+    for (int i = 0; i < k; ++i) {
+        int e = (int)eids[i];
+        if (L->slot_of[e] >= 0) {
+            if (!L->snap_valid || bm_has(L->snap_resident, e)) L->st[1]++;
+            else L->st[2]++;
+        } else {
+            L->st[3]++;
+            miss_eids[n_miss++] = e;
+        }
+    }
+    L->snap_valid = 0;
+    for (int i = 0; i < n_miss; ++i) {
+        int s = take_slot(L, want);
+        bind(L, miss_eids[i], s);
+        miss_slots[i] = s;
+    }
+    L->st[4] += (uint64_t)n_miss * L->expert_bytes;
+    for (int i = 0; i < k; ++i) {
+        int s = L->slot_of[eids[i]];
+        refresh(L, s);
+        out_slots[i] = (uint32_t)s;
+    }
+    count_runs(L, miss_eids, n_miss);
+    return n_miss;
+}
+
+/* Returns the number of experts fetched; fetch_eids/fetch_slots (<= 32) in insertion order. */
+int o_layer_start_prefetch(int l, const int32_t *preds, int n, int max_fetch,
+                           int32_t *fetch_eids, int32_t *fetch_slots) {
+    if (l < 0 || l >= O_MAX_LAYERS) return 0;
+    OLayer *L = &g_o[l];
+    memset(L->snap_resident, 0, sizeof(L->snap_resident));
+    memset(L->snap_pred, 0, sizeof(L->snap_pred));
+    memset(L->snap_fetched, 0, sizeof(L->snap_fetched));
+    for (int e = 0; e < O_NUM_EXPERTS; ++e)
+        if (L->slot_of[e] >= 0) bm_set(L->snap_resident, e);
+    L->snap_valid = 1;
+    int cap = (max_fetch > 0 && max_fetch < 32) ? max_fetch : 32;
+    uint64_t protect[8] = {0};
+    int32_t pick[32];
+    int np = 0;
+    for (int i = 0; i < n; ++i) {
+        int e = preds[i];
+        if (e < 0 || e >= O_NUM_EXPERTS) continue;
+        bm_set(L->snap_pred, e);
+        bm_set(protect, e);
+        if (L->slot_of[e] < 0 && np < cap) {
+            pick[np++] = e;
+            bm_set(L->snap_fetched, e);
+        }
+    }
+    for (int i = 0; i < np; ++i) {
+        int e = pick[np - 1 - i];
+        int s = take_slot(L, protect);
+        bind(L, e, s);
+        fetch_eids[i] = e;
+        fetch_slots[i] = s;
+    }
+    L->st[5] += (uint64_t)np * L->expert_bytes;
+    count_runs(L, fetch_eids, np);
+    return np;
+}
+
+void o_layer_load_sync(int l, const int32_t *eids, const int32_t *slots, int n, int is_prefill) {
+    (void)slots;
+    if (l < 0 || l >= O_MAX_LAYERS || n <= 0) return;
+    OLayer *L = &g_o[l];
+    if (is_prefill) L->st[9] += (uint64_t)n * L->expert_bytes;
+    count_runs(L, eids, n);
+}
+
+void o_layer_get_lru_state(int l, int32_t *eids, int32_t *slots, int *count) {
+    if (l < 0 || l >= O_MAX_LAYERS) { *count = 0; return; }
+    OLayer *L = &g_o[l];
+    int c = 0;
+    for (int s = L->lru_end; s >= 0; s = L->newer[s]) { eids[c] = L->eid_of[s]; slots[c] = s; ++c; }
+    *count = c;
+}
+
+void o_layer_set_lru_state(int l, const int32_t *eids, const int32_t *slots, int n,
+                           uint64_t add_req, uint64_t add_hits, uint64_t add_miss) {
+    if (l < 0 || l >= O_MAX_LAYERS) return;
+    OLayer *L = &g_o[l];
+    L->st[6] += add_req; L->st[7] += add_hits; L->st[8] += add_miss;
+    for (int i = 0; i < O_NUM_EXPERTS; ++i) L->slot_of[i] = L->eid_of[i] = L->older[i] = L->newer[i] = -1;
+    L->lru_end = L->mru_end = -1;
+    L->snap_valid = 0;
+    uint8_t used[O_NUM_EXPERTS] = {0};
+    for (int i = 0; i < n; ++i) { used[slots[i]] = 1; bind(L, eids[i], slots[i]); }
+    L->n_free = 0;
+    for (int s = L->capacity - 1; s >= 0; --s) if (!used[s]) L->free_stack[L->n_free++] = (int16_t)s;
+}
+
+void o_layer_get_stats(int l, uint64_t *out) {
+    if (l < 0 || l >= O_MAX_LAYERS) return;
+    memcpy(out, g_o[l].st, sizeof(g_o[l].st));
+}
+
+void o_get_decode_totals(int num_layers, uint64_t *out6) {
+    uint64_t t[6] = {0};
+    if (num_layers > O_MAX_LAYERS) num_layers = O_MAX_LAYERS;
+    for (int l = 1; l < num_layers; ++l) {
+        const uint64_t *st = g_o[l].st;
+        t[0] += st[1]; t[1] += st[2]; t[2] += st[3]; t[3] += st[0]; t[4] += st[4]; t[5] += st[5];
+    }
+    memcpy(out6, t, sizeof(t));
+}

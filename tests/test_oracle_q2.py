@@ -1,0 +1,177 @@
+"""The numpy oracle against the reference's golden vectors and closed forms (CPU only)."""
+import numpy as np
+import pytest
+
+from oracle import q2
+
+
+def _bf(d, name):
+    return q2.to_f64(d[name], "bf16")
+
+
+def _router_w(d, prefix="moe.gate"):
+    return q2.dequantize(d[f"{prefix}.weight"], d[f"{prefix}.scales"], d[f"{prefix}.biases"], 8, 64, "bf16")
+
+
+@pytest.mark.parametrize("xname,iname,sname", [("moe.x_dec", "moe.inds_dec", "moe.scores_dec"),
+                                               ("moe.x_pre", "moe.inds_pre", "moe.scores_pre")])
+def test_router_ids_exact_against_golden(golden_moe, xname, iname, sname):
+    d = golden_moe
+    x = _bf(d, xname).reshape(-1, 256)
+    logits = q2.round_to(x @ _router_w(d).T, "bf16")
+    inds, scores, _ = q2.route(logits, 4, "bf16")
+    ref_i = d[iname].reshape(-1, 4)
+    assert np.array_equal(inds, ref_i), "router ids and their order must match the fixture exactly"
+
+
+def test_router_scores_against_golden(golden_moe):
+    """scores are bit-exact on 20 of 21 rows; the 21st (prefill row 12) is explained exactly by
+    one router logit that MLX's 8-bit quantized matmul rounds one bf16 ulp below the correctly
+    rounded value (0.42 ulp from the true dot product): moving that logit by one ulp makes the
+    row bit-exact too."""
+    d = golden_moe
+    W = _router_w(d)
+    rows = 0
+    for xname, sname in [("moe.x_dec", "moe.scores_dec"), ("moe.x_pre", "moe.scores_pre")]:
+        x = _bf(d, xname).reshape(-1, 256)
+        logits = q2.round_to(x @ W.T, "bf16")
+        _, scores, _ = q2.route(logits, 4, "bf16")
+        ref = _bf(d, sname).reshape(-1, 4)
+        ok = (scores == ref).all(axis=1)
+        rows += int(ok.sum())
+        for t in np.nonzero(~ok)[0]:
+            assert xname == "moe.x_pre" and t == 12
+            l = logits[t].copy()
+            l[2] -= 2.0 ** (np.floor(np.log2(abs(l[2]))) - 7)
+            _, s2, _ = q2.route(l[None], 4, "bf16")
+            assert np.array_equal(s2[0], ref[t])
+    assert rows == 20
+
+
+def test_score_sum_rule_is_sequential(golden_moe):
+    """Negative control: one exact sum rounded once reproduces fewer rows than the
+    left-to-right rounded sum used by the oracle."""
+    d = golden_moe
+    x = _bf(d, "moe.x_pre").reshape(-1, 256)
+    logits = q2.round_to(x @ _router_w(d).T, "bf16")
+    inds, scores, gates = q2.route(logits, 4, "bf16")
+    g = np.take_along_axis(gates, inds.astype(np.int64), -1)
+    once = q2.round_to(g / q2.round_to(g.sum(-1, keepdims=True), "bf16"), "bf16")
+    ref = _bf(d, "moe.scores_pre").reshape(-1, 4)
+    assert (scores == ref).all(1).sum() > (once == ref).all(1).sum()
+
+
+@pytest.mark.parametrize("which", ["nowrite", "write"])
+def test_predictor_against_golden(golden_moe, which):
+    d = golden_moe
+    W = _router_w(d, "pred_next.gate")
+    m = _bf(d, f"hc.r1.m_{which}").reshape(-1)
+    logits = q2.round_to(m @ W.T, "bf16")
+    got = q2.predict_topm(logits[None], 12).ravel()
+    assert np.array_equal(got, d[f"pred_next.top12_{which}"].ravel().astype(np.int32))
+
+
+def _expert(d, e):
+    t = lambda p: (d[f"moe.switch_{p}.weight"][e], d[f"moe.switch_{p}.scales"][e], d[f"moe.switch_{p}.biases"][e])
+    return t("gate"), t("up"), t("down")
+
+
+@pytest.mark.parametrize("suffix", ["dec", "pre"])
+def test_switch_glu_against_golden(golden_moe, suffix):
+    """Routed SwitchGLU + weighted combine + shared expert output vs `moe.y_*`, at the
+    reference's own gather_qmm-vs-dequant tolerance (test_prefill_qproj.py:106: 0.02*max|ref|)."""
+    d = golden_moe
+    X = _bf(d, f"moe.x_{suffix}").reshape(-1, 256)
+    I = d[f"moe.inds_{suffix}"].reshape(-1, 4)
+    S = _bf(d, f"moe.scores_{suffix}").reshape(-1, 4)
+    SH = _bf(d, f"moe.sh_{suffix}").reshape(-1, 256)
+    Y = _bf(d, f"moe.y_{suffix}").reshape(-1, 256)
+    out = np.stack([q2.moe_combine(X[t], I[t], S[t], lambda e: _expert(d, e), bits=2, group=64,
+                                   sdtype="bf16", act_dtype="bf16") + SH[t] for t in range(len(X))])
+    err = np.abs(q2.round_to(out, "bf16") - Y).max()
+    assert err <= 0.02 * np.abs(Y).max()
+    # negative control: dropping the bias term breaks the match by a wide margin
+    def no_bias(e):
+        return tuple((w, s, np.zeros_like(b)) for (w, s, b) in _expert(d, e))
+    bad = np.stack([q2.moe_combine(X[t], I[t], S[t], no_bias, bits=2, group=64, sdtype="bf16")
+                    + SH[t] for t in range(len(X))])
+    assert np.abs(bad - Y).max() > 5 * 0.02 * np.abs(Y).max()
+
+
+def test_codes_pack_roundtrip_and_lsb_first():
+    rng = np.random.default_rng(0)
+    q = rng.integers(0, 4, size=(3, 64)).astype(np.uint8)
+    w = q2.pack_codes(q, 2)
+    assert w.shape == (3, 4)
+    assert np.array_equal(q2.unpack_codes(w, 2), q)
+    # code j sits at bits 2j..2j+1: a word with only code 0 == 3 is the integer 3
+    one = np.zeros((1, 16), np.uint8)
+    one[0, 0] = 3
+    assert q2.pack_codes(one, 2)[0, 0] == 3
+    one[0, 0], one[0, 15] = 0, 1
+    assert q2.pack_codes(one, 2)[0, 0] == 1 << 30
+
+
+def test_dequant_closed_form():
+    # W = s*q + b: for codes 0..3 in every group, the dequantised row is s*[0,1,2,3,...] + b
+    q = np.tile(np.arange(4, dtype=np.uint8), 32)[None]          # 1 row, 128 inputs, 2 groups
+    w = q2.pack_codes(q, 2)
+    s = np.array([[0.5, -2.0]], np.float16)
+    b = np.array([[1.0, 0.25]], np.float16)
+    W = q2.dequantize(w, s, b, 2, 64)
+    want = np.concatenate([0.5 * np.tile(np.arange(4), 16) + 1.0, -2.0 * np.tile(np.arange(4), 16) + 0.25])
+    assert np.array_equal(W[0], want)
+    # qmatvec == brute-force double loop
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(128)
+    y = q2.qmatvec(x, w, s, b, 2, 64)
+    assert np.isclose(y[0], sum(x[i] * want[i] for i in range(128)))
+
+
+def test_topk_tie_rule_bruteforce():
+    """Stable ascending order: equal values keep ascending index; at the k boundary the higher
+    index wins; the predictor emits descending values, equal values in ascending index."""
+    v = np.array([1.0, 3.0, 2.0, 3.0, 2.0, 0.5])
+    assert q2.topk_ascending(v, 3).tolist() == [4, 1, 3]           # 2.0@4 beats 2.0@2
+    assert q2.predict_topm(v[None], 3)[0].tolist() == [1, 3, 4]
+    # brute force against a lexicographic (value, index) ordering on random small ties
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        v = rng.integers(0, 4, size=9).astype(np.float64)
+        k = int(rng.integers(1, 9))
+        keys = sorted(range(9), key=lambda i: (v[i], i))
+        assert q2.topk_ascending(v, k).tolist() == keys[-k:]
+        top = keys[-k:]
+        assert q2.predict_topm(v[None], k)[0].tolist() == sorted(top, key=lambda i: (-v[i], i))
+
+
+def test_round_to_fp16_matches_numpy_and_bf16_rne():
+    x = np.array([1.0, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, 65504.0, 1e-8])
+    assert np.array_equal(q2.round_to(x, "f16"), x.astype(np.float32).astype(np.float16).astype(np.float64))
+    # bf16 ties to even: 1 + 2^-8 is halfway between 1 and 1 + 2^-7 -> 1
+    assert q2.round_to(np.array([1.0 + 2 ** -8]), "bf16")[0] == 1.0
+    assert q2.round_to(np.array([1.0 + 3 * 2 ** -8]), "bf16")[0] == 1.0 + 2 ** -6
+
+
+def test_prefill_plan_reference_shapes():
+    """Chunk/slot bookkeeping on the reference test's shapes (test_prefill_qproj.py:80-81):
+    slots are ranks within each chunk, every chunk slot < capacity, the rebuilt LRU is a
+    bijection with the last chunk's slots newest, and hit/miss accounting sums to M."""
+    rng = np.random.default_rng(0)
+    shapes = [(63, 19), (190, 55), (404, 102), (128, 33), (99, 26), (22, 9), (73, 25), (372, 102),
+              (61, 17), (80, 25), (587, 102), (246, 39), (64, 16), (2000, 90), (5, 2), (1500, 102)]
+    for rows, ne in shapes:
+        ids = rng.permutation(np.concatenate([np.arange(ne), rng.integers(0, ne, rows - ne)]))
+        prior = rng.choice(512, size=30, replace=False)
+        plan = q2.prefill_plan(ids + 100, list(prior), list(range(30)), 102)
+        assert plan["add_req"] == rows
+        new_e, new_s = plan["new_lru"]
+        assert len(set(new_s)) == len(new_s) and len(set(new_e)) == len(new_e)
+        assert all(0 <= s < 102 for s in new_s)
+        last = plan["chunks"][-1]
+        n_last = last[1] - last[0]
+        assert sorted(new_s[-n_last:]) == list(range(n_last))
+        assert new_e[-n_last:] == [int(e) for e in plan["uniq"][last[0]:last[1]]]
+        misses = len(set(int(e) for e in ids + 100) - set(int(p) for p in prior))
+        assert plan["add_misses"] == misses and plan["add_hits"] == rows - misses
+        assert q2.k_hdr(rows, 102) == max(1, min(102, max(rows, 16) // 4))
