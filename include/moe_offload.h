@@ -1,0 +1,147 @@
+/*
+ * moe_offload.h -- C-ABI of libmoe_offload.so, the MI355X (gfx950) routed-expert decode path.
+ *
+ * Part 1 replaces the reference's native expert cache, mlx-qwen38/expert_io.c, symbol for
+ * symbol (the ctypes bindings of mlx-qwen38/loader.py:100-220 bind them unchanged).  Part 2 is
+ * the compute the reference gets from MLX built-ins (gather_qmm, softmax, argpartition), as
+ * hand-written HIP kernels.  Part 3 has no counterpart in the reference (device-driven slot
+ * tables, streams, pinned host memory, error reporting).
+ *
+ * Conventions: plain pointers and sizes only.  Device pointers are HIP device addresses
+ * (e.g. torch tensors' data_ptr()); `stream` is a hipStream_t (0 = null stream).  As in the
+ * reference, entry points given an out-of-range layer return silently; every other failure is
+ * recorded and reported by c_last_error() (int-returning entry points also return -1).
+ */
+#ifndef MOE_OFFLOAD_H
+#define MOE_OFFLOAD_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- Part 1: expert cache (expert_io.c) -------------------------------------------------- */
+
+/* expert_io.c:430-448.  Creates the copy stream; num_threads is accepted and unused (copies go
+ * to the DMA engines). */
+void c_io_init(int num_threads);
+/* cpp/src/expert_io.h:15 (superset ABI).  Drains copies and releases every layer. */
+void c_io_shutdown(void);
+/* expert_io.c:497-520.  fd == -1: base_offsets[t] are host addresses of tensor t's expert store
+ * (pinned via c_host_alloc for overlap / device staging); fd >= 0: file offsets as in the
+ * reference.  base_ptrs[t] are device slot pools; slot_inds_ptr receives slot ids (device or
+ * host memory).  capacity in 1..512. */
+void c_layer_init(int layer_idx, int fd, int capacity, const uint64_t* base_offsets,
+                  const uint64_t* row_bytes, const uint64_t* base_ptrs, uint64_t slot_inds_ptr);
+/* expert_io.c:450-468 */
+void c_layer_reset_cache(int layer_idx);
+/* expert_io.c:470-495 */
+void c_layer_reset_stats(int layer_idx);
+/* expert_io.c:583-685.  Returns the number of demand misses; writes k slot ids to slot_inds.
+ * async_io != 0 leaves the copies in flight (join: c_layer_wait_prefetch). k in 1..16. */
+int c_layer_step_decode_ex(int layer_idx, const uint32_t* eids, int k, int async_io);
+/* expert_io.c:687-689 (synchronous) */
+int c_layer_step_decode(int layer_idx, const uint32_t* eids, int k);
+/* expert_io.c:692-699 */
+int c_layer_step_decode10(int layer_idx, uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3,
+                          uint32_t e4, uint32_t e5, uint32_t e6, uint32_t e7, uint32_t e8,
+                          uint32_t e9);
+/* expert_io.c:701-708 */
+int c_layer_step_decode10_async(int layer_idx, uint32_t e0, uint32_t e1, uint32_t e2,
+                                uint32_t e3, uint32_t e4, uint32_t e5, uint32_t e6, uint32_t e7,
+                                uint32_t e8, uint32_t e9);
+/* expert_io.c:527-581.  n <= 32. */
+void c_layer_start_prefetch(int layer_idx, const int32_t* pred_eids, int pred_count, int max_fetch);
+/* expert_io.c:814-822 */
+void c_layer_start_prefetch10(int layer_idx, int max_fetch, int32_t e0, int32_t e1, int32_t e2,
+                              int32_t e3, int32_t e4, int32_t e5, int32_t e6, int32_t e7,
+                              int32_t e8, int32_t e9);
+/* expert_io.c:824-832 */
+void c_layer_start_prefetch12(int layer_idx, int max_fetch, int32_t e0, int32_t e1, int32_t e2,
+                              int32_t e3, int32_t e4, int32_t e5, int32_t e6, int32_t e7,
+                              int32_t e8, int32_t e9, int32_t e10, int32_t e11);
+/* expert_io.c:522-525.  Joins every in-flight copy on the GPU side: the compute stream waits;
+ * the host does not block (c_sync_copies blocks). */
+void c_layer_wait_prefetch(int layer_idx);
+/* expert_io.c:710-724.  Blocking copy of (eid -> slot) pairs; counts prefill bytes. */
+void c_layer_load_sync(int layer_idx, const int32_t* eids, const int32_t* slots, int count,
+                       int is_prefill);
+/* expert_io.c:726-747.  LRU -> MRU order. */
+void c_layer_get_lru_state(int layer_idx, int32_t* out_eids, int32_t* out_slots, int* out_count);
+/* expert_io.c:749-789 */
+void c_layer_set_lru_state(int layer_idx, const int32_t* ordered_eids, const int32_t* ordered_slots,
+                           int count, uint64_t add_prefill_requests, uint64_t add_prefill_hits,
+                           uint64_t add_prefill_misses);
+/* expert_io.c:791-812.  out[18]; byte counters use the layer's real expert bytes. */
+void c_layer_get_stats(int layer_idx, uint64_t* out_stats);
+/* expert_io.c:834-852.  out[6] summed over layers 1..num_layers-1. */
+void c_get_decode_totals(int num_layers, uint64_t* out6);
+
+/* ---- Part 2: compute (MLX built-ins of the reference) ------------------------------------- */
+
+/* loader.py:903-908 + loader.py:237-242,950-958 (cpp/src/layers.cpp:311-341).  Optional
+ * RMSNorm of an fp32 residual h_in (norm_w fp16, may be null) into x_out, else fp16 x_in;
+ * logits = x.W^T (fp16 [n_exp][hidden]); softmax; top-k ids (ascending gate) and fp16 scores;
+ * when w_next != null, the next layer's top-m prediction (descending).  workspace:
+ * moe_router_workspace_bytes(n_exp) bytes of device memory, zeroed once before first use. */
+int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_in, void* x_out,
+               const void* w, const void* w_next, int hidden, int n_exp, int k, int m,
+               void* workspace, uint32_t* ids_out, void* scores_out, int32_t* pred_out,
+               void* stream);
+uint64_t moe_router_workspace_bytes(int n_exp);
+/* Bytes of one Q2 expert blob (layout in csrc/moe_common.h). */
+uint64_t moe_q2_expert_bytes(int hidden, int inter, int group);
+/* gather_qmm gate+up + SwiGLU (loader.py:564, kernels.cpp:1027-1040,1090-1094):
+ * h_out[k][inter] fp16 from x fp16 [hidden] over pool blobs selected by slots[k]; pool holds
+ * n_slots blobs of `stride` bytes (a slot id >= n_slots contributes zeros). */
+int moe_q2_gate_up(const void* x, const void* pool, uint64_t stride, int n_slots,
+                   const uint32_t* slots, int k, int hidden, int inter, int group, void* h_out,
+                   void* stream);
+/* gather_qmm down + weighted combine (loader.py:964-965): y_out fp32 [hidden] =
+ * residual + sum_j scores[j] * down_j(h_j), or per-expert rows y_out[k][hidden]. */
+int moe_q2_down(const void* h, const void* pool, uint64_t stride, int n_slots,
+                const uint32_t* slots, const void* scores, int k, int hidden, int inter, int group,
+                const void* residual, float* y_out, int per_expert, void* stream);
+/* Both of the above (h_ws: k*inter fp16 workspace). */
+int moe_q2_switch_glu(const void* x, const void* pool, uint64_t stride, int n_slots,
+                      const uint32_t* slots, const void* scores, int k, int hidden, int inter,
+                      int group, const void* residual, void* h_ws, float* y_out, int per_expert,
+                      void* stream);
+
+/* ---- Part 3: no counterpart in the reference ----------------------------------------------- */
+
+/* Last recorded failure ("" if none) / clear it. */
+const char* c_last_error(void);
+void c_clear_error(void);
+/* Stream that Part-1 entry points order their slot-id writes and waits on. */
+int c_set_compute_stream(void* stream);
+/* Pinned, device-mapped host memory for expert stores. */
+void* c_host_alloc(uint64_t bytes);
+int c_host_free(void* p);
+/* Declare tensor 0 of a layer as a Q2 blob pool (row_bytes[0] == moe_q2_expert_bytes). */
+int c_layer_set_format(int layer_idx, int hidden, int inter, int group);
+/* SwitchGLU over the layer's pool with its current slot ids; orders after pending copies. */
+int c_layer_switch_glu(int layer_idx, const void* x, const void* scores, const void* residual,
+                       void* h_ws, float* y_out, int per_expert, int k, void* stream);
+/* Move a layer's slot table to device memory (on != 0) or back.  Device-driven layers take
+ * their ids from device memory and stage misses with a kernel that reads the pinned store. */
+int c_layer_set_device_mode(int layer_idx, int on);
+/* Device-driven decode step / prefetch (same decisions as c_layer_step_decode_ex /
+ * c_layer_start_prefetch), queued on `stream`; stage_ctas <= 0 picks a default grid. */
+int c_layer_step_decode_dev(int layer_idx, const uint32_t* ids_dev, int k, int stage_ctas,
+                            void* stream);
+int c_layer_start_prefetch_dev(int layer_idx, const int32_t* preds_dev, int m, int max_fetch,
+                               int stage_ctas, void* stream);
+/* Device address of a device-driven layer's table; 0 otherwise. */
+uint64_t c_layer_device_table(int layer_idx);
+/* Status word of the last device-side operation (0 ok, 1 id out of range, 2 repeated id);
+ * blocks.  (The reference accepts repeated ids and leaks a slot; both paths here reject them.) */
+int c_layer_table_status(int layer_idx);
+/* Block the host until every queued copy has landed. */
+int c_sync_copies(void);
+int c_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_OFFLOAD_H */

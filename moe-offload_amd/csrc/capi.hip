@@ -1,0 +1,590 @@
+// C-ABI of libmoe_offload: the expert-cache entry points of mlx-qwen38/expert_io.c
+// (same names, argument meaning and silent-ignore behaviour for out-of-range layers), plus the
+// gfx950 compute entry points of the routed-expert decode path.  Declarations with the
+// reference interface each one replaces are in include/moe_offload.h.
+//
+// Storage tiers.  The reference reads experts from an SSD file into slot buffers in unified
+// memory.  Here a layer's pool is device memory (HBM) and its experts live in a host expert
+// store; `c_layer_init` keeps the reference signature:
+//   fd == -1 : base_offsets[t] are host addresses of tensor t's store (expert e at
+//              base_offsets[t] + e * row_bytes[t]); pinned memory (c_host_alloc) is required
+//              for overlap and for device-driven staging.
+//   fd >= 0  : base_offsets[t] are file offsets, as in the reference; reads go through a
+//              pinned bounce buffer (host-driven staging only).
+//   base_ptrs[t] : device address of tensor t's slot pool (slot s at + s * row_bytes[t]).
+//   A tensor with row_bytes > 0 but a zero source or destination is accounting-only.
+//
+// Ordering (host-driven layers).  Copies run on a library-owned non-blocking stream.  Before
+// copying into a layer's pool the copy stream waits for the last kernel that read it (WAR);
+// before a kernel reads the pool the compute stream waits for the copies (RAW).  Waiting is
+// GPU-side: c_layer_wait_prefetch makes the compute stream wait for every pending copy and
+// returns without blocking the host; the synchronous calls (c_layer_step_decode,
+// c_layer_load_sync) also block the host until their copies have landed.
+#include <hip/hip_fp16.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <unistd.h>
+
+#include <mutex>
+
+#include "moe_common.h"
+#include "slot_table_host.h"
+
+namespace {
+
+struct LayerState {
+    bool init = false;
+    int fd = -1;
+    int capacity = 0;
+    uint64_t src[MOE_NUM_TENSORS] = {};
+    uint64_t row_bytes[MOE_NUM_TENSORS] = {};
+    uint64_t dst[MOE_NUM_TENSORS] = {};
+    uint64_t dev_src[MOE_NUM_TENSORS] = {};   // device-visible store addresses (pinned stores)
+    uint32_t* slot_inds = nullptr;
+    bool slot_inds_device = false;
+    SlotTable tab;                            // authoritative for host-driven layers
+    SlotTable* dtab = nullptr;                // authoritative for device-driven layers
+    bool device_mode = false;
+    hipEvent_t copy_done = nullptr, read_done = nullptr;
+    bool copy_pending = false, read_recorded = false;
+    // Q2 blob format of tensor 0 (for c_layer_switch_glu)
+    int hidden = 0, inter = 0, group = 0;
+    uint8_t* bounce = nullptr;                // pinned bounce buffer for file-backed stores
+    size_t bounce_bytes = 0;
+};
+
+LayerState g_layers[MOE_MAX_LAYERS];
+hipStream_t g_compute = nullptr;             // caller's stream (null stream by default)
+hipStream_t g_copy = nullptr;
+bool g_ready = false;
+std::mutex g_err_mu;
+char g_err[1024] = {0};
+
+bool valid_layer(int l) { return l >= 0 && l < MOE_MAX_LAYERS; }
+
+int ensure_runtime() {
+    if (g_ready) return 0;
+    HIP_TRY(hipStreamCreateWithFlags(&g_copy, hipStreamNonBlocking));
+    g_ready = true;
+    return 0;
+}
+
+int ensure_events(LayerState& L) {
+    if (!L.copy_done) HIP_TRY(hipEventCreateWithFlags(&L.copy_done, hipEventDisableTiming));
+    if (!L.read_done) HIP_TRY(hipEventCreateWithFlags(&L.read_done, hipEventDisableTiming));
+    return 0;
+}
+
+uint64_t expert_bytes_of(const LayerState& L) {
+    uint64_t b = 0;
+    for (int t = 0; t < MOE_NUM_TENSORS; ++t) b += L.row_bytes[t];
+    return b;
+}
+
+// Pull a device-mode table back to the host copy (blocking) / push the host copy to device.
+int pull_table(LayerState& L) {
+    if (!L.device_mode) return 0;
+    HIP_TRY(hipMemcpyAsync(&L.tab, L.dtab, sizeof(SlotTable), hipMemcpyDeviceToHost, g_compute));
+    HIP_TRY(hipStreamSynchronize(g_compute));
+    return 0;
+}
+
+int push_table(LayerState& L) {
+    if (!L.device_mode) return 0;
+    HIP_TRY(hipMemcpyAsync(L.dtab, &L.tab, sizeof(SlotTable), hipMemcpyHostToDevice, g_compute));
+    HIP_TRY(hipStreamSynchronize(g_compute));
+    return 0;
+}
+
+// Read `n` bytes of a file at `off` fully (short reads retried; errors reported).
+int pread_full(int fd, uint8_t* buf, size_t n, uint64_t off) {
+    while (n > 0) {
+        ssize_t r = pread(fd, buf, n, (off_t)off);
+        if (r <= 0) {
+            moe_set_error("pread(fd=%d, off=%llu) failed or hit end of file", fd, (unsigned long long)off);
+            return -1;
+        }
+        buf += r;
+        n -= (size_t)r;
+        off += (uint64_t)r;
+    }
+    return 0;
+}
+
+// Queue the copies store[eid] -> pool[slot] for every tensor on the copy stream.
+int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* slots, int n) {
+    if (n <= 0) return 0;
+    bool any = false;
+    for (int t = 0; t < MOE_NUM_TENSORS; ++t) any |= (L.row_bytes[t] && L.src[t] && L.dst[t]);
+    if (!any) return 0;                       // accounting-only layer
+    if (ensure_runtime()) return -1;
+    if (ensure_events(L)) return -1;
+    if (L.read_recorded) HIP_TRY(hipStreamWaitEvent(g_copy, L.read_done, 0));
+    if (L.fd >= 0) {
+        size_t need = (size_t)n * expert_bytes_of(L);
+        if (need > L.bounce_bytes) {
+            HIP_TRY(hipStreamSynchronize(g_copy));
+            if (L.bounce) HIP_TRY(hipHostFree(L.bounce));
+            L.bounce = nullptr;
+            HIP_TRY(hipHostMalloc((void**)&L.bounce, need, hipHostMallocDefault));
+            L.bounce_bytes = need;
+        } else if (L.copy_pending) {
+            // the bounce buffer is reused: earlier copies out of it must have finished
+            HIP_TRY(hipEventSynchronize(L.copy_done));
+        }
+        size_t off = 0;
+        for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
+            uint64_t rb = L.row_bytes[t];
+            if (!rb || !L.dst[t]) continue;
+            for (int i = 0; i < n; ++i) {
+                if (pread_full(L.fd, L.bounce + off, rb, L.src[t] + (uint64_t)eids[i] * rb)) return -1;
+                HIP_TRY(hipMemcpyAsync((void*)(L.dst[t] + (uint64_t)slots[i] * rb), L.bounce + off, rb,
+                                       hipMemcpyHostToDevice, g_copy));
+                off += rb;
+            }
+        }
+    } else {
+        for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
+            uint64_t rb = L.row_bytes[t];
+            if (!rb || !L.src[t] || !L.dst[t]) continue;
+            for (int i = 0; i < n; ++i)
+                HIP_TRY(hipMemcpyAsync((void*)(L.dst[t] + (uint64_t)slots[i] * rb),
+                                       (const void*)(L.src[t] + (uint64_t)eids[i] * rb), rb,
+                                       hipMemcpyHostToDevice, g_copy));
+        }
+    }
+    HIP_TRY(hipEventRecord(L.copy_done, g_copy));
+    L.copy_pending = true;
+    (void)layer;
+    return 0;
+}
+
+int wait_copies_gpu(LayerState& L, hipStream_t s) {
+    if (!L.copy_pending) return 0;
+    HIP_TRY(hipStreamWaitEvent(s, L.copy_done, 0));
+    L.copy_pending = false;
+    return 0;
+}
+
+int write_slot_inds(LayerState& L, const uint32_t* slots, int k) {
+    if (!L.slot_inds) return 0;
+    if (L.slot_inds_device) return launch_store_u32(L.slot_inds, slots, k, g_compute);
+    memcpy(L.slot_inds, slots, (size_t)k * sizeof(uint32_t));
+    return 0;
+}
+
+int step_host(int layer, const uint32_t* eids, int k, int async_io) {
+    LayerState& L = g_layers[layer];
+    if (!L.init) { moe_set_error("layer %d not initialised", layer); return -1; }
+    if (k <= 0 || k > MOE_MAX_K || k > L.capacity) {
+        moe_set_error("step: k=%d must be in 1..%d and <= capacity %d", k, MOE_MAX_K, L.capacity);
+        return -1;
+    }
+    for (int i = 0; i < k; ++i) {
+        if (eids[i] >= MOE_NUM_EXPERTS) { moe_set_error("step: expert id %u out of range", eids[i]); return -1; }
+        for (int j = 0; j < i; ++j)
+            if (eids[j] == eids[i]) { moe_set_error("step: expert id %u repeated", eids[i]); return -1; }
+    }
+    if (pull_table(L)) return -1;
+    uint32_t out[MOE_MAX_K];
+    int n_miss = slot_host::step(&L.tab, eids, k, out);
+    if (push_table(L)) return -1;
+    if (write_slot_inds(L, out, k)) return -1;
+    if (issue_copies(layer, L, L.tab.copy_eid, L.tab.copy_slot, L.tab.n_copy)) return -1;
+    if (!async_io && L.copy_pending) HIP_TRY(hipEventSynchronize(L.copy_done));
+    return n_miss;
+}
+
+}  // namespace
+
+void moe_set_error(const char* fmt, ...) {
+    std::lock_guard<std::mutex> g(g_err_mu);
+    if (g_err[0]) return;                     // keep the first failure
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+extern "C" {
+
+// ---- errors, streams, host memory ---------------------------------------------------------
+
+const char* c_last_error(void) { return g_err; }
+
+void c_clear_error(void) {
+    std::lock_guard<std::mutex> g(g_err_mu);
+    g_err[0] = 0;
+}
+
+int c_set_compute_stream(void* stream) {
+    g_compute = (hipStream_t)stream;
+    return 0;
+}
+
+void* c_host_alloc(uint64_t bytes) {
+    void* p = nullptr;
+    hipError_t e = hipHostMalloc(&p, (size_t)bytes, hipHostMallocMapped);
+    if (e != hipSuccess) {
+        moe_set_error("hipHostMalloc(%llu) -> %s", (unsigned long long)bytes, hipGetErrorString(e));
+        return nullptr;
+    }
+    return p;
+}
+
+int c_host_free(void* p) {
+    if (p) HIP_TRY(hipHostFree(p));
+    return 0;
+}
+
+// ---- expert_io.c entry points ---------------------------------------------------------------
+
+void c_io_init(int num_threads) {
+    // Copies are queued to the DMA engines, not worker threads; the copy stream is created on
+    // first use so that accounting-only tables work without a GPU.
+    (void)num_threads;
+}
+
+void c_io_shutdown(void) {
+    if (!g_ready) return;
+    (void)hipStreamSynchronize(g_copy);
+    for (int l = 0; l < MOE_MAX_LAYERS; ++l) {
+        LayerState& L = g_layers[l];
+        if (L.bounce) (void)hipHostFree(L.bounce);
+        if (L.dtab) (void)hipFree(L.dtab);
+        if (L.copy_done) (void)hipEventDestroy(L.copy_done);
+        if (L.read_done) (void)hipEventDestroy(L.read_done);
+        L = LayerState();
+    }
+    (void)hipStreamDestroy(g_copy);
+    g_copy = nullptr;
+    g_ready = false;
+}
+
+void c_layer_reset_cache(int layer) {
+    if (!valid_layer(layer)) return;
+    LayerState& L = g_layers[layer];
+    if (pull_table(L)) return;
+    slot_host::reset_cache(&L.tab);
+    push_table(L);
+}
+
+void c_layer_reset_stats(int layer) {
+    if (!valid_layer(layer)) return;
+    LayerState& L = g_layers[layer];
+    if (pull_table(L)) return;
+    slot_host::reset_stats(&L.tab);
+    push_table(L);
+}
+
+void c_layer_init(int layer, int fd, int capacity, const uint64_t* base_offsets, const uint64_t* row_bytes,
+                  const uint64_t* base_ptrs, uint64_t slot_inds_ptr) {
+    if (!valid_layer(layer)) return;
+    if (capacity < 1 || capacity > MOE_NUM_EXPERTS) {
+        moe_set_error("c_layer_init: capacity %d out of range 1..%d", capacity, MOE_NUM_EXPERTS);
+        return;
+    }
+    LayerState& L = g_layers[layer];
+    if (L.copy_pending) (void)hipEventSynchronize(L.copy_done);
+    if (L.bounce) (void)hipHostFree(L.bounce);
+    if (L.dtab) (void)hipFree(L.dtab);
+    hipEvent_t cd = L.copy_done, rd = L.read_done;
+    L = LayerState();
+    L.copy_done = cd;
+    L.read_done = rd;
+    L.fd = fd;
+    L.capacity = capacity;
+    for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
+        L.src[t] = base_offsets ? base_offsets[t] : 0;
+        L.row_bytes[t] = row_bytes ? row_bytes[t] : 0;
+        L.dst[t] = base_ptrs ? base_ptrs[t] : 0;
+        L.dev_src[t] = 0;
+        if (fd < 0 && L.src[t]) {
+            void* dp = nullptr;
+            if (hipHostGetDevicePointer(&dp, (void*)L.src[t], 0) == hipSuccess) L.dev_src[t] = (uint64_t)dp;
+            else (void)hipGetLastError();
+        }
+    }
+    L.slot_inds = (uint32_t*)slot_inds_ptr;
+    L.slot_inds_device = false;
+    if (L.slot_inds) {
+        hipPointerAttribute_t a;
+        if (hipPointerGetAttributes(&a, L.slot_inds) == hipSuccess) L.slot_inds_device = (a.type == hipMemoryTypeDevice);
+        else (void)hipGetLastError();
+    }
+    slot_host::init(&L.tab, capacity, expert_bytes_of(L));
+    L.init = true;
+}
+
+int c_layer_step_decode_ex(int layer, const uint32_t* eids, int k, int async_io) {
+    if (!valid_layer(layer)) return 0;
+    return step_host(layer, eids, k, async_io);
+}
+
+int c_layer_step_decode(int layer, const uint32_t* eids, int k) {
+    return c_layer_step_decode_ex(layer, eids, k, 0);
+}
+
+int c_layer_step_decode10(int layer, uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, uint32_t e4,
+                          uint32_t e5, uint32_t e6, uint32_t e7, uint32_t e8, uint32_t e9) {
+    uint32_t e[10] = {e0, e1, e2, e3, e4, e5, e6, e7, e8, e9};
+    return c_layer_step_decode_ex(layer, e, 10, 0);
+}
+
+int c_layer_step_decode10_async(int layer, uint32_t e0, uint32_t e1, uint32_t e2, uint32_t e3, uint32_t e4,
+                                uint32_t e5, uint32_t e6, uint32_t e7, uint32_t e8, uint32_t e9) {
+    uint32_t e[10] = {e0, e1, e2, e3, e4, e5, e6, e7, e8, e9};
+    return c_layer_step_decode_ex(layer, e, 10, 1);
+}
+
+void c_layer_start_prefetch(int layer, const int32_t* preds, int n, int max_fetch) {
+    if (!valid_layer(layer)) return;
+    LayerState& L = g_layers[layer];
+    if (!L.init) { moe_set_error("layer %d not initialised", layer); return; }
+    if (n < 0 || n > MOE_MAX_PREFETCH) { moe_set_error("prefetch: %d predictions (max %d)", n, MOE_MAX_PREFETCH); return; }
+    if (pull_table(L)) return;
+    slot_host::prefetch(&L.tab, preds, n, max_fetch);
+    if (push_table(L)) return;
+    issue_copies(layer, L, L.tab.copy_eid, L.tab.copy_slot, L.tab.n_copy);
+}
+
+void c_layer_start_prefetch10(int layer, int max_fetch, int32_t e0, int32_t e1, int32_t e2, int32_t e3,
+                              int32_t e4, int32_t e5, int32_t e6, int32_t e7, int32_t e8, int32_t e9) {
+    int32_t p[10] = {e0, e1, e2, e3, e4, e5, e6, e7, e8, e9};
+    c_layer_start_prefetch(layer, p, 10, max_fetch);
+}
+
+void c_layer_start_prefetch12(int layer, int max_fetch, int32_t e0, int32_t e1, int32_t e2, int32_t e3,
+                              int32_t e4, int32_t e5, int32_t e6, int32_t e7, int32_t e8, int32_t e9,
+                              int32_t e10, int32_t e11) {
+    int32_t p[12] = {e0, e1, e2, e3, e4, e5, e6, e7, e8, e9, e10, e11};
+    c_layer_start_prefetch(layer, p, 12, max_fetch);
+}
+
+void c_layer_wait_prefetch(int layer) {
+    (void)layer;                              // joins every layer's in-flight copies
+    for (int l = 0; l < MOE_MAX_LAYERS; ++l)
+        if (g_layers[l].init) wait_copies_gpu(g_layers[l], g_compute);
+}
+
+void c_layer_load_sync(int layer, const int32_t* eids, const int32_t* slots, int n, int is_prefill) {
+    if (!valid_layer(layer) || n <= 0) return;
+    LayerState& L = g_layers[layer];
+    if (!L.init) { moe_set_error("layer %d not initialised", layer); return; }
+    for (int i = 0; i < n; ++i)
+        if (eids[i] < 0 || eids[i] >= MOE_NUM_EXPERTS || slots[i] < 0 || slots[i] >= L.capacity) {
+            moe_set_error("load_sync: pair (%d, %d) out of range", eids[i], slots[i]);
+            return;
+        }
+    if (pull_table(L)) return;
+    if (is_prefill) L.tab.stats[ST_PRE_BYTES] += (uint64_t)n * L.tab.expert_bytes;
+    slot_host::count_runs(&L.tab, eids, n);
+    if (push_table(L)) return;
+    if (issue_copies(layer, L, eids, slots, n)) return;
+    if (L.copy_pending) {
+        (void)hipEventSynchronize(L.copy_done);
+        wait_copies_gpu(L, g_compute);
+    }
+}
+
+void c_layer_get_lru_state(int layer, int32_t* out_eids, int32_t* out_slots, int* out_count) {
+    if (!valid_layer(layer)) { *out_count = 0; return; }
+    LayerState& L = g_layers[layer];
+    if (pull_table(L)) { *out_count = 0; return; }
+    *out_count = slot_host::get_state(&L.tab, out_eids, out_slots);
+}
+
+void c_layer_set_lru_state(int layer, const int32_t* eids, const int32_t* slots, int n, uint64_t add_req,
+                           uint64_t add_hits, uint64_t add_miss) {
+    if (!valid_layer(layer)) return;
+    LayerState& L = g_layers[layer];
+    for (int i = 0; i < n; ++i)
+        if (eids[i] < 0 || eids[i] >= MOE_NUM_EXPERTS || slots[i] < 0 || slots[i] >= L.capacity) {
+            moe_set_error("set_lru_state: pair (%d, %d) out of range", eids[i], slots[i]);
+            return;
+        }
+    if (pull_table(L)) return;
+    slot_host::set_state(&L.tab, eids, slots, n, add_req, add_hits, add_miss);
+    push_table(L);
+}
+
+void c_layer_get_stats(int layer, uint64_t* out) {
+    if (!valid_layer(layer)) return;
+    LayerState& L = g_layers[layer];
+    if (pull_table(L)) return;
+    memcpy(out, L.tab.stats, sizeof(L.tab.stats));
+}
+
+void c_get_decode_totals(int num_layers, uint64_t* out6) {
+    uint64_t t[6] = {0};
+    if (num_layers > MOE_MAX_LAYERS) num_layers = MOE_MAX_LAYERS;
+    for (int l = 1; l < num_layers; ++l) {
+        LayerState& L = g_layers[l];
+        if (!L.init) continue;
+        if (pull_table(L)) break;
+        const uint64_t* st = L.tab.stats;
+        t[0] += st[ST_DEC_LRU_HIT];
+        t[1] += st[ST_DEC_PREF_HIT];
+        t[2] += st[ST_DEC_MISS];
+        t[3] += st[ST_DEC_REQ];
+        t[4] += st[ST_DEC_BYTES];
+        t[5] += st[ST_PREF_BYTES];
+    }
+    memcpy(out6, t, sizeof(t));
+}
+
+// ---- device-driven slot tables ----------------------------------------------------------------
+
+int c_layer_set_device_mode(int layer, int on) {
+    if (!valid_layer(layer) || !g_layers[layer].init) { moe_set_error("set_device_mode: bad layer %d", layer); return -1; }
+    LayerState& L = g_layers[layer];
+    if (on && !L.device_mode) {
+        if (L.fd >= 0) { moe_set_error("device-driven staging needs a pinned host store (fd == -1)"); return -1; }
+        for (int t = 0; t < MOE_NUM_TENSORS; ++t)
+            if (L.row_bytes[t] && L.src[t] && L.dst[t] && !L.dev_src[t]) {
+                moe_set_error("device-driven staging: tensor %d store is not pinned host memory", t);
+                return -1;
+            }
+        if (!L.slot_inds || !L.slot_inds_device) { moe_set_error("device-driven layers need a device slot_inds buffer"); return -1; }
+        if (!L.dtab) HIP_TRY(hipMalloc((void**)&L.dtab, sizeof(SlotTable)));
+        L.device_mode = true;
+        return push_table(L);
+    }
+    if (!on && L.device_mode) {
+        if (pull_table(L)) return -1;
+        L.device_mode = false;
+    }
+    return 0;
+}
+
+uint64_t c_layer_device_table(int layer) {
+    if (!valid_layer(layer)) return 0;
+    return (uint64_t)g_layers[layer].dtab;
+}
+
+static int stage_device(LayerState& L, hipStream_t s, int ctas) {
+    for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
+        uint64_t rb = L.row_bytes[t];
+        if (!rb || !L.dev_src[t] || !L.dst[t]) continue;
+        if (launch_stage(L.dtab, (const uint8_t*)L.dev_src[t], rb, (uint8_t*)L.dst[t], rb, rb, ctas, s)) return -1;
+    }
+    return 0;
+}
+
+int c_layer_step_decode_dev(int layer, const uint32_t* ids_dev, int k, int stage_ctas, void* stream) {
+    if (!valid_layer(layer) || !g_layers[layer].init || !g_layers[layer].device_mode) {
+        moe_set_error("step_decode_dev: layer %d is not a device-driven layer", layer);
+        return -1;
+    }
+    LayerState& L = g_layers[layer];
+    if (k <= 0 || k > MOE_MAX_K || k > L.capacity) { moe_set_error("step_decode_dev: k=%d out of range", k); return -1; }
+    hipStream_t s = (hipStream_t)stream;
+    if (launch_slot_step(L.dtab, ids_dev, k, L.slot_inds, s)) return -1;
+    return stage_device(L, s, stage_ctas);
+}
+
+int c_layer_start_prefetch_dev(int layer, const int32_t* preds_dev, int m, int max_fetch, int stage_ctas,
+                               void* stream) {
+    if (!valid_layer(layer) || !g_layers[layer].init || !g_layers[layer].device_mode) {
+        moe_set_error("start_prefetch_dev: layer %d is not a device-driven layer", layer);
+        return -1;
+    }
+    LayerState& L = g_layers[layer];
+    hipStream_t s = (hipStream_t)stream;
+    if (launch_slot_prefetch(L.dtab, preds_dev, m, max_fetch, s)) return -1;
+    return stage_device(L, s, stage_ctas);
+}
+
+int c_layer_table_status(int layer) {
+    if (!valid_layer(layer)) return -1;
+    LayerState& L = g_layers[layer];
+    if (pull_table(L)) return -1;
+    return L.tab.status;
+}
+
+// ---- compute entry points ---------------------------------------------------------------------
+
+uint64_t moe_router_workspace_bytes(int n_exp) { return (uint64_t)(2 * n_exp) * sizeof(float) + 256; }
+
+int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_in, void* x_out, const void* w,
+               const void* w_next, int hidden, int n_exp, int k, int m, void* workspace, uint32_t* ids_out,
+               void* scores_out, int32_t* pred_out, void* stream) {
+    float* scratch = (float*)workspace;
+    unsigned* counter = (unsigned*)((uint8_t*)workspace + (size_t)(2 * n_exp) * sizeof(float));
+    return launch_router(h_in, (const __half*)norm_w, eps, (const __half*)x_in, (__half*)x_out,
+                         (const __half*)w, (const __half*)w_next, hidden, n_exp, k, m, scratch, counter,
+                         ids_out, (__half*)scores_out, pred_out, (hipStream_t)stream);
+}
+
+uint64_t moe_q2_expert_bytes(int hidden, int inter, int group) {
+    return (uint64_t)blob_layout(hidden, inter, group).bytes;
+}
+
+int moe_q2_gate_up(const void* x, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots, int k,
+                   int hidden, int inter, int group, void* h_out, void* stream) {
+    return launch_q2_gate_up((const __half*)x, (const uint8_t*)pool, stride, n_slots, slots, k, hidden, inter, group,
+                             (__half*)h_out, (hipStream_t)stream);
+}
+
+int moe_q2_down(const void* h, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots,
+                const void* scores, int k, int hidden, int inter, int group, const void* residual, float* y_out,
+                int per_expert, void* stream) {
+    return launch_q2_down((const __half*)h, (const uint8_t*)pool, stride, n_slots, slots, (const __half*)scores, k, hidden,
+                          inter, group, (const __half*)residual, y_out, per_expert, (hipStream_t)stream);
+}
+
+int moe_q2_switch_glu(const void* x, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots,
+                      const void* scores, int k, int hidden, int inter, int group, const void* residual, void* h_ws,
+                      float* y_out, int per_expert, void* stream) {
+    if (moe_q2_gate_up(x, pool, stride, n_slots, slots, k, hidden, inter, group, h_ws, stream)) return -1;
+    return moe_q2_down(h_ws, pool, stride, n_slots, slots, scores, k, hidden, inter, group, residual, y_out, per_expert,
+                       stream);
+}
+
+int c_layer_set_format(int layer, int hidden, int inter, int group) {
+    if (!valid_layer(layer) || !g_layers[layer].init) { moe_set_error("set_format: bad layer %d", layer); return -1; }
+    LayerState& L = g_layers[layer];
+    uint64_t want = blob_layout(hidden, inter, group).bytes;
+    if (L.row_bytes[0] != want) {
+        moe_set_error("set_format: tensor 0 row bytes %llu != Q2 blob bytes %llu", (unsigned long long)L.row_bytes[0],
+                      (unsigned long long)want);
+        return -1;
+    }
+    L.hidden = hidden;
+    L.inter = inter;
+    L.group = group;
+    return 0;
+}
+
+// SwitchGLU over the layer's slot pool with the slot ids of its last decode step.  Orders the
+// compute stream after the layer's pending copies and records the read for later copies.
+int c_layer_switch_glu(int layer, const void* x, const void* scores, const void* residual, void* h_ws,
+                       float* y_out, int per_expert, int k, void* stream) {
+    if (!valid_layer(layer) || !g_layers[layer].init || !g_layers[layer].hidden) {
+        moe_set_error("layer_switch_glu: layer %d has no Q2 format (c_layer_set_format)", layer);
+        return -1;
+    }
+    LayerState& L = g_layers[layer];
+    if (!L.slot_inds_device) { moe_set_error("layer_switch_glu: slot_inds must be device memory"); return -1; }
+    hipStream_t s = (hipStream_t)stream;
+    if (wait_copies_gpu(L, s)) return -1;
+    if (ensure_events(L)) return -1;
+    if (moe_q2_switch_glu(x, (const void*)L.dst[0], L.row_bytes[0], L.capacity, L.slot_inds, scores, k, L.hidden, L.inter,
+                          L.group, residual, h_ws, y_out, per_expert, stream))
+        return -1;
+    HIP_TRY(hipEventRecord(L.read_done, s));
+    L.read_recorded = true;
+    return 0;
+}
+
+// Host-blocking join of every copy queued so far.
+int c_sync_copies(void) {
+    if (!g_ready) return 0;
+    HIP_TRY(hipStreamSynchronize(g_copy));
+    return 0;
+}
+
+int c_abi_version(void) { return 1; }
+
+}  // extern "C"

@@ -1,0 +1,120 @@
+// Shared definitions for libmoe_offload (gfx950).
+//
+// Expert blob: every routed expert of a layer is one contiguous byte range, in the slot pool
+// (HBM) and in the host expert store alike, so that one miss is one copy.  For hidden H,
+// intermediate I and group G (2-bit codes, 16 per uint32, LSB first, MLX affine format):
+//
+//   gate codes [I][H/16] u32 | up codes [I][H/16] u32 | down codes [H][I/16] u32 |
+//   gate sb [I][H/G] | up sb [I][H/G] | down sb [H][I/G]
+//
+// where each sb entry is the pair (scale, bias) as two fp16 halves of one 32-bit word.  The
+// code arrays are byte-for-byte the MLX `weight` arrays of one expert; the sb arrays
+// interleave MLX's separate `scales`/`biases`.  At H=2048, I=512, G=64 an expert is
+// 983,040 bytes (786,432 of codes, 196,608 of scale/bias).
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define MOE_MAX_LAYERS 64
+#define MOE_NUM_EXPERTS 512
+#define MOE_NUM_TENSORS 9
+#define MOE_MAX_K 16
+#define MOE_MAX_PREFETCH 32
+
+struct BlobLayout {
+    int hidden, inter, group;
+    size_t gate_codes, up_codes, down_codes, gate_sb, up_sb, down_sb, bytes;
+};
+
+static inline __host__ __device__ BlobLayout blob_layout(int hidden, int inter, int group) {
+    BlobLayout L;
+    L.hidden = hidden;
+    L.inter = inter;
+    L.group = group;
+    size_t gu = (size_t)inter * hidden / 4;          // 2-bit codes: 4 per byte
+    size_t dn = (size_t)hidden * inter / 4;
+    size_t gsb = (size_t)inter * (hidden / group) * 4;
+    size_t dsb = (size_t)hidden * (inter / group) * 4;
+    L.gate_codes = 0;
+    L.up_codes = gu;
+    L.down_codes = 2 * gu;
+    L.gate_sb = 2 * gu + dn;
+    L.up_sb = L.gate_sb + gsb;
+    L.down_sb = L.up_sb + gsb;
+    L.bytes = L.down_sb + dsb;
+    return L;
+}
+
+// Per-layer slot table.  The reference keeps a doubly linked list over slots
+// (mlx-qwen38/expert_io.c:43-91); this keeps the same order as recency stamps: a resident
+// slot carries stamp > 0, the LRU end is the smallest stamp, moving a slot to the MRU end
+// gives it the next clock value.  Every list operation of the reference maps to a stamp
+// operation with the same resulting order, so decisions are identical; the stamp form lets
+// the device kernel pick victims with wave-wide reductions instead of pointer chasing.
+// The same struct lives in host memory (host-driven layers) or device memory (device-driven
+// layers) so tables can be copied either way.
+struct SlotTable {
+    int32_t capacity;
+    int32_t n_free;
+    uint32_t clock;
+    int32_t snap_valid;
+    uint64_t snap_resident[8];
+    uint64_t snap_pred[8];
+    uint64_t snap_fetched[8];
+    uint64_t stats[18];
+    uint64_t expert_bytes;
+    int16_t slot_of[MOE_NUM_EXPERTS];   // expert id -> slot, -1 when not resident
+    int16_t eid_of[MOE_NUM_EXPERTS];    // slot -> expert id, -1 when empty
+    int16_t free_stack[MOE_NUM_EXPERTS];
+    uint32_t stamp[MOE_NUM_EXPERTS];    // 0 = slot not on the recency list
+    // Result of the last device-side operation: the copies it needs (eid, slot).
+    int32_t n_copy;
+    int32_t copy_eid[MOE_MAX_PREFETCH];
+    int32_t copy_slot[MOE_MAX_PREFETCH];
+    int32_t status;                     // 0 ok; nonzero: rejected input (device kernels)
+};
+
+// Stats word indices (same order as c_layer_get_stats, expert_io.c:791-812).
+enum {
+    ST_DEC_REQ = 0, ST_DEC_LRU_HIT, ST_DEC_PREF_HIT, ST_DEC_MISS, ST_DEC_BYTES, ST_PREF_BYTES,
+    ST_PRE_REQ, ST_PRE_HIT, ST_PRE_MISS, ST_PRE_BYTES,
+    ST_PRED_HITS, ST_PRED_ACTUAL, ST_PRED_TOTAL,
+    ST_MISS_PREF_HITS, ST_MISS_ACTUAL, ST_MISS_FETCHED,
+    ST_UNCOAL, ST_COAL
+};
+
+#define STAMP_RENORM_AT 0xF0000000u
+
+// Error reporting: entry points record the first failure; c_last_error() returns it.
+void moe_set_error(const char* fmt, ...);
+
+#define HIP_TRY(expr)                                                                  \
+    do {                                                                               \
+        hipError_t _e = (expr);                                                        \
+        if (_e != hipSuccess) {                                                        \
+            moe_set_error("%s:%d %s -> %s", __FILE__, __LINE__, #expr, hipGetErrorString(_e)); \
+            return -1;                                                                 \
+        }                                                                              \
+    } while (0)
+
+// Kernel launchers implemented in the .hip translation units (return 0 / -1).
+int launch_router(const float* h_in, const __half* norm_w, float eps, const __half* x_in,
+                  __half* x_out, const __half* w, const __half* w_next, int hidden, int n_exp,
+                  int k, int m, float* scratch, unsigned* counter, uint32_t* ids_out,
+                  __half* scores_out, int32_t* pred_out, hipStream_t s);
+int launch_q2_gate_up(const __half* x, const uint8_t* pool, size_t expert_stride, int n_slots,
+                      const uint32_t* slots, int k, int hidden, int inter, int group,
+                      __half* h_out, hipStream_t s);
+int launch_q2_down(const __half* h, const uint8_t* pool, size_t expert_stride, int n_slots,
+                   const uint32_t* slots, const __half* scores, int k, int hidden, int inter,
+                   int group, const __half* residual, float* y_out, int per_expert,
+                   hipStream_t s);
+int launch_slot_step(SlotTable* t, const uint32_t* ids, int k, uint32_t* slot_inds,
+                     hipStream_t s);
+int launch_slot_prefetch(SlotTable* t, const int32_t* preds, int m, int max_fetch,
+                         hipStream_t s);
+int launch_stage(const SlotTable* t, const uint8_t* store, size_t store_stride,
+                 uint8_t* pool, size_t pool_stride, size_t bytes, int ctas, hipStream_t s);
+int launch_store_u32(uint32_t* dst, const uint32_t* vals, int n, hipStream_t s);

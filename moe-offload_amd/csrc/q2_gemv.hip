@@ -1,0 +1,323 @@
+// Q2 (2-bit affine, group 64) gather-GEMV for batch-1 SwitchGLU decode on gfx950.
+//
+// Reference semantics: mlx-qwen38/loader.py:557-564,964-965 (`_slot_glu` = gather_qmm x3 over the
+// slot pool + SwiGLU, then the score-weighted sum), cpp/src/layers.cpp:343-362,
+// cpp/src/kernels.cpp:1027-1040,1090-1094:  y = sum_j s_j * D_j( silu(G_j x) * (U_j x) ),
+// W = scale * q + bias per group of 64 inputs, q = 2-bit codes, 16 per uint32, LSB first.
+//
+// Data path.  One 16-byte load per lane is exactly one group (64 codes) of one weight row, so
+// a wave reads whole rows with fully coalesced 128-bit loads; the matching (scale, bias) pair
+// is one 32-bit load.  Codes are expanded in registers without integer->float conversions:
+// OR-ing a code pair into the mantissa of fp16 1024.0 gives the exact halves 1024 + c*4^p,
+// which feed v_dot2_f32_f16 against the matching activation pair.  Per 32-bit word that is
+// 9 bit operations + 8 dot2 for 16 codes.  With 5 accumulators (one per power 4^p):
+//     sum_i c_i x_i = sum_p 4^-p A_p - 1024 * sum_i x_i 4^-p(i)
+// and the second term is a per-(vector, group) constant computed once.
+// Accumulation is fp32; the activation vector is fp16 (x) or fp16-rounded (h).
+//
+// Kernels
+//   k_q2_gate_up<GPR>: rows of gate and up for one selected expert; lanes 0-31 gate, 32-63 up,
+//                      GPR = hidden/64 lanes per row.  Writes h = silu(g)*u as fp16 [k][inter].
+//   k_q2_down<GPR>:    8 output rows per block x all k experts (4 waves split the experts);
+//                      h is staged in LDS in dot2 pair order; the block reduces over experts in
+//                      a fixed order and writes y = residual + sum_j s_j y_j (fp32), or the
+//                      per-expert rows when per_expert != 0.
+#include <hip/hip_fp16.h>
+
+#include "moe_common.h"
+
+namespace {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+
+constexpr uint32_t kMagic = 0x64006400u;   // fp16 1024.0 in both halves
+
+// Dot of one group (4 words = 64 codes) with 32 activation pairs laid out as
+// P[8*w + j] = (a[16w + j], a[16w + j + 8]), j = 0..7.
+__device__ __forceinline__ float q2_group_dot(uint4 c, const h2_t* P) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f, a4 = 0.f;
+    const uint32_t words[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t v = words[w];
+        const uint32_t v2 = v >> 10;
+        const h2_t* p = P + 8 * w;
+        a0 = __builtin_amdgcn_fdot2(as_h2((v & 0x00030003u) | kMagic), p[0], a0, false);
+        a1 = __builtin_amdgcn_fdot2(as_h2((v & 0x000C000Cu) | kMagic), p[1], a1, false);
+        a2 = __builtin_amdgcn_fdot2(as_h2((v & 0x00300030u) | kMagic), p[2], a2, false);
+        a3 = __builtin_amdgcn_fdot2(as_h2((v & 0x00C000C0u) | kMagic), p[3], a3, false);
+        a4 = __builtin_amdgcn_fdot2(as_h2((v & 0x03000300u) | kMagic), p[4], a4, false);
+        a0 = __builtin_amdgcn_fdot2(as_h2((v2 & 0x00030003u) | kMagic), p[5], a0, false);
+        a1 = __builtin_amdgcn_fdot2(as_h2((v2 & 0x000C000Cu) | kMagic), p[6], a1, false);
+        a2 = __builtin_amdgcn_fdot2(as_h2((v2 & 0x00300030u) | kMagic), p[7], a2, false);
+    }
+    return a0 + 0.25f * a1 + 0.0625f * a2 + 0.015625f * a3 + 0.00390625f * a4;
+}
+
+// Weight of input position j (0..15) inside a word in the offset constant: 4^-class.
+__device__ __forceinline__ float pos_weight(int j) {
+    int p = j & 7;
+    int cls = (p <= 4) ? p : p - 5;
+    return 1.0f / (float)(1 << (2 * cls));
+}
+
+// Build the 32 pairs and the two constants for activation slice a[0..63] (fp16 values,
+// 16-byte aligned).
+__device__ __forceinline__ void build_pairs(const __half* a, h2_t* P, float& cst, float& sum) {
+    uint4 q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = reinterpret_cast<const uint4*>(a)[i];
+    const uint16_t* hv = reinterpret_cast<const uint16_t*>(q);
+    float c = 0.f, s = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint16_t lo = hv[16 * w + j], hi = hv[16 * w + j + 8];
+            P[8 * w + j] = as_h2((uint32_t)lo | ((uint32_t)hi << 16));
+            float f = __half2float(__ushort_as_half(lo)) + __half2float(__ushort_as_half(hi));
+            s += f;
+            c += pos_weight(j) * f;
+        }
+    }
+    cst = 1024.0f * c;
+    sum = s;
+}
+
+__device__ __forceinline__ float sb_apply(uint32_t sb, float dot, float cst, float sum) {
+    float sc = __half2float(__ushort_as_half((uint16_t)(sb & 0xFFFFu)));
+    float bi = __half2float(__ushort_as_half((uint16_t)(sb >> 16)));
+    return sc * (dot - cst) + bi * sum;
+}
+
+constexpr int kGuRowsPerIter = 4;   // iterations per wave (each covers 32/GPR rows)
+
+template <int GPR>
+__global__ __launch_bounds__(256) void k_q2_gate_up(
+    const __half* __restrict__ x, const uint8_t* __restrict__ pool, size_t stride,
+    const uint32_t* __restrict__ slots, int n_slots, int inter, BlobLayout L, __half* __restrict__ h_out) {
+    constexpr int RPI = 32 / GPR;                       // rows per wave instruction
+    constexpr int ROWS_PER_WAVE = RPI * kGuRowsPerIter;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int j = blockIdx.y;
+    const int proj = lane >> 5, sub = lane & 31;
+    const int rl = sub / GPR, g = sub % GPR;
+    const int row_base = (blockIdx.x * 4 + wv) * ROWS_PER_WAVE;
+
+    const uint32_t slot = slots[j];
+    const bool ok = slot < (uint32_t)n_slots;         // an invalid slot reads nothing, yields 0
+    const uint8_t* blob = pool + (size_t)(ok ? slot : 0) * stride;
+    const uint8_t* codes = blob + (proj ? L.up_codes : L.gate_codes);
+    const uint32_t* sbv = reinterpret_cast<const uint32_t*>(blob + (proj ? L.up_sb : L.gate_sb));
+    const size_t row_bytes = (size_t)GPR * 16;
+
+    uint4 c[kGuRowsPerIter];
+    uint32_t sb[kGuRowsPerIter];
+#pragma unroll
+    for (int it = 0; it < kGuRowsPerIter; ++it) {
+        int row = row_base + it * RPI + rl;
+        if (ok && row < inter) {
+            c[it] = *reinterpret_cast<const uint4*>(codes + (size_t)row * row_bytes + g * 16);
+            sb[it] = sbv[(size_t)row * GPR + g];
+        } else {
+            c[it] = make_uint4(0, 0, 0, 0);
+            sb[it] = 0;
+        }
+    }
+
+    h2_t P[32];
+    float cst, sum;
+    build_pairs(x + g * 64, P, cst, sum);
+
+#pragma unroll
+    for (int it = 0; it < kGuRowsPerIter; ++it) {
+        float part = sb_apply(sb[it], q2_group_dot(c[it], P), cst, sum);
+#pragma unroll
+        for (int o = GPR / 2; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
+        float up = __shfl(part, lane + 32, 64);
+        int row = row_base + it * RPI + rl;
+        if (proj == 0 && g == 0 && row < inter) {
+            float gt = part;
+            float hval = gt / (1.0f + __expf(-gt)) * up;
+            h_out[(size_t)j * inter + row] = __float2half_rn(hval);
+        }
+    }
+}
+
+constexpr int kDownRows = 8;      // output rows per block (one wave instruction at GPR = 8)
+
+template <int GPR>
+__global__ __launch_bounds__(256) void k_q2_down(
+    const __half* __restrict__ h, const uint8_t* __restrict__ pool, size_t stride,
+    const uint32_t* __restrict__ slots, int n_slots, const __half* __restrict__ scores, int k, int hidden,
+    BlobLayout L, const __half* __restrict__ residual, float* __restrict__ y_out, int per_expert) {
+    constexpr int LPR = GPR;                       // lanes per row
+    constexpr int RPI = 64 / LPR;                  // rows per wave instruction
+    constexpr int ITERS = (kDownRows + RPI - 1) / RPI;
+    constexpr int MAXJ = (MOE_MAX_K + 3) / 4;      // experts per wave
+    __shared__ h2_t hp[MOE_MAX_K][GPR][32];
+    __shared__ float hc[MOE_MAX_K][GPR][2];
+    __shared__ float red[4][kDownRows];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int g = lane % LPR, rl = lane / LPR;
+    const int row0 = blockIdx.x * kDownRows;
+    const int inter = GPR * 64;
+
+    // Issue this wave's weight loads first (experts wv, wv+4, ...).
+    uint4 c[MAXJ][ITERS];
+    uint32_t sb[MAXJ][ITERS];
+#pragma unroll
+    for (int q = 0; q < MAXJ; ++q) {
+        int j = wv + 4 * q;
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            int row = row0 + it * RPI + rl;
+            const uint32_t slot = j < k ? slots[j] : 0u;
+            if (j < k && slot < (uint32_t)n_slots && row < hidden && it * RPI + rl < kDownRows) {
+                const uint8_t* blob = pool + (size_t)slot * stride;
+                c[q][it] = *reinterpret_cast<const uint4*>(blob + L.down_codes + (size_t)row * GPR * 16 + g * 16);
+                sb[q][it] = reinterpret_cast<const uint32_t*>(blob + L.down_sb)[(size_t)row * GPR + g];
+            } else {
+                c[q][it] = make_uint4(0, 0, 0, 0);
+                sb[q][it] = 0;
+            }
+        }
+    }
+
+    // Stage h[k][inter] into LDS as dot2 pairs and per-(expert, group) constants.
+    for (int t = tid; t < k * GPR * 32; t += 256) {
+        int jj = t / (GPR * 32), rem = t % (GPR * 32), gg = rem / 32, pi = rem % 32;
+        int w = pi >> 3, p = pi & 7;
+        const __half* src = h + (size_t)jj * inter + gg * 64 + 16 * w + p;
+        h2_t pr;
+        pr.x = __builtin_bit_cast(_Float16, src[0]);
+        pr.y = __builtin_bit_cast(_Float16, src[8]);
+        hp[jj][gg][pi] = pr;
+    }
+    __syncthreads();
+    for (int t = tid; t < k * GPR; t += 256) {
+        int jj = t / GPR, gg = t % GPR;
+        float cc = 0.f, ss = 0.f;
+        for (int pi = 0; pi < 32; ++pi) {
+            h2_t pr = hp[jj][gg][pi];
+            float f = (float)pr.x + (float)pr.y;
+            ss += f;
+            cc += pos_weight(pi & 7) * f;
+        }
+        hc[jj][gg][0] = 1024.0f * cc;
+        hc[jj][gg][1] = ss;
+    }
+    __syncthreads();
+
+    float acc[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) acc[it] = 0.f;
+#pragma unroll
+    for (int q = 0; q < MAXJ; ++q) {
+        int j = wv + 4 * q;
+        if (j >= k) break;
+        h2_t P[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) P[i] = hp[j][g][i];
+        const float cst = hc[j][g][0], sum = hc[j][g][1];
+        const float sj = scores ? __half2float(scores[j]) : 1.0f;
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            float part = sb_apply(sb[q][it], q2_group_dot(c[q][it], P), cst, sum);
+#pragma unroll
+            for (int o = LPR / 2; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
+            int rloc = it * RPI + rl;
+            if (per_expert) {
+                int row = row0 + rloc;
+                if (g == 0 && rloc < kDownRows && row < hidden) y_out[(size_t)j * hidden + row] = part;
+            } else {
+                acc[it] += sj * part;
+            }
+        }
+    }
+    if (per_expert) return;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        int rloc = it * RPI + rl;
+        if (g == 0 && rloc < kDownRows) red[wv][rloc] = acc[it];
+    }
+    __syncthreads();
+    if (tid < kDownRows) {
+        int row = row0 + tid;
+        if (row < hidden) {
+            float y = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+            if (residual) y += __half2float(residual[row]);
+            y_out[row] = y;
+        }
+    }
+}
+
+template <int GPR>
+int gate_up_t(const __half* x, const uint8_t* pool, size_t stride, const uint32_t* slots, int n_slots, int k,
+              int inter, BlobLayout L, __half* h_out, hipStream_t s) {
+    constexpr int rows_per_block = 4 * (32 / GPR) * kGuRowsPerIter;
+    dim3 grid((inter + rows_per_block - 1) / rows_per_block, k);
+    hipLaunchKernelGGL((k_q2_gate_up<GPR>), grid, dim3(256), 0, s, x, pool, stride, slots, n_slots, inter, L, h_out);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+template <int GPR>
+int down_t(const __half* h, const uint8_t* pool, size_t stride, const uint32_t* slots, int n_slots,
+           const __half* scores, int k, int hidden, BlobLayout L, const __half* residual,
+           float* y_out, int per_expert, hipStream_t s) {
+    dim3 grid((hidden + kDownRows - 1) / kDownRows);
+    hipLaunchKernelGGL((k_q2_down<GPR>), grid, dim3(256), 0, s, h, pool, stride, slots, n_slots, scores, k,
+                       hidden, L, residual, y_out, per_expert);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+bool check_shape(const char* who, int k, int hidden, int inter, int group) {
+    if (group != 64) { moe_set_error("%s: group=%d unsupported (kernels take group 64)", who, group); return false; }
+    if (k <= 0 || k > MOE_MAX_K) { moe_set_error("%s: k=%d out of range 1..%d", who, k, MOE_MAX_K); return false; }
+    if (hidden % 64 || inter % 64 || hidden <= 0 || inter <= 0) {
+        moe_set_error("%s: hidden=%d inter=%d must be positive multiples of 64", who, hidden, inter);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+int launch_q2_gate_up(const __half* x, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots,
+                      int k, int hidden, int inter, int group, __half* h_out, hipStream_t s) {
+    if (!check_shape("q2_gate_up", k, hidden, inter, group)) return -1;
+    if (n_slots <= 0 || !pool || !slots || !x || !h_out) { moe_set_error("q2_gate_up: empty pool or null pointer"); return -1; }
+    BlobLayout L = blob_layout(hidden, inter, group);
+    if (stride < L.bytes) { moe_set_error("q2_gate_up: expert stride %zu < blob bytes %zu", stride, L.bytes); return -1; }
+    switch (hidden / 64) {
+        case 1: return gate_up_t<1>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
+        case 2: return gate_up_t<2>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
+        case 4: return gate_up_t<4>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
+        case 8: return gate_up_t<8>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
+        case 16: return gate_up_t<16>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
+        case 32: return gate_up_t<32>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
+        default: moe_set_error("q2_gate_up: hidden=%d unsupported (64*{1,2,4,8,16,32})", hidden); return -1;
+    }
+}
+
+int launch_q2_down(const __half* h, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots,
+                   const __half* scores, int k, int hidden, int inter, int group,
+                   const __half* residual, float* y_out, int per_expert, hipStream_t s) {
+    if (!check_shape("q2_down", k, hidden, inter, group)) return -1;
+    if (n_slots <= 0 || !pool || !slots || !h || !y_out) { moe_set_error("q2_down: empty pool or null pointer"); return -1; }
+    BlobLayout L = blob_layout(hidden, inter, group);
+    if (stride < L.bytes) { moe_set_error("q2_down: expert stride %zu < blob bytes %zu", stride, L.bytes); return -1; }
+    switch (inter / 64) {
+        case 1: return down_t<1>(h, pool, stride, slots, n_slots, scores, k, hidden, L, residual, y_out, per_expert, s);
+        case 2: return down_t<2>(h, pool, stride, slots, n_slots, scores, k, hidden, L, residual, y_out, per_expert, s);
+        case 4: return down_t<4>(h, pool, stride, slots, n_slots, scores, k, hidden, L, residual, y_out, per_expert, s);
+        case 8: return down_t<8>(h, pool, stride, slots, n_slots, scores, k, hidden, L, residual, y_out, per_expert, s);
+        case 16: return down_t<16>(h, pool, stride, slots, n_slots, scores, k, hidden, L, residual, y_out, per_expert, s);
+        default: moe_set_error("q2_down: inter=%d unsupported (64*{1,2,4,8,16})", inter); return -1;
+    }
+}

@@ -1,0 +1,41 @@
+"""Shared helpers for the GPU parity tests (inputs are seeded; the oracle is the checker)."""
+from __future__ import annotations
+
+import numpy as np
+
+from moe_offload import q2format, synth
+from oracle import q2
+
+H, E, K, I, G = 2048, 512, 10, 512, 64
+
+
+def experts_np(n_exp=E, hidden=H, inter=I, seed=1, scale_std=0.02):
+    """MLX-layout experts and their blobs."""
+    gate, up, down = synth.q2_experts(n_exp, hidden, inter, seed=seed, scale_std=scale_std)
+    blobs = q2format.to_blobs(gate, up, down, hidden, inter)
+    return (gate, up, down), blobs
+
+
+def expert_fn(mlx):
+    gate, up, down = mlx
+    return lambda e: ((gate[0][e], gate[1][e], gate[2][e]), (up[0][e], up[1][e], up[2][e]),
+                      (down[0][e], down[1][e], down[2][e]))
+
+
+def oracle_moe(x16, inds, scores16, mlx, residual=None):
+    """fp64 oracle of sum_j s_j SwitchGLU_{e_j}(x) (+ residual)."""
+    y = q2.moe_combine(x16.astype(np.float64), inds, scores16.astype(np.float64), expert_fn(mlx),
+                       bits=2, group=64)
+    if residual is not None:
+        y = y + residual.astype(np.float64)
+    return y
+
+
+def assert_close_rms(got, want, tol=1e-2, what=""):
+    """max|err| <= tol * RMS(want) -- the decode output bar."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    rms = np.sqrt(np.mean(want ** 2))
+    err = np.abs(got - want).max()
+    assert err <= tol * rms, f"{what}: max|err| {err:.3e} > {tol} x RMS {rms:.3e}"
+    return err / rms

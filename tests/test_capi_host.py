@@ -1,0 +1,162 @@
+"""The C-ABI library without a GPU: it loads, exports every declared symbol, and its host slot
+table (the expert_io.c entry points on accounting-only layers) reproduces the golden traces
+written by the reference's own expert_io.c."""
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+from moe_offload import _lib
+
+HEADER = ROOT / "include" / "moe_offload.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b((?:c|moe)_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_symbols()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    # the ctypes table covers exactly the header
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_q2_blob_bytes_match_layout():
+    from moe_offload import q2format
+    L = _lib.lib()
+    for h, i in [(2048, 512), (256, 128), (2560, 640)]:
+        assert L.moe_q2_expert_bytes(h, i, 64) == q2format.expert_bytes(h, i)
+    assert q2format.expert_bytes(2048, 512) == 983_040
+    assert q2format.expert_bytes(2560, 640) == 1_228_800 + 307_200  # codes + fp16 scale/bias
+
+
+class CLayer:
+    """One accounting-only layer of the product library (no copies: null stores/pools)."""
+
+    def __init__(self, layer, cap, expert_bytes=1_536_000):
+        self.L, self.layer, self.cap = _lib.lib(), layer, cap
+        self.slot_buf = (ctypes.c_uint32 * 16)()
+        z = (ctypes.c_uint64 * 9)()
+        rb = (ctypes.c_uint64 * 9)(expert_bytes, *([0] * 8))
+        self.L.c_layer_init(layer, -1, cap, z, rb, z, ctypes.addressof(self.slot_buf))
+        _lib.check_error("c_layer_init")
+
+    def step(self, ids):
+        a = (ctypes.c_uint32 * len(ids))(*ids)
+        n = self.L.c_layer_step_decode_ex(self.layer, a, len(ids), 1)
+        _lib.check(n, "step")
+        return list(self.slot_buf[:len(ids)]), n
+
+    def prefetch(self, preds, cap):
+        if len(preds) == 12:
+            self.L.c_layer_start_prefetch12(self.layer, cap, *preds)
+        else:
+            a = (ctypes.c_int32 * max(1, len(preds)))(*preds)
+            self.L.c_layer_start_prefetch(self.layer, a, len(preds), cap)
+        _lib.check_error("prefetch")
+
+    def state(self):
+        e, s, c = (ctypes.c_int32 * 512)(), (ctypes.c_int32 * 512)(), ctypes.c_int()
+        self.L.c_layer_get_lru_state(self.layer, e, s, ctypes.byref(c))
+        return [list(e[:c.value]), list(s[:c.value])]
+
+    def set_state(self, e, s, r, h, m):
+        n = len(e)
+        self.L.c_layer_set_lru_state(self.layer, (ctypes.c_int32 * max(n, 1))(*e), (ctypes.c_int32 * max(n, 1))(*s),
+                                     n, r, h, m)
+        _lib.check_error("set_state")
+
+    def load_sync(self, e, s):
+        n = len(e)
+        self.L.c_layer_load_sync(self.layer, (ctypes.c_int32 * n)(*e), (ctypes.c_int32 * n)(*s), n, 1)
+        _lib.check_error("load_sync")
+
+    def stats(self):
+        o = (ctypes.c_uint64 * 18)()
+        self.L.c_layer_get_stats(self.layer, o)
+        return list(o)
+
+
+def test_host_table_reproduces_reference_layer_traces(lru_traces):
+    for scen in lru_traces["scenarios"]:
+        L = CLayer(40, scen["capacity"])
+        for op in scen["ops"]:
+            if op["op"] == "prefetch":
+                L.prefetch(op["preds"], op["cap"])
+            elif op["op"] == "step":
+                slots, n = L.step(op["ids"])
+                assert slots == op["slots"] and n == op["n_miss"], scen["name"]
+            elif op["op"] == "set_state":
+                L.set_state(op["eids"], op["slots"], *op["add"])
+            elif op["op"] == "load_sync":
+                L.load_sync(op["eids"], op["slots"])
+            assert L.stats() == op["stats"], (scen["name"], op["op"])
+            if "state" in op:
+                assert L.state() == op["state"]
+        assert L.state() == scen["final_state"]
+
+
+def test_host_table_reproduces_reference_stack_traces(lru_traces):
+    lib = _lib.lib()
+    for stk in lru_traces["stacks"]:
+        n_layers = stk["n_layers"]
+        layers = {int(l): CLayer(int(l), c) for l, c in stk["capacities"].items()}
+        for op in stk["ops"]:
+            L = layers[op["layer"]]
+            if op["op"] == "prefetch":
+                L.prefetch(op["preds"], op["cap"])
+            else:
+                slots, n = L.step(op["ids"])
+                assert slots == op["slots"] and n == op["n_miss"]
+        for l, st in stk["layer_stats"].items():
+            assert layers[int(l)].stats() == st
+        out = (ctypes.c_uint64 * 6)()
+        lib.c_get_decode_totals(n_layers, out)
+        assert list(out) == stk["totals"]
+        for l in layers:
+            lib.c_layer_reset_stats(l)
+
+
+def test_out_of_range_layer_is_ignored_and_bad_input_reported():
+    lib = _lib.lib()
+    out = (ctypes.c_uint64 * 18)(*range(18))
+    lib.c_layer_get_stats(99, out)            # silently ignored, as in the reference
+    assert list(out) == list(range(18))
+    assert lib.c_layer_step_decode10(-1, *range(10)) == 0
+    L = CLayer(41, 16)
+    a = (ctypes.c_uint32 * 10)(*([600] + list(range(9))))
+    assert lib.c_layer_step_decode_ex(41, a, 10, 1) == -1
+    with pytest.raises(_lib.NativeError, match="out of range"):
+        _lib.check_error("x")
+    b = (ctypes.c_uint32 * 17)(*range(17))
+    assert lib.c_layer_step_decode_ex(41, b, 17, 1) == -1     # k > 16
+    lib.c_clear_error()
+    assert L.stats()[0] == 0                                    # rejected calls changed nothing
+
+
+def test_stamp_renormalisation_keeps_order():
+    """Long runs relabel recency stamps; the decisions must not change.  Drive one layer with
+    many steps against the oracle's linked-list restatement (cheap proxy for clock wrap)."""
+    from oracle import lru as olru
+    rng = np.random.default_rng(9)
+    L = CLayer(42, 20)
+    O = olru.CLru(42, 20)
+    for t in range(3000):
+        if t % 3 == 0:
+            preds = rng.choice(80, size=12, replace=False).tolist()
+            L.prefetch(preds, 3)
+            O.prefetch(preds, 3)
+        ids = rng.choice(80, size=10, replace=False).tolist()
+        s1, n1 = L.step(ids)
+        s2, m2 = O.step(ids)
+        assert s1 == s2 and n1 == len(m2)
+    assert L.state() == [list(v) for v in O.get_state()]
+    assert L.stats()[:16] == O.stats()[:16]
