@@ -89,6 +89,11 @@ int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_i
                void* workspace, uint32_t* ids_out, void* scores_out, int32_t* pred_out,
                void* stream);
 uint64_t moe_router_workspace_bytes(int n_exp);
+/* Builder-defined glue between stacked MoE layers (no reference counterpart: the reference
+ * mixes hyper-connections there, loader.py:61,992): x_out fp16 = RMSNorm(h_in fp32) * norm_w,
+ * the same arithmetic as moe_router's prologue. */
+int moe_rmsnorm(const float* h_in, const void* norm_w, float eps, int hidden, void* x_out,
+                void* stream);
 /* Bytes of one Q2 expert blob (layout in csrc/moe_common.h). */
 uint64_t moe_q2_expert_bytes(int hidden, int inter, int group);
 /* gather_qmm gate+up + SwiGLU (loader.py:564, kernels.cpp:1027-1040,1090-1094):
@@ -123,6 +128,8 @@ int c_layer_set_format(int layer_idx, int hidden, int inter, int group);
 /* SwitchGLU over the layer's pool with its current slot ids; orders after pending copies. */
 int c_layer_switch_glu(int layer_idx, const void* x, const void* scores, const void* residual,
                        void* h_ws, float* y_out, int per_expert, int k, void* stream);
+/* Record that work queued on `stream` so far reads the layer's pool (copies into it wait). */
+int c_layer_mark_read(int layer_idx, void* stream);
 /* Move a layer's slot table to device memory (on != 0) or back.  Device-driven layers take
  * their ids from device memory and stage misses with a kernel that reads the pinned store. */
 int c_layer_set_device_mode(int layer_idx, int on);

@@ -517,6 +517,10 @@ int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_i
                          ids_out, (__half*)scores_out, pred_out, (hipStream_t)stream);
 }
 
+int moe_rmsnorm(const float* h_in, const void* norm_w, float eps, int hidden, void* x_out, void* stream) {
+    return launch_rmsnorm(h_in, (const __half*)norm_w, eps, hidden, (__half*)x_out, (hipStream_t)stream);
+}
+
 uint64_t moe_q2_expert_bytes(int hidden, int inter, int group) {
     return (uint64_t)blob_layout(hidden, inter, group).bytes;
 }
@@ -574,6 +578,16 @@ int c_layer_switch_glu(int layer, const void* x, const void* scores, const void*
                           L.group, residual, h_ws, y_out, per_expert, stream))
         return -1;
     HIP_TRY(hipEventRecord(L.read_done, s));
+    L.read_recorded = true;
+    return 0;
+}
+
+// Record that work queued so far on `stream` reads the layer's pool (later copies wait for it).
+int c_layer_mark_read(int layer, void* stream) {
+    if (!valid_layer(layer) || !g_layers[layer].init) { moe_set_error("mark_read: bad layer %d", layer); return -1; }
+    LayerState& L = g_layers[layer];
+    if (ensure_events(L)) return -1;
+    HIP_TRY(hipEventRecord(L.read_done, (hipStream_t)stream));
     L.read_recorded = true;
     return 0;
 }

@@ -104,6 +104,8 @@ int launch_router(const float* h_in, const __half* norm_w, float eps, const __ha
                   __half* x_out, const __half* w, const __half* w_next, int hidden, int n_exp,
                   int k, int m, float* scratch, unsigned* counter, uint32_t* ids_out,
                   __half* scores_out, int32_t* pred_out, hipStream_t s);
+int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidden, __half* x_out,
+                   hipStream_t s);
 int launch_q2_gate_up(const __half* x, const uint8_t* pool, size_t expert_stride, int n_slots,
                       const uint32_t* slots, int k, int hidden, int inter, int group,
                       __half* h_out, hipStream_t s);

@@ -9,8 +9,8 @@
 // rule on the raw logits and emits descending value, equal values in ascending id.
 //
 // Arithmetic: fp16 x fp16 products are exact in fp32 and are accumulated in fp64; the sum is
-// rounded once through fp32 to fp16.  The softmax and renormalisation run in fp64 and round
-// through fp32 to fp16.  Rounded results therefore do not depend on summation order.
+// rounded once, directly, to fp16.  The softmax, renormalisation and RMSNorm run in fp64 and
+// round once to fp16.  Rounded results therefore do not depend on summation order.
 //
 // Launch: one block per 16 weight rows (4 waves x 4 rows).  Every block writes its rounded
 // logits to scratch, then counts itself done on a device-scope counter; the block that
@@ -46,17 +46,18 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return v;
 }
 
-__device__ __forceinline__ float round_f16(double v) {
-    return __half2float(__float2half_rn((float)v));
+// One rounding, f64 -> f16 (round to nearest even); never through f32, which would round twice.
+__device__ __forceinline__ uint16_t f16_bits(double v) {
+    return __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
-__device__ __forceinline__ uint16_t f16_bits(float v) {
-    return __half_as_ushort(__float2half_rn(v));
+__device__ __forceinline__ float round_f16(double v) {
+    return (float)(_Float16)v;
 }
 
 // Order-preserving map of an fp16 value to uint16 (signed values; -0 folded onto +0).
 __device__ __forceinline__ uint32_t f16_order(float v) {
-    uint16_t b = f16_bits(v == 0.0f ? 0.0f : v);
+    uint16_t b = f16_bits(v == 0.0f ? 0.0 : (double)v);
     return (b & 0x8000u) ? (uint32_t)(~b & 0xFFFFu) : (uint32_t)(b | 0x8000u);
 }
 
@@ -89,7 +90,7 @@ __global__ __launch_bounds__(kThreads) void k_router(
             if (norm_w) v *= (double)__half2float(norm_w[i]);
             float r = round_f16(v);
             xs[i] = r;
-            if (x_out && blockIdx.x == 0) x_out[i] = __float2half_rn(r);
+            if (x_out && blockIdx.x == 0) x_out[i] = __ushort_as_half(f16_bits(v));
         }
     } else {
         for (int i = tid; i < hidden; i += kThreads) xs[i] = __half2float(x_in[i]);
@@ -148,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void k_router(
         for (int i = 0; i < per_lane; ++i) {
             int e = lane + 64 * i;
             // gates are >= 0, so fp16 bit patterns order like the values; id breaks ties upward
-            key[i] = (e < n_exp) ? (((uint32_t)f16_bits((float)(lv[i] / sum)) << 16) | (uint32_t)e) : 0u;
+            key[i] = (e < n_exp) ? (((uint32_t)f16_bits(lv[i] / sum) << 16) | (uint32_t)e) : 0u;
         }
         uint32_t picked[MOE_MAX_K];
         for (int r = 0; r < k; ++r) {
@@ -169,7 +170,7 @@ __global__ __launch_bounds__(kThreads) void k_router(
                 gsel[j] = (double)__half2float(__ushort_as_half((uint16_t)(kk >> 16)));
                 s = (double)round_f16(s + gsel[j]);
             }
-            for (int j = 0; j < k; ++j) scores_out[j] = __float2half_rn((float)(gsel[j] / s));
+            for (int j = 0; j < k; ++j) scores_out[j] = __ushort_as_half(f16_bits(gsel[j] / s));
         }
     } else if (wv == 1 && w_next && m > 0) {
         uint32_t key[kMaxExperts / 64];
@@ -206,7 +207,37 @@ __global__ __launch_bounds__(kThreads) void k_router(
     if (tid == 0) atomicExch(counter, 0u);
 }
 
+// Standalone RMSNorm (one block): x_out = fp16(h / sqrt(mean(h^2) + eps) * w), fp64 math,
+// one rounding; the same arithmetic as the router's prologue.
+__global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ h_in, const __half* __restrict__ norm_w,
+                                                       float eps, int hidden, __half* __restrict__ x_out) {
+    __shared__ double red[kThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    double ss = 0.0;
+    for (int i = tid; i < hidden; i += kThreads) {
+        double v = h_in[i];
+        ss += v * v;
+    }
+    ss = wave_sum_f64(ss);
+    if (lane == 0) red[wv] = ss;
+    __syncthreads();
+    double tot = red[0] + red[1] + red[2] + red[3];
+    double denom = sqrt(tot / hidden + (double)eps);
+    for (int i = tid; i < hidden; i += kThreads) {
+        double v = (double)h_in[i] / denom;
+        if (norm_w) v *= (double)__half2float(norm_w[i]);
+        x_out[i] = __ushort_as_half(f16_bits(v));
+    }
+}
+
 }  // namespace
+
+int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidden, __half* x_out, hipStream_t s) {
+    if (!h_in || !x_out || hidden <= 0) { moe_set_error("rmsnorm: bad arguments"); return -1; }
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, s, h_in, norm_w, eps, hidden, x_out);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
 
 int launch_router(const float* h_in, const __half* norm_w, float eps, const __half* x_in,
                   __half* x_out, const __half* w, const __half* w_next, int hidden, int n_exp,

@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_router": (_c_int, [_c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int,
                             _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "moe_router_workspace_bytes": (_c_u64, [_c_int]),
+    "moe_rmsnorm": (_c_int, [_c_vp, _c_vp, _c_f, _c_int, _c_vp, _c_vp]),
     "moe_q2_expert_bytes": (_c_u64, [_c_int, _c_int, _c_int]),
     "moe_q2_gate_up": (_c_int, [_c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp,
                                 _c_vp]),
@@ -59,6 +60,7 @@ SIGNATURES: dict[str, tuple] = {
     "c_host_free": (_c_int, [_c_vp]),
     "c_layer_set_format": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     "c_layer_switch_glu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
+    "c_layer_mark_read": (_c_int, [_c_int, _c_vp]),
     "c_layer_set_device_mode": (_c_int, [_c_int, _c_int]),
     "c_layer_step_decode_dev": (_c_int, [_c_int, _c_vp, _c_int, _c_int, _c_vp]),
     "c_layer_start_prefetch_dev": (_c_int, [_c_int, _c_vp, _c_int, _c_int, _c_int, _c_vp]),

@@ -1,0 +1,379 @@
+"""Drop-in host API of the reference loader (`mlx-qwen38/loader.py`) on MI355X.
+
+Names, arguments and return values follow the reference:
+  compute_layer_capacities  loader.py:245-303
+  CachedSwitchGLU           loader.py:306-749   (per-layer slot cache + SwitchGLU)
+  OffloadEngine             loader.py:1004-1343 (capacities, stats, greedy decode loop)
+Storage differs by design: the slot pool is HBM (a torch uint8 tensor of Q2 blobs) and the
+"SSD" tier is a pinned host expert store (HostExpertStore) or, for file-backed layers, a
+file read through the library's pinned bounce buffers.  The cache decisions, counters and
+slot ids come from libmoe_offload.so (the expert_io.c ABI); the compute is its HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import time
+from pathlib import Path
+from typing import Any
+
+import numpy as np
+import torch
+
+from . import _lib, ops, q2format
+
+NUM_LAYERS = 48
+NUM_EXPERTS = 512
+TOP_K = 10
+PREFETCH_TOP_M = 12
+PREFETCH_MAX_CAP = 3
+MAX_K = 16
+
+
+def compute_layer_capacities(budget_gb: float | None = None, budget_pct: float | None = None,
+                             alloc_mode: str = "even", num_layers: int = NUM_LAYERS,
+                             num_experts: int = NUM_EXPERTS, expert_bytes: int = 983_040,
+                             analysis_summary: str | Path | None = None) -> dict[int, int]:
+    """Slots per cached layer 1..num_layers-1 (layer 0 is pinned), as loader.py:245-303:
+    budget_pct -> max(16, min(E, round(pct/100 * E))) per layer; budget_gb -> total slots
+    round(budget / expert_bytes) clamped to [16, E] per layer, split evenly (the first
+    remainder layers get one more) or in proportion to per-layer active-expert counts."""
+    n = num_layers - 1
+    if budget_pct is not None:
+        frac = budget_pct / 100.0 if budget_pct > 1.0 else budget_pct
+        per = max(16, min(num_experts, round(frac * num_experts)))
+        total = n * per
+    else:
+        if budget_gb is None:
+            budget_gb = 7.5
+        total = int(round((budget_gb * 1e9) / expert_bytes))
+        total = max(n * 16, min(n * num_experts, total))
+    if alloc_mode == "proportional" and analysis_summary is not None and Path(analysis_summary).exists():
+        summary = json.loads(Path(analysis_summary).read_text(encoding="utf-8"))
+        info = summary["expert_concentration"]["per_layer"]
+        w = np.array([float(info[il]["active_experts_decode"]) for il in range(1, num_layers)], np.float64)
+        raw = w / w.sum() * total
+        caps = np.clip(np.floor(raw).astype(int), 16, num_experts)
+        rem = total - int(caps.sum())
+        fr = raw - np.floor(raw)
+        if rem > 0:
+            for idx in np.argsort(-fr):
+                if rem == 0:
+                    break
+                if caps[idx] < num_experts:
+                    caps[idx] += 1
+                    rem -= 1
+        elif rem < 0:
+            for idx in np.argsort(fr):
+                if rem == 0:
+                    break
+                if caps[idx] > 16:
+                    caps[idx] -= 1
+                    rem += 1
+        return {il: int(caps[il - 1]) for il in range(1, num_layers)}
+    base, rem = divmod(total, n)
+    return {il: min(num_experts, max(16, base + (1 if (il - 1) < rem else 0))) for il in range(1, num_layers)}
+
+
+class HostExpertStore:
+    """Pinned, device-mapped host memory with every expert blob of layers [first_layer, n_layers)."""
+
+    def __init__(self, n_layers: int, n_exp: int, blob_bytes: int, first_layer: int = 0):
+        self.n_layers, self.n_exp, self.blob_bytes, self.first = n_layers, n_exp, blob_bytes, first_layer
+        self._ptr: dict[int, int] = {}
+        L = _lib.lib()
+        for l in range(first_layer, n_layers):
+            p = L.c_host_alloc(n_exp * blob_bytes)
+            if not p:
+                self.close()
+                raise _lib.NativeError(f"host store alloc failed: {_lib.last_error()}")
+            self._ptr[l] = p
+        _lib.lib().c_clear_error()
+
+    def layer_ptr(self, l: int) -> int:
+        return self._ptr[l]
+
+    def view(self, l: int) -> np.ndarray:
+        """uint8 [n_exp, blob_bytes] numpy view of layer l's store (shares memory)."""
+        return np.ctypeslib.as_array(ctypes.cast(self._ptr[l], ctypes.POINTER(ctypes.c_uint8)),
+                                     shape=(self.n_exp, self.blob_bytes))
+
+    def tensor(self, l: int) -> torch.Tensor:
+        return torch.from_numpy(self.view(l))
+
+    def close(self):
+        L = _lib.lib()
+        for p in self._ptr.values():
+            L.c_host_free(p)
+        self._ptr.clear()
+
+
+class CachedSwitchGLU:
+    """Per-layer slot cache over an HBM pool + Q2 SwitchGLU (loader.py:306-749).
+
+    `store` is a HostExpertStore (fd == -1 path); the pool holds `capacity` blobs.
+    decode: __call__(x [1,1,H] fp16, indices [1,1,k]) -> per-expert outputs [1,1,k,H], exactly
+    like SwitchGLU; forward_combined() returns the score-weighted sum directly.
+    """
+
+    def __init__(self, store: HostExpertStore, layer_idx: int, capacity: int, hidden: int = 2048,
+                 inter: int = 512, group: int = 64, device: str | torch.device = "cuda"):
+        self.layer_idx, self.capacity = layer_idx, capacity
+        self.hidden, self.inter, self.group = hidden, inter, group
+        self.store = store
+        self.blob_bytes = q2format.expert_bytes(hidden, inter, group)
+        assert store.blob_bytes == self.blob_bytes
+        dev = torch.device(device)
+        self.pool = torch.zeros((capacity, self.blob_bytes), dtype=torch.uint8, device=dev)
+        self._slot_inds_buf = torch.zeros(MAX_K, dtype=torch.int32, device=dev)
+        self._h_ws = torch.zeros(MAX_K * inter, dtype=torch.float16, device=dev)
+        L = _lib.lib()
+        L.c_set_compute_stream(ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+        u64 = ctypes.c_uint64 * 9
+        L.c_layer_init(layer_idx, -1, capacity, u64(store.layer_ptr(layer_idx), *[0] * 8),
+                       u64(self.blob_bytes, *[0] * 8), u64(self.pool.data_ptr(), *[0] * 8),
+                       self._slot_inds_buf.data_ptr())
+        _lib.check_error("c_layer_init")
+        _lib.check(L.c_layer_set_format(layer_idx, hidden, inter, group), "c_layer_set_format")
+        self._c_stats_buf = (ctypes.c_uint64 * 18)()
+        self.reset_stats()
+
+    # -- cache management (loader.py:421-555) --
+    def reset_cache(self) -> None:
+        self.wait_prefetch()
+        _lib.lib().c_layer_reset_cache(self.layer_idx)
+
+    def reset_stats(self) -> None:
+        _lib.lib().c_layer_reset_stats(self.layer_idx)
+
+    def sync_stats_from_c(self) -> None:
+        st = self._c_stats_buf
+        _lib.lib().c_layer_get_stats(self.layer_idx, st)
+        (self.decode_requests, self.decode_lru_hits, self.decode_prefetch_hits, self.decode_demand_misses,
+         self.decode_demand_bytes, self.decode_prefetch_bytes, self.prefill_requests, self.prefill_lru_hits,
+         self.prefill_demand_misses, self.prefill_demand_bytes, self.pred_top16_hits, self.pred_top16_total_actual,
+         self.pred_top16_total_pred, self.miss_pref_hits, self.miss_pref_total_actual_misses,
+         self.miss_pref_total_fetched, self.uncoalesced_tensor_reads, self.coalesced_preadv_calls) = [int(v) for v in st]
+
+    def start_prefetch(self, pred_eids: list[int], max_fetch: int = PREFETCH_MAX_CAP) -> None:
+        L = _lib.lib()
+        n = len(pred_eids)
+        if n == 10:
+            L.c_layer_start_prefetch10(self.layer_idx, max_fetch, *pred_eids)
+        elif n == 12:
+            L.c_layer_start_prefetch12(self.layer_idx, max_fetch, *pred_eids)
+        else:
+            L.c_layer_start_prefetch(self.layer_idx, (ctypes.c_int32 * max(n, 1))(*pred_eids), n, max_fetch)
+        _lib.check_error("start_prefetch")
+
+    def wait_prefetch(self) -> None:
+        _lib.lib().c_layer_wait_prefetch(self.layer_idx)
+
+    def step(self, eids: list[int]) -> int:
+        n = _lib.lib().c_layer_step_decode_ex(self.layer_idx, (ctypes.c_uint32 * len(eids))(*eids), len(eids), 1)
+        return _lib.check(n, "step_decode")
+
+    # -- compute --
+    def forward_combined(self, x: torch.Tensor, indices, scores: torch.Tensor, residual: torch.Tensor | None = None,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+        """sum_j scores[j] * SwitchGLU_{indices[j]}(x) (+ residual), fp32 [H]; one token."""
+        eids = [int(e) for e in (indices.reshape(-1).tolist() if torch.is_tensor(indices) else indices)]
+        k = len(eids)
+        self.step(eids)
+        out = out if out is not None else torch.empty(self.hidden, dtype=torch.float32, device=x.device)
+        rc = _lib.lib().c_layer_switch_glu(self.layer_idx, x.data_ptr(), scores.data_ptr(),
+                                           residual.data_ptr() if residual is not None else None,
+                                           self._h_ws.data_ptr(), out.data_ptr(), 0, k,
+                                           torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "c_layer_switch_glu")
+        return out
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        B, Lq, K = indices.shape
+        if Lq == 1 and B == 1:
+            eids = [int(e) for e in indices.reshape(-1).tolist()]
+            self.step(eids)
+            out = torch.empty((K, self.hidden), dtype=torch.float32, device=x.device)
+            xr = x.reshape(-1).to(torch.float16).contiguous()
+            rc = _lib.lib().c_layer_switch_glu(self.layer_idx, xr.data_ptr(), None, None, self._h_ws.data_ptr(),
+                                               out.data_ptr(), 1, K, torch.cuda.current_stream().cuda_stream)
+            _lib.check(rc, "c_layer_switch_glu")
+            return out.to(x.dtype).reshape(1, 1, K, self.hidden)
+        from .prefill import cached_prefill
+        return cached_prefill(self, x, indices)
+
+    def get_layer_stats(self) -> dict[str, Any]:
+        """Same keys as loader.py:701-739 (bytes are real blob bytes)."""
+        self.sync_stats_from_c()
+        dec_req = max(1, self.decode_requests)
+        pre_req = max(1, self.prefill_requests)
+        return {
+            "layer": self.layer_idx,
+            "capacity_experts": self.capacity,
+            "capacity_mb": round(self.capacity * self.blob_bytes / 1e6, 3),
+            "decode_requests": self.decode_requests,
+            "decode_lru_hits": self.decode_lru_hits,
+            "decode_prefetch_hits": self.decode_prefetch_hits,
+            "decode_demand_misses": self.decode_demand_misses,
+            "decode_pure_hit_rate": round(self.decode_lru_hits / dec_req, 5),
+            "decode_effective_hit_rate": round((self.decode_lru_hits + self.decode_prefetch_hits) / dec_req, 5),
+            "decode_demand_bytes": self.decode_demand_bytes,
+            "decode_prefetch_bytes": self.decode_prefetch_bytes,
+            "decode_total_bytes": self.decode_demand_bytes + self.decode_prefetch_bytes,
+            "prefill_requests": self.prefill_requests,
+            "prefill_lru_hits": self.prefill_lru_hits,
+            "prefill_demand_misses": self.prefill_demand_misses,
+            "prefill_hit_rate": round(self.prefill_lru_hits / pre_req, 5),
+            "prefill_demand_bytes": self.prefill_demand_bytes,
+            "top16_router_recall": round(self.pred_top16_hits / max(1, self.pred_top16_total_actual), 5),
+            "top16_router_precision": round(self.pred_top16_hits / max(1, self.pred_top16_total_pred), 5),
+            "miss_prefetch_recall": round(self.miss_pref_hits / max(1, self.miss_pref_total_actual_misses), 5),
+            "miss_prefetch_precision": round(self.miss_pref_hits / max(1, self.miss_pref_total_fetched), 5),
+            "uncoalesced_tensor_reads": self.uncoalesced_tensor_reads,
+            "coalesced_preadv_calls": self.coalesced_preadv_calls,
+        }
+
+    def close(self) -> None:
+        self.wait_prefetch()
+        torch.cuda.synchronize()
+        _lib.lib().c_sync_copies()
+        _lib.lib().c_layer_init(self.layer_idx, -1, 16, None, None, None, 0)
+
+
+class OffloadEngine:
+    """Routed-expert offload engine (loader.py:1004-1343) over the synthetic decode stack.
+
+    There is no checkpoint, tokenizer or attention here (out of scope): a "token" is a hidden
+    state fed to the 48-layer routed-expert stack; `generate_greedy` runs that stack and reports
+    the reference's timing and hit-rate keys.
+    """
+
+    def __init__(self, model_path=None, budget_gb: float | None = None, budget_pct: float | None = 20.0,
+                 alloc_mode: str = "even", prefetch: bool = True, prefetch_top_m: int = PREFETCH_TOP_M,
+                 prefetch_cap: int = PREFETCH_MAX_CAP, mode: str = "device", n_layers: int = NUM_LAYERS,
+                 hidden: int = 2048, inter: int = 512, seed: int = 0):
+        from .stack import DecodeStack, StackConfig
+        t0 = time.perf_counter()
+        self.model_path, self.alloc_mode = model_path, alloc_mode
+        self.prefetch, self.prefetch_top_m, self.prefetch_cap = prefetch, prefetch_top_m, prefetch_cap
+        cfg = StackConfig(n_layers=n_layers, hidden=hidden, inter=inter, budget_pct=budget_pct, budget_gb=budget_gb,
+                          prefetch=prefetch, top_m=prefetch_top_m, prefetch_cap=prefetch_cap, seed=seed)
+        self.model = DecodeStack(cfg, mode=mode)
+        self.capacities = self.model.capacities
+        self.total_cached_slots = sum(self.capacities.values())
+        self.cache_budget_bytes = self.total_cached_slots * self.model.blob_bytes
+        self.layer0_pinned_bytes = cfg.n_exp * self.model.blob_bytes
+        self.cached_modules = {l: l for l in range(1, n_layers)}
+        self.tokenizer = None
+        self.load_seconds = time.perf_counter() - t0
+
+    def set_prefetch(self, enabled: bool, top_m: int | None = None, cap: int | None = None) -> None:
+        self.prefetch = self.model.cfg.prefetch = enabled
+        if top_m is not None:
+            self.prefetch_top_m = self.model.cfg.top_m = top_m
+        if cap is not None:
+            self.prefetch_cap = self.model.cfg.prefetch_cap = cap
+        self.model.graph = None
+
+    def reset_caches(self) -> None:
+        self.model.reset_caches()
+
+    def reset_stats(self) -> None:
+        self.model.reset_stats()
+
+    def _snapshot_decode_totals(self) -> tuple[int, int, int, int, int, int]:
+        return tuple(self.model.decode_totals())
+
+    def generate_greedy(self, user_content=None, max_new_tokens: int = 128, reset_cache_before: bool = False,
+                        reset_stats_before: bool = False, seed: int = 1234) -> dict[str, Any]:
+        """Decode `max_new_tokens` synthetic tokens (hidden states ~ N(0,1) seeded from
+        user_content) and report the reference's keys (loader.py:1223-1244)."""
+        if reset_cache_before:
+            self.reset_caches()
+        if reset_stats_before:
+            self.reset_stats()
+        c = self.model.cfg
+        if isinstance(user_content, str):
+            seed = sum(user_content.encode()) + seed
+        gen = torch.Generator(device=self.model.device)
+        gen.manual_seed(seed)
+        xs = torch.randn((max_new_tokens, c.hidden), device=self.model.device, generator=gen).half()
+        s_start = self._snapshot_decode_totals()
+        s_mid = s_start
+        mid = min(32, max_new_tokens // 2) if max_new_tokens >= 16 else max_new_tokens // 2
+        lat = []
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for d in range(max_new_tokens):
+            ts = time.perf_counter()
+            self.model.decode_token(xs[d])
+            torch.cuda.synchronize()
+            lat.append(round((time.perf_counter() - ts) * 1000.0, 3))
+            if d + 1 == mid:
+                s_mid = self._snapshot_decode_totals()
+        dec = time.perf_counter() - t0
+        s_end = self._snapshot_decode_totals()
+        tot_req = max(1, s_end[3] - s_start[3])
+        w1_req, w2_req = max(1, s_mid[3] - s_start[3]), max(1, s_end[3] - s_mid[3])
+        w1 = sum(lat[:mid]) / 1000.0
+        w2 = sum(lat[mid:]) / 1000.0
+        return {
+            "prompt_tokens": 0,
+            "decode_tokens": max_new_tokens,
+            "decode_seconds": round(dec, 4),
+            "decode_tok_per_s": round(max_new_tokens / dec, 3),
+            "prompt_pure_lru_hit_rate": round((s_end[0] - s_start[0]) / tot_req, 5),
+            "prompt_effective_hit_rate": round((s_end[0] - s_start[0] + s_end[1] - s_start[1]) / tot_req, 5),
+            "prompt_mb_per_token": round((s_end[4] - s_start[4] + s_end[5] - s_start[5]) / max(1, max_new_tokens) / 1e6, 3),
+            "first_window_tokens": mid,
+            "first_window_pure_hit_rate": round((s_mid[0] - s_start[0]) / w1_req, 5),
+            "first_window_effective_hit_rate": round((s_mid[0] - s_start[0] + s_mid[1] - s_start[1]) / w1_req, 5),
+            "first_window_tok_per_s": round(mid / max(1e-6, w1), 3),
+            "steady_window_tokens": max_new_tokens - mid,
+            "steady_window_pure_hit_rate": round((s_end[0] - s_mid[0]) / w2_req, 5),
+            "steady_window_effective_hit_rate": round((s_end[0] - s_mid[0] + s_end[1] - s_mid[1]) / w2_req, 5),
+            "steady_window_tok_per_s": round((max_new_tokens - mid) / max(1e-6, w2), 3),
+            "step_latencies_ms": lat,
+        }
+
+    def collect_stats(self, total_decode_tokens: int, total_prefill_tokens: int = 0) -> dict[str, Any]:
+        n = self.model.cfg.n_layers
+        per = []
+        for l in range(1, n):
+            st = self.model.layer_stats(l)
+            per.append({"layer": l, "capacity_experts": self.capacities[l], "decode_requests": st[0],
+                        "decode_lru_hits": st[1], "decode_prefetch_hits": st[2], "decode_demand_misses": st[3],
+                        "decode_demand_bytes": st[4], "decode_prefetch_bytes": st[5], "prefill_requests": st[6],
+                        "prefill_lru_hits": st[7], "prefill_demand_misses": st[8], "prefill_demand_bytes": st[9],
+                        "pred_hits": st[10], "pred_actual": st[11], "pred_total": st[12], "miss_pref_hits": st[13],
+                        "miss_actual": st[14], "miss_fetched": st[15]})
+        req = sum(p["decode_requests"] for p in per)
+        lru = sum(p["decode_lru_hits"] for p in per)
+        pref = sum(p["decode_prefetch_hits"] for p in per)
+        dem_b = sum(p["decode_demand_bytes"] for p in per)
+        pref_b = sum(p["decode_prefetch_bytes"] for p in per)
+        dec_tok = max(1, total_decode_tokens)
+        return {
+            "budget_summary": {
+                "alloc_mode": self.alloc_mode, "prefetch_enabled": self.prefetch,
+                "prefetch_top_m": self.prefetch_top_m if self.prefetch else 0,
+                "prefetch_cap": self.prefetch_cap if self.prefetch else 0,
+                "layer0_pinned_experts": self.model.cfg.n_exp, "layer0_pinned_bytes": self.layer0_pinned_bytes,
+                "cached_layers_count": n - 1, "total_cached_slots": self.total_cached_slots,
+                "cache_budget_bytes": self.cache_budget_bytes,
+            },
+            "decode_aggregate": {
+                "total_decode_tokens": total_decode_tokens, "total_requests": req, "lru_hits": lru,
+                "prefetch_hits": pref, "demand_misses": sum(p["decode_demand_misses"] for p in per),
+                "pure_lru_hit_rate": round(lru / max(1, req), 5),
+                "effective_hit_rate": round((lru + pref) / max(1, req), 5),
+                "top_m_router_recall": round(sum(p["pred_hits"] for p in per) / max(1, sum(p["pred_actual"] for p in per)), 5),
+                "miss_prefetch_recall": round(sum(p["miss_pref_hits"] for p in per) / max(1, sum(p["miss_actual"] for p in per)), 5),
+                "demand_bytes_read": dem_b, "prefetch_bytes_read": pref_b,
+                "total_mb_per_token": round((dem_b + pref_b) / dec_tok / 1e6, 3),
+            },
+            "per_layer": per,
+        }
+
+    def close(self) -> None:
+        self.model.close()

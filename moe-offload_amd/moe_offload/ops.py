@@ -65,6 +65,15 @@ def router(w: torch.Tensor, k: int, *, x: torch.Tensor | None = None, h: torch.T
     return ids, scores, (pred if w_next is not None else None)
 
 
+def rmsnorm(h: torch.Tensor, norm_w: torch.Tensor | None, eps: float = 1e-6, out: torch.Tensor | None = None):
+    """fp16 RMSNorm of an fp32 vector (fp64 math, one rounding)."""
+    assert h.dtype == torch.float32 and h.is_contiguous()
+    out = out if out is not None else torch.empty(h.numel(), dtype=torch.float16, device=h.device)
+    rc = _lib.lib().moe_rmsnorm(_p(h), _p(norm_w), eps, h.numel(), _p(out), _stream())
+    _lib.check(rc, "moe_rmsnorm")
+    return out
+
+
 def q2_switch_glu(x: torch.Tensor, pool: torch.Tensor, slots: torch.Tensor, hidden: int, inter: int,
                   group: int = 64, scores: torch.Tensor | None = None, residual: torch.Tensor | None = None,
                   per_expert: bool = False, h_ws: torch.Tensor | None = None, out: torch.Tensor | None = None):

@@ -1,0 +1,293 @@
+"""Stacked routed-expert decode (the 48-layer workload) on one MI355X.
+
+Each layer l has an fp16 router W_l [E, H], Q2 g64 SwitchGLU experts (inter I) and an fp16
+RMSNorm after it (builder-defined glue; the reference mixes hyper-connections there,
+`mlx-qwen38/loader.py:61,992`):
+
+    x_0 = token hidden state (fp16)
+    ids_l, scores_l      = router(x_l; W_l)                       (loader.py:903-908)
+    pred_{l+1}           = top-m(W_{l+1} . x_l)                    (loader.py:950-958)
+    h_l                  = x_l + sum_j scores_j SwitchGLU_{ids_j}(x_l)   (fp32)
+    x_{l+1}              = RMSNorm_l(h_l)  (fp16, eps 1e-6; fused into the next router)
+
+Layer 0's experts are resident in HBM (the reference pins them, loader.py:1059-1060);
+layers 1..L-1 keep `capacity` slots in HBM, fed from a pinned host expert store.  The slot
+tables follow the reference's call order per token: prefetch(1) after layer 0, then step(l)
+followed by prefetch(l+1) (loader.py:920-977).
+
+Two drivers:
+  mode="device"  slot tables live on the GPU; a layer is router -> slot step -> staging kernel
+                 -> gate/up -> down with no host round trip; next-layer prefetch (table update +
+                 staging) runs on a side stream and joins before the next layer's step.  A whole
+                 token can be captured into one HIP graph.
+  mode="host"    the reference's shape: one device->host read of the ids per layer, the host
+                 slot table (expert_io.c ABI), DMA copies on the library's copy stream.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib, q2format
+from .loader import HostExpertStore, compute_layer_capacities
+
+
+@dataclass
+class StackConfig:
+    n_layers: int = 48
+    hidden: int = 2048
+    n_exp: int = 512
+    top_k: int = 10
+    inter: int = 512
+    group: int = 64
+    budget_pct: float | None = 20.0
+    budget_gb: float | None = None
+    prefetch: bool = True
+    top_m: int = 12
+    prefetch_cap: int = 3
+    eps: float = 1e-6
+    seed: int = 0
+    layer_base: int = 0          # first C-ABI layer index used (tables are global to the library)
+    stage_ctas: int = 0          # staging kernel grid (0 = library default)
+
+
+def random_blobs(n_exp: int, hidden: int, inter: int, group: int, gen: torch.Generator, device,
+                 scale_std: float = 0.02) -> torch.Tensor:
+    """Synthetic Q2 experts as blobs, generated on the GPU: codes ~ U{0..3} (uniform random
+    bytes), scale ~ N(0, scale_std) fp16, bias = -1.5 * scale."""
+    o = q2format.blob_offsets(hidden, inter, group)
+    blobs = torch.empty((n_exp, o["bytes"]), dtype=torch.uint8, device=device)
+    code_bytes = o["gate_sb"]
+    blobs[:, :code_bytes] = torch.randint(0, 256, (n_exp, code_bytes), dtype=torch.uint8, device=device,
+                                          generator=gen)
+    n_pairs = (o["bytes"] - code_bytes) // 4
+    s = (torch.randn((n_exp, n_pairs), device=device, generator=gen) * scale_std).half()
+    b = (-1.5 * s.float()).half()
+    sb = torch.stack([s, b], dim=-1).contiguous().view(torch.uint8).view(n_exp, n_pairs * 4)
+    blobs[:, code_bytes:] = sb
+    return blobs
+
+
+class DecodeStack:
+    def __init__(self, cfg: StackConfig = StackConfig(), mode: str = "device", device="cuda"):
+        assert mode in ("device", "host")
+        self.cfg, self.mode = cfg, mode
+        self.device = torch.device(device)
+        c = cfg
+        L = _lib.lib()
+        self.L = L
+        self.blob_bytes = q2format.expert_bytes(c.hidden, c.inter, c.group)
+        caps = compute_layer_capacities(budget_gb=c.budget_gb, budget_pct=c.budget_pct, num_layers=c.n_layers,
+                                        num_experts=c.n_exp, expert_bytes=self.blob_bytes)
+        self.capacities = caps
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(c.seed)
+        dev = self.device
+        self.router_w = (torch.randn((c.n_layers, c.n_exp, c.hidden), device=dev, generator=gen) * 0.02).half()
+        self.norm_w = (1.0 + 0.1 * torch.randn((c.n_layers, c.hidden), device=dev, generator=gen)).half()
+        # layer 0: every expert resident
+        self.pool0 = random_blobs(c.n_exp, c.hidden, c.inter, c.group, gen, dev)
+        # layers 1..: pinned host store + HBM slot pools
+        self.store = HostExpertStore(c.n_layers, c.n_exp, self.blob_bytes, first_layer=1)
+        self.pools, self.slot_inds = {}, {}
+        for l in range(1, c.n_layers):
+            blobs = random_blobs(c.n_exp, c.hidden, c.inter, c.group, gen, dev)
+            self.store.tensor(l).copy_(blobs)
+            del blobs
+            self.pools[l] = torch.zeros((caps[l], self.blob_bytes), dtype=torch.uint8, device=dev)
+            self.slot_inds[l] = torch.zeros(16, dtype=torch.int32, device=dev)
+        torch.cuda.synchronize()
+        L.c_set_compute_stream(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        u64 = ctypes.c_uint64 * 9
+        for l in range(1, c.n_layers):
+            li = self.cidx(l)
+            L.c_layer_init(li, -1, caps[l], u64(self.store.layer_ptr(l), *[0] * 8), u64(self.blob_bytes, *[0] * 8),
+                           u64(self.pools[l].data_ptr(), *[0] * 8), self.slot_inds[l].data_ptr())
+            _lib.check(L.c_layer_set_format(li, c.hidden, c.inter, c.group), "set_format")
+            if mode == "device":
+                _lib.check(L.c_layer_set_device_mode(li, 1), "set_device_mode")
+        _lib.check_error("c_layer_init")
+        # per-layer outputs / workspaces (fixed addresses, so a token can be graph-captured)
+        k = c.top_k
+        self.ids = torch.zeros((c.n_layers, k), dtype=torch.int32, device=dev)
+        self.scores = torch.zeros((c.n_layers, k), dtype=torch.float16, device=dev)
+        self.pred = torch.zeros((c.n_layers, max(c.top_m, 1)), dtype=torch.int32, device=dev)
+        self.xs = torch.zeros((c.n_layers + 1, c.hidden), dtype=torch.float16, device=dev)
+        self.hs = torch.zeros((c.n_layers, c.hidden), dtype=torch.float32, device=dev)
+        self.h_ws = torch.zeros((c.top_k * c.inter,), dtype=torch.float16, device=dev)
+        self.router_ws = [torch.zeros(int(L.moe_router_workspace_bytes(c.n_exp)), dtype=torch.uint8, device=dev)
+                          for _ in range(c.n_layers)]
+        self.side = torch.cuda.Stream(device=dev)
+        self.ev_pred = [torch.cuda.Event() for _ in range(c.n_layers)]
+        self.ev_pref = [torch.cuda.Event() for _ in range(c.n_layers)]
+        self.timing = None           # optional list of (layer, kind, start_event, end_event)
+        self.graph = None
+
+    # C-ABI layer index of stack layer l
+    def cidx(self, l: int) -> int:
+        return self.cfg.layer_base + l
+
+    def reset_caches(self):
+        for l in range(1, self.cfg.n_layers):
+            self.L.c_layer_reset_cache(self.cidx(l))
+        _lib.check_error("reset_cache")
+
+    def reset_stats(self):
+        for l in range(1, self.cfg.n_layers):
+            self.L.c_layer_reset_stats(self.cidx(l))
+
+    def layer_stats(self, l: int) -> list[int]:
+        o = (ctypes.c_uint64 * 18)()
+        self.L.c_layer_get_stats(self.cidx(l), o)
+        return list(o)
+
+    # ---- one token ---------------------------------------------------------------------------
+    def _router(self, l: int):
+        c = self.cfg
+        wn = self.router_w[l + 1] if (c.prefetch and l + 1 < c.n_layers) else None
+        x_in = self.xs[0] if l == 0 else None
+        h_in = None if l == 0 else self.hs[l - 1]
+        rc = self.L.moe_router(h_in.data_ptr() if h_in is not None else None,
+                               self.norm_w[l - 1].data_ptr() if l > 0 else None, c.eps,
+                               x_in.data_ptr() if x_in is not None else None,
+                               self.xs[l].data_ptr() if l > 0 else None,
+                               self.router_w[l].data_ptr(), wn.data_ptr() if wn is not None else None,
+                               c.hidden, c.n_exp, c.top_k, c.top_m if wn is not None else 0,
+                               self.router_ws[l].data_ptr(), self.ids[l].data_ptr(), self.scores[l].data_ptr(),
+                               self.pred[l].data_ptr(), torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "router")
+
+    def _glu(self, l: int):
+        c = self.cfg
+        stream = torch.cuda.current_stream().cuda_stream
+        L = self.L
+        if l == 0:
+            pool, stride, n_slots, slots = self.pool0.data_ptr(), self.blob_bytes, c.n_exp, self.ids[0].data_ptr()
+        else:
+            pool, stride, n_slots = self.pools[l].data_ptr(), self.blob_bytes, self.capacities[l]
+            slots = self.slot_inds[l].data_ptr()
+        if self.timing is None:
+            if l == 0 or self.mode == "device":
+                # device-driven layers are ordered by the stream alone (no copy/read events)
+                rc = L.moe_q2_switch_glu(self.xs[l].data_ptr(), pool, stride, n_slots, slots, self.scores[l].data_ptr(),
+                                         c.top_k, c.hidden, c.inter, c.group, self.xs[l].data_ptr(),
+                                         self.h_ws.data_ptr(), self.hs[l].data_ptr(), 0, stream)
+            else:
+                rc = L.c_layer_switch_glu(self.cidx(l), self.xs[l].data_ptr(), self.scores[l].data_ptr(),
+                                          self.xs[l].data_ptr(), self.h_ws.data_ptr(), self.hs[l].data_ptr(), 0,
+                                          c.top_k, stream)
+            _lib.check(rc, "switch_glu")
+            return
+        # instrumented: gate/up and down launched separately between HIP events on this stream
+        if l > 0 and self.mode == "host":
+            L.c_layer_wait_prefetch(self.cidx(l))
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record()
+        _lib.check(L.moe_q2_gate_up(self.xs[l].data_ptr(), pool, stride, n_slots, slots, c.top_k, c.hidden, c.inter,
+                                    c.group, self.h_ws.data_ptr(), stream), "gate_up")
+        ev[1].record()
+        _lib.check(L.moe_q2_down(self.h_ws.data_ptr(), pool, stride, n_slots, slots, self.scores[l].data_ptr(),
+                                 c.top_k, c.hidden, c.inter, c.group, self.xs[l].data_ptr(), self.hs[l].data_ptr(),
+                                 0, stream), "down")
+        ev[2].record()
+        if l > 0 and self.mode == "host":
+            _lib.check(L.c_layer_mark_read(self.cidx(l), stream), "mark_read")
+        self.timing.append((l, ev[0], ev[1], ev[2]))
+
+    def decode_token_device(self):
+        """Device-driven token: no host synchronisation; reads xs[0], writes xs[n_layers]."""
+        c = self.cfg
+        main = torch.cuda.current_stream()
+        for l in range(c.n_layers):
+            if l >= 1 and c.prefetch:
+                main.wait_event(self.ev_pref[l])           # prefetch(l) landed (table + slots)
+            self._router(l)
+            if l >= 1:
+                _lib.check(self.L.c_layer_step_decode_dev(self.cidx(l), self.ids[l].data_ptr(), c.top_k,
+                                                          c.stage_ctas, main.cuda_stream), "step_dev")
+            if c.prefetch and l + 1 < c.n_layers:
+                self.ev_pred[l].record(main)
+                self.side.wait_event(self.ev_pred[l])
+                _lib.check(self.L.c_layer_start_prefetch_dev(self.cidx(l + 1), self.pred[l].data_ptr(), c.top_m,
+                                                             c.prefetch_cap, c.stage_ctas, self.side.cuda_stream),
+                           "prefetch_dev")
+                self.ev_pref[l + 1].record(self.side)
+            self._glu(l)
+        _lib.check(self.L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
+                                      c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), main.cuda_stream), "rmsnorm")
+
+    def decode_token_host(self):
+        """Reference-shaped token: one device->host read of (ids, pred) per layer."""
+        c = self.cfg
+        L = self.L
+        main = torch.cuda.current_stream()
+        L.c_set_compute_stream(ctypes.c_void_p(main.cuda_stream))
+        for l in range(c.n_layers):
+            self._router(l)
+            if l == 0:
+                self._glu(0)
+                if c.prefetch and c.n_layers > 1:
+                    p = self.pred[0, :c.top_m].tolist()
+                    L.c_layer_start_prefetch(self.cidx(1), (ctypes.c_int32 * c.top_m)(*p), c.top_m, c.prefetch_cap)
+                continue
+            sel = torch.cat([self.ids[l], self.pred[l, :c.top_m]]).tolist()      # the one sync per layer
+            ids, pred = sel[:c.top_k], sel[c.top_k:]
+            n = L.c_layer_step_decode_ex(self.cidx(l), (ctypes.c_uint32 * c.top_k)(*ids), c.top_k, 1)
+            _lib.check(n, "step")
+            self._glu(l)                                  # waits for this layer's copies on the GPU
+            if c.prefetch and l + 1 < c.n_layers:
+                L.c_layer_start_prefetch(self.cidx(l + 1), (ctypes.c_int32 * c.top_m)(*pred), c.top_m,
+                                         c.prefetch_cap)
+        _lib.check_error("decode_token_host")
+        _lib.check(L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
+                                 c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), main.cuda_stream), "rmsnorm")
+
+    def decode_token(self, x0: torch.Tensor | None = None) -> torch.Tensor:
+        if x0 is not None:
+            self.xs[0].copy_(x0)
+        if self.mode == "device":
+            if self.graph is not None:
+                self.graph.replay()
+            else:
+                self.decode_token_device()
+        else:
+            self.decode_token_host()
+        return self.xs[self.cfg.n_layers]
+
+    def capture_graph(self):
+        """Capture one device-driven token into a HIP graph (replayed by decode_token)."""
+        assert self.mode == "device"
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                self.decode_token_device()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.graph = g
+
+    def decode_totals(self) -> list[int]:
+        o = (ctypes.c_uint64 * 6)()
+        self.L.c_get_decode_totals(self.cidx(self.cfg.n_layers), o)
+        return list(o)
+
+    def close(self):
+        torch.cuda.synchronize()
+        self.L.c_sync_copies()
+        for l in range(1, self.cfg.n_layers):
+            self.L.c_layer_init(self.cidx(l), -1, 16, None, None, None, 0)
+        self.graph = None
+        self.store.close()
+
+    # algorithmic bytes of the routed experts touched per token (the roofline numerator)
+    def routed_bytes_per_token(self) -> int:
+        return self.cfg.n_layers * self.cfg.top_k * self.blob_bytes
+
+    def router_bytes_per_token(self) -> int:
+        c = self.cfg
+        per = c.n_exp * c.hidden * 2
+        return c.n_layers * per + (c.n_layers - 1) * per * int(c.prefetch)

@@ -15,9 +15,9 @@ Predictor (`loader.py:237-242`, `layers.cpp:327-341`): top-m of the raw logits, 
   the same stable ascending rule, emitted in descending value order (equal values keep
   ascending id order).
 
-Arithmetic convention shared with the HIP kernels: dot products and the softmax are evaluated
-in float64 and rounded once through float32 to the storage dtype, so that two correct
-implementations agree bit for bit on every rounded value.
+Arithmetic convention shared with the HIP kernels: dot products, the softmax and RMSNorm are
+evaluated in float64 and rounded once, directly, to fp16, so that two correct implementations
+agree bit for bit on every rounded value.
 
 Pinning:
   dequant / SwitchGLU  -> golden `moe.y_dec`, `moe.y_pre` (fixtures.safetensors) within
@@ -48,12 +48,16 @@ def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
 
 
 def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
-    """Round float64 values to `dtype` ('f16' | 'bf16' | 'f32') through float32; returns float64."""
-    x32 = np.asarray(x, dtype=np.float64).astype(np.float32)
+    """Round float64 values to `dtype`; returns float64.
+
+    'f16' rounds once, directly from float64 (round-to-nearest-even), as the HIP kernels do;
+    'bf16' goes through float32 like MLX's fp32 compute followed by a cast."""
+    x64 = np.asarray(x, dtype=np.float64)
+    if dtype == "f16":
+        return x64.astype(np.float16).astype(np.float64)
+    x32 = x64.astype(np.float32)
     if dtype == "f32":
         return x32.astype(np.float64)
-    if dtype == "f16":
-        return x32.astype(np.float16).astype(np.float64)
     if dtype == "bf16":
         return bf16_bits_to_f32(f32_to_bf16_bits(x32)).astype(np.float64)
     raise ValueError(dtype)

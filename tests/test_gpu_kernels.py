@@ -110,7 +110,7 @@ def test_switch_glu_per_expert_and_gate_up(dev, layer):
         gg = q2.qmatvec(x.astype(np.float64), *g, 2, 64)
         uu = q2.qmatvec(x.astype(np.float64), *u, 2, 64)
         hh = q2.silu(gg) * uu
-        assert_close_rms(h[j], hh, 2e-3, f"h expert {e}")
+        assert_close_rms(h[j], hh, 4e-3, f"h expert {e}")  # h is stored as fp16
         assert_close_rms(y[j], q2.qmatvec(hh, *d, 2, 64), 1e-2, f"y expert {e}")
 
 

@@ -151,7 +151,7 @@ def config2_store(L):
     yield mlx, ptr, blob
     torch.cuda.synchronize()
     L.c_sync_copies()
-    for layer in (63, 64):
+    for layer in (57, 58):
         L.c_layer_init(layer, -1, 16, None, None, None, 0)
     L.c_host_free(ptr)
 
@@ -166,7 +166,7 @@ def test_config2_single_layer_decode(L, lru_traces, config2_store, mode):
     ids_all = synth.expert_id_stream(steps=128, k=K, seed=2)
     assert ids_all.tolist() == [op["ids"] for op in steps]
     cap = 102
-    layer = 63 if mode == "host" else 64
+    layer = 57 if mode == "host" else 58
     pool = torch.zeros((cap, blob), dtype=torch.uint8, device="cuda")
     slots = torch.zeros(16, dtype=torch.int32, device="cuda")
     _init_layer(L, layer, cap, store_ptr=ptr, blob=blob, pool_ptr=pool.data_ptr(), slot_ptr=slots.data_ptr())

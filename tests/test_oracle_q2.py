@@ -145,9 +145,15 @@ def test_topk_tie_rule_bruteforce():
         assert q2.predict_topm(v[None], k)[0].tolist() == sorted(top, key=lambda i: (-v[i], i))
 
 
-def test_round_to_fp16_matches_numpy_and_bf16_rne():
+def test_round_to_fp16_is_single_rounding_and_bf16_rne():
     x = np.array([1.0, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, 65504.0, 1e-8])
-    assert np.array_equal(q2.round_to(x, "f16"), x.astype(np.float32).astype(np.float16).astype(np.float64))
+    # exact ties go to even
+    assert q2.round_to(x, "f16").tolist()[:3] == [1.0, 1.0, 1.0 + 2 ** -9]
+    # just above a tie: one rounding goes up; rounding through float32 would land on the tie
+    # and go to even (the double-rounding trap)
+    y = np.array([1.0 + 2 ** -11 + 2 ** -40])
+    assert q2.round_to(y, "f16")[0] == 1.0 + 2 ** -10
+    assert y.astype(np.float32).astype(np.float16)[0] == 1.0
     # bf16 ties to even: 1 + 2^-8 is halfway between 1 and 1 + 2^-7 -> 1
     assert q2.round_to(np.array([1.0 + 2 ** -8]), "bf16")[0] == 1.0
     assert q2.round_to(np.array([1.0 + 3 * 2 ** -8]), "bf16")[0] == 1.0 + 2 ** -6
