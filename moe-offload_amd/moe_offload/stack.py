@@ -51,6 +51,7 @@ class StackConfig:
     seed: int = 0
     layer_base: int = 0          # first C-ABI layer index used (tables are global to the library)
     stage_ctas: int = 0          # staging kernel grid (0 = library default)
+    resident: bool = False       # every layer's experts in HBM (no slot tables, no staging)
 
 
 def random_blobs(n_exp: int, hidden: int, inter: int, group: int, gen: torch.Generator, device,
@@ -89,9 +90,17 @@ class DecodeStack:
         self.norm_w = (1.0 + 0.1 * torch.randn((c.n_layers, c.hidden), device=dev, generator=gen)).half()
         # layer 0: every expert resident
         self.pool0 = random_blobs(c.n_exp, c.hidden, c.inter, c.group, gen, dev)
+        self.pools, self.slot_inds = {}, {}
+        if c.resident:
+            # all layers resident: pools hold every expert and slot == expert id
+            self.store = None
+            self.full_pools = [self.pool0] + [random_blobs(c.n_exp, c.hidden, c.inter, c.group, gen, dev)
+                                              for _ in range(1, c.n_layers)]
+            self._init_buffers()
+            return
+        self.full_pools = None
         # layers 1..: pinned host store + HBM slot pools
         self.store = HostExpertStore(c.n_layers, c.n_exp, self.blob_bytes, first_layer=1)
-        self.pools, self.slot_inds = {}, {}
         for l in range(1, c.n_layers):
             blobs = random_blobs(c.n_exp, c.hidden, c.inter, c.group, gen, dev)
             self.store.tensor(l).copy_(blobs)
@@ -109,7 +118,11 @@ class DecodeStack:
             if mode == "device":
                 _lib.check(L.c_layer_set_device_mode(li, 1), "set_device_mode")
         _lib.check_error("c_layer_init")
+        self._init_buffers()
+
+    def _init_buffers(self):
         # per-layer outputs / workspaces (fixed addresses, so a token can be graph-captured)
+        c, L, dev = self.cfg, self.L, self.device
         k = c.top_k
         self.ids = torch.zeros((c.n_layers, k), dtype=torch.int32, device=dev)
         self.scores = torch.zeros((c.n_layers, k), dtype=torch.float16, device=dev)
@@ -130,11 +143,15 @@ class DecodeStack:
         return self.cfg.layer_base + l
 
     def reset_caches(self):
+        if self.cfg.resident:
+            return
         for l in range(1, self.cfg.n_layers):
             self.L.c_layer_reset_cache(self.cidx(l))
         _lib.check_error("reset_cache")
 
     def reset_stats(self):
+        if self.cfg.resident:
+            return
         for l in range(1, self.cfg.n_layers):
             self.L.c_layer_reset_stats(self.cidx(l))
 
@@ -163,13 +180,14 @@ class DecodeStack:
         c = self.cfg
         stream = torch.cuda.current_stream().cuda_stream
         L = self.L
-        if l == 0:
-            pool, stride, n_slots, slots = self.pool0.data_ptr(), self.blob_bytes, c.n_exp, self.ids[0].data_ptr()
+        if l == 0 or c.resident:
+            pool = (self.full_pools[l] if c.resident else self.pool0).data_ptr()
+            stride, n_slots, slots = self.blob_bytes, c.n_exp, self.ids[l].data_ptr()
         else:
             pool, stride, n_slots = self.pools[l].data_ptr(), self.blob_bytes, self.capacities[l]
             slots = self.slot_inds[l].data_ptr()
         if self.timing is None:
-            if l == 0 or self.mode == "device":
+            if l == 0 or self.mode == "device" or c.resident:
                 # device-driven layers are ordered by the stream alone (no copy/read events)
                 rc = L.moe_q2_switch_glu(self.xs[l].data_ptr(), pool, stride, n_slots, slots, self.scores[l].data_ptr(),
                                          c.top_k, c.hidden, c.inter, c.group, self.xs[l].data_ptr(),
@@ -181,7 +199,7 @@ class DecodeStack:
             _lib.check(rc, "switch_glu")
             return
         # instrumented: gate/up and down launched separately between HIP events on this stream
-        if l > 0 and self.mode == "host":
+        if l > 0 and self.mode == "host" and not c.resident:
             L.c_layer_wait_prefetch(self.cidx(l))
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         ev[0].record()
@@ -192,7 +210,7 @@ class DecodeStack:
                                  c.top_k, c.hidden, c.inter, c.group, self.xs[l].data_ptr(), self.hs[l].data_ptr(),
                                  0, stream), "down")
         ev[2].record()
-        if l > 0 and self.mode == "host":
+        if l > 0 and self.mode == "host" and not c.resident:
             _lib.check(L.c_layer_mark_read(self.cidx(l), stream), "mark_read")
         self.timing.append((l, ev[0], ev[1], ev[2]))
 
@@ -201,6 +219,10 @@ class DecodeStack:
         c = self.cfg
         main = torch.cuda.current_stream()
         for l in range(c.n_layers):
+            if c.resident:
+                self._router(l)
+                self._glu(l)
+                continue
             if l >= 1 and c.prefetch:
                 main.wait_event(self.ev_pref[l])           # prefetch(l) landed (table + slots)
             self._router(l)
@@ -247,7 +269,7 @@ class DecodeStack:
     def decode_token(self, x0: torch.Tensor | None = None) -> torch.Tensor:
         if x0 is not None:
             self.xs[0].copy_(x0)
-        if self.mode == "device":
+        if self.mode == "device" or self.cfg.resident:
             if self.graph is not None:
                 self.graph.replay()
             else:
@@ -271,16 +293,21 @@ class DecodeStack:
         self.graph = g
 
     def decode_totals(self) -> list[int]:
+        if self.cfg.resident:
+            return [0] * 6
         o = (ctypes.c_uint64 * 6)()
         self.L.c_get_decode_totals(self.cidx(self.cfg.n_layers), o)
         return list(o)
 
     def close(self):
         torch.cuda.synchronize()
+        self.graph = None
+        if self.cfg.resident:
+            self.full_pools = None
+            return
         self.L.c_sync_copies()
         for l in range(1, self.cfg.n_layers):
             self.L.c_layer_init(self.cidx(l), -1, 16, None, None, None, 0)
-        self.graph = None
         self.store.close()
 
     # algorithmic bytes of the routed experts touched per token (the roofline numerator)
