@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--cpu-sample-s", type=float, default=15.0, help="CPU baseline time budget (seconds)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--extras", action="store_true", help="add per-kernel and cache details to the JSON line")
+    ap.add_argument("--stage-ctas", type=int, default=2, help="staging blocks per copied expert")
+    ap.add_argument("--skip-resident", action="store_true", help="headline pass only (for sweeps)")
     return ap.parse_args()
 
 
@@ -105,19 +107,26 @@ def timed_tokens(st, xs, warmup, steps, use_graph):
     return elapsed, tot0, st.decode_totals()
 
 
-def gemv_timing(st, xs, warmup, steps):
-    """HIP events around the gate/up and down launches (eager, same stream), per launch."""
-    import numpy as np
+KINDS = ["router", "gate_up", "down", "stage", "slot_table"]
+
+
+def kernel_timing(st, xs, warmup, steps):
+    """Kernel durations over `steps` eager tokens: every library launch is dispatched with a
+    start/stop HIP event pair on its own stream, stamped at the kernel's begin and end."""
+    import ctypes
+
     import torch
+
+    from moe_offload import _lib
     st.graph = None
-    st.timing = []
+    L = st.L
+    _lib.check(L.c_timing_begin(steps * st.cfg.n_layers * 6 + 256), "timing_begin")
     for i in range(warmup, warmup + steps):
         st.decode_token(xs[i])
     torch.cuda.synchronize()
-    gu = [a.elapsed_time(b) for (_, a, b, _) in st.timing]
-    dn = [b.elapsed_time(c) for (_, _, b, c) in st.timing]
-    st.timing = None
-    return float(np.mean(gu)) / 1e3, float(np.mean(dn)) / 1e3
+    ms, n = (ctypes.c_double * 5)(), (ctypes.c_int * 5)()
+    _lib.check(L.c_timing_end(ms, n), "timing_end")
+    return {k: {"launches": n[i], "avg_us": (ms[i] / n[i] * 1e3) if n[i] else 0.0} for i, k in enumerate(KINDS)}
 
 
 def main():
@@ -138,7 +147,8 @@ def main():
     use_graph = args.mode == "device" and not args.no_graph
 
     # ---- headline: 20% cache, misses staged from the pinned host store ---------------------
-    cfg = StackConfig(n_layers=args.layers, budget_pct=args.budget_pct, prefetch=not args.no_prefetch)
+    cfg = StackConfig(n_layers=args.layers, budget_pct=args.budget_pct, prefetch=not args.no_prefetch,
+                      stage_ctas=args.stage_ctas)
     t0 = time.perf_counter()
     st = DecodeStack(cfg, mode=args.mode)
     setup_s = time.perf_counter() - t0
@@ -149,15 +159,23 @@ def main():
     req = max(1, tot1[3] - tot0[3])
     staged = (tot1[4] - tot0[4]) + (tot1[5] - tot0[5])
     caps = st.capacities
+    head_k = kernel_timing(st, xs, args.warmup, min(args.steps, 32)) if args.extras else None
     st.close()
     del st
     torch.cuda.empty_cache()
+    if args.skip_resident:
+        print(json.dumps({"value": round(tok_s, 2), "stage_ctas": args.stage_ctas,
+                          "staged_gb_per_s": round(staged / elapsed / 1e9, 2),
+                          "headline_kernels_us": {k: round(v["avg_us"], 2) for k, v in (head_k or {}).items()
+                                                  if v["launches"]}}), flush=True)
+        return
 
     # ---- resident pass: every expert in HBM, the GEMV's own roofline -------------------------
     rcfg = StackConfig(n_layers=args.layers, prefetch=False, resident=True)
     rst = DecodeStack(rcfg, mode="device")
     r_elapsed, _, _ = timed_tokens(rst, xs, args.warmup, args.steps, not args.no_graph)
-    gu_avg, dn_avg = gemv_timing(rst, xs, args.warmup, args.steps)
+    res_k = kernel_timing(rst, xs, args.warmup, args.steps)
+    gu_avg, dn_avg = res_k["gate_up"]["avg_us"] / 1e6, res_k["down"]["avg_us"] / 1e6
     o = q2format.blob_offsets(cfg.hidden, cfg.inter, cfg.group)
     gu_bytes = cfg.top_k * 2 * ((o["down_codes"] - o["up_codes"]) + (o["up_sb"] - o["gate_sb"]))
     dn_bytes = cfg.top_k * ((o["gate_sb"] - o["down_codes"]) + (o["bytes"] - o["down_sb"]))
@@ -188,7 +206,7 @@ def main():
                    "driver": args.mode + ("+graph" if use_graph else ""), "tokens": args.steps, "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_q2_gate_up", "measured_in": "resident pass (all experts in HBM), HIP events",
+                     "kernel": "k_q2_gate_up", "measured_in": "resident pass (all experts in HBM), per-launch HIP events stamped at kernel begin/end",
                      "bytes_per_launch": gu_bytes, "avg_launch_us": round(gu_avg * 1e6, 3)},
         "cache": {"effective_hit_rate": round((tot1[0] - tot0[0] + tot1[1] - tot0[1]) / req, 4),
                   "pure_lru_hit_rate": round((tot1[0] - tot0[0]) / req, 4),
@@ -199,7 +217,10 @@ def main():
                      "routed_frac_of_peak": round(routed * args.steps / r_elapsed / 1e9 / HBM_PEAK_GBS, 4)},
     }
     if args.extras:
-        line["extras"] = {"setup_s": round(setup_s, 1), "down_avg_launch_us": round(dn_avg * 1e6, 3),
+        line["extras"] = {"setup_s": round(setup_s, 1),
+                          "resident_kernels_us": {k: round(v["avg_us"], 3) for k, v in res_k.items() if v["launches"]},
+                          "headline_kernels_us": {k: round(v["avg_us"], 3) for k, v in head_k.items() if v["launches"]},
+                          "down_avg_launch_us": round(dn_avg * 1e6, 3),
                           "down_gbs": round(dn_bytes / dn_avg / 1e9, 1),
                           "gemv_pair_gbs": round((gu_bytes + dn_bytes) / (gu_avg + dn_avg) / 1e9, 1),
                           "routed_bytes_per_token": routed}

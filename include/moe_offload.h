@@ -89,6 +89,8 @@ int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_i
                void* workspace, uint32_t* ids_out, void* scores_out, int32_t* pred_out,
                void* stream);
 uint64_t moe_router_workspace_bytes(int n_exp);
+/* The single f64 -> f16 rounding every kernel uses (exposed so tests can check it directly). */
+int moe_f64_to_f16(const double* in, uint16_t* out, int n, void* stream);
 /* Builder-defined glue between stacked MoE layers (no reference counterpart: the reference
  * mixes hyper-connections there, loader.py:61,992): x_out fp16 = RMSNorm(h_in fp32) * norm_w,
  * the same arithmetic as moe_router's prologue. */
@@ -134,11 +136,15 @@ int c_layer_mark_read(int layer_idx, void* stream);
  * their ids from device memory and stage misses with a kernel that reads the pinned store. */
 int c_layer_set_device_mode(int layer_idx, int on);
 /* Device-driven decode step / prefetch (same decisions as c_layer_step_decode_ex /
- * c_layer_start_prefetch), queued on `stream`; stage_ctas <= 0 picks a default grid. */
+ * c_layer_start_prefetch), queued on `stream`; stage_ctas == 0 picks a default staging grid,
+ * stage_ctas < 0 updates the table only (queue the copies with c_layer_stage_dev). */
 int c_layer_step_decode_dev(int layer_idx, const uint32_t* ids_dev, int k, int stage_ctas,
                             void* stream);
 int c_layer_start_prefetch_dev(int layer_idx, const int32_t* preds_dev, int m, int max_fetch,
                                int stage_ctas, void* stream);
+/* Queue the copies of the layer's last device-side decode step (list 0) or prefetch (list 1)
+ * on `stream` (the two lists are kept apart so a step may run while prefetch copies queue). */
+int c_layer_stage_dev(int layer_idx, int list, int stage_ctas, void* stream);
 /* Device address of a device-driven layer's table; 0 otherwise. */
 uint64_t c_layer_device_table(int layer_idx);
 /* Status word of the last device-side operation (0 ok, 1 id out of range, 2 repeated id);
@@ -146,6 +152,11 @@ uint64_t c_layer_device_table(int layer_idx);
 int c_layer_table_status(int layer_idx);
 /* Block the host until every queued copy has landed. */
 int c_sync_copies(void);
+/* Per-kernel timing: launches between begin and end are dispatched with start/stop events
+ * stamped at the kernel's own begin/end; end() sums durations per kind (0 router, 1 gate/up,
+ * 2 down, 3 staging, 4 slot table) into out_ms[5] and counts into out_n[5]. */
+int c_timing_begin(int capacity);
+int c_timing_end(double* out_ms, int* out_n);
 int c_abi_version(void);
 
 #ifdef __cplusplus

@@ -27,6 +27,7 @@
 #include <unistd.h>
 
 #include <mutex>
+#include <vector>
 
 #include "moe_common.h"
 #include "slot_table_host.h"
@@ -196,7 +197,24 @@ int step_host(int layer, const uint32_t* eids, int k, int async_io) {
     return n_miss;
 }
 
+// ---- kernel timing -------------------------------------------------------------------------
+struct KtSlot { int kind; hipEvent_t start, stop; };
+std::vector<KtSlot> g_kt;                    // event pool (grows to the requested capacity)
+size_t g_kt_used = 0, g_kt_cap = 0;
+bool g_kt_on = false;
+
 }  // namespace
+
+bool kt_enabled() { return g_kt_on; }
+
+void kt_events(int kind, hipEvent_t* start, hipEvent_t* stop) {
+    *start = *stop = nullptr;
+    if (g_kt_used >= g_kt_cap) return;
+    KtSlot& k = g_kt[g_kt_used++];
+    k.kind = kind;
+    *start = k.start;
+    *stop = k.stop;
+}
 
 void moe_set_error(const char* fmt, ...) {
     std::lock_guard<std::mutex> g(g_err_mu);
@@ -346,7 +364,7 @@ void c_layer_start_prefetch(int layer, const int32_t* preds, int n, int max_fetc
     if (pull_table(L)) return;
     slot_host::prefetch(&L.tab, preds, n, max_fetch);
     if (push_table(L)) return;
-    issue_copies(layer, L, L.tab.copy_eid, L.tab.copy_slot, L.tab.n_copy);
+    issue_copies(layer, L, L.tab.pf_copy_eid, L.tab.pf_copy_slot, L.tab.pf_n_copy);
 }
 
 void c_layer_start_prefetch10(int layer, int max_fetch, int32_t e0, int32_t e1, int32_t e2, int32_t e3,
@@ -463,15 +481,16 @@ uint64_t c_layer_device_table(int layer) {
     return (uint64_t)g_layers[layer].dtab;
 }
 
-static int stage_device(LayerState& L, hipStream_t s, int ctas) {
+static int stage_device(LayerState& L, int list, hipStream_t s, int ctas) {
     for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
         uint64_t rb = L.row_bytes[t];
         if (!rb || !L.dev_src[t] || !L.dst[t]) continue;
-        if (launch_stage(L.dtab, (const uint8_t*)L.dev_src[t], rb, (uint8_t*)L.dst[t], rb, rb, ctas, s)) return -1;
+        if (launch_stage(L.dtab, list, (const uint8_t*)L.dev_src[t], rb, (uint8_t*)L.dst[t], rb, rb, ctas, s)) return -1;
     }
     return 0;
 }
 
+// stage_ctas < 0: update the table only (the copies are queued later with c_layer_stage_dev).
 int c_layer_step_decode_dev(int layer, const uint32_t* ids_dev, int k, int stage_ctas, void* stream) {
     if (!valid_layer(layer) || !g_layers[layer].init || !g_layers[layer].device_mode) {
         moe_set_error("step_decode_dev: layer %d is not a device-driven layer", layer);
@@ -481,7 +500,7 @@ int c_layer_step_decode_dev(int layer, const uint32_t* ids_dev, int k, int stage
     if (k <= 0 || k > MOE_MAX_K || k > L.capacity) { moe_set_error("step_decode_dev: k=%d out of range", k); return -1; }
     hipStream_t s = (hipStream_t)stream;
     if (launch_slot_step(L.dtab, ids_dev, k, L.slot_inds, s)) return -1;
-    return stage_device(L, s, stage_ctas);
+    return stage_ctas < 0 ? 0 : stage_device(L, 0, s, stage_ctas);
 }
 
 int c_layer_start_prefetch_dev(int layer, const int32_t* preds_dev, int m, int max_fetch, int stage_ctas,
@@ -493,7 +512,18 @@ int c_layer_start_prefetch_dev(int layer, const int32_t* preds_dev, int m, int m
     LayerState& L = g_layers[layer];
     hipStream_t s = (hipStream_t)stream;
     if (launch_slot_prefetch(L.dtab, preds_dev, m, max_fetch, s)) return -1;
-    return stage_device(L, s, stage_ctas);
+    return stage_ctas < 0 ? 0 : stage_device(L, 1, s, stage_ctas);
+}
+
+// Queue the copies listed by the layer's last device-side decode step (list 0) or prefetch
+// (list 1).
+int c_layer_stage_dev(int layer, int list, int stage_ctas, void* stream) {
+    if (!valid_layer(layer) || !g_layers[layer].init || !g_layers[layer].device_mode) {
+        moe_set_error("stage_dev: layer %d is not a device-driven layer", layer);
+        return -1;
+    }
+    if (list != 0 && list != 1) { moe_set_error("stage_dev: list %d (0 = decode step, 1 = prefetch)", list); return -1; }
+    return stage_device(g_layers[layer], list, (hipStream_t)stream, stage_ctas < 0 ? 0 : stage_ctas);
 }
 
 int c_layer_table_status(int layer) {
@@ -515,6 +545,10 @@ int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_i
     return launch_router(h_in, (const __half*)norm_w, eps, (const __half*)x_in, (__half*)x_out,
                          (const __half*)w, (const __half*)w_next, hidden, n_exp, k, m, scratch, counter,
                          ids_out, (__half*)scores_out, pred_out, (hipStream_t)stream);
+}
+
+int moe_f64_to_f16(const double* in, uint16_t* out, int n, void* stream) {
+    return launch_f64_to_f16(in, out, n, (hipStream_t)stream);
 }
 
 int moe_rmsnorm(const float* h_in, const void* norm_w, float eps, int hidden, void* x_out, void* stream) {
@@ -596,6 +630,38 @@ int c_layer_mark_read(int layer, void* stream) {
 int c_sync_copies(void) {
     if (!g_ready) return 0;
     HIP_TRY(hipStreamSynchronize(g_copy));
+    return 0;
+}
+
+// Start timing every kernel launch of this library (up to `capacity` launches).
+int c_timing_begin(int capacity) {
+    if (capacity <= 0) { moe_set_error("timing_begin: capacity %d", capacity); return -1; }
+    while (g_kt.size() < (size_t)capacity) {
+        KtSlot k{0, nullptr, nullptr};
+        HIP_TRY(hipEventCreate(&k.start));
+        HIP_TRY(hipEventCreate(&k.stop));
+        g_kt.push_back(k);
+    }
+    g_kt_cap = (size_t)capacity;
+    g_kt_used = 0;
+    g_kt_on = true;
+    return 0;
+}
+
+// Stop timing; blocks until the timed kernels finished.  out_ms[kind] = summed kernel
+// durations (ms), out_n[kind] = launches (kinds: router, gate_up, down, stage, slot table).
+int c_timing_end(double* out_ms, int* out_n) {
+    g_kt_on = false;
+    for (int i = 0; i < TK_KINDS; ++i) { out_ms[i] = 0.0; out_n[i] = 0; }
+    for (size_t i = 0; i < g_kt_used; ++i) {
+        KtSlot& k = g_kt[i];
+        HIP_TRY(hipEventSynchronize(k.stop));
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, k.start, k.stop));
+        out_ms[k.kind] += ms;
+        out_n[k.kind] += 1;
+    }
+    g_kt_used = 0;
     return 0;
 }
 

@@ -14,6 +14,7 @@
 #pragma once
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -69,10 +70,14 @@ struct SlotTable {
     int16_t eid_of[MOE_NUM_EXPERTS];    // slot -> expert id, -1 when empty
     int16_t free_stack[MOE_NUM_EXPERTS];
     uint32_t stamp[MOE_NUM_EXPERTS];    // 0 = slot not on the recency list
-    // Result of the last device-side operation: the copies it needs (eid, slot).
+    // Copies the last decode step (list 0) and the last prefetch (list 1) need: (eid, slot).
+    // Two lists, so a step may run while the previous prefetch's copies are still queued.
     int32_t n_copy;
     int32_t copy_eid[MOE_MAX_PREFETCH];
     int32_t copy_slot[MOE_MAX_PREFETCH];
+    int32_t pf_n_copy;
+    int32_t pf_copy_eid[MOE_MAX_PREFETCH];
+    int32_t pf_copy_slot[MOE_MAX_PREFETCH];
     int32_t status;                     // 0 ok; nonzero: rejected input (device kernels)
 };
 
@@ -99,11 +104,29 @@ void moe_set_error(const char* fmt, ...);
         }                                                                              \
     } while (0)
 
+// Optional per-launch kernel timing: when enabled, launchers dispatch through
+// hipExtLaunchKernelGGL with a start/stop event pair, which the runtime stamps at the kernel's
+// own begin/end; kinds index the accumulated totals.
+enum { TK_ROUTER = 0, TK_GATE_UP, TK_DOWN, TK_STAGE, TK_SLOT, TK_KINDS };
+bool kt_enabled();
+void kt_events(int kind, hipEvent_t* start, hipEvent_t* stop);   // both null when disabled / full
+
+#define MOE_LAUNCH(kind, kernel, grid, block, shmem, stream, ...)                            \
+    do {                                                                                     \
+        hipEvent_t _ks = nullptr, _ke = nullptr;                                             \
+        if (kt_enabled()) kt_events(kind, &_ks, &_ke);                                       \
+        if (_ks)                                                                             \
+            hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, _ks, _ke, 0, __VA_ARGS__); \
+        else                                                                                 \
+            hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);             \
+    } while (0)
+
 // Kernel launchers implemented in the .hip translation units (return 0 / -1).
 int launch_router(const float* h_in, const __half* norm_w, float eps, const __half* x_in,
                   __half* x_out, const __half* w, const __half* w_next, int hidden, int n_exp,
                   int k, int m, float* scratch, unsigned* counter, uint32_t* ids_out,
                   __half* scores_out, int32_t* pred_out, hipStream_t s);
+int launch_f64_to_f16(const double* in, uint16_t* out, int n, hipStream_t s);
 int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidden, __half* x_out,
                    hipStream_t s);
 int launch_q2_gate_up(const __half* x, const uint8_t* pool, size_t expert_stride, int n_slots,
@@ -117,6 +140,6 @@ int launch_slot_step(SlotTable* t, const uint32_t* ids, int k, uint32_t* slot_in
                      hipStream_t s);
 int launch_slot_prefetch(SlotTable* t, const int32_t* preds, int m, int max_fetch,
                          hipStream_t s);
-int launch_stage(const SlotTable* t, const uint8_t* store, size_t store_stride,
+int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t store_stride,
                  uint8_t* pool, size_t pool_stride, size_t bytes, int ctas, hipStream_t s);
 int launch_store_u32(uint32_t* dst, const uint32_t* vals, int n, hipStream_t s);

@@ -260,7 +260,7 @@ int gate_up_t(const __half* x, const uint8_t* pool, size_t stride, const uint32_
               int inter, BlobLayout L, __half* h_out, hipStream_t s) {
     constexpr int rows_per_block = 4 * (32 / GPR) * kGuRowsPerIter;
     dim3 grid((inter + rows_per_block - 1) / rows_per_block, k);
-    hipLaunchKernelGGL((k_q2_gate_up<GPR>), grid, dim3(256), 0, s, x, pool, stride, slots, n_slots, inter, L, h_out);
+    MOE_LAUNCH(TK_GATE_UP, (k_q2_gate_up<GPR>), grid, dim3(256), 0, s, x, pool, stride, slots, n_slots, inter, L, h_out);
     HIP_TRY(hipGetLastError());
     return 0;
 }
@@ -270,7 +270,7 @@ int down_t(const __half* h, const uint8_t* pool, size_t stride, const uint32_t* 
            const __half* scores, int k, int hidden, BlobLayout L, const __half* residual,
            float* y_out, int per_expert, hipStream_t s) {
     dim3 grid((hidden + kDownRows - 1) / kDownRows);
-    hipLaunchKernelGGL((k_q2_down<GPR>), grid, dim3(256), 0, s, h, pool, stride, slots, n_slots, scores, k,
+    MOE_LAUNCH(TK_DOWN, (k_q2_down<GPR>), grid, dim3(256), 0, s, h, pool, stride, slots, n_slots, scores, k,
                        hidden, L, residual, y_out, per_expert);
     HIP_TRY(hipGetLastError());
     return 0;

@@ -12,10 +12,11 @@
 // rounded once, directly, to fp16.  The softmax, renormalisation and RMSNorm run in fp64 and
 // round once to fp16.  Rounded results therefore do not depend on summation order.
 //
-// Launch: one block per 16 weight rows (4 waves x 4 rows).  Every block writes its rounded
-// logits to scratch, then counts itself done on a device-scope counter; the block that
-// arrives last runs the selection (wave 0: softmax/top-k, wave 1: predictor) and re-arms the
-// counter, so no grid-wide wait is ever needed.
+// Launch: one weight row per wave (4 per block), every wave's loads issued before the input
+// vector is ready.  Every block writes its rounded logits to scratch, then counts itself done
+// on a device-scope counter; the block that arrives last runs the selection (wave 0:
+// softmax/top-k with DPP wave maxima, wave 1: predictor) and re-arms the counter, so no
+// grid-wide wait is ever needed.
 #include <hip/hip_fp16.h>
 
 #include "moe_common.h"
@@ -23,8 +24,7 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerWave = 4;
-constexpr int kRowsPerBlock = 4 * kRowsPerWave;
+constexpr int kRowsPerBlock = 4;          // one weight row per wave
 constexpr int kMaxHidden = 4096;
 constexpr int kMaxExperts = 1024;
 
@@ -40,178 +40,42 @@ __device__ __forceinline__ double wave_max_f64(double v) {
     return v;
 }
 
+// Wave-wide max of a uint32 with DPP inside each 16-lane row, then the four row results.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
-    return v;
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+    uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
 }
 
-// One rounding, f64 -> f16 (round to nearest even); never through f32, which would round twice.
-__device__ __forceinline__ uint16_t f16_bits(double v) {
-    return __builtin_bit_cast(uint16_t, (_Float16)v);
+}  // namespace
+
+// f64 -> f16 with a single round-to-nearest-even: truncate to f32, set the sticky bit when
+// inexact (round-to-odd with 24 >= 11 + 2 bits), then let the f32 -> f16 conversion round.
+static __device__ __forceinline__ uint16_t f64_to_f16_bits(double d) {
+    float f = __double2float_rz(d);
+    if ((double)f != d) f = __uint_as_float(__float_as_uint(f) | 1u);
+    return __half_as_ushort(__float2half_rn(f));
 }
+
+namespace {
 
 __device__ __forceinline__ float round_f16(double v) {
-    return (float)(_Float16)v;
+    return __half2float(__ushort_as_half(f64_to_f16_bits(v)));
 }
 
 // Order-preserving map of an fp16 value to uint16 (signed values; -0 folded onto +0).
-__device__ __forceinline__ uint32_t f16_order(float v) {
-    uint16_t b = f16_bits(v == 0.0f ? 0.0 : (double)v);
+__device__ __forceinline__ uint32_t f16_order(uint16_t b) {
+    if (b == 0x8000u) b = 0;
     return (b & 0x8000u) ? (uint32_t)(~b & 0xFFFFu) : (uint32_t)(b | 0x8000u);
 }
 
-__global__ __launch_bounds__(kThreads) void k_router(
-    const float* __restrict__ h_in, const __half* __restrict__ norm_w, float eps,
-    const __half* __restrict__ x_in, __half* __restrict__ x_out,
-    const __half* __restrict__ w, const __half* __restrict__ w_next,
-    int hidden, int n_exp, int k, int m,
-    float* __restrict__ scratch, unsigned* __restrict__ counter,
-    uint32_t* __restrict__ ids_out, __half* __restrict__ scores_out, int32_t* __restrict__ pred_out) {
-    __shared__ float xs[kMaxHidden];
-    __shared__ double red[kThreads / 64];
-    __shared__ int is_last;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-
-    // ---- input vector (exact fp16 values held as float) -------------------------------------
-    if (h_in) {
-        double ss = 0.0;
-        for (int i = tid; i < hidden; i += kThreads) {
-            double v = h_in[i];
-            ss += v * v;
-        }
-        ss = wave_sum_f64(ss);
-        if (lane == 0) red[wv] = ss;
-        __syncthreads();
-        double tot = red[0] + red[1] + red[2] + red[3];
-        double denom = sqrt(tot / hidden + (double)eps);
-        for (int i = tid; i < hidden; i += kThreads) {
-            double v = (double)h_in[i] / denom;
-            if (norm_w) v *= (double)__half2float(norm_w[i]);
-            float r = round_f16(v);
-            xs[i] = r;
-            if (x_out && blockIdx.x == 0) x_out[i] = __ushort_as_half(f16_bits(v));
-        }
-    } else {
-        for (int i = tid; i < hidden; i += kThreads) xs[i] = __half2float(x_in[i]);
-    }
-    __syncthreads();
-
-    // ---- logits: 4 rows per wave, 16 bytes per lane per 512 columns -------------------------
-    const int total_rows = n_exp * (w_next ? 2 : 1);
-    const int row0 = blockIdx.x * kRowsPerBlock + wv * kRowsPerWave;
-#pragma unroll
-    for (int rr = 0; rr < kRowsPerWave; ++rr) {
-        int row = row0 + rr;
-        if (row >= total_rows) break;
-        const __half* wr = (row < n_exp) ? (w + (size_t)row * hidden) : (w_next + (size_t)(row - n_exp) * hidden);
-        double acc = 0.0;
-        for (int c0 = lane * 8; c0 < hidden; c0 += 512) {
-            uint4 q = *reinterpret_cast<const uint4*>(wr + c0);
-            const __half* hv = reinterpret_cast<const __half*>(&q);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc += (double)(__half2float(hv[j]) * xs[c0 + j]);
-        }
-        acc = wave_sum_f64(acc);
-        if (lane == 0) scratch[row] = round_f16(acc);
-    }
-
-    // ---- last block selects -----------------------------------------------------------------
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        unsigned prev = atomicAdd(counter, 1u);
-        is_last = (prev == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    const int per_lane = (n_exp + 63) / 64;
-
-    if (wv == 0) {
-        // softmax over n_exp logits in fp64, gates rounded to fp16
-        double lv[kMaxExperts / 64];
-        double mx = -1e300;
-        for (int i = 0; i < per_lane; ++i) {
-            int e = lane + 64 * i;
-            lv[i] = (e < n_exp) ? (double)__hip_atomic_load(&scratch[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -1e300;
-            mx = fmax(mx, lv[i]);
-        }
-        mx = wave_max_f64(mx);
-        double sum = 0.0;
-        for (int i = 0; i < per_lane; ++i) {
-            int e = lane + 64 * i;
-            lv[i] = (e < n_exp) ? exp(lv[i] - mx) : 0.0;
-            sum += lv[i];
-        }
-        sum = wave_sum_f64(sum);
-        uint32_t key[kMaxExperts / 64];
-        for (int i = 0; i < per_lane; ++i) {
-            int e = lane + 64 * i;
-            // gates are >= 0, so fp16 bit patterns order like the values; id breaks ties upward
-            key[i] = (e < n_exp) ? (((uint32_t)f16_bits(lv[i] / sum) << 16) | (uint32_t)e) : 0u;
-        }
-        uint32_t picked[MOE_MAX_K];
-        for (int r = 0; r < k; ++r) {
-            uint32_t best = 0;
-            for (int i = 0; i < per_lane; ++i) best = max(best, key[i]);
-            best = wave_max_u32(best);
-            for (int i = 0; i < per_lane; ++i)
-                if (key[i] == best) key[i] = 0;
-            picked[r] = best;
-        }
-        if (lane == 0) {
-            // ascending order = reverse of extraction order
-            double gsel[MOE_MAX_K];
-            double s = 0.0;
-            for (int j = 0; j < k; ++j) {
-                uint32_t kk = picked[k - 1 - j];
-                ids_out[j] = kk & 0xFFFFu;
-                gsel[j] = (double)__half2float(__ushort_as_half((uint16_t)(kk >> 16)));
-                s = (double)round_f16(s + gsel[j]);
-            }
-            for (int j = 0; j < k; ++j) scores_out[j] = __ushort_as_half(f16_bits(gsel[j] / s));
-        }
-    } else if (wv == 1 && w_next && m > 0) {
-        uint32_t key[kMaxExperts / 64];
-        for (int i = 0; i < per_lane; ++i) {
-            int e = lane + 64 * i;
-            float v = (e < n_exp) ? __hip_atomic_load(&scratch[n_exp + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
-            key[i] = (e < n_exp) ? ((f16_order(v) << 16) | (uint32_t)e) : 0u;
-        }
-        uint32_t picked[MOE_MAX_PREFETCH];
-        for (int r = 0; r < m; ++r) {
-            uint32_t best = 0;
-            for (int i = 0; i < per_lane; ++i) best = max(best, key[i]);
-            best = wave_max_u32(best);
-            for (int i = 0; i < per_lane; ++i)
-                if (key[i] == best) key[i] = 0;
-            picked[r] = best;
-        }
-        if (lane == 0) {
-            // picked is descending by (value, id); equal values must come out in ascending id
-            int i = 0;
-            while (i < m) {
-                int j = i;
-                while (j + 1 < m && (picked[j + 1] >> 16) == (picked[i] >> 16)) ++j;
-                for (int a = i, b = j; a < b; ++a, --b) {
-                    uint32_t t = picked[a];
-                    picked[a] = picked[b];
-                    picked[b] = t;
-                }
-                i = j + 1;
-            }
-            for (int r = 0; r < m; ++r) pred_out[r] = (int32_t)(picked[r] & 0xFFFFu);
-        }
-    }
-    if (tid == 0) atomicExch(counter, 0u);
-}
-
-// Standalone RMSNorm (one block): x_out = fp16(h / sqrt(mean(h^2) + eps) * w), fp64 math,
-// one rounding; the same arithmetic as the router's prologue.
-__global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ h_in, const __half* __restrict__ norm_w,
-                                                       float eps, int hidden, __half* __restrict__ x_out) {
-    __shared__ double red[kThreads / 64];
+// fp64 RMSNorm of h (fp32 [hidden]) into fp16 bits in LDS; every block computes it.
+__device__ void norm_into_lds(const float* __restrict__ h_in, const __half* __restrict__ norm_w, float eps,
+                              int hidden, uint16_t* xs, __half* x_out, double* red) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     double ss = 0.0;
     for (int i = tid; i < hidden; i += kThreads) {
@@ -221,16 +85,211 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ 
     ss = wave_sum_f64(ss);
     if (lane == 0) red[wv] = ss;
     __syncthreads();
-    double tot = red[0] + red[1] + red[2] + red[3];
-    double denom = sqrt(tot / hidden + (double)eps);
+    const double tot = red[0] + red[1] + red[2] + red[3];
+    const double denom = sqrt(tot / hidden + (double)eps);
     for (int i = tid; i < hidden; i += kThreads) {
         double v = (double)h_in[i] / denom;
         if (norm_w) v *= (double)__half2float(norm_w[i]);
-        x_out[i] = __ushort_as_half(f16_bits(v));
+        uint16_t b = f64_to_f16_bits(v);
+        xs[i] = b;
+        if (x_out) x_out[i] = __ushort_as_half(b);
     }
 }
 
+__global__ __launch_bounds__(kThreads) void k_router(
+    const float* __restrict__ h_in, const __half* __restrict__ norm_w, float eps,
+    const __half* __restrict__ x_in, __half* __restrict__ x_out,
+    const __half* __restrict__ w, const __half* __restrict__ w_next,
+    int hidden, int n_exp, int k, int m,
+    float* __restrict__ scratch, unsigned* __restrict__ counter,
+    uint32_t* __restrict__ ids_out, __half* __restrict__ scores_out, int32_t* __restrict__ pred_out) {
+    __shared__ __align__(16) uint16_t xs[kMaxHidden];
+    __shared__ double red[kThreads / 64];
+    __shared__ int is_last;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int total_rows = n_exp * (w_next ? 2 : 1);
+    const int row = blockIdx.x * kRowsPerBlock + wv;
+    const __half* wr = nullptr;
+    if (row < total_rows) wr = (row < n_exp) ? (w + (size_t)row * hidden) : (w_next + (size_t)(row - n_exp) * hidden);
+
+    // Issue this wave's weight loads before anything waits (hidden <= 4096: 4 x 16 B / lane / 2048).
+    constexpr int kMaxChunks = kMaxHidden / 512;
+    uint4 q[kMaxChunks];
+    const int chunks = hidden / 512;
+    const int tail = hidden % 512;                 // hidden is a multiple of 8
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c)
+        if (wr && c < chunks) q[c] = *reinterpret_cast<const uint4*>(wr + c * 512 + lane * 8);
+    uint4 qt = make_uint4(0, 0, 0, 0);
+    if (wr && tail && lane * 8 < tail) qt = *reinterpret_cast<const uint4*>(wr + chunks * 512 + lane * 8);
+
+    if (h_in) {
+        norm_into_lds(h_in, norm_w, eps, hidden, xs, (x_out && blockIdx.x == 0) ? x_out : nullptr, red);
+    } else {
+        for (int i = tid * 8; i < hidden; i += kThreads * 8)
+            *reinterpret_cast<uint4*>(&xs[i]) = *reinterpret_cast<const uint4*>(x_in + i);
+    }
+    __syncthreads();
+
+    if (wr) {
+        double acc = 0.0;
+#pragma unroll
+        for (int c = 0; c <= kMaxChunks; ++c) {
+            uint4 wq, xq;
+            if (c < kMaxChunks) {
+                if (c >= chunks) continue;
+                wq = q[c];
+                xq = *reinterpret_cast<const uint4*>(&xs[c * 512 + lane * 8]);
+            } else {
+                if (!(tail && lane * 8 < tail)) continue;
+                wq = qt;
+                xq = *reinterpret_cast<const uint4*>(&xs[chunks * 512 + lane * 8]);
+            }
+            const __half* hw = reinterpret_cast<const __half*>(&wq);
+            const __half* hx = reinterpret_cast<const __half*>(&xq);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc += (double)(__half2float(hw[j]) * __half2float(hx[j]));
+        }
+        acc = wave_sum_f64(acc);
+        // publish with an agent-scope atomic store (written through to the device coherence
+        // point), so the only ordering needed before counting in is this wave's store completion
+        if (lane == 0) __hip_atomic_store(&scratch[row], round_f16(acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // ---- the last block to finish selects ---------------------------------------------------
+    // Every logit store of this block has completed (vmcnt(0)) before the block counts itself
+    // done; the last block reads the logits with agent-scope atomic loads.  No L2 write-back
+    // or invalidate is needed for data that only ever moves through agent-scope atomics.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) is_last = (__hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1);
+    __syncthreads();
+    if (!is_last) return;
+
+    __shared__ uint32_t keys[kMaxExperts];
+    __shared__ uint32_t pkeys[kMaxExperts];
+    __shared__ double redm[kThreads / 64], reds[kThreads / 64];
+    const int n_pad = ((n_exp + 63) / 64) * 64;
+    // softmax over the logits in fp64, spread over the whole block
+    constexpr int kPer = kMaxExperts / kThreads;
+    double lv[kPer];
+    double mx = -1e300;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        int e = tid + kThreads * i;
+        lv[i] = (e < n_exp) ? (double)__hip_atomic_load(&scratch[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -1e300;
+        mx = fmax(mx, lv[i]);
+        if (w_next && m > 0 && e < n_pad) {
+            float v = (e < n_exp) ? __hip_atomic_load(&scratch[n_exp + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+            pkeys[e] = (e < n_exp) ? ((f16_order(__half_as_ushort(__float2half_rn(v))) << 16) | (uint32_t)e) : 0u;
+        }
+    }
+    mx = wave_max_f64(mx);
+    if (lane == 0) redm[wv] = mx;
+    __syncthreads();
+    mx = fmax(fmax(redm[0], redm[1]), fmax(redm[2], redm[3]));
+    double sum = 0.0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        int e = tid + kThreads * i;
+        lv[i] = (e < n_exp) ? exp(lv[i] - mx) : 0.0;
+        sum += lv[i];
+    }
+    sum = wave_sum_f64(sum);
+    if (lane == 0) reds[wv] = sum;
+    __syncthreads();
+    sum = (reds[0] + reds[1]) + (reds[2] + reds[3]);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        int e = tid + kThreads * i;
+        // gates are >= 0, so fp16 bit patterns order like the values; id breaks ties upward
+        if (e < n_pad) keys[e] = (e < n_exp) ? (((uint32_t)f64_to_f16_bits(lv[i] / sum) << 16) | (uint32_t)e) : 0u;
+    }
+    __syncthreads();
+    const int per_lane = n_pad / 64;
+
+    if (wv == 0) {
+        uint32_t key[kMaxExperts / 64];
+#pragma unroll
+        for (int i = 0; i < kMaxExperts / 64; ++i) key[i] = (i < per_lane) ? keys[lane + 64 * i] : 0u;
+        uint32_t mine = 0;                        // lane j keeps the j-th largest key
+        for (int r = 0; r < k; ++r) {
+            uint32_t best = 0;
+#pragma unroll
+            for (int i = 0; i < kMaxExperts / 64; ++i) best = max(best, key[i]);
+            best = wave_max_u32(best);
+#pragma unroll
+            for (int i = 0; i < kMaxExperts / 64; ++i)
+                if (key[i] == best) key[i] = 0;
+            if (lane == r) mine = best;
+        }
+        // output position of the r-th largest is k-1-r (ascending gate order)
+        const int pos = k - 1 - lane;
+        const float g = __half2float(__ushort_as_half((uint16_t)(mine >> 16)));
+        // left-to-right sum over ascending order, each partial rounded to fp16; the gates are
+        // fp16 values in ascending order, so every partial sum is exact in fp32 before rounding
+        float s = 0.0f;
+        for (int j = 0; j < k; ++j) {
+            float gj = __shfl(g, k - 1 - j, 64);
+            s = __half2float(__float2half_rn(s + gj));
+        }
+        if (lane < k) {
+            ids_out[pos] = mine & 0xFFFFu;
+            scores_out[pos] = __float2half_rn(g / s);   // correctly rounded f32 division, then f16
+        }
+    } else if (wv == 1 && w_next && m > 0) {
+        uint32_t key[kMaxExperts / 64];
+#pragma unroll
+        for (int i = 0; i < kMaxExperts / 64; ++i) key[i] = (i < per_lane) ? pkeys[lane + 64 * i] : 0u;
+        uint32_t mine = 0;
+        for (int r = 0; r < m; ++r) {
+            uint32_t best = 0;
+#pragma unroll
+            for (int i = 0; i < kMaxExperts / 64; ++i) best = max(best, key[i]);
+            best = wave_max_u32(best);
+#pragma unroll
+            for (int i = 0; i < kMaxExperts / 64; ++i)
+                if (key[i] == best) key[i] = 0;
+            if (lane == r) mine = best;
+        }
+        // lanes 0..m-1 hold descending (value, id); equal values must come out in ascending id:
+        // within a run of equal values, lane r takes the id of its mirror position in the run
+        const uint32_t val = mine >> 16;
+        int first = lane, last = lane;
+        for (int q2 = 0; q2 < m; ++q2) {
+            uint32_t vq = (uint32_t)__shfl((int)val, q2, 64);
+            if (vq == val && q2 < first) first = q2;
+            if (vq == val && q2 > last) last = q2;
+        }
+        const int src = first + last - lane;
+        const int id = __shfl((int)(mine & 0xFFFFu), src, 64);
+        if (lane < m) pred_out[lane] = id;
+    }
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Standalone RMSNorm (one block): x_out = fp16(h / sqrt(mean(h^2) + eps) * w), fp64 math,
+// one rounding; the same arithmetic as the router's prologue.
+__global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ h_in, const __half* __restrict__ norm_w,
+                                                       float eps, int hidden, __half* __restrict__ x_out) {
+    __shared__ __align__(16) uint16_t xs[kMaxHidden];
+    __shared__ double red[kThreads / 64];
+    norm_into_lds(h_in, norm_w, eps, hidden, xs, x_out, red);
+}
+
+__global__ void k_f64_to_f16(const double* __restrict__ in, uint16_t* __restrict__ out, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = f64_to_f16_bits(in[i]);
+}
+
 }  // namespace
+
+int launch_f64_to_f16(const double* in, uint16_t* out, int n, hipStream_t s) {
+    if (n <= 0 || !in || !out) { moe_set_error("f64_to_f16: bad arguments"); return -1; }
+    hipLaunchKernelGGL(k_f64_to_f16, dim3((n + 255) / 256), dim3(256), 0, s, in, out, n);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
 
 int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidden, __half* x_out, hipStream_t s) {
     if (!h_in || !x_out || hidden <= 0) { moe_set_error("rmsnorm: bad arguments"); return -1; }
@@ -260,8 +319,8 @@ int launch_router(const float* h_in, const __half* norm_w, float eps, const __ha
         return -1;
     }
     int rows = n_exp * (w_next ? 2 : 1);
-    int grid = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    hipLaunchKernelGGL(k_router, dim3(grid), dim3(kThreads), 0, s, h_in, norm_w, eps, x_in, x_out,
+    int grid = (rows + kRowsPerBlock - 1) / kRowsPerBlock;      // one row per wave
+    MOE_LAUNCH(TK_ROUTER, k_router, dim3(grid), dim3(kThreads), 0, s, h_in, norm_w, eps, x_in, x_out,
                        w, w_next, hidden, n_exp, k, w_next ? m : 0, scratch, counter, ids_out,
                        scores_out, pred_out);
     HIP_TRY(hipGetLastError());

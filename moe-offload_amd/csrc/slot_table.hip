@@ -310,12 +310,12 @@ __global__ __launch_bounds__(64) void k_slot_prefetch(SlotTable* __restrict__ t,
     __syncthreads();
     store_table(t, L, lane);
     if (lane < np) {
-        t->copy_eid[lane] = L.list_e[lane];
-        t->copy_slot[lane] = L.list_s[lane];
+        t->pf_copy_eid[lane] = L.list_e[lane];
+        t->pf_copy_slot[lane] = L.list_s[lane];
     }
     if (lane == 0) {
         t->snap_valid = 1;
-        t->n_copy = np;
+        t->pf_n_copy = np;
         t->clock = clock;
         t->n_free = n_free;
         t->status = 0;
@@ -324,35 +324,35 @@ __global__ __launch_bounds__(64) void k_slot_prefetch(SlotTable* __restrict__ t,
     }
 }
 
-// Copy the blobs listed in the table's copy list: store[eid] -> pool[slot].  16-byte units,
-// four in flight per thread; the store is pinned host memory read over PCIe.
-__global__ __launch_bounds__(256) void k_stage(const SlotTable* __restrict__ t, const uint8_t* __restrict__ store,
-                                               size_t store_stride, uint8_t* __restrict__ pool,
-                                               size_t pool_stride, size_t bytes) {
-    const int n = min(t->n_copy, MOE_MAX_PREFETCH);
-    if (n <= 0) return;
-    const size_t units = bytes / 16;
-    const size_t total = units * (size_t)n;
-    const size_t step = (size_t)gridDim.x * blockDim.x;
-    size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (; u < total; u += 4 * step) {
-        uint4 v[4];
-        size_t idx[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            idx[i] = u + (size_t)i * step;
-            if (idx[i] < total) {
-                size_t c = idx[i] / units, off = (idx[i] % units) * 16;
-                v[i] = *reinterpret_cast<const uint4*>(store + (size_t)t->copy_eid[c] * store_stride + off);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (idx[i] < total) {
-                size_t c = idx[i] / units, off = (idx[i] % units) * 16;
-                *reinterpret_cast<uint4*>(pool + (size_t)t->copy_slot[c] * pool_stride + off) = v[i];
-            }
-        }
+// Copy the blobs listed in the table's copy list: store[eid] -> pool[slot].  blockIdx.y picks
+// the copy, blockIdx.x strides over its 16-byte units, four in flight per thread; the store is
+// pinned host memory read over PCIe (a kernel copy sustains the link rate with blob-sized
+// pieces, where one DMA request per blob does not).
+__global__ __launch_bounds__(256) void k_stage(const SlotTable* __restrict__ t, int list,
+                                               const uint8_t* __restrict__ store, size_t store_stride,
+                                               uint8_t* __restrict__ pool, size_t pool_stride, size_t bytes) {
+    const int c = blockIdx.y;
+    const int n = list ? t->pf_n_copy : t->n_copy;
+    if (c >= min(n, MOE_MAX_PREFETCH)) return;
+    const int eid = list ? t->pf_copy_eid[c] : t->copy_eid[c];
+    const int slot = list ? t->pf_copy_slot[c] : t->copy_slot[c];
+    if (eid < 0 || eid >= MOE_NUM_EXPERTS || slot < 0 || slot >= t->capacity) return;
+    const uint4* src = reinterpret_cast<const uint4*>(store + (size_t)eid * store_stride);
+    uint4* dst = reinterpret_cast<uint4*>(pool + (size_t)slot * pool_stride);
+    const unsigned units = (unsigned)(bytes / 16);
+    const unsigned step = gridDim.x * blockDim.x;
+    // Four independent 16-byte loads in flight per thread, held in named registers (an array
+    // here gets moved to LDS by the compiler, which serialises the loads behind LDS writes).
+    for (unsigned u = blockIdx.x * blockDim.x + threadIdx.x; u < units; u += 4 * step) {
+        const bool m1 = u + step < units, m2 = u + 2 * step < units, m3 = u + 3 * step < units;
+        uint4 a = src[u], b = {}, c = {}, d = {};
+        if (m1) b = src[u + step];
+        if (m2) c = src[u + 2 * step];
+        if (m3) d = src[u + 3 * step];
+        dst[u] = a;
+        if (m1) dst[u + step] = b;
+        if (m2) dst[u + 2 * step] = c;
+        if (m3) dst[u + 3 * step] = d;
     }
 }
 
@@ -367,27 +367,32 @@ __global__ void k_store_u32(uint32_t* dst, U32x16 vals, int n) {
 
 int launch_slot_step(SlotTable* t, const uint32_t* ids, int k, uint32_t* slot_inds, hipStream_t s) {
     if (k <= 0 || k > MOE_MAX_K) { moe_set_error("slot_step: k=%d out of range", k); return -1; }
-    hipLaunchKernelGGL(k_slot_step, dim3(1), dim3(64), 0, s, t, ids, k, slot_inds);
+    MOE_LAUNCH(TK_SLOT, k_slot_step, dim3(1), dim3(64), 0, s, t, ids, k, slot_inds);
     HIP_TRY(hipGetLastError());
     return 0;
 }
 
 int launch_slot_prefetch(SlotTable* t, const int32_t* preds, int m, int max_fetch, hipStream_t s) {
     if (m < 0 || m > MOE_MAX_PREFETCH) { moe_set_error("slot_prefetch: m=%d out of range", m); return -1; }
-    hipLaunchKernelGGL(k_slot_prefetch, dim3(1), dim3(64), 0, s, t, preds, m, max_fetch);
+    MOE_LAUNCH(TK_SLOT, k_slot_prefetch, dim3(1), dim3(64), 0, s, t, preds, m, max_fetch);
     HIP_TRY(hipGetLastError());
     return 0;
 }
 
-int launch_stage(const SlotTable* t, const uint8_t* store, size_t store_stride, uint8_t* pool,
+int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t store_stride, uint8_t* pool,
                  size_t pool_stride, size_t bytes, int ctas, hipStream_t s) {
     if (bytes % 16 || store_stride % 16 || pool_stride % 16 || bytes > pool_stride || bytes > store_stride) {
         moe_set_error("stage: bytes=%zu strides=%zu/%zu must be multiples of 16 with bytes <= stride",
                       bytes, store_stride, pool_stride);
         return -1;
     }
-    if (ctas <= 0) ctas = 1024;
-    hipLaunchKernelGGL(k_stage, dim3(ctas), dim3(256), 0, s, t, store, store_stride, pool, pool_stride, bytes);
+    if (bytes / 16 > 0xFFFFFFFFull) { moe_set_error("stage: blob of %zu bytes too large", bytes); return -1; }
+    // ctas = blocks per copy; the grid covers the largest possible copy list, empty rows exit.
+    // 2 blocks x 256 threads x 4 x 16 B in flight per copy already saturate PCIe; more only
+    // crowds other kernels' memory requests.
+    if (ctas <= 0) ctas = 2;
+    MOE_LAUNCH(TK_STAGE, k_stage, dim3(ctas, MOE_MAX_PREFETCH), dim3(256), 0, s, t, list, store, store_stride,
+               pool, pool_stride, bytes);
     HIP_TRY(hipGetLastError());
     return 0;
 }

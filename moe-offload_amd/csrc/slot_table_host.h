@@ -45,6 +45,7 @@ static inline void reset_cache(SlotTable* t) {
     t->clock = 0;
     t->snap_valid = 0;
     t->n_copy = 0;
+    t->pf_n_copy = 0;
 }
 
 static inline void reset_stats(SlotTable* t) { memset(t->stats, 0, sizeof(t->stats)); }
@@ -153,7 +154,7 @@ static inline int prefetch(SlotTable* t, const int32_t* preds, int n, int max_fe
     for (int e = 0; e < MOE_NUM_EXPERTS; ++e)
         if (t->slot_of[e] >= 0) bm_put(t->snap_resident, e);
     t->snap_valid = 1;
-    t->n_copy = 0;
+    t->pf_n_copy = 0;
     int cap = (max_fetch > 0 && max_fetch < 32) ? max_fetch : 32;
     uint64_t protect[8] = {0};
     int32_t pick[MOE_MAX_PREFETCH];
@@ -172,12 +173,12 @@ static inline int prefetch(SlotTable* t, const int32_t* preds, int n, int max_fe
         int e = pick[np - 1 - i];
         int s = take_slot(t, protect);
         bind(t, e, s);
-        t->copy_eid[i] = e;
-        t->copy_slot[i] = s;
+        t->pf_copy_eid[i] = e;
+        t->pf_copy_slot[i] = s;
     }
-    t->n_copy = np;
+    t->pf_n_copy = np;
     t->stats[ST_PREF_BYTES] += (uint64_t)np * t->expert_bytes;
-    count_runs(t, t->copy_eid, np);
+    count_runs(t, t->pf_copy_eid, np);
     return np;
 }
 

@@ -45,6 +45,7 @@ SIGNATURES: dict[str, tuple] = {
                             _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "moe_router_workspace_bytes": (_c_u64, [_c_int]),
     "moe_rmsnorm": (_c_int, [_c_vp, _c_vp, _c_f, _c_int, _c_vp, _c_vp]),
+    "moe_f64_to_f16": (_c_int, [_c_vp, _c_vp, _c_int, _c_vp]),
     "moe_q2_expert_bytes": (_c_u64, [_c_int, _c_int, _c_int]),
     "moe_q2_gate_up": (_c_int, [_c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp,
                                 _c_vp]),
@@ -64,9 +65,12 @@ SIGNATURES: dict[str, tuple] = {
     "c_layer_set_device_mode": (_c_int, [_c_int, _c_int]),
     "c_layer_step_decode_dev": (_c_int, [_c_int, _c_vp, _c_int, _c_int, _c_vp]),
     "c_layer_start_prefetch_dev": (_c_int, [_c_int, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
+    "c_layer_stage_dev": (_c_int, [_c_int, _c_int, _c_int, _c_vp]),
     "c_layer_device_table": (_c_u64, [_c_int]),
     "c_layer_table_status": (_c_int, [_c_int]),
     "c_sync_copies": (_c_int, []),
+    "c_timing_begin": (_c_int, [_c_int]),
+    "c_timing_end": (_c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
     "c_abi_version": (_c_int, []),
 }
 

@@ -50,7 +50,8 @@ class StackConfig:
     eps: float = 1e-6
     seed: int = 0
     layer_base: int = 0          # first C-ABI layer index used (tables are global to the library)
-    stage_ctas: int = 0          # staging kernel grid (0 = library default)
+    stage_ctas: int = 2          # staging blocks per copied expert (enough to fill PCIe; more
+                                 # only floods the L2 miss queues with slow host reads)
     resident: bool = False       # every layer's experts in HBM (no slot tables, no staging)
 
 
@@ -135,7 +136,8 @@ class DecodeStack:
         self.side = torch.cuda.Stream(device=dev)
         self.ev_pred = [torch.cuda.Event() for _ in range(c.n_layers)]
         self.ev_pref = [torch.cuda.Event() for _ in range(c.n_layers)]
-        self.timing = None           # optional list of (layer, kind, start_event, end_event)
+        self.ev_copy = [torch.cuda.Event() for _ in range(c.n_layers)]
+        self.ev_demand = [torch.cuda.Event() for _ in range(c.n_layers)]
         self.graph = None
 
     # C-ABI layer index of stack layer l
@@ -180,42 +182,34 @@ class DecodeStack:
         c = self.cfg
         stream = torch.cuda.current_stream().cuda_stream
         L = self.L
-        if l == 0 or c.resident:
-            pool = (self.full_pools[l] if c.resident else self.pool0).data_ptr()
-            stride, n_slots, slots = self.blob_bytes, c.n_exp, self.ids[l].data_ptr()
-        else:
-            pool, stride, n_slots = self.pools[l].data_ptr(), self.blob_bytes, self.capacities[l]
-            slots = self.slot_inds[l].data_ptr()
-        if self.timing is None:
-            if l == 0 or self.mode == "device" or c.resident:
-                # device-driven layers are ordered by the stream alone (no copy/read events)
-                rc = L.moe_q2_switch_glu(self.xs[l].data_ptr(), pool, stride, n_slots, slots, self.scores[l].data_ptr(),
-                                         c.top_k, c.hidden, c.inter, c.group, self.xs[l].data_ptr(),
-                                         self.h_ws.data_ptr(), self.hs[l].data_ptr(), 0, stream)
+        if l == 0 or self.mode == "device" or c.resident:
+            # device-driven layers are ordered by the stream alone (no copy/read events)
+            if l == 0 or c.resident:
+                pool = (self.full_pools[l] if c.resident else self.pool0).data_ptr()
+                n_slots, slots = c.n_exp, self.ids[l].data_ptr()
             else:
-                rc = L.c_layer_switch_glu(self.cidx(l), self.xs[l].data_ptr(), self.scores[l].data_ptr(),
-                                          self.xs[l].data_ptr(), self.h_ws.data_ptr(), self.hs[l].data_ptr(), 0,
-                                          c.top_k, stream)
-            _lib.check(rc, "switch_glu")
-            return
-        # instrumented: gate/up and down launched separately between HIP events on this stream
-        if l > 0 and self.mode == "host" and not c.resident:
-            L.c_layer_wait_prefetch(self.cidx(l))
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        ev[0].record()
-        _lib.check(L.moe_q2_gate_up(self.xs[l].data_ptr(), pool, stride, n_slots, slots, c.top_k, c.hidden, c.inter,
-                                    c.group, self.h_ws.data_ptr(), stream), "gate_up")
-        ev[1].record()
-        _lib.check(L.moe_q2_down(self.h_ws.data_ptr(), pool, stride, n_slots, slots, self.scores[l].data_ptr(),
-                                 c.top_k, c.hidden, c.inter, c.group, self.xs[l].data_ptr(), self.hs[l].data_ptr(),
-                                 0, stream), "down")
-        ev[2].record()
-        if l > 0 and self.mode == "host" and not c.resident:
-            _lib.check(L.c_layer_mark_read(self.cidx(l), stream), "mark_read")
-        self.timing.append((l, ev[0], ev[1], ev[2]))
+                pool, n_slots, slots = self.pools[l].data_ptr(), self.capacities[l], self.slot_inds[l].data_ptr()
+            rc = L.moe_q2_switch_glu(self.xs[l].data_ptr(), pool, self.blob_bytes, n_slots, slots,
+                                     self.scores[l].data_ptr(), c.top_k, c.hidden, c.inter, c.group,
+                                     self.xs[l].data_ptr(), self.h_ws.data_ptr(), self.hs[l].data_ptr(), 0, stream)
+        else:
+            rc = L.c_layer_switch_glu(self.cidx(l), self.xs[l].data_ptr(), self.scores[l].data_ptr(),
+                                      self.xs[l].data_ptr(), self.h_ws.data_ptr(), self.hs[l].data_ptr(), 0,
+                                      c.top_k, stream)
+        _lib.check(rc, "switch_glu")
 
     def decode_token_device(self):
-        """Device-driven token: no host synchronisation; reads xs[0], writes xs[n_layers]."""
+        """Device-driven token: no host synchronisation; reads xs[0], writes xs[n_layers].
+
+        Main stream, layer l: router(l) -> [join prefetch table(l)] -> slot step(l) ->
+        [join prefetch copies(l)] -> demand copies(l) -> gate/up -> down.
+        Side stream: prefetch table(l+1) as soon as router(l) has produced the prediction;
+        prefetch copies(l+1) once the demand copies of layer l are queued ahead of them.
+
+        The PCIe link is the bottleneck of this workload, so the order is chosen to keep it
+        busy: demand copies first (they gate this layer's GEMV), prefetch copies next, running
+        under this layer's GEMV and the next layer's router and step.  The demand copies of a
+        layer wait for its prefetch copies because both may target the same slot."""
         c = self.cfg
         main = torch.cuda.current_stream()
         for l in range(c.n_layers):
@@ -223,19 +217,29 @@ class DecodeStack:
                 self._router(l)
                 self._glu(l)
                 continue
-            if l >= 1 and c.prefetch:
-                main.wait_event(self.ev_pref[l])           # prefetch(l) landed (table + slots)
             self._router(l)
             if l >= 1:
-                _lib.check(self.L.c_layer_step_decode_dev(self.cidx(l), self.ids[l].data_ptr(), c.top_k,
-                                                          c.stage_ctas, main.cuda_stream), "step_dev")
+                if c.prefetch:
+                    main.wait_event(self.ev_pref[l])       # table of prefetch(l) updated
+                _lib.check(self.L.c_layer_step_decode_dev(self.cidx(l), self.ids[l].data_ptr(), c.top_k, -1,
+                                                          main.cuda_stream), "step_dev")
             if c.prefetch and l + 1 < c.n_layers:
                 self.ev_pred[l].record(main)
                 self.side.wait_event(self.ev_pred[l])
                 _lib.check(self.L.c_layer_start_prefetch_dev(self.cidx(l + 1), self.pred[l].data_ptr(), c.top_m,
-                                                             c.prefetch_cap, c.stage_ctas, self.side.cuda_stream),
+                                                             c.prefetch_cap, -1, self.side.cuda_stream),
                            "prefetch_dev")
                 self.ev_pref[l + 1].record(self.side)
+            if l >= 1:
+                if c.prefetch:
+                    main.wait_event(self.ev_copy[l])       # prefetch copies(l) landed
+                _lib.check(self.L.c_layer_stage_dev(self.cidx(l), 0, c.stage_ctas, main.cuda_stream), "stage_demand")
+            if c.prefetch and l + 1 < c.n_layers:
+                self.ev_demand[l].record(main)
+                self.side.wait_event(self.ev_demand[l])
+                _lib.check(self.L.c_layer_stage_dev(self.cidx(l + 1), 1, c.stage_ctas, self.side.cuda_stream),
+                           "stage_prefetch")
+                self.ev_copy[l + 1].record(self.side)
             self._glu(l)
         _lib.check(self.L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
                                       c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), main.cuda_stream), "rmsnorm")

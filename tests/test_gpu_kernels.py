@@ -139,3 +139,26 @@ def test_switch_glu_golden_fixture_shapes(dev, golden_moe):
                                   scores=torch.from_numpy(S[t]).to(dev)).cpu().numpy()
             full = bf(f"moe.y_{suffix}").reshape(-1, 256)[t]
             assert np.abs(y - Y[t]).max() <= 0.02 * np.abs(full).max() + 1e-4
+
+
+def test_f64_to_f16_single_rounding(dev):
+    """The kernels' f64 -> f16 rounding equals numpy's (one round-to-nearest-even) on exact
+    ties, values one f64 ulp either side of ties, subnormals, the overflow edge and random
+    values."""
+    from moe_offload import _lib
+    rng = np.random.default_rng(3)
+    h = rng.integers(0, 0x7C00, size=20000).astype(np.uint16).view(np.float16).astype(np.float64)
+    nxt = np.nextafter(h.astype(np.float16), np.float16(np.inf)).astype(np.float64)
+    mid = (h + nxt) / 2
+    vals = np.concatenate([h, mid, np.nextafter(mid, np.inf), np.nextafter(mid, -np.inf),
+                           rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 5, 20000),
+                           [65504.0, 65519.99, 65520.0, 2.0 ** -25, 2.0 ** -24 * 1.5, 0.0, -0.0, 1e-300]])
+    vals = np.concatenate([vals, -vals])
+    src = torch.from_numpy(vals).to(dev)
+    out = torch.empty(vals.size, dtype=torch.int16, device=dev)
+    assert _lib.lib().moe_f64_to_f16(src.data_ptr(), out.data_ptr(), vals.size,
+                                     torch.cuda.current_stream().cuda_stream) == 0
+    got = out.cpu().numpy().view(np.uint16)
+    want = vals.astype(np.float16).view(np.uint16)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(vals[i], hex(got[i]), hex(want[i])) for i in bad[:5]]
