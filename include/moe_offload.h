@@ -115,6 +115,34 @@ int moe_q2_switch_glu(const void* x, const void* pool, uint64_t stride, int n_sl
                       int group, const void* residual, void* h_ws, float* y_out, int per_expert,
                       void* stream);
 
+/* Prefill grouped GEMM (loader.py:566-699 sorted gather_qmm via prefill_qproj.py:18-40;
+ * cpp/src/layers.cpp:364-600).  The n_rows (token, k) rows are sorted by expert; segment u
+ * covers sorted rows [seg_start[u], seg_start[u+1]) and uses pool blob seg_slot[u] (seg_slot
+ * null: blob u, the reference's chunk-local slot = rank in chunk).  All index arrays are
+ * device memory.  gate_up: h_out[r][inter] fp16 = silu(G x_{row_token[r]}) * (U x_{row_token[r]});
+ * down: y_out[row_out[r]][hidden] fp16 = D h[r] (row_out null: row r).  A row whose token is
+ * out of range computes from zeros; rows whose output row or slot is out of range are not
+ * written.  Requires hidden, inter multiples of 64 and
+ * <= 2560, group 64.  MFMA (v_mfma_f32_16x16x32_f16), fp32 accumulation. */
+int moe_q2_grouped_gate_up(const void* x, int n_tokens, const int32_t* row_token, int n_rows,
+                           const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
+                           const void* pool, uint64_t stride, int n_slots, int hidden, int inter,
+                           int group, void* h_out, void* stream);
+int moe_q2_grouped_down(const void* h, int n_rows, const int32_t* row_out, int n_out_rows,
+                        const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
+                        const void* pool, uint64_t stride, int n_slots, int hidden, int inter,
+                        int group, void* y_out, void* stream);
+/* Both of the above (h_ws: n_rows*inter fp16 workspace). */
+int moe_q2_grouped_switch_glu(const void* x, int n_tokens, const int32_t* row_token,
+                              const int32_t* row_out, int n_rows, int n_out_rows,
+                              const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
+                              const void* pool, uint64_t stride, int n_slots, int hidden,
+                              int inter, int group, void* h_ws, void* y_out, void* stream);
+/* Score-weighted sum of per-(token, k) rows (loader.py:964-965): out fp32 [n_tokens][hidden] =
+ * residual + sum_j scores[t][j] * y[t*k + j] (fp16 y, scores, residual; residual may be null). */
+int moe_pair_combine(const void* y, const void* scores, const void* residual, int n_tokens, int k,
+                     int hidden, float* out, void* stream);
+
 /* ---- Part 3: no counterpart in the reference ----------------------------------------------- */
 
 /* Last recorded failure ("" if none) / clear it. */
@@ -130,6 +158,13 @@ int c_layer_set_format(int layer_idx, int hidden, int inter, int group);
 /* SwitchGLU over the layer's pool with its current slot ids; orders after pending copies. */
 int c_layer_switch_glu(int layer_idx, const void* x, const void* scores, const void* residual,
                        void* h_ws, float* y_out, int per_expert, int k, void* stream);
+/* Prefill grouped SwitchGLU over the layer's pool, segment u reading slot u (the chunk-local
+ * slot of loader.py:653-664); orders after pending copies and records the read so the next
+ * chunk's copies (c_layer_load_sync) wait for it.  Arguments as moe_q2_grouped_switch_glu. */
+int c_layer_grouped_switch_glu(int layer_idx, const void* x, int n_tokens, const int32_t* row_token,
+                               const int32_t* row_out, int n_rows, int n_out_rows,
+                               const int32_t* seg_start, int n_seg, void* h_ws, void* y_out,
+                               void* stream);
 /* Record that work queued on `stream` so far reads the layer's pool (copies into it wait). */
 int c_layer_mark_read(int layer_idx, void* stream);
 /* Move a layer's slot table to device memory (on != 0) or back.  Device-driven layers take
@@ -154,7 +189,9 @@ int c_layer_table_status(int layer_idx);
 int c_sync_copies(void);
 /* Per-kernel timing: launches between begin and end are dispatched with start/stop events
  * stamped at the kernel's own begin/end; end() sums durations per kind (0 router, 1 gate/up,
- * 2 down, 3 staging, 4 slot table) into out_ms[5] and counts into out_n[5]. */
+ * 2 down, 3 staging, 4 slot table, 5 grouped gate/up, 6 grouped down, 7 pair combine) into
+ * out_ms[MOE_TIMING_KINDS] and counts into out_n[MOE_TIMING_KINDS]. */
+#define MOE_TIMING_KINDS 8
 int c_timing_begin(int capacity);
 int c_timing_end(double* out_ms, int* out_n);
 int c_abi_version(void);

@@ -30,6 +30,7 @@
 #include <vector>
 
 #include "moe_common.h"
+#include "moe_offload.h"
 #include "slot_table_host.h"
 
 namespace {
@@ -616,6 +617,67 @@ int c_layer_switch_glu(int layer, const void* x, const void* scores, const void*
     return 0;
 }
 
+int moe_q2_grouped_gate_up(const void* x, int n_tokens, const int32_t* row_token, int n_rows, const int32_t* seg_start,
+                           const int32_t* seg_slot, int n_seg, const void* pool, uint64_t stride, int n_slots,
+                           int hidden, int inter, int group, void* h_out, void* stream) {
+    return launch_q2_grouped_gate_up((const __half*)x, n_tokens, row_token, n_rows, seg_start, seg_slot, n_seg,
+                                     (const uint8_t*)pool, stride, n_slots, hidden, inter, group, (__half*)h_out,
+                                     (hipStream_t)stream);
+}
+
+int moe_q2_grouped_down(const void* h, int n_rows, const int32_t* row_out, int n_out_rows, const int32_t* seg_start,
+                        const int32_t* seg_slot, int n_seg, const void* pool, uint64_t stride, int n_slots, int hidden,
+                        int inter, int group, void* y_out, void* stream) {
+    return launch_q2_grouped_down((const __half*)h, n_rows, row_out, n_out_rows, seg_start, seg_slot, n_seg,
+                                  (const uint8_t*)pool, stride, n_slots, hidden, inter, group, (__half*)y_out,
+                                  (hipStream_t)stream);
+}
+
+int moe_q2_grouped_switch_glu(const void* x, int n_tokens, const int32_t* row_token, const int32_t* row_out, int n_rows,
+                              int n_out_rows, const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
+                              const void* pool, uint64_t stride, int n_slots, int hidden, int inter, int group,
+                              void* h_ws, void* y_out, void* stream) {
+    if (moe_q2_grouped_gate_up(x, n_tokens, row_token, n_rows, seg_start, seg_slot, n_seg, pool, stride, n_slots, hidden,
+                               inter, group, h_ws, stream))
+        return -1;
+    return moe_q2_grouped_down(h_ws, n_rows, row_out, n_out_rows, seg_start, seg_slot, n_seg, pool, stride, n_slots,
+                               hidden, inter, group, y_out, stream);
+}
+
+int moe_pair_combine(const void* y, const void* scores, const void* residual, int n_tokens, int k, int hidden,
+                     float* out, void* stream) {
+    return launch_pair_combine((const __half*)y, (const __half*)scores, (const __half*)residual, n_tokens, k, hidden, out,
+                               (hipStream_t)stream);
+}
+
+// Grouped SwitchGLU over the layer's slot pool, segment u reading slot u (the chunk-local slot =
+// rank of the expert in the chunk).  Orders `stream` after the layer's pending copies and records
+// the read, so copies queued for the next chunk wait for it.
+int c_layer_grouped_switch_glu(int layer, const void* x, int n_tokens, const int32_t* row_token,
+                               const int32_t* row_out, int n_rows, int n_out_rows, const int32_t* seg_start,
+                               int n_seg, void* h_ws, void* y_out, void* stream) {
+    if (!valid_layer(layer) || !g_layers[layer].init || !g_layers[layer].hidden) {
+        moe_set_error("layer_grouped_switch_glu: layer %d has no Q2 format (c_layer_set_format)", layer);
+        return -1;
+    }
+    LayerState& L = g_layers[layer];
+    if (!L.dst[0]) { moe_set_error("layer_grouped_switch_glu: layer %d has no pool", layer); return -1; }
+    if (n_seg > L.capacity) {
+        moe_set_error("layer_grouped_switch_glu: %d segments > capacity %d", n_seg, L.capacity);
+        return -1;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    if (wait_copies_gpu(L, s)) return -1;
+    if (ensure_events(L)) return -1;
+    if (moe_q2_grouped_switch_glu(x, n_tokens, row_token, row_out, n_rows, n_out_rows, seg_start, nullptr, n_seg,
+                                  (const void*)L.dst[0], L.row_bytes[0], L.capacity, L.hidden, L.inter, L.group, h_ws,
+                                  y_out, stream))
+        return -1;
+    HIP_TRY(hipEventRecord(L.read_done, s));
+    L.read_recorded = true;
+    return 0;
+}
+
 // Record that work queued so far on `stream` reads the layer's pool (later copies wait for it).
 int c_layer_mark_read(int layer, void* stream) {
     if (!valid_layer(layer) || !g_layers[layer].init) { moe_set_error("mark_read: bad layer %d", layer); return -1; }
@@ -649,7 +711,8 @@ int c_timing_begin(int capacity) {
 }
 
 // Stop timing; blocks until the timed kernels finished.  out_ms[kind] = summed kernel
-// durations (ms), out_n[kind] = launches (kinds: router, gate_up, down, stage, slot table).
+// durations (ms), out_n[kind] = launches, for the MOE_TIMING_KINDS kinds.
+static_assert(TK_KINDS == MOE_TIMING_KINDS, "kernel kinds out of step with the header");
 int c_timing_end(double* out_ms, int* out_n) {
     g_kt_on = false;
     for (int i = 0; i < TK_KINDS; ++i) { out_ms[i] = 0.0; out_n[i] = 0; }

@@ -107,7 +107,7 @@ void moe_set_error(const char* fmt, ...);
 // Optional per-launch kernel timing: when enabled, launchers dispatch through
 // hipExtLaunchKernelGGL with a start/stop event pair, which the runtime stamps at the kernel's
 // own begin/end; kinds index the accumulated totals.
-enum { TK_ROUTER = 0, TK_GATE_UP, TK_DOWN, TK_STAGE, TK_SLOT, TK_KINDS };
+enum { TK_ROUTER = 0, TK_GATE_UP, TK_DOWN, TK_STAGE, TK_SLOT, TK_PF_GATE_UP, TK_PF_DOWN, TK_COMBINE, TK_KINDS };
 bool kt_enabled();
 void kt_events(int kind, hipEvent_t* start, hipEvent_t* stop);   // both null when disabled / full
 
@@ -143,3 +143,13 @@ int launch_slot_prefetch(SlotTable* t, const int32_t* preds, int m, int max_fetc
 int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t store_stride,
                  uint8_t* pool, size_t pool_stride, size_t bytes, int ctas, hipStream_t s);
 int launch_store_u32(uint32_t* dst, const uint32_t* vals, int n, hipStream_t s);
+int launch_q2_grouped_gate_up(const __half* x, int n_tokens, const int32_t* row_token, int n_rows,
+                              const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
+                              const uint8_t* pool, size_t stride, int n_slots, int hidden, int inter,
+                              int group, __half* h_out, hipStream_t s);
+int launch_q2_grouped_down(const __half* h, int n_rows, const int32_t* row_out, int n_out_rows,
+                           const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
+                           const uint8_t* pool, size_t stride, int n_slots, int hidden, int inter,
+                           int group, __half* y_out, hipStream_t s);
+int launch_pair_combine(const __half* y, const __half* scores, const __half* residual, int n_tokens,
+                        int k, int hidden, float* out, hipStream_t s);

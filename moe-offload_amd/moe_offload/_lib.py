@@ -53,6 +53,13 @@ SIGNATURES: dict[str, tuple] = {
                              _c_vp, _c_vp, _c_int, _c_vp]),
     "moe_q2_switch_glu": (_c_int, [_c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
                                    _c_vp, _c_vp, _c_vp, _c_int, _c_vp]),
+    "moe_q2_grouped_gate_up": (_c_int, [_c_vp, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_u64, _c_int,
+                                        _c_int, _c_int, _c_int, _c_vp, _c_vp]),
+    "moe_q2_grouped_down": (_c_int, [_c_vp, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_u64, _c_int,
+                                     _c_int, _c_int, _c_int, _c_vp, _c_vp]),
+    "moe_q2_grouped_switch_glu": (_c_int, [_c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp,
+                                           _c_u64, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    "moe_pair_combine": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
     # no reference counterpart
     "c_last_error": (ctypes.c_char_p, []),
     "c_clear_error": (None, []),
@@ -62,6 +69,8 @@ SIGNATURES: dict[str, tuple] = {
     "c_layer_set_format": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     "c_layer_switch_glu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
     "c_layer_mark_read": (_c_int, [_c_int, _c_vp]),
+    "c_layer_grouped_switch_glu": (_c_int, [_c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_int, _c_vp,
+                                            _c_vp, _c_vp]),
     "c_layer_set_device_mode": (_c_int, [_c_int, _c_int]),
     "c_layer_step_decode_dev": (_c_int, [_c_int, _c_vp, _c_int, _c_int, _c_vp]),
     "c_layer_start_prefetch_dev": (_c_int, [_c_int, _c_vp, _c_int, _c_int, _c_int, _c_vp]),

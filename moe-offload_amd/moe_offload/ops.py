@@ -116,3 +116,55 @@ def q2_down(h, pool, slots, hidden, inter, group=64, scores=None, residual=None,
                                 _p(residual), _p(out), int(per_expert), _stream())
     _lib.check(rc, "moe_q2_down")
     return out
+
+
+def q2_grouped_gate_up(x, row_token, seg_start, pool, hidden, inter, group=64, seg_slot=None, h_out=None):
+    """h[r] = silu(G x[row_token[r]]) * (U x[row_token[r]]) for rows sorted by expert.
+
+    x: fp16 [n_tok, hidden]; row_token int32 [M]; seg_start int32 [n_seg + 1] (segment u = rows
+    seg_start[u]:seg_start[u+1], weights pool[seg_slot[u]], or pool[u] when seg_slot is None).
+    Returns fp16 [M, inter].
+    """
+    n_tok, M, n_seg = x.shape[0], row_token.numel(), seg_start.numel() - 1
+    h_out = h_out if h_out is not None else torch.empty((M, inter), dtype=torch.float16, device=x.device)
+    rc = _lib.lib().moe_q2_grouped_gate_up(_p(x), n_tok, _p(row_token), M, _p(seg_start), _p(seg_slot), n_seg,
+                                           _p(pool), pool.shape[1], pool.shape[0], hidden, inter, group, _p(h_out),
+                                           _stream())
+    _lib.check(rc, "moe_q2_grouped_gate_up")
+    return h_out
+
+
+def q2_grouped_down(h, seg_start, pool, hidden, inter, group=64, row_out=None, n_out_rows=None, seg_slot=None,
+                    out=None):
+    """y[row_out[r]] = D h[r] (fp16) for rows sorted by expert; row_out None writes row r."""
+    M, n_seg = h.shape[0], seg_start.numel() - 1
+    n_out = n_out_rows if n_out_rows is not None else M
+    out = out if out is not None else torch.empty((n_out, hidden), dtype=torch.float16, device=h.device)
+    rc = _lib.lib().moe_q2_grouped_down(_p(h), M, _p(row_out), n_out, _p(seg_start), _p(seg_slot), n_seg, _p(pool),
+                                        pool.shape[1], pool.shape[0], hidden, inter, group, _p(out), _stream())
+    _lib.check(rc, "moe_q2_grouped_down")
+    return out
+
+
+def q2_grouped_switch_glu(x, row_token, seg_start, pool, hidden, inter, group=64, row_out=None, n_out_rows=None,
+                          seg_slot=None, h_ws=None, out=None):
+    """Both grouped projections: fp16 [n_out_rows, hidden] per-(token, k) SwitchGLU outputs."""
+    n_tok, M, n_seg = x.shape[0], row_token.numel(), seg_start.numel() - 1
+    n_out = n_out_rows if n_out_rows is not None else M
+    h_ws = h_ws if h_ws is not None else torch.empty((M, inter), dtype=torch.float16, device=x.device)
+    out = out if out is not None else torch.empty((n_out, hidden), dtype=torch.float16, device=x.device)
+    rc = _lib.lib().moe_q2_grouped_switch_glu(_p(x), n_tok, _p(row_token), _p(row_out), M, n_out, _p(seg_start),
+                                              _p(seg_slot), n_seg, _p(pool), pool.shape[1], pool.shape[0], hidden,
+                                              inter, group, _p(h_ws), _p(out), _stream())
+    _lib.check(rc, "moe_q2_grouped_switch_glu")
+    return out
+
+
+def pair_combine(y, scores, residual=None, out=None):
+    """out fp32 [n_tok, hidden] = residual + sum_j scores[t, j] * y[t*k + j]."""
+    n_tok, k = scores.shape
+    hidden = y.shape[-1]
+    out = out if out is not None else torch.empty((n_tok, hidden), dtype=torch.float32, device=y.device)
+    rc = _lib.lib().moe_pair_combine(_p(y), _p(scores), _p(residual), n_tok, k, hidden, _p(out), _stream())
+    _lib.check(rc, "moe_pair_combine")
+    return out

@@ -181,3 +181,34 @@ def test_prefill_plan_reference_shapes():
         misses = len(set(int(e) for e in ids + 100) - set(int(p) for p in prior))
         assert plan["add_misses"] == misses and plan["add_hits"] == rows - misses
         assert q2.k_hdr(rows, 102) == max(1, min(102, max(rows, 16) // 4))
+
+
+def test_prefill_plan_slot_contents_brute_force():
+    """Replays the plan against a physical model of the pool (slot -> expert held) starting from
+    the prior LRU: before each chunk's GEMM every chunk expert sits in the slot of its rank, a
+    slot is loaded exactly when it held another expert, and the rebuilt LRU names what the
+    slots hold.  A plan that reused stale slots or loaded into the wrong slot fails here."""
+    rng = np.random.default_rng(1)
+    for trial in range(200):
+        cap = int(rng.choice([16, 24, 102]))
+        n_prior = int(rng.integers(0, cap + 1))
+        prior_e = [int(e) for e in rng.choice(512, size=n_prior, replace=False)]
+        prior_s = [int(s) for s in rng.choice(cap, size=n_prior, replace=False)]
+        m = int(rng.integers(0, 400))
+        hot = rng.choice(512, size=int(rng.integers(1, 300)), replace=False)
+        ids = rng.choice(hot, size=m)
+        plan = q2.prefill_plan(ids, prior_e, prior_s, cap)
+        held = dict(zip(prior_s, prior_e))
+        for u0, u1, le, ls in plan["chunks"]:
+            chunk = [int(e) for e in plan["uniq"][u0:u1]]
+            want_loads = [(s, e) for s, e in enumerate(chunk) if held.get(s) != e]
+            assert list(zip(ls, le)) == want_loads, trial
+            for e, s in zip(le, ls):
+                held[s] = e
+            assert all(held[s] == e for s, e in enumerate(chunk)), trial
+        new_e, new_s = plan["new_lru"]
+        # stale entries (slots whose expert moved to another slot) are dropped, the rest kept
+        assert all(held[s] == e for e, s in zip(new_e, new_s)), trial
+        assert len(set(new_e)) == len(new_e)
+        uniq = set(int(e) for e in ids)
+        assert plan["add_misses"] == len(uniq - set(prior_e)) and plan["add_req"] == m
