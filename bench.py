@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--extras", action="store_true", help="add per-kernel and cache details to the JSON line")
     ap.add_argument("--stage-ctas", type=int, default=2, help="staging blocks per copied expert")
     ap.add_argument("--skip-resident", action="store_true", help="headline pass only (for sweeps)")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill grouped-GEMM pass")
+    ap.add_argument("--prefill-only", action="store_true", help="run only the prefill pass and print it")
     return ap.parse_args()
 
 
@@ -107,26 +109,128 @@ def timed_tokens(st, xs, warmup, steps, use_graph):
     return elapsed, tot0, st.decode_totals()
 
 
-KINDS = ["router", "gate_up", "down", "stage", "slot_table"]
+KINDS = ["router", "gate_up", "down", "stage", "slot_table", "grouped_gate_up", "grouped_down", "pair_combine"]
 
 
-def kernel_timing(st, xs, warmup, steps):
-    """Kernel durations over `steps` eager tokens: every library launch is dispatched with a
-    start/stop HIP event pair on its own stream, stamped at the kernel's begin and end."""
+def timed_kernels(run, calls, launches_per_call):
+    """Kernel durations over `calls` invocations of run(i): every library launch is dispatched
+    with a start/stop HIP event pair on its own stream, stamped at the kernel's begin and end."""
     import ctypes
 
     import torch
 
     from moe_offload import _lib
-    st.graph = None
-    L = st.L
-    _lib.check(L.c_timing_begin(steps * st.cfg.n_layers * 6 + 256), "timing_begin")
-    for i in range(warmup, warmup + steps):
-        st.decode_token(xs[i])
+    L = _lib.lib()
+    _lib.check(L.c_timing_begin(calls * launches_per_call + 256), "timing_begin")
+    for i in range(calls):
+        run(i)
     torch.cuda.synchronize()
-    ms, n = (ctypes.c_double * 5)(), (ctypes.c_int * 5)()
+    ms, n = (ctypes.c_double * len(KINDS))(), (ctypes.c_int * len(KINDS))()
     _lib.check(L.c_timing_end(ms, n), "timing_end")
     return {k: {"launches": n[i], "avg_us": (ms[i] / n[i] * 1e3) if n[i] else 0.0} for i, k in enumerate(KINDS)}
+
+
+def kernel_timing(st, xs, warmup, steps):
+    """Per-kernel durations over `steps` eager decode tokens."""
+    st.graph = None
+    return timed_kernels(lambda i: st.decode_token(xs[warmup + i]), steps, st.cfg.n_layers * 6)
+
+
+def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, cached=True):
+    """One 512-token prefill chunk through one layer (tokens sorted by expert, grouped GEMM on
+    MFMA): (a) every expert resident in HBM -- the kernels' own HBM / MFMA rooflines;
+    (b) through a cached layer of 102 slots, misses loaded from the pinned host store per chunk."""
+    import numpy as np
+    import torch
+
+    from moe_offload import ops, prefill, q2format, synth
+    from moe_offload.loader import CachedSwitchGLU, HostExpertStore, compute_layer_capacities
+    from moe_offload.stack import random_blobs
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
+    pool = random_blobs(n_exp, hidden, inter, 64, gen, dev)
+    ids, scores = synth.prefill_routing(n_tok, k, n_exp)
+    x = torch.randn((n_tok, hidden), device=dev, generator=gen).half()
+    row_tok, row_out, seg, slot = [torch.from_numpy(a).to(dev) for a in prefill.resident_plan(ids, k)]
+    sc = torch.from_numpy(scores).to(dev)
+    m = ids.size
+    h_ws = torch.empty((m, inter), dtype=torch.float16, device=dev)
+    y = torch.empty((m, hidden), dtype=torch.float16, device=dev)
+    out = torch.empty((n_tok, hidden), dtype=torch.float32, device=dev)
+
+    def chunk(_i):
+        ops.q2_grouped_switch_glu(x, row_tok, seg, pool, hidden, inter, row_out=row_out, n_out_rows=m,
+                                  seg_slot=slot, h_ws=h_ws, out=y)
+        ops.pair_combine(y, sc, out=out)
+
+    for i in range(3):
+        chunk(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(iters):
+        chunk(i)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / iters
+    kt = timed_kernels(chunk, iters, 3)
+    gu, dn, cb = (kt[n]["avg_us"] * 1e-6 for n in ("grouped_gate_up", "grouped_down", "pair_combine"))
+    n_used = int(slot.numel())
+    blob = q2format.expert_bytes(hidden, inter, 64)
+    o = q2format.blob_offsets(hidden, inter, 64)
+    gu_bytes = n_used * ((o["down_codes"]) + (o["down_sb"] - o["gate_sb"]))
+    dn_bytes = n_used * ((o["gate_sb"] - o["down_codes"]) + (o["bytes"] - o["down_sb"]))
+    counts = np.diff(prefill.resident_plan(ids, k)[2])
+    tiles = int(np.sum((counts + 15) // 16))
+    flops = m * 6 * hidden * inter                         # useful: 2*H*I per projection per row
+    mfma_flops = tiles * 16 * 6 * hidden * inter           # issued (rows padded to 16-row tiles)
+    res = {
+        "workload": f"{n_tok}-token prefill chunk through one layer, top-{k} of {n_exp} (long-tailed: "
+                    f"max {int(counts.max())} rows/expert, {n_used} experts touched), hidden {hidden}, inter {inter}, "
+                    f"Q2 g64, all experts resident in HBM",
+        "ms_per_chunk": round(wall * 1e3, 4),
+        "tok_s": round(n_tok / wall, 1),
+        "kernels_us": {"grouped_gate_up": round(gu * 1e6, 2), "grouped_down": round(dn * 1e6, 2),
+                       "pair_combine": round(cb * 1e6, 2)},
+        "expert_bytes": n_used * blob,
+        "hbm_gb_s": round((gu_bytes + dn_bytes) / (gu + dn) / 1e9, 1),
+        "hbm_frac": round((gu_bytes + dn_bytes) / (gu + dn) / 1e9 / HBM_PEAK_GBS, 4),
+        "gate_up_gb_s": round(gu_bytes / gu / 1e9, 1),
+        "down_gb_s": round(dn_bytes / dn / 1e9, 1),
+        "mfma_util": round(flops / (gu + dn) / 2.5e15, 4),
+        "mfma_issued_util": round(mfma_flops / (gu + dn) / 2.5e15, 4),
+    }
+    del pool
+    torch.cuda.empty_cache()
+    if not cached:
+        return res
+    cap = compute_layer_capacities(budget_pct=20.0, num_layers=48, num_experts=n_exp, expert_bytes=blob)[1]
+    store = HostExpertStore(1, n_exp, blob)
+    mod = None
+    try:
+        src = random_blobs(n_exp, hidden, inter, 64, gen, dev)
+        store.view(0)[:] = src.cpu().numpy()
+        del src
+        mod = CachedSwitchGLU(store, 0, cap, hidden, inter)
+        times, staged = [], []
+        for i in range(3):
+            mod.reset_cache()
+            mod.reset_stats()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            mod(x[None], torch.from_numpy(ids).to(dev)[None])
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+            mod.sync_stats_from_c()
+            staged.append(mod.prefill_demand_bytes)
+        t = float(np.median(times))
+        res["cached_layer"] = {"slots": cap, "chunks": -(-n_used // cap), "ms_per_chunk": round(t * 1e3, 3),
+                               "tok_s": round(n_tok / t, 1), "staged_mb": round(staged[-1] / 1e6, 1),
+                               "staged_gb_s": round(staged[-1] / t / 1e9, 2)}
+    finally:
+        if mod is not None:
+            mod.close()
+        store.close()
+    return res
 
 
 def main():
@@ -141,6 +245,9 @@ def main():
     from moe_offload.stack import DecodeStack, StackConfig
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_pass()}), flush=True)
+        return
     n_tok = args.warmup + args.steps
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
@@ -224,6 +331,8 @@ def main():
                           "down_gbs": round(dn_bytes / dn_avg / 1e9, 1),
                           "gemv_pair_gbs": round((gu_bytes + dn_bytes) / (gu_avg + dn_avg) / 1e9, 1),
                           "routed_bytes_per_token": routed}
+    if not args.no_prefill:
+        line["prefill"] = prefill_pass()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_sample_s)
     print(json.dumps(line), flush=True)

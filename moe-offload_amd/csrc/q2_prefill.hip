@@ -9,21 +9,21 @@
 // with W = scale * q + bias per group of 64 inputs (2-bit codes, 16 per u32, LSB first).
 //
 // Tiling.  The rows of a segment form M tiles of 16 (v_mfma_f32_16x16x32_f16).  A block of 4
-// waves owns 16 consecutive output rows per subtile and 4 subtiles per wave (gate/up: 2 x 16
-// rows of each projection = 128 intermediate rows per block; down: 4 x 16 = 256 output rows).
-// Per 256-wide K chunk j a lane (n = lane & 15, kq = lane >> 4) loads group 4j + kq of weight
-// row n: one 16-byte load of 64 codes plus one (scale, bias) word.
+// waves shares the M tile; each wave owns 4 subtiles of 16 weight rows (gate/up: 2 x 16 rows of
+// each projection = 128 intermediate rows per block; down: 4 x 16 = 256 output rows).  Per
+// 256-wide K chunk j a lane (n = lane & 15, kq = lane >> 4) loads group 4j + kq of weight row n
+// (one 16-byte load of 64 codes plus the (scale, bias) word) and the same group of activation
+// row n of the M tile (8 x 16 bytes, from L1/L2).  Nothing is staged in LDS: the next chunk's
+// loads are in flight while the current chunk is multiplied.
 //
 // Dequantisation.  A 2-bit code in the low bits of a nibble is the fp4 (e2m1) value q/2, so
 // w & 0x33333333 (even codes) and (w >> 2) & 0x33333333 (odd codes) are 8 fp4 values each;
-// v_cvt_scalef32_pk_f16_fp4 turns a byte into two exact halves and one v_pk_mul_f16 by 2*scale
-// gives scale*q rounded once to fp16.  The bias contributes sum_g b[n,g] * sum_{k in g} x[m,k]:
-// one more pair of MFMAs per subtile and 8 chunks, with B = the lane's 8 biases and A = the
-// per-group row sums of the tile split into fp16 hi + lo.
+// v_cvt_scalef32_pk_f16_fp4 turns a byte into two exact halves, and one v_pk_fma_f16 with
+// (2*scale, bias) gives the fp16 weight scale*q + bias rounded once (MLX's dequantised weight).
 //
-// K order.  Inside an MFMA the K positions are permuted identically for A and B: activations
-// are staged in LDS with each 16-element chunk stored as [x0 x2 .. x14 | x1 x3 .. x15], which
-// is the order of the even / odd codes of one 32-bit word.
+// K order.  Inside an MFMA the K positions are permuted identically for A and B: the even codes
+// of a 32-bit word pair with activations [x0 x2 .. x14] of its 16 inputs and the odd codes with
+// [x1 x3 .. x15]; the activation halves are regrouped in registers with v_perm_b32.
 #include <hip/hip_fp16.h>
 
 #include "moe_common.h"
@@ -39,15 +39,6 @@ constexpr int kSub = 4;          // 16-row weight subtiles per wave
 constexpr int kMaxChunks = 10;   // K <= 2560
 constexpr int kGateUp = 0, kDown = 1;
 
-template <int NCH>
-struct Tile {
-    static constexpr int KP = NCH * 256 + 8;          // LDS row stride (halves); +8 staggers banks
-    static constexpr int NB = (NCH + 7) / 8;          // bias MFMA blocks
-    static constexpr size_t XS_BYTES = (size_t)kMT * KP * 2;
-    static constexpr size_t SX_HALVES = (size_t)NB * kMT * 4 * 8;
-    static constexpr size_t LDS_BYTES = XS_BYTES + 2 * SX_HALVES * 2;
-};
-
 // Block index -> work item, keeping consecutive work items on one XCD (blocks are dealt to the
 // 8 XCDs round robin), so the blocks of one segment share that XCD's L2 for the activations.
 __device__ __forceinline__ int xcd_order(int b, int nb) {
@@ -55,72 +46,29 @@ __device__ __forceinline__ int xcd_order(int b, int nb) {
     return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
 }
 
-// Stage the M tile (rows row0 .. row0+cnt-1 of the source; mapped through row_map when given)
-// into LDS in the permuted K order, with the per-group row sums for the bias MFMA.
-template <int NCH>
-__device__ __forceinline__ void stage_tile(const __half* __restrict__ src, int K, const int32_t* __restrict__ row_map,
-                                           int n_src_rows, int row0, int cnt, _Float16* xs, _Float16* sx_hi,
-                                           _Float16* sx_lo) {
-    using T = Tile<NCH>;
-    constexpr int GROUPS = T::NB * 32;                 // groups covered by the bias fragments
-    const int kg = K / 64;
-    for (int it = threadIdx.x; it < kMT * GROUPS; it += blockDim.x) {
-        const int m = it / GROUPS, g = it % GROUPS;
-        int srow = -1;
-        if (m < cnt) {
-            const int r = row0 + m;
-            srow = row_map ? row_map[r] : r;
-            if (srow < 0 || srow >= n_src_rows) srow = -1;
-        }
-        uint32_t w[32];
-        if (srow >= 0 && g < kg) {
-            const uint4* p = reinterpret_cast<const uint4*>(src + (size_t)srow * K + (size_t)g * 64);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                uint4 v = p[i];
-                w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; ++i) w[i] = 0;
-        }
-        float sum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            f16x2 v = __builtin_bit_cast(f16x2, w[i]);
-            sum += (float)v.x;
-            sum += (float)v.y;
-        }
-        if (g < NCH * 4) {
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-                const uint32_t* r = w + 8 * cc;       // x[16cc .. 16cc+15] as 8 words of 2 halves
-                uint4 ev, od;
-                ev.x = (r[0] & 0xFFFFu) | (r[1] << 16); od.x = (r[0] >> 16) | (r[1] & 0xFFFF0000u);
-                ev.y = (r[2] & 0xFFFFu) | (r[3] << 16); od.y = (r[2] >> 16) | (r[3] & 0xFFFF0000u);
-                ev.z = (r[4] & 0xFFFFu) | (r[5] << 16); od.z = (r[4] >> 16) | (r[5] & 0xFFFF0000u);
-                ev.w = (r[6] & 0xFFFFu) | (r[7] << 16); od.w = (r[6] >> 16) | (r[7] & 0xFFFF0000u);
-                uint4* d = reinterpret_cast<uint4*>(xs + (size_t)m * T::KP + g * 64 + cc * 16);
-                d[0] = ev;
-                d[1] = od;
-            }
-        }
-        const _Float16 hi = (_Float16)sum;
-        const _Float16 lo = (_Float16)(sum - (float)hi);
-        const int chunk = g >> 2, kq = g & 3, jb = chunk >> 3, j = chunk & 7;
-        const int at = ((jb * kMT + m) * 4 + kq) * 8 + j;
-        sx_hi[at] = hi;
-        sx_lo[at] = lo;
-    }
-}
-
-__device__ __forceinline__ f16x8 dequant8(uint32_t bits, f16x2 s2) {
+__device__ __forceinline__ f16x8 dequant8(uint32_t bits, f16x2 s2, f16x2 b2) {
     f16x2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(bits, 1.0f, 0);
     f16x2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(bits, 1.0f, 1);
     f16x2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(bits, 1.0f, 2);
     f16x2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(bits, 1.0f, 3);
-    a *= s2; b *= s2; c *= s2; d *= s2;
+    a = __builtin_elementwise_fma(a, s2, b2);
+    b = __builtin_elementwise_fma(b, s2, b2);
+    c = __builtin_elementwise_fma(c, s2, b2);
+    d = __builtin_elementwise_fma(d, s2, b2);
     return (f16x8){a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+// 16 activations x[0..15] (two 16-byte words, natural order) -> (even, odd) MFMA fragments.
+__device__ __forceinline__ void split_even_odd(uint4 lo, uint4 hi, f16x8& ev, f16x8& od) {
+    const uint32_t r[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    uint32_t e[4], o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        e[i] = __builtin_amdgcn_perm(r[2 * i + 1], r[2 * i], 0x05040100u);
+        o[i] = __builtin_amdgcn_perm(r[2 * i + 1], r[2 * i], 0x07060302u);
+    }
+    ev = __builtin_bit_cast(f16x8, make_uint4(e[0], e[1], e[2], e[3]));
+    od = __builtin_bit_cast(f16x8, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
 template <int NCH, int MODE>
@@ -130,12 +78,6 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
     const int32_t* __restrict__ seg_start, const int32_t* __restrict__ seg_slot, int n_seg, int n_rows,
     const uint8_t* __restrict__ pool, size_t stride, int n_slots, BlobLayout L, int tiles_per_seg,
     __half* __restrict__ out) {
-    using T = Tile<NCH>;
-    extern __shared__ __align__(16) unsigned char lds[];
-    _Float16* xs = reinterpret_cast<_Float16*>(lds);
-    _Float16* sx_hi = reinterpret_cast<_Float16*>(lds + T::XS_BYTES);
-    _Float16* sx_lo = sx_hi + T::SX_HALVES;
-
     const int K = MODE == kGateUp ? L.hidden : L.inter;          // contraction length
     const int N = MODE == kGateUp ? L.inter : L.hidden;          // output rows per projection
     const int kg = K / 64;
@@ -146,13 +88,15 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
     r0 = r0 < 0 ? 0 : (r0 > n_rows ? n_rows : r0);
     r1 = r1 < r0 ? r0 : (r1 > n_rows ? n_rows : r1);
     const int slot = seg_slot ? seg_slot[seg] : seg;
-    if (r1 == r0 || slot < 0 || slot >= n_slots) return;          // uniform per block
+    if (r1 == r0 || slot < 0 || slot >= n_slots) return;
 
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int n = lane & 15, kq = lane >> 4;
     const uint8_t* blob = pool + (size_t)slot * stride;
     const size_t code_row = (size_t)K / 4, sb_row = (size_t)kg;   // bytes / words per weight row
 
+    // Weight row of lane n in subtile s = base_s + n: a wave-uniform base per subtile plus one
+    // per-lane offset shared by all subtiles.
     const uint8_t* codes[kSub];
     const uint32_t* sbp[kSub];
     bool rv[kSub];
@@ -160,89 +104,115 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
 #pragma unroll
     for (int s = 0; s < kSub; ++s) {
         size_t co, so;
-        int row;
+        int base;
         if (MODE == kGateUp) {
-            row = tile * 128 + wv * 32 + (s >> 1) * 16 + n;
+            base = tile * 128 + wv * 32 + (s >> 1) * 16;
             co = (s & 1) ? L.up_codes : L.gate_codes;
             so = (s & 1) ? L.up_sb : L.gate_sb;
         } else {
-            row = tile * 256 + wv * 64 + s * 16 + n;
+            base = tile * 256 + wv * 64 + s * 16;
             co = L.down_codes;
             so = L.down_sb;
         }
-        col[s] = row;
-        rv[s] = row < N;
-        const int rr = rv[s] ? row : 0;
-        codes[s] = blob + co + (size_t)rr * code_row;
-        sbp[s] = reinterpret_cast<const uint32_t*>(blob + so) + (size_t)rr * sb_row;
+        col[s] = base + n;
+        rv[s] = base + n < N;
+        codes[s] = blob + co + (size_t)base * code_row;
+        sbp[s] = reinterpret_cast<const uint32_t*>(blob + so) + (size_t)base * sb_row;
     }
+    const size_t lane_code = (size_t)n * code_row + (size_t)kq * 16, lane_sb = (size_t)n * sb_row + kq;
+
+    // Activation chunks are staged in LDS, shared by the 4 waves: 16 rows x 32 units of 16 bytes
+    // (256 inputs) per buffer, unit v of row m stored at m * 32 + (v ^ m) so that the 16 lanes
+    // reading one unit column of the tile hit distinct banks.  Each thread stages 2 units.
+    __shared__ uint4 a_lds[2][kMT * 32];
+    const int t = threadIdx.x;
+    const int sm0 = t >> 5, sm1 = sm0 + 8, sv = t & 31;       // the two units this thread stages
 
     for (int m0 = r0; m0 < r1; m0 += kMT) {
         const int cnt = (r1 - m0) < kMT ? (r1 - m0) : kMT;
-        __syncthreads();                                   // previous tile's LDS reads done
-        stage_tile<NCH>(src, K, row_map, n_src_rows, m0, cnt, xs, sx_hi, sx_lo);
-        __syncthreads();
+        // source rows of the two staged units; a row past the tile or naming an out-of-range
+        // source row is staged as zeros
+        auto src_row = [&](int m) {
+            if (m >= cnt) return -1;
+            const int r = m0 + m;
+            const int sr = row_map ? row_map[r] : r;
+            return (sr < 0 || sr >= n_src_rows) ? -1 : sr;
+        };
+        const int sr0 = src_row(sm0), sr1 = src_row(sm1);
+        const uint4* ar0 = reinterpret_cast<const uint4*>(src + (size_t)(sr0 < 0 ? 0 : sr0) * K);
+        const uint4* ar1 = reinterpret_cast<const uint4*>(src + (size_t)(sr1 < 0 ? 0 : sr1) * K);
 
         f32x4 acc[kSub];
 #pragma unroll
         for (int s = 0; s < kSub; ++s) acc[s] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        f16x8 bias[kSub];
-#pragma unroll
-        for (int s = 0; s < kSub; ++s) bias[s] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
 
-        uint4 cw[kSub], nw[kSub];
-        uint32_t sw[kSub], ns[kSub];
-#pragma unroll
-        for (int s = 0; s < kSub; ++s) {
-            const bool ok = rv[s] && kq < kg;
-            cw[s] = ok ? *reinterpret_cast<const uint4*>(codes[s] + kq * 16) : make_uint4(0, 0, 0, 0);
-            sw[s] = ok ? sbp[s][kq] : 0u;
-        }
-#pragma unroll
-        for (int j = 0; j < NCH; ++j) {
-            if (j + 1 < NCH) {
-                const int g = 4 * (j + 1) + kq;
-#pragma unroll
-                for (int s = 0; s < kSub; ++s) {
-                    const bool ok = rv[s] && g < kg;
-                    nw[s] = ok ? *reinterpret_cast<const uint4*>(codes[s] + (size_t)g * 16) : make_uint4(0, 0, 0, 0);
-                    ns[s] = ok ? sbp[s][g] : 0u;
-                }
-            }
-            f16x2 s2[kSub];
+        uint4 cw[2][kSub];
+        uint32_t sw[2][kSub];
+        uint4 xs0, xs1;                                        // staged activation units in flight
+        auto load = [&](int j, int b) {
+            const bool gv = 4 * j + kq < kg;
 #pragma unroll
             for (int s = 0; s < kSub; ++s) {
-                const f16x2 sb = __builtin_bit_cast(f16x2, sw[s]);
+                const bool ok = rv[s] && gv;
+                cw[b][s] = ok ? *reinterpret_cast<const uint4*>(codes[s] + lane_code + (size_t)j * 64)
+                              : make_uint4(0, 0, 0, 0);
+                sw[b][s] = ok ? sbp[s][lane_sb + 4 * j] : 0u;
+            }
+            const int u = 32 * j + sv;                         // 16-byte unit within the row
+            const bool uv = u * 8 < K;
+            xs0 = (sr0 >= 0 && uv) ? ar0[u] : make_uint4(0, 0, 0, 0);
+            xs1 = (sr1 >= 0 && uv) ? ar1[u] : make_uint4(0, 0, 0, 0);
+        };
+        auto stage = [&](int b) {
+            a_lds[b][sm0 * 32 + (sv ^ sm0)] = xs0;
+            a_lds[b][sm1 * 32 + (sv ^ sm1)] = xs1;
+        };
+        auto compute = [&](int b) {
+            f16x2 s2[kSub], b2[kSub];
+#pragma unroll
+            for (int s = 0; s < kSub; ++s) {
+                const f16x2 sb = __builtin_bit_cast(f16x2, sw[b][s]);
                 const _Float16 two_s = sb.x * (_Float16)2.0f;
                 s2[s] = (f16x2){two_s, two_s};
-                bias[s][j & 7] = sb.y;
+                b2[s] = (f16x2){sb.y, sb.y};
             }
-            const _Float16* arow = xs + (size_t)n * T::KP + (size_t)(16 * j + 4 * kq) * 16;
+            const uint4* arow = a_lds[b] + n * 32;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const f16x8 a_ev = *reinterpret_cast<const f16x8*>(arow + q * 16);
-                const f16x8 a_od = *reinterpret_cast<const f16x8*>(arow + q * 16 + 8);
+                const int v = 8 * kq + 2 * q;
+                f16x8 a_ev, a_od;
+                split_even_odd(arow[v ^ n], arow[(v + 1) ^ n], a_ev, a_od);
 #pragma unroll
                 for (int s = 0; s < kSub; ++s) {
-                    const uint32_t w = q == 0 ? cw[s].x : q == 1 ? cw[s].y : q == 2 ? cw[s].z : cw[s].w;
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_ev, dequant8(w & 0x33333333u, s2[s]), acc[s], 0, 0, 0);
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_od, dequant8((w >> 2) & 0x33333333u, s2[s]), acc[s], 0, 0, 0);
+                    const uint32_t w = q == 0 ? cw[b][s].x : q == 1 ? cw[b][s].y : q == 2 ? cw[b][s].z : cw[b][s].w;
+                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_ev, dequant8(w & 0x33333333u, s2[s], b2[s]),
+                                                                  acc[s], 0, 0, 0);
+                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_od, dequant8((w >> 2) & 0x33333333u, s2[s], b2[s]),
+                                                                  acc[s], 0, 0, 0);
                 }
             }
-            if ((j & 7) == 7 || j == NCH - 1) {
-                const int at = (((j >> 3) * kMT + n) * 4 + kq) * 8;
-                const f16x8 ah = *reinterpret_cast<const f16x8*>(sx_hi + at);
-                const f16x8 al = *reinterpret_cast<const f16x8*>(sx_lo + at);
-#pragma unroll
-                for (int s = 0; s < kSub; ++s) {
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bias[s], acc[s], 0, 0, 0);
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bias[s], acc[s], 0, 0, 0);
-                    bias[s] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-                }
-            }
+        };
+        // Pipeline: while chunk j is multiplied out of LDS buffer j & 1, chunk j + 1's weights
+        // (registers) and activations (registers, then LDS buffer (j + 1) & 1) are in flight.
+        // One barrier per chunk: the buffer written after compute(j) was last read by
+        // compute(j - 1), which every wave finished before the previous barrier.
+        __syncthreads();                                       // previous tile's reads are done
+        load(0, 0);
+        stage(0);
+        __syncthreads();
+#pragma unroll 1
+        for (int j = 0; j < NCH; j += 2) {
+            if (j + 1 < NCH) load(j + 1, 1);
+            compute(0);
             if (j + 1 < NCH) {
-#pragma unroll
-                for (int s = 0; s < kSub; ++s) { cw[s] = nw[s]; sw[s] = ns[s]; }
+                stage(1);
+                __syncthreads();
+                if (j + 2 < NCH) load(j + 2, 0);
+                compute(1);
+                if (j + 2 < NCH) {
+                    stage(0);
+                    __syncthreads();
+                }
             }
         }
 
@@ -274,13 +244,6 @@ template <int NCH, int MODE>
 int launch_proj(const __half* src, int n_src_rows, const int32_t* row_map, const int32_t* row_out, int n_out_rows,
                 const int32_t* seg_start, const int32_t* seg_slot, int n_seg, int n_rows, const uint8_t* pool,
                 size_t stride, int n_slots, const BlobLayout& L, __half* out, hipStream_t s) {
-    using T = Tile<NCH>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        HIP_TRY(hipFuncSetAttribute((const void*)k_q2g_proj<NCH, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)T::LDS_BYTES));
-        attr_set = true;
-    }
     const int N = MODE == kGateUp ? L.inter : L.hidden;
     const int rows_per_block = MODE == kGateUp ? 128 : 256;
     const int tiles = (N + rows_per_block - 1) / rows_per_block;
@@ -288,8 +251,8 @@ int launch_proj(const __half* src, int n_src_rows, const int32_t* row_map, const
     if (nb <= 0) return 0;
     if (nb > 0x7FFFFFFFLL) { moe_set_error("grouped q2: grid too large"); return -1; }
     MOE_LAUNCH(MODE == kGateUp ? TK_PF_GATE_UP : TK_PF_DOWN, (k_q2g_proj<NCH, MODE>), dim3((unsigned)nb), dim3(256),
-               T::LDS_BYTES, s, src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg, n_rows, pool,
-               stride, n_slots, L, tiles, out);
+               0, s, src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg, n_rows, pool, stride,
+               n_slots, L, tiles, out);
     HIP_TRY(hipGetLastError());
     return 0;
 }
