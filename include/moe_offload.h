@@ -177,6 +177,15 @@ int c_layer_step_decode_dev(int layer_idx, const uint32_t* ids_dev, int k, int s
                             void* stream);
 int c_layer_start_prefetch_dev(int layer_idx, const int32_t* preds_dev, int m, int max_fetch,
                                int stage_ctas, void* stream);
+/* moe_router whose last block also runs the decode step of device-driven layer step_layer with
+ * the selected ids (slot ids into its slot_inds) and the prefetch of device-driven layer
+ * pf_layer with the prediction (-1: none).  Same decisions as moe_router followed by
+ * c_layer_step_decode_dev(step_layer, ids) and c_layer_start_prefetch_dev(pf_layer, pred),
+ * without their two launches; copies are then queued with c_layer_stage_dev. */
+int c_router_tables_dev(int step_layer, int pf_layer, int max_fetch, const float* h_in,
+                        const void* norm_w, float eps, const void* x_in, void* x_out, const void* w,
+                        const void* w_next, int hidden, int n_exp, int k, int m, void* workspace,
+                        uint32_t* ids_out, void* scores_out, int32_t* pred_out, void* stream);
 /* Queue the copies of the layer's last device-side decode step (list 0) or prefetch (list 1)
  * on `stream` (the two lists are kept apart so a step may run while prefetch copies queue). */
 int c_layer_stage_dev(int layer_idx, int list, int stage_ctas, void* stream);

@@ -545,7 +545,46 @@ int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_i
     unsigned* counter = (unsigned*)((uint8_t*)workspace + (size_t)(2 * n_exp) * sizeof(float));
     return launch_router(h_in, (const __half*)norm_w, eps, (const __half*)x_in, (__half*)x_out,
                          (const __half*)w, (const __half*)w_next, hidden, n_exp, k, m, scratch, counter,
-                         ids_out, (__half*)scores_out, pred_out, (hipStream_t)stream);
+                         ids_out, (__half*)scores_out, pred_out, nullptr, nullptr, nullptr, 0, (hipStream_t)stream);
+}
+
+// Router whose last block also runs the decode step of layer step_layer (its selected ids, slot
+// ids into that layer's slot_inds) and the prefetch of layer pf_layer (the prediction); either
+// layer may be -1.  Both must be device-driven layers.  Same decisions as
+// c_layer_step_decode_dev + c_layer_start_prefetch_dev after moe_router.
+int c_router_tables_dev(int step_layer, int pf_layer, int max_fetch, const float* h_in, const void* norm_w, float eps,
+                        const void* x_in, void* x_out, const void* w, const void* w_next, int hidden, int n_exp, int k,
+                        int m, void* workspace, uint32_t* ids_out, void* scores_out, int32_t* pred_out, void* stream) {
+    SlotTable* st = nullptr;
+    SlotTable* pt = nullptr;
+    uint32_t* slots = nullptr;
+    if (step_layer >= 0) {
+        if (!valid_layer(step_layer) || !g_layers[step_layer].init || !g_layers[step_layer].device_mode) {
+            moe_set_error("router_tables_dev: layer %d is not a device-driven layer", step_layer);
+            return -1;
+        }
+        LayerState& L = g_layers[step_layer];
+        if (k > L.capacity) { moe_set_error("router_tables_dev: k=%d > capacity %d", k, L.capacity); return -1; }
+        if (!L.slot_inds || !L.slot_inds_device) {
+            moe_set_error("router_tables_dev: layer %d slot_inds must be device memory", step_layer);
+            return -1;
+        }
+        st = L.dtab;
+        slots = L.slot_inds;
+    }
+    if (pf_layer >= 0) {
+        if (!valid_layer(pf_layer) || !g_layers[pf_layer].init || !g_layers[pf_layer].device_mode) {
+            moe_set_error("router_tables_dev: layer %d is not a device-driven layer", pf_layer);
+            return -1;
+        }
+        if (!w_next || m <= 0) { moe_set_error("router_tables_dev: prefetch needs the next router and m > 0"); return -1; }
+        pt = g_layers[pf_layer].dtab;
+    }
+    float* scratch = (float*)workspace;
+    unsigned* counter = (unsigned*)((uint8_t*)workspace + (size_t)(2 * n_exp) * sizeof(float));
+    return launch_router(h_in, (const __half*)norm_w, eps, (const __half*)x_in, (__half*)x_out,
+                         (const __half*)w, (const __half*)w_next, hidden, n_exp, k, m, scratch, counter,
+                         ids_out, (__half*)scores_out, pred_out, st, slots, pt, max_fetch, (hipStream_t)stream);
 }
 
 int moe_f64_to_f16(const double* in, uint16_t* out, int n, void* stream) {

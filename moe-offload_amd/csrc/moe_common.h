@@ -125,7 +125,8 @@ void kt_events(int kind, hipEvent_t* start, hipEvent_t* stop);   // both null wh
 int launch_router(const float* h_in, const __half* norm_w, float eps, const __half* x_in,
                   __half* x_out, const __half* w, const __half* w_next, int hidden, int n_exp,
                   int k, int m, float* scratch, unsigned* counter, uint32_t* ids_out,
-                  __half* scores_out, int32_t* pred_out, hipStream_t s);
+                  __half* scores_out, int32_t* pred_out, SlotTable* step_tab, uint32_t* slot_inds,
+                  SlotTable* pf_tab, int max_fetch, hipStream_t s);
 int launch_f64_to_f16(const double* in, uint16_t* out, int n, hipStream_t s);
 int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidden, __half* x_out,
                    hipStream_t s);

@@ -17,9 +17,15 @@
 // on a device-scope counter; the block that arrives last runs the selection (wave 0:
 // softmax/top-k with DPP wave maxima, wave 1: predictor) and re-arms the counter, so no
 // grid-wide wait is ever needed.
+//
+// Optionally the last block continues with the slot-table work of the decode path
+// (expert_io.c:583-685 and 527-581): wave 0 runs the decode step of this layer's table with the
+// selected ids, wave 1 the prefetch of the next layer's table with the prediction, so neither
+// needs a launch of its own.
 #include <hip/hip_fp16.h>
 
 #include "moe_common.h"
+#include "slot_table_dev.h"
 
 namespace {
 
@@ -102,7 +108,8 @@ __global__ __launch_bounds__(kThreads) void k_router(
     const __half* __restrict__ w, const __half* __restrict__ w_next,
     int hidden, int n_exp, int k, int m,
     float* __restrict__ scratch, unsigned* __restrict__ counter,
-    uint32_t* __restrict__ ids_out, __half* __restrict__ scores_out, int32_t* __restrict__ pred_out) {
+    uint32_t* __restrict__ ids_out, __half* __restrict__ scores_out, int32_t* __restrict__ pred_out,
+    SlotTable* __restrict__ step_tab, uint32_t* __restrict__ slot_inds, SlotTable* __restrict__ pf_tab, int max_fetch) {
     __shared__ __align__(16) uint16_t xs[kMaxHidden];
     __shared__ double red[kThreads / 64];
     __shared__ int is_last;
@@ -168,6 +175,8 @@ __global__ __launch_bounds__(kThreads) void k_router(
 
     __shared__ uint32_t keys[kMaxExperts];
     __shared__ uint32_t pkeys[kMaxExperts];
+    __shared__ uint32_t sel_ids[MOE_MAX_K];
+    __shared__ int32_t sel_pred[MOE_MAX_PREFETCH];
     __shared__ double redm[kThreads / 64], reds[kThreads / 64];
     const int n_pad = ((n_exp + 63) / 64) * 64;
     // softmax over the logits in fp64, spread over the whole block
@@ -235,6 +244,7 @@ __global__ __launch_bounds__(kThreads) void k_router(
         }
         if (lane < k) {
             ids_out[pos] = mine & 0xFFFFu;
+            sel_ids[pos] = mine & 0xFFFFu;
             scores_out[pos] = __float2half_rn(g / s);   // correctly rounded f32 division, then f16
         }
     } else if (wv == 1 && w_next && m > 0) {
@@ -263,7 +273,16 @@ __global__ __launch_bounds__(kThreads) void k_router(
         }
         const int src = first + last - lane;
         const int id = __shfl((int)(mine & 0xFFFFu), src, 64);
-        if (lane < m) pred_out[lane] = id;
+        if (lane < m) {
+            pred_out[lane] = id;
+            sel_pred[lane] = id;
+        }
+    }
+    if (step_tab || pf_tab) {
+        __shared__ slot_dev::LdsTable tabs[2];
+        __syncthreads();
+        if (wv == 0 && step_tab) slot_dev::dev_slot_step(step_tab, tabs[0], sel_ids, k, slot_inds, lane);
+        if (wv == 1 && pf_tab && w_next && m > 0) slot_dev::dev_slot_prefetch(pf_tab, tabs[1], sel_pred, m, max_fetch, lane);
     }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -301,7 +320,8 @@ int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidde
 int launch_router(const float* h_in, const __half* norm_w, float eps, const __half* x_in,
                   __half* x_out, const __half* w, const __half* w_next, int hidden, int n_exp,
                   int k, int m, float* scratch, unsigned* counter, uint32_t* ids_out,
-                  __half* scores_out, int32_t* pred_out, hipStream_t s) {
+                  __half* scores_out, int32_t* pred_out, SlotTable* step_tab, uint32_t* slot_inds,
+                  SlotTable* pf_tab, int max_fetch, hipStream_t s) {
     if (hidden <= 0 || hidden > kMaxHidden || hidden % 8 != 0) {
         moe_set_error("router: hidden=%d unsupported (multiple of 8, <= %d)", hidden, kMaxHidden);
         return -1;
@@ -314,7 +334,8 @@ int launch_router(const float* h_in, const __half* norm_w, float eps, const __ha
         moe_set_error("router: predictor m=%d unsupported", m);
         return -1;
     }
-    if (!w || !scratch || !counter || !ids_out || !scores_out || (!h_in && !x_in) || (w_next && !pred_out)) {
+    if (!w || !scratch || !counter || !ids_out || !scores_out || (!h_in && !x_in) || (w_next && !pred_out) ||
+        (step_tab && !slot_inds)) {
         moe_set_error("router: null pointer argument");
         return -1;
     }
@@ -322,7 +343,7 @@ int launch_router(const float* h_in, const __half* norm_w, float eps, const __ha
     int grid = (rows + kRowsPerBlock - 1) / kRowsPerBlock;      // one row per wave
     MOE_LAUNCH(TK_ROUTER, k_router, dim3(grid), dim3(kThreads), 0, s, h_in, norm_w, eps, x_in, x_out,
                        w, w_next, hidden, n_exp, k, w_next ? m : 0, scratch, counter, ids_out,
-                       scores_out, pred_out);
+                       scores_out, pred_out, step_tab, slot_inds, pf_tab, max_fetch);
     HIP_TRY(hipGetLastError());
     return 0;
 }

@@ -1,327 +1,24 @@
-// Device-side slot table (one wave per layer operation) and miss staging for gfx950.
+// Device-side slot table and miss staging for gfx950.
 //
-// The decisions are those of mlx-qwen38/expert_io.c: decode step 583-685, prefetch 527-581,
-// victim choice 404-426 (free stack first, else the oldest resident slot whose expert is not
-// protected, else the oldest resident slot).  The table is held in recency-stamp form
-// (SlotTable): the oldest resident slot is the one with the smallest stamp, and refreshing a
-// slot gives it the next clock value.
-//
-// Each operation copies the table into LDS (one wave, ~4.5 KB), decides, and writes it back,
-// so the host never has to read the router's ids: the step and prefetch run on the stream
-// right after the router, and their copy lists drive k_stage, which pulls the missing expert
-// blobs from the pinned (host-mapped) expert store into the HBM slot pool.
+// k_slot_step / k_slot_prefetch run one table operation in one wave (slot_table_dev.h), so the
+// host never has to read the router's ids: the step and prefetch run on the stream right after
+// the router (or inside it, see router.hip), and their copy lists drive k_stage, which pulls the
+// missing expert blobs from the pinned (host-mapped) expert store into the HBM slot pool.
 #include "moe_common.h"
+#include "slot_table_dev.h"
 
 namespace {
 
-struct LdsTable {
-    int16_t slot_of[MOE_NUM_EXPERTS];
-    int16_t eid_of[MOE_NUM_EXPERTS];
-    uint32_t stamp[MOE_NUM_EXPERTS];
-    uint32_t protect[16];      // bitmap over expert ids
-    uint32_t resident[16];
-    uint32_t pred[16];
-    uint32_t fetched[16];
-    int32_t list_e[MOE_MAX_PREFETCH];
-    int32_t list_s[MOE_MAX_PREFETCH];
-    int32_t n_list;
-};
-
-__device__ __forceinline__ bool bit(const uint32_t* bm, int e) { return (bm[e >> 5] >> (e & 31)) & 1u; }
-
-__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        uint64_t w = __shfl_xor(v, o, 64);
-        v = w < v ? w : v;
-    }
-    return v;
-}
-
-__device__ void load_table(const SlotTable* t, LdsTable& L, int lane) {
-    const int cap = t->capacity;
-    for (int i = lane; i < MOE_NUM_EXPERTS; i += 64) {
-        L.slot_of[i] = t->slot_of[i];
-        L.eid_of[i] = i < cap ? t->eid_of[i] : (int16_t)-1;
-        L.stamp[i] = i < cap ? t->stamp[i] : 0u;
-    }
-    if (lane < 16) {
-        L.protect[lane] = 0;
-        L.resident[lane] = 0;
-        L.pred[lane] = 0;
-        L.fetched[lane] = 0;
-    }
-    if (lane == 0) L.n_list = 0;
-    __syncthreads();
-}
-
-__device__ void store_table(SlotTable* t, const LdsTable& L, int lane) {
-    const int cap = t->capacity;
-    for (int i = lane; i < MOE_NUM_EXPERTS; i += 64) {
-        t->slot_of[i] = L.slot_of[i];
-        if (i < cap) {
-            t->eid_of[i] = L.eid_of[i];
-            t->stamp[i] = L.stamp[i];
-        }
-    }
-}
-
-// Relabel stamps by rank when the clock nears wrap-around (order unchanged).
-__device__ void renorm(SlotTable* t, LdsTable& L, int lane, uint32_t& clock) {
-    if (clock < STAMP_RENORM_AT) return;
-    const int cap = t->capacity;
-    uint32_t newst[MOE_NUM_EXPERTS / 64];
-    for (int i = 0; i < MOE_NUM_EXPERTS / 64; ++i) {
-        int s = lane + 64 * i;
-        newst[i] = 0;
-        if (s < cap && L.stamp[s]) {
-            uint32_t mine = L.stamp[s], rank = 1;
-            for (int q = 0; q < cap; ++q) rank += (L.stamp[q] && L.stamp[q] < mine);
-            newst[i] = rank;
-        }
-    }
-    __syncthreads();
-    uint32_t n = 0;
-    for (int i = 0; i < MOE_NUM_EXPERTS / 64; ++i) {
-        int s = lane + 64 * i;
-        if (s < cap) { L.stamp[s] = newst[i]; n += newst[i] != 0; }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o, 64);
-    clock = n;
-    __syncthreads();
-}
-
-// One victim for a slot allocation (uniform across the wave). Returns the slot.
-__device__ int take_slot(SlotTable* t, LdsTable& L, int lane, int& n_free, const uint32_t* protect) {
-    if (n_free > 0) {
-        --n_free;
-        return t->free_stack[n_free];
-    }
-    const int cap = t->capacity;
-    uint64_t best = ~0ull, oldest = ~0ull;
-    for (int s = lane; s < cap; s += 64) {
-        uint32_t st = L.stamp[s];
-        if (!st) continue;
-        uint64_t key = ((uint64_t)st << 32) | (uint32_t)s;
-        oldest = key < oldest ? key : oldest;
-        int e = L.eid_of[s];
-        if (e >= 0 && !bit(protect, e)) best = key < best ? key : best;
-    }
-    best = wave_min_u64(best);
-    oldest = wave_min_u64(oldest);
-    uint64_t pick = (best != ~0ull) ? best : oldest;
-    int s = (int)(pick & 0xFFFFFFFFu);
-    __syncthreads();
-    if (lane == 0 && pick != ~0ull) {
-        int e = L.eid_of[s];
-        if (e >= 0) L.slot_of[e] = -1;
-        L.eid_of[s] = -1;
-        L.stamp[s] = 0;
-    }
-    __syncthreads();
-    return pick == ~0ull ? -1 : s;
-}
-
-// Bind expert e to slot s at the MRU end (an already-resident expert is only refreshed).
-__device__ void bind(LdsTable& L, int lane, int e, int s, uint32_t& clock) {
-    if (lane == 0) {
-        int cur = L.slot_of[e];
-        if (cur >= 0) {
-            L.stamp[cur] = ++clock;
-        } else {
-            L.slot_of[e] = (int16_t)s;
-            L.eid_of[s] = (int16_t)e;
-            L.stamp[s] = ++clock;
-        }
-    }
-    clock = __shfl(clock, 0, 64);
-    __syncthreads();
-}
-
-__device__ void count_runs(SlotTable* t, const int32_t* e, int n) {
-    if (n <= 0) return;
-    int32_t v[MOE_MAX_PREFETCH];
-    for (int i = 0; i < n; ++i) v[i] = e[i];
-    for (int i = 1; i < n; ++i) {
-        int32_t x = v[i];
-        int j = i;
-        while (j > 0 && v[j - 1] > x) { v[j] = v[j - 1]; --j; }
-        v[j] = x;
-    }
-    int runs = 1;
-    for (int i = 1; i < n; ++i) runs += (v[i] != v[i - 1] + 1);
-    t->stats[ST_UNCOAL] += (uint64_t)n * MOE_NUM_TENSORS;
-    t->stats[ST_COAL] += (uint64_t)runs * MOE_NUM_TENSORS;
-}
-
 __global__ __launch_bounds__(64) void k_slot_step(SlotTable* __restrict__ t, const uint32_t* __restrict__ ids,
                                                   int k, uint32_t* __restrict__ slot_inds) {
-    __shared__ LdsTable L;
-    const int lane = threadIdx.x;
-    load_table(t, L, lane);
-    uint32_t clock = t->clock;
-    int n_free = t->n_free;
-    renorm(t, L, lane, clock);
-
-    int e = -1;
-    bool bad = false;
-    if (lane < k) {
-        uint32_t v = ids[lane];
-        bad = v >= MOE_NUM_EXPERTS;
-        e = bad ? -1 : (int)v;
-    }
-    if (__any(bad)) {                      // reject: leave the table untouched
-        if (lane == 0) { t->status = 1; t->n_copy = 0; }
-        return;
-    }
-    if (lane < k) L.list_s[lane] = e;
-    __syncthreads();
-    bool dup = false;
-    for (int q = 0; q < lane && lane < k; ++q) dup |= (L.list_s[q] == e);
-    if (__any(dup)) {                      // repeated id: reject, table untouched
-        if (lane == 0) { t->status = 2; t->n_copy = 0; }
-        return;
-    }
-    if (e >= 0) atomicOr(&L.protect[e >> 5], 1u << (e & 31));
-    __syncthreads();
-
-    const bool snap = t->snap_valid != 0;
-    if (lane == 0) t->stats[ST_DEC_REQ] += (uint64_t)k;
-    if (snap && lane < 16) {
-        // per 32-bit word of the bitmaps (the counters are sums of popcounts)
-        const uint32_t* sr = reinterpret_cast<const uint32_t*>(t->snap_resident);
-        const uint32_t* sp = reinterpret_cast<const uint32_t*>(t->snap_pred);
-        const uint32_t* sf = reinterpret_cast<const uint32_t*>(t->snap_fetched);
-        uint32_t want = L.protect[lane], before_missing = want & ~sr[lane];
-        uint32_t c0 = __popc(want & sp[lane]), c1 = __popc(want), c2 = __popc(sp[lane]);
-        uint32_t c3 = __popc(before_missing & sf[lane]), c4 = __popc(before_missing), c5 = __popc(sf[lane]);
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) {
-            c0 += __shfl_xor(c0, o, 16); c1 += __shfl_xor(c1, o, 16); c2 += __shfl_xor(c2, o, 16);
-            c3 += __shfl_xor(c3, o, 16); c4 += __shfl_xor(c4, o, 16); c5 += __shfl_xor(c5, o, 16);
-        }
-        if (lane == 0) {
-            t->stats[ST_PRED_HITS] += c0; t->stats[ST_PRED_ACTUAL] += c1; t->stats[ST_PRED_TOTAL] += c2;
-            t->stats[ST_MISS_PREF_HITS] += c3; t->stats[ST_MISS_ACTUAL] += c4; t->stats[ST_MISS_FETCHED] += c5;
-        }
-    }
-
-    // classify in id order
-    const bool resident = (e >= 0) && L.slot_of[e] >= 0;
-    const bool miss = (e >= 0) && !resident;
-    bool lru_hit = false;
-    if (resident) {
-        const uint32_t* sr = reinterpret_cast<const uint32_t*>(t->snap_resident);
-        lru_hit = !snap || ((sr[e >> 5] >> (e & 31)) & 1u);
-    }
-    const uint64_t miss_mask = __ballot(miss);
-    const int n_miss = __popcll(miss_mask);
-    const int n_lru = __popcll(__ballot(lru_hit));
-    const int n_pref = __popcll(__ballot(resident && !lru_hit));
-    if (lane == 0) {
-        t->stats[ST_DEC_LRU_HIT] += n_lru;
-        t->stats[ST_DEC_PREF_HIT] += n_pref;
-        t->stats[ST_DEC_MISS] += n_miss;
-        t->snap_valid = 0;
-    }
-    if (miss) {
-        int rank = __popcll(miss_mask & ((1ull << lane) - 1));
-        L.list_e[rank] = e;
-    }
-    __syncthreads();
-
-    for (int r = 0; r < n_miss; ++r) {
-        int me = L.list_e[r];
-        int s = take_slot(t, L, lane, n_free, L.protect);
-        bind(L, lane, me, s, clock);
-        if (lane == 0) L.list_s[r] = s;
-    }
-    __syncthreads();
-    if (lane < n_miss) {
-        t->copy_eid[lane] = L.list_e[lane];
-        t->copy_slot[lane] = L.list_s[lane];
-    }
-    __syncthreads();
-
-    // refresh every id in order; for a repeated id only its last occurrence counts
-    if (e >= 0) {                          // ids are distinct: refresh in id order
-        int my_slot = L.slot_of[e];
-        if (my_slot >= 0) L.stamp[my_slot] = clock + 1 + lane;
-        slot_inds[lane] = (uint32_t)my_slot;
-    }
-    clock += (uint32_t)k;
-    __syncthreads();
-
-    store_table(t, L, lane);
-    if (lane == 0) {
-        t->n_copy = n_miss;
-        t->clock = clock;
-        t->n_free = n_free;
-        t->status = 0;
-        t->stats[ST_DEC_BYTES] += (uint64_t)n_miss * t->expert_bytes;
-        count_runs(t, L.list_e, n_miss);
-    }
+    __shared__ slot_dev::LdsTable L;
+    slot_dev::dev_slot_step(t, L, ids, k, slot_inds, threadIdx.x);
 }
 
 __global__ __launch_bounds__(64) void k_slot_prefetch(SlotTable* __restrict__ t, const int32_t* __restrict__ preds,
                                                       int m, int max_fetch) {
-    __shared__ LdsTable L;
-    const int lane = threadIdx.x;
-    load_table(t, L, lane);
-    uint32_t clock = t->clock;
-    int n_free = t->n_free;
-    renorm(t, L, lane, clock);
-
-    // residency snapshot
-    for (int e = lane; e < MOE_NUM_EXPERTS; e += 64)
-        if (L.slot_of[e] >= 0) atomicOr(&L.resident[e >> 5], 1u << (e & 31));
-    __syncthreads();
-    if (lane == 0) {
-        int cap = (max_fetch > 0 && max_fetch < 32) ? max_fetch : 32;
-        int np = 0;
-        for (int i = 0; i < m; ++i) {
-            int e = preds[i];
-            if (e < 0 || e >= MOE_NUM_EXPERTS) continue;
-            L.pred[e >> 5] |= 1u << (e & 31);
-            L.protect[e >> 5] |= 1u << (e & 31);
-            if (L.slot_of[e] < 0 && np < cap) {
-                L.list_e[np++] = e;
-                L.fetched[e >> 5] |= 1u << (e & 31);
-            }
-        }
-        L.n_list = np;
-    }
-    __syncthreads();
-    const int np = L.n_list;
-    if (lane < 16) {
-        reinterpret_cast<uint32_t*>(t->snap_resident)[lane] = L.resident[lane];
-        reinterpret_cast<uint32_t*>(t->snap_pred)[lane] = L.pred[lane];
-        reinterpret_cast<uint32_t*>(t->snap_fetched)[lane] = L.fetched[lane];
-    }
-    int32_t order_e[MOE_MAX_PREFETCH];
-    for (int i = 0; i < np; ++i) order_e[i] = L.list_e[np - 1 - i];   // reverse rank order
-    __syncthreads();
-    for (int i = 0; i < np; ++i) {
-        int s = take_slot(t, L, lane, n_free, L.protect);
-        bind(L, lane, order_e[i], s, clock);
-        if (lane == 0) { L.list_e[i] = order_e[i]; L.list_s[i] = s; }
-    }
-    __syncthreads();
-    store_table(t, L, lane);
-    if (lane < np) {
-        t->pf_copy_eid[lane] = L.list_e[lane];
-        t->pf_copy_slot[lane] = L.list_s[lane];
-    }
-    if (lane == 0) {
-        t->snap_valid = 1;
-        t->pf_n_copy = np;
-        t->clock = clock;
-        t->n_free = n_free;
-        t->status = 0;
-        t->stats[ST_PREF_BYTES] += (uint64_t)np * t->expert_bytes;
-        count_runs(t, L.list_e, np);
-    }
+    __shared__ slot_dev::LdsTable L;
+    slot_dev::dev_slot_prefetch(t, L, preds, m, max_fetch, threadIdx.x);
 }
 
 // Copy the blobs listed in the table's copy list: store[eid] -> pool[slot].  blockIdx.y picks

@@ -69,6 +69,8 @@ SIGNATURES: dict[str, tuple] = {
     "c_layer_set_format": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     "c_layer_switch_glu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
     "c_layer_mark_read": (_c_int, [_c_int, _c_vp]),
+    "c_router_tables_dev": (_c_int, [_c_int, _c_int, _c_int, _c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_vp, _c_vp, _c_int,
+                                     _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "c_layer_grouped_switch_glu": (_c_int, [_c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_int, _c_vp,
                                             _c_vp, _c_vp]),
     "c_layer_set_device_mode": (_c_int, [_c_int, _c_int]),

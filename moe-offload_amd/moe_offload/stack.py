@@ -53,6 +53,8 @@ class StackConfig:
     stage_ctas: int = 2          # staging blocks per copied expert (enough to fill PCIe; more
                                  # only floods the L2 miss queues with slow host reads)
     resident: bool = False       # every layer's experts in HBM (no slot tables, no staging)
+    fused_tables: bool = True    # device mode: the router's last block runs the slot-table step
+                                 # and the next layer's prefetch (no separate table launches)
 
 
 def random_blobs(n_exp: int, hidden: int, inter: int, group: int, gen: torch.Generator, device,
@@ -163,11 +165,26 @@ class DecodeStack:
         return list(o)
 
     # ---- one token ---------------------------------------------------------------------------
-    def _router(self, l: int):
+    def _router(self, l: int, tables: bool = False):
         c = self.cfg
         wn = self.router_w[l + 1] if (c.prefetch and l + 1 < c.n_layers) else None
         x_in = self.xs[0] if l == 0 else None
         h_in = None if l == 0 else self.hs[l - 1]
+        if tables:
+            step_layer = self.cidx(l) if l >= 1 else -1
+            pf_layer = self.cidx(l + 1) if wn is not None else -1
+            rc = self.L.c_router_tables_dev(step_layer, pf_layer, c.prefetch_cap,
+                                            h_in.data_ptr() if h_in is not None else None,
+                                            self.norm_w[l - 1].data_ptr() if l > 0 else None, c.eps,
+                                            x_in.data_ptr() if x_in is not None else None,
+                                            self.xs[l].data_ptr() if l > 0 else None,
+                                            self.router_w[l].data_ptr(), wn.data_ptr() if wn is not None else None,
+                                            c.hidden, c.n_exp, c.top_k, c.top_m if wn is not None else 0,
+                                            self.router_ws[l].data_ptr(), self.ids[l].data_ptr(),
+                                            self.scores[l].data_ptr(), self.pred[l].data_ptr(),
+                                            torch.cuda.current_stream().cuda_stream)
+            _lib.check(rc, "router_tables")
+            return
         rc = self.L.moe_router(h_in.data_ptr() if h_in is not None else None,
                                self.norm_w[l - 1].data_ptr() if l > 0 else None, c.eps,
                                x_in.data_ptr() if x_in is not None else None,
@@ -217,6 +234,9 @@ class DecodeStack:
                 self._router(l)
                 self._glu(l)
                 continue
+            if c.fused_tables:
+                self._layer_fused(l, main)
+                continue
             self._router(l)
             if l >= 1:
                 if c.prefetch:
@@ -243,6 +263,26 @@ class DecodeStack:
             self._glu(l)
         _lib.check(self.L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
                                       c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), main.cuda_stream), "rmsnorm")
+
+    def _layer_fused(self, l: int, main):
+        """One layer of the device-driven token with the table work inside the router:
+        main: router + step(l) + prefetch table(l+1) -> [join prefetch copies(l)] ->
+        demand copies(l) -> gate/up -> down;  side: prefetch copies(l+1) after the demand
+        copies of layer l (demand first: they gate this layer's GEMV)."""
+        c = self.cfg
+        self._router(l, tables=True)
+        pf = c.prefetch and l + 1 < c.n_layers
+        if l >= 1:
+            if c.prefetch:
+                main.wait_event(self.ev_copy[l])
+            _lib.check(self.L.c_layer_stage_dev(self.cidx(l), 0, c.stage_ctas, main.cuda_stream), "stage_demand")
+        if pf:
+            self.ev_demand[l].record(main)
+            self.side.wait_event(self.ev_demand[l])
+            _lib.check(self.L.c_layer_stage_dev(self.cidx(l + 1), 1, c.stage_ctas, self.side.cuda_stream),
+                       "stage_prefetch")
+            self.ev_copy[l + 1].record(self.side)
+        self._glu(l)
 
     def decode_token_host(self):
         """Reference-shaped token: one device->host read of (ids, pred) per layer."""

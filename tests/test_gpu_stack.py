@@ -5,7 +5,9 @@
   router ids/scores/prediction exact, RMSNorm exact, SwitchGLU + residual within 1e-2 x RMS;
 * the per-layer id/prediction stream replayed through the oracle LRU in the reference's call
   order (prefetch(1) after layer 0, then step(l), prefetch(l+1); loader.py:920-977) gives the
-  same slots and counters as the library.
+  same slots and counters as the library;
+* the table work fused into the router and the separate table kernels agree; a graph replay
+  equals eager execution.
 """
 import numpy as np
 import pytest
@@ -20,9 +22,9 @@ pytestmark = pytest.mark.gpu
 N_LAYERS, N_TOK = 6, 12
 
 
-def run_stack(mode, layer_base, graph=False):
+def run_stack(mode, layer_base, graph=False, fused=True):
     from moe_offload.stack import DecodeStack, StackConfig
-    cfg = StackConfig(n_layers=N_LAYERS, seed=5, layer_base=layer_base)
+    cfg = StackConfig(n_layers=N_LAYERS, seed=5, layer_base=layer_base, fused_tables=fused)
     st = DecodeStack(cfg, mode=mode)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(99)
@@ -103,6 +105,21 @@ def test_slot_sequence_matches_oracle_lru(runs):
                 layers[l + 1].prefetch(r["pred"][l].tolist(), c.prefetch_cap)
     for l in range(1, N_LAYERS):
         assert layers[l].stats() == stats[l], l
+
+
+def test_separate_table_launches_match_fused(runs):
+    """The router with the table work in its last block and the separate step / prefetch
+    kernels take identical decisions."""
+    (_, d, ds), _ = runs
+    st, u, us = run_stack("device", 0, fused=False)
+    try:
+        for t in range(N_TOK):
+            assert np.array_equal(u[t]["xs"], d[t]["xs"]), f"token {t}"
+            for l in range(1, N_LAYERS):
+                assert np.array_equal(u[t]["slots"][l], d[t]["slots"][l]), (t, l)
+        assert us == ds
+    finally:
+        st.close()
 
 
 def test_graph_replay_matches_eager(runs):
