@@ -29,6 +29,9 @@ for p in (str(ROOT), str(ROOT / "moe-offload_amd")):
 
 METRIC = "MoE decode tok/s, 48L top-10/512 Q2 @20% cache; achieved HBM GB/s"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per k_q2_gate_up launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE, scaled by a
+# known-size copy (profiles/decode_gemv_traffic_pmc.md); a counter run cannot happen inside bench.
+GATE_UP_TRAFFIC_BYTES = 6_713_344
 
 
 def parse():
@@ -45,9 +48,10 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--extras", action="store_true", help="add per-kernel and cache details to the JSON line")
     ap.add_argument("--stage-ctas", type=int, default=2, help="staging blocks per copied expert")
-    ap.add_argument("--skip-resident", action="store_true", help="headline pass only (for sweeps)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill grouped-GEMM pass")
-    ap.add_argument("--prefill-only", action="store_true", help="run only the prefill pass and print it")
+    ap.add_argument("--only", choices=["headline", "resident", "prefill", "calib", "floor"], default=None,
+                    help="run one pass and print its own JSON line (for sweeps and profiling); "
+                         "calib runs the known-size copy kernel used to scale memory counters")
     return ap.parse_args()
 
 
@@ -233,6 +237,67 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
     return res
 
 
+def launch_floor(byte_counts, grids=(320, 640, 1280, 2560), reps=50):
+    """Fastest single launch that only streams B bytes from HBM (moe_calibrate_stream over a
+    512 MiB region, a fresh offset each launch so the reads miss the caches), best grid."""
+    import torch
+
+    from moe_offload import _lib
+    L = _lib.lib()
+    region = 512 << 20
+    buf = torch.ones(region // 4, dtype=torch.float32, device="cuda")
+    out = torch.zeros(1, dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream()
+    res = {}
+    for nb in byte_counts:
+        best = None
+        for grid in grids:
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for i in range(reps + 5):
+                off = ((i * nb) % (region - nb)) & ~255
+                if i >= 5:
+                    ev[i - 5][0].record(s)
+                _lib.check(L.moe_calibrate_stream(buf.data_ptr() + off, nb, grid, out.data_ptr(), s.cuda_stream),
+                           "calibrate_stream")
+                if i >= 5:
+                    ev[i - 5][1].record(s)
+            torch.cuda.synchronize()
+            us = sum(a.elapsed_time(b) for a, b in ev) / reps * 1e3
+            best = us if best is None or us < best else best
+        res[nb] = best
+    del buf
+    torch.cuda.empty_cache()
+    return res
+
+
+def resident_pass(args, cfg, gen, n_tok, xs=None):
+    """48 layers with every expert in HBM (no cache, no staging): the GEMV kernels' own roofline."""
+    import torch
+
+    from moe_offload import q2format
+    from moe_offload.stack import DecodeStack, StackConfig
+    if xs is None:
+        xs = torch.randn((n_tok, cfg.hidden), device="cuda", generator=gen).half()
+    rcfg = StackConfig(n_layers=args.layers, prefetch=False, resident=True)
+    rst = DecodeStack(rcfg, mode="device")
+    r_elapsed, _, _ = timed_tokens(rst, xs, args.warmup, args.steps, not args.no_graph)
+    res_k = kernel_timing(rst, xs, args.warmup, args.steps)
+    gu_avg, dn_avg = res_k["gate_up"]["avg_us"] / 1e6, res_k["down"]["avg_us"] / 1e6
+    o = q2format.blob_offsets(cfg.hidden, cfg.inter, cfg.group)
+    gu_bytes = cfg.top_k * 2 * ((o["down_codes"] - o["up_codes"]) + (o["up_sb"] - o["gate_sb"]))
+    dn_bytes = cfg.top_k * ((o["gate_sb"] - o["down_codes"]) + (o["bytes"] - o["down_sb"]))
+    routed = rst.routed_bytes_per_token()
+    rst.close()
+    del rst
+    torch.cuda.empty_cache()
+    return {"tok_s": round(args.steps / r_elapsed, 1), "ms_per_token": round(r_elapsed / args.steps * 1e3, 4),
+            "routed_gb_per_s": round(routed * args.steps / r_elapsed / 1e9, 1),
+            "routed_frac_of_peak": round(routed * args.steps / r_elapsed / 1e9 / HBM_PEAK_GBS, 4),
+            "kernels_us": {k: round(v["avg_us"], 3) for k, v in res_k.items() if v["launches"]},
+            "_gu_avg": gu_avg, "_dn_avg": dn_avg, "_gu_bytes": gu_bytes, "_dn_bytes": dn_bytes, "_kernels": res_k,
+            "_routed": routed, "_elapsed": r_elapsed}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -245,8 +310,22 @@ def main():
     from moe_offload.stack import DecodeStack, StackConfig
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
-    if args.prefill_only:
+    if args.only == "prefill":
         print(json.dumps({"prefill": prefill_pass()}), flush=True)
+        return
+    if args.only == "floor":
+        fl = launch_floor([3_276_800, 6_553_600, 9_830_400, 64 << 20])
+        print(json.dumps({"launch_floor_us": {str(k): round(v, 2) for k, v in fl.items()}}), flush=True)
+        return
+    if args.only == "calib":
+        nb = 64 << 20
+        a = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        b = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        for _ in range(10):
+            _lib.check(_lib.lib().moe_calibrate_copy(b.data_ptr(), a.data_ptr(), nb,
+                                                     torch.cuda.current_stream().cuda_stream), "calibrate_copy")
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes": nb, "launches": 10}), flush=True)
         return
     n_tok = args.warmup + args.steps
     gen = torch.Generator(device="cuda")
@@ -256,6 +335,10 @@ def main():
     # ---- headline: 20% cache, misses staged from the pinned host store ---------------------
     cfg = StackConfig(n_layers=args.layers, budget_pct=args.budget_pct, prefetch=not args.no_prefetch,
                       stage_ctas=args.stage_ctas)
+    if args.only == "resident":
+        res = resident_pass(args, cfg, gen, n_tok)
+        print(json.dumps({"resident": {k: v for k, v in res.items() if not k.startswith("_")}}), flush=True)
+        return
     t0 = time.perf_counter()
     st = DecodeStack(cfg, mode=args.mode)
     setup_s = time.perf_counter() - t0
@@ -270,7 +353,7 @@ def main():
     st.close()
     del st
     torch.cuda.empty_cache()
-    if args.skip_resident:
+    if args.only == "headline":
         print(json.dumps({"value": round(tok_s, 2), "stage_ctas": args.stage_ctas,
                           "staged_gb_per_s": round(staged / elapsed / 1e9, 2),
                           "headline_kernels_us": {k: round(v["avg_us"], 2) for k, v in (head_k or {}).items()
@@ -278,19 +361,13 @@ def main():
         return
 
     # ---- resident pass: every expert in HBM, the GEMV's own roofline -------------------------
-    rcfg = StackConfig(n_layers=args.layers, prefetch=False, resident=True)
-    rst = DecodeStack(rcfg, mode="device")
-    r_elapsed, _, _ = timed_tokens(rst, xs, args.warmup, args.steps, not args.no_graph)
-    res_k = kernel_timing(rst, xs, args.warmup, args.steps)
-    gu_avg, dn_avg = res_k["gate_up"]["avg_us"] / 1e6, res_k["down"]["avg_us"] / 1e6
-    o = q2format.blob_offsets(cfg.hidden, cfg.inter, cfg.group)
-    gu_bytes = cfg.top_k * 2 * ((o["down_codes"] - o["up_codes"]) + (o["up_sb"] - o["gate_sb"]))
-    dn_bytes = cfg.top_k * ((o["gate_sb"] - o["down_codes"]) + (o["bytes"] - o["down_sb"]))
+    res = resident_pass(args, cfg, gen, n_tok, xs)
+    gu_avg, dn_avg, gu_bytes, dn_bytes, res_k = res.pop("_gu_avg"), res.pop("_dn_avg"), res.pop("_gu_bytes"), \
+        res.pop("_dn_bytes"), res.pop("_kernels")
     gu_gbs = gu_bytes / gu_avg / 1e9
-    routed = rst.routed_bytes_per_token()
-    rst.close()
-    del rst
-    torch.cuda.empty_cache()
+    floor_us = launch_floor([gu_bytes])[gu_bytes]
+    routed = res.pop("_routed")
+    r_elapsed = res.pop("_elapsed")
 
     line = {
         "metric": METRIC,
@@ -312,20 +389,20 @@ def main():
                                f"batch 1, {args.steps} tokens",
                    "driver": args.mode + ("+graph" if use_graph else ""), "tokens": args.steps, "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
                      "kernel": "k_q2_gate_up", "measured_in": "resident pass (all experts in HBM), per-launch HIP events stamped at kernel begin/end",
-                     "bytes_per_launch": gu_bytes, "avg_launch_us": round(gu_avg * 1e6, 3)},
+                     "bytes_per_launch": gu_bytes, "avg_launch_us": round(gu_avg * 1e6, 3),
+                     "launch_floor_us": round(floor_us, 3),
+                     "frac_of_launch_floor": round(floor_us / (gu_avg * 1e6), 4)},
         "cache": {"effective_hit_rate": round((tot1[0] - tot0[0] + tot1[1] - tot0[1]) / req, 4),
                   "pure_lru_hit_rate": round((tot1[0] - tot0[0]) / req, 4),
                   "staged_mb_per_token": round(staged / args.steps / 1e6, 2),
                   "staged_gb_per_s": round(staged / elapsed / 1e9, 2)},
-        "resident": {"tok_s": round(args.steps / r_elapsed, 1), "ms_per_token": round(r_elapsed / args.steps * 1e3, 4),
-                     "routed_gb_per_s": round(routed * args.steps / r_elapsed / 1e9, 1),
-                     "routed_frac_of_peak": round(routed * args.steps / r_elapsed / 1e9 / HBM_PEAK_GBS, 4)},
+        "resident": {k: v for k, v in res.items() if k != "kernels_us"},
     }
     if args.extras:
         line["extras"] = {"setup_s": round(setup_s, 1),
-                          "resident_kernels_us": {k: round(v["avg_us"], 3) for k, v in res_k.items() if v["launches"]},
+                          "resident_kernels_us": res["kernels_us"],
                           "headline_kernels_us": {k: round(v["avg_us"], 3) for k, v in head_k.items() if v["launches"]},
                           "down_avg_launch_us": round(dn_avg * 1e6, 3),
                           "down_gbs": round(dn_bytes / dn_avg / 1e9, 1),

@@ -203,6 +203,12 @@ int c_sync_copies(void);
 #define MOE_TIMING_KINDS 8
 int c_timing_begin(int capacity);
 int c_timing_end(double* out_ms, int* out_n);
+/* Plain device-to-device copy of `bytes` (multiple of 16): the known-size reference for scaling
+ * per-dispatch memory counters (FETCH_SIZE, WRITE_SIZE) to bytes. */
+int moe_calibrate_copy(void* dst, const void* src, uint64_t bytes, void* stream);
+/* Read-only streaming of `bytes` (multiple of 16) with `grid` blocks of 256 threads: the
+ * single-launch floor for a kernel of that many HBM bytes (out: 4-byte device scratch). */
+int moe_calibrate_stream(const void* src, uint64_t bytes, int grid, float* out, void* stream);
 int c_abi_version(void);
 
 #ifdef __cplusplus

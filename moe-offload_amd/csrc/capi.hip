@@ -767,6 +767,14 @@ int c_timing_end(double* out_ms, int* out_n) {
     return 0;
 }
 
+int moe_calibrate_copy(void* dst, const void* src, uint64_t bytes, void* stream) {
+    return launch_copy_calib(dst, src, (size_t)bytes, (hipStream_t)stream);
+}
+
+int moe_calibrate_stream(const void* src, uint64_t bytes, int grid, float* out, void* stream) {
+    return launch_stream_calib(src, (size_t)bytes, grid, out, (hipStream_t)stream);
+}
+
 int c_abi_version(void) { return 1; }
 
 }  // extern "C"

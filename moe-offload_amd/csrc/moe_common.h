@@ -144,6 +144,8 @@ int launch_slot_prefetch(SlotTable* t, const int32_t* preds, int m, int max_fetc
 int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t store_stride,
                  uint8_t* pool, size_t pool_stride, size_t bytes, int ctas, hipStream_t s);
 int launch_store_u32(uint32_t* dst, const uint32_t* vals, int n, hipStream_t s);
+int launch_copy_calib(void* dst, const void* src, size_t bytes, hipStream_t s);
+int launch_stream_calib(const void* src, size_t bytes, int grid, float* out, hipStream_t s);
 int launch_q2_grouped_gate_up(const __half* x, int n_tokens, const int32_t* row_token, int n_rows,
                               const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
                               const uint8_t* pool, size_t stride, int n_slots, int hidden, int inter,

@@ -53,6 +53,24 @@ __global__ __launch_bounds__(256) void k_stage(const SlotTable* __restrict__ t, 
     }
 }
 
+// Plain device copy of a known byte count: the reference reading for scaling memory counters
+// (FETCH_SIZE / WRITE_SIZE per dispatch) to bytes.
+__global__ __launch_bounds__(256) void k_copy_calib(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+// Streams `n16` 16-byte units and reduces them: the fastest a single launch reading that many
+// bytes from HBM can be (no dependent loads, no outputs), for comparing kernels of the same size.
+__global__ __launch_bounds__(256) void k_stream_calib(const uint4* __restrict__ src, size_t n16, float* __restrict__ out) {
+    float acc = 0.f;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x) {
+        const uint4 v = src[i];
+        acc += __uint_as_float(v.x & 0x3f800000u) + __uint_as_float(v.w & 0x3f800000u);
+    }
+    if (acc == -1.0f) out[0] = acc;                  // never true for the inputs used; keeps the loads
+}
+
 struct U32x16 { uint32_t v[16]; };
 
 __global__ void k_store_u32(uint32_t* dst, U32x16 vals, int n) {
@@ -90,6 +108,23 @@ int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t stor
     if (ctas <= 0) ctas = 2;
     MOE_LAUNCH(TK_STAGE, k_stage, dim3(ctas, MOE_MAX_PREFETCH), dim3(256), 0, s, t, list, store, store_stride,
                pool, pool_stride, bytes);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int launch_copy_calib(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    if (!dst || !src || bytes == 0 || bytes % 16) { moe_set_error("copy_calib: bytes must be a positive multiple of 16"); return -1; }
+    hipLaunchKernelGGL(k_copy_calib, dim3(1024), dim3(256), 0, s, (const uint4*)src, (uint4*)dst, bytes / 16);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int launch_stream_calib(const void* src, size_t bytes, int grid, float* out, hipStream_t s) {
+    if (!src || !out || bytes == 0 || bytes % 16 || grid <= 0) {
+        moe_set_error("stream_calib: bytes must be a positive multiple of 16, grid > 0");
+        return -1;
+    }
+    hipLaunchKernelGGL(k_stream_calib, dim3(grid), dim3(256), 0, s, (const uint4*)src, bytes / 16, out);
     HIP_TRY(hipGetLastError());
     return 0;
 }

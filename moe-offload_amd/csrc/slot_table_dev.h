@@ -22,6 +22,7 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 struct LdsTable {
+    uint64_t stats[18];        // the table's counters, written back once at the end
     int16_t slot_of[MOE_NUM_EXPERTS];
     int16_t eid_of[MOE_NUM_EXPERTS];
     uint32_t stamp[MOE_NUM_EXPERTS];
@@ -59,6 +60,7 @@ __device__ inline void load_table(const SlotTable* t, LdsTable& L, int lane) {
         L.fetched[lane] = 0;
     }
     if (lane == 0) L.n_list = 0;
+    if (lane < 18) L.stats[lane] = t->stats[lane];
     wave_sync();
 }
 
@@ -146,7 +148,7 @@ __device__ inline void bind(LdsTable& L, int lane, int e, int s, uint32_t& clock
     wave_sync();
 }
 
-__device__ inline void count_runs(SlotTable* t, const int32_t* e, int n) {
+__device__ inline void count_runs(LdsTable& L, const int32_t* e, int n) {
     if (n <= 0) return;
     int32_t v[MOE_MAX_PREFETCH];
     for (int i = 0; i < n; ++i) v[i] = e[i];
@@ -158,8 +160,8 @@ __device__ inline void count_runs(SlotTable* t, const int32_t* e, int n) {
     }
     int runs = 1;
     for (int i = 1; i < n; ++i) runs += (v[i] != v[i - 1] + 1);
-    t->stats[ST_UNCOAL] += (uint64_t)n * MOE_NUM_TENSORS;
-    t->stats[ST_COAL] += (uint64_t)runs * MOE_NUM_TENSORS;
+    L.stats[ST_UNCOAL] += (uint64_t)n * MOE_NUM_TENSORS;
+    L.stats[ST_COAL] += (uint64_t)runs * MOE_NUM_TENSORS;
 }
 
 // Decode step of expert_io.c:583-685 for k ids (one wave; ids may live in LDS or global memory).
@@ -193,7 +195,7 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
     wave_sync();
 
     const bool snap = t->snap_valid != 0;
-    if (lane == 0) t->stats[ST_DEC_REQ] += (uint64_t)k;
+    if (lane == 0) L.stats[ST_DEC_REQ] += (uint64_t)k;
     if (snap && lane < 16) {
         // per 32-bit word of the bitmaps (the counters are sums of popcounts)
         const uint32_t* sr = reinterpret_cast<const uint32_t*>(t->snap_resident);
@@ -208,8 +210,8 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
             c3 += __shfl_xor(c3, o, 16); c4 += __shfl_xor(c4, o, 16); c5 += __shfl_xor(c5, o, 16);
         }
         if (lane == 0) {
-            t->stats[ST_PRED_HITS] += c0; t->stats[ST_PRED_ACTUAL] += c1; t->stats[ST_PRED_TOTAL] += c2;
-            t->stats[ST_MISS_PREF_HITS] += c3; t->stats[ST_MISS_ACTUAL] += c4; t->stats[ST_MISS_FETCHED] += c5;
+            L.stats[ST_PRED_HITS] += c0; L.stats[ST_PRED_ACTUAL] += c1; L.stats[ST_PRED_TOTAL] += c2;
+            L.stats[ST_MISS_PREF_HITS] += c3; L.stats[ST_MISS_ACTUAL] += c4; L.stats[ST_MISS_FETCHED] += c5;
         }
     }
 
@@ -226,9 +228,9 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
     const int n_lru = __popcll(__ballot(lru_hit));
     const int n_pref = __popcll(__ballot(resident && !lru_hit));
     if (lane == 0) {
-        t->stats[ST_DEC_LRU_HIT] += n_lru;
-        t->stats[ST_DEC_PREF_HIT] += n_pref;
-        t->stats[ST_DEC_MISS] += n_miss;
+        L.stats[ST_DEC_LRU_HIT] += n_lru;
+        L.stats[ST_DEC_PREF_HIT] += n_pref;
+        L.stats[ST_DEC_MISS] += n_miss;
         t->snap_valid = 0;
     }
     if (miss) {
@@ -265,9 +267,11 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
         t->clock = clock;
         t->n_free = n_free;
         t->status = 0;
-        t->stats[ST_DEC_BYTES] += (uint64_t)n_miss * t->expert_bytes;
-        count_runs(t, L.list_e, n_miss);
+        L.stats[ST_DEC_BYTES] += (uint64_t)n_miss * t->expert_bytes;
+        count_runs(L, L.list_e, n_miss);
     }
+    wave_sync();
+    if (lane < 18) t->stats[lane] = L.stats[lane];
 }
 
 // Prefetch of expert_io.c:527-581 for m predictions (one wave).
@@ -324,9 +328,11 @@ __device__ inline void dev_slot_prefetch(SlotTable* __restrict__ t, LdsTable& L,
         t->clock = clock;
         t->n_free = n_free;
         t->status = 0;
-        t->stats[ST_PREF_BYTES] += (uint64_t)np * t->expert_bytes;
-        count_runs(t, L.list_e, np);
+        L.stats[ST_PREF_BYTES] += (uint64_t)np * t->expert_bytes;
+        count_runs(L, L.list_e, np);
     }
+    wave_sync();
+    if (lane < 18) t->stats[lane] = L.stats[lane];
 }
 
 }  // namespace slot_dev

@@ -82,6 +82,8 @@ SIGNATURES: dict[str, tuple] = {
     "c_sync_copies": (_c_int, []),
     "c_timing_begin": (_c_int, [_c_int]),
     "c_timing_end": (_c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),
+    "moe_calibrate_copy": (_c_int, [_c_vp, _c_vp, _c_u64, _c_vp]),
+    "moe_calibrate_stream": (_c_int, [_c_vp, _c_u64, _c_int, _c_vp, _c_vp]),
     "c_abi_version": (_c_int, []),
 }
 
