@@ -108,15 +108,41 @@ class HostExpertStore:
         self._ptr.clear()
 
 
+class FileExpertStore:
+    """The on-disk tier: one expert blob file per layer (q2format.write_blob_file).  Misses are
+    read with pread into a pinned bounce buffer and copied to HBM (expert_io.c:113-185 reads the
+    reference's safetensors shard the same way, one row per tensor)."""
+
+    def __init__(self, paths: dict[int, str]):
+        import os
+        self.paths = dict(paths)
+        self.fds: dict[int, int] = {}
+        self.headers: dict[int, dict] = {}
+        for l, p in self.paths.items():
+            self.headers[l] = q2format.read_blob_header(p)
+            self.fds[l] = os.open(p, os.O_RDONLY)
+        bb = {h["blob_bytes"] for h in self.headers.values()}
+        if len(bb) != 1:
+            raise ValueError("layers of one store must share the blob size")
+        self.blob_bytes = bb.pop()
+
+    def close(self):
+        import os
+        for fd in self.fds.values():
+            os.close(fd)
+        self.fds.clear()
+
+
 class CachedSwitchGLU:
     """Per-layer slot cache over an HBM pool + Q2 SwitchGLU (loader.py:306-749).
 
-    `store` is a HostExpertStore (fd == -1 path); the pool holds `capacity` blobs.
+    `store` is a HostExpertStore (pinned host memory, fd == -1) or a FileExpertStore (the on-disk
+    tier, fd >= 0); the pool holds `capacity` blobs.
     decode: __call__(x [1,1,H] fp16, indices [1,1,k]) -> per-expert outputs [1,1,k,H], exactly
     like SwitchGLU; forward_combined() returns the score-weighted sum directly.
     """
 
-    def __init__(self, store: HostExpertStore, layer_idx: int, capacity: int, hidden: int = 2048,
+    def __init__(self, store: "HostExpertStore | FileExpertStore", layer_idx: int, capacity: int, hidden: int = 2048,
                  inter: int = 512, group: int = 64, device: str | torch.device = "cuda"):
         self.layer_idx, self.capacity = layer_idx, capacity
         self.hidden, self.inter, self.group = hidden, inter, group
@@ -130,7 +156,11 @@ class CachedSwitchGLU:
         L = _lib.lib()
         L.c_set_compute_stream(ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
         u64 = ctypes.c_uint64 * 9
-        L.c_layer_init(layer_idx, -1, capacity, u64(store.layer_ptr(layer_idx), *[0] * 8),
+        if isinstance(store, FileExpertStore):
+            fd, base = store.fds[layer_idx], store.headers[layer_idx]["data_offset"]
+        else:
+            fd, base = -1, store.layer_ptr(layer_idx)
+        L.c_layer_init(layer_idx, fd, capacity, u64(base, *[0] * 8),
                        u64(self.blob_bytes, *[0] * 8), u64(self.pool.data_ptr(), *[0] * 8),
                        self._slot_inds_buf.data_ptr())
         _lib.check_error("c_layer_init")
