@@ -47,8 +47,7 @@ def parse():
     ap.add_argument("--cpu-sample-s", type=float, default=15.0, help="CPU baseline time budget (seconds)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--extras", action="store_true", help="add per-kernel and cache details to the JSON line")
-    ap.add_argument("--stage-ctas", type=int, default=2, help="staging blocks per prefetched expert")
-    ap.add_argument("--demand-ctas", type=int, default=2, help="staging blocks per demand-missed expert")
+    ap.add_argument("--stage-ctas", type=int, default=2, help="staging blocks per copied expert")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill grouped-GEMM pass")
     ap.add_argument("--only", choices=["headline", "resident", "prefill", "calib", "floor"], default=None,
                     help="run one pass and print its own JSON line (for sweeps and profiling); "
@@ -335,7 +334,7 @@ def main():
 
     # ---- headline: 20% cache, misses staged from the pinned host store ---------------------
     cfg = StackConfig(n_layers=args.layers, budget_pct=args.budget_pct, prefetch=not args.no_prefetch,
-                      stage_ctas=args.stage_ctas, demand_ctas=args.demand_ctas)
+                      stage_ctas=args.stage_ctas)
     if args.only == "resident":
         res = resident_pass(args, cfg, gen, n_tok)
         print(json.dumps({"resident": {k: v for k, v in res.items() if not k.startswith("_")}}), flush=True)
@@ -355,7 +354,7 @@ def main():
     del st
     torch.cuda.empty_cache()
     if args.only == "headline":
-        print(json.dumps({"value": round(tok_s, 2), "stage_ctas": args.stage_ctas, "demand_ctas": args.demand_ctas,
+        print(json.dumps({"value": round(tok_s, 2), "stage_ctas": args.stage_ctas,
                           "staged_gb_per_s": round(staged / elapsed / 1e9, 2),
                           "headline_kernels_us": {k: round(v["avg_us"], 2) for k, v in (head_k or {}).items()
                                                   if v["launches"]}}), flush=True)

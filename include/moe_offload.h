@@ -185,21 +185,7 @@ int c_layer_start_prefetch_dev(int layer_idx, const int32_t* preds_dev, int m, i
 int c_router_tables_dev(int step_layer, int pf_layer, int max_fetch, const float* h_in,
                         const void* norm_w, float eps, const void* x_in, void* x_out, const void* w,
                         const void* w_next, int hidden, int n_exp, int k, int m, void* workspace,
-                        uint32_t* ids_out, void* scores_out, int32_t* pred_out, void* sync,
-                        void* stream);
-/* Device-side handshakes of the staged decode (sync may be null above: no flag published).
- * `sync` is moe_stage_sync_bytes() of zeroed device memory shared by one stack of layers.
- * A token starts with c_token_begin; with sync, c_router_tables_dev marks the prefetch list of
- * pf_layer ready, and c_layer_stage_dev_sync waits for the flags in wait_mask (1 = this layer's
- * prefetch list ready, 2 = the previous layer's demand copies landed, 4 = this layer's
- * prefetch copies landed) before copying, then marks its own copies landed; max_copies bounds
- * the list (the decode step's k, or the prefetch cap: a longer list is not fully copied).  Every wait is
- * bounded; one that gives up records the layer in the sync block's error word (offset 4) and
- * continues. */
-uint64_t moe_stage_sync_bytes(void);
-int c_token_begin(void* sync, void* stream);
-int c_layer_stage_dev_sync(int layer_idx, int list, int stage_ctas, void* sync, int wait_mask,
-                           int max_copies, void* stream);
+                        uint32_t* ids_out, void* scores_out, int32_t* pred_out, void* stream);
 /* Queue the copies of the layer's last device-side decode step (list 0) or prefetch (list 1)
  * on `stream` (the two lists are kept apart so a step may run while prefetch copies queue). */
 int c_layer_stage_dev(int layer_idx, int list, int stage_ctas, void* stream);

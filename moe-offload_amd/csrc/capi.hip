@@ -482,21 +482,11 @@ uint64_t c_layer_device_table(int layer) {
     return (uint64_t)g_layers[layer].dtab;
 }
 
-static int stage_device(LayerState& L, int list, hipStream_t s, int ctas, StageSync* sync = nullptr, int layer = -1,
-                        int wait_mask = 0, int max_copies = MOE_MAX_PREFETCH) {
-    int n_staged = 0;
-    for (int t = 0; t < MOE_NUM_TENSORS; ++t) n_staged += (L.row_bytes[t] && L.dev_src[t] && L.dst[t]) ? 1 : 0;
-    if (sync && n_staged != 1) {
-        moe_set_error("stage_dev_sync: layer %d stages %d tensors (the flag handshake needs one blob tensor)", layer,
-                      n_staged);
-        return -1;
-    }
+static int stage_device(LayerState& L, int list, hipStream_t s, int ctas) {
     for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
         uint64_t rb = L.row_bytes[t];
         if (!rb || !L.dev_src[t] || !L.dst[t]) continue;
-        if (launch_stage(L.dtab, list, (const uint8_t*)L.dev_src[t], rb, (uint8_t*)L.dst[t], rb, rb, ctas, s, sync,
-                         layer, wait_mask, max_copies))
-            return -1;
+        if (launch_stage(L.dtab, list, (const uint8_t*)L.dev_src[t], rb, (uint8_t*)L.dst[t], rb, rb, ctas, s)) return -1;
     }
     return 0;
 }
@@ -537,28 +527,6 @@ int c_layer_stage_dev(int layer, int list, int stage_ctas, void* stream) {
     return stage_device(g_layers[layer], list, (hipStream_t)stream, stage_ctas < 0 ? 0 : stage_ctas);
 }
 
-// As c_layer_stage_dev, ordered by device-side flags instead of stream events: the launch
-// waits for the flags in wait_mask (SYNC_WAIT_*) and publishes this list's done flag.
-int c_layer_stage_dev_sync(int layer, int list, int stage_ctas, void* sync, int wait_mask, int max_copies,
-                           void* stream) {
-    if (!valid_layer(layer) || !g_layers[layer].init || !g_layers[layer].device_mode) {
-        moe_set_error("stage_dev_sync: layer %d is not a device-driven layer", layer);
-        return -1;
-    }
-    if (list != 0 && list != 1) { moe_set_error("stage_dev_sync: list %d (0 = decode step, 1 = prefetch)", list); return -1; }
-    if (!sync) { moe_set_error("stage_dev_sync: null sync"); return -1; }
-    if (max_copies <= 0 || max_copies > MOE_MAX_PREFETCH) {
-        moe_set_error("stage_dev_sync: max_copies %d out of range", max_copies);
-        return -1;
-    }
-    return stage_device(g_layers[layer], list, (hipStream_t)stream, stage_ctas < 0 ? 0 : stage_ctas, (StageSync*)sync,
-                        layer, wait_mask, max_copies);
-}
-
-uint64_t moe_stage_sync_bytes(void) { return sizeof(StageSync); }
-
-int c_token_begin(void* sync, void* stream) { return launch_token_begin((StageSync*)sync, (hipStream_t)stream); }
-
 int c_layer_table_status(int layer) {
     if (!valid_layer(layer)) return -1;
     LayerState& L = g_layers[layer];
@@ -586,8 +554,7 @@ int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_i
 // c_layer_step_decode_dev + c_layer_start_prefetch_dev after moe_router.
 int c_router_tables_dev(int step_layer, int pf_layer, int max_fetch, const float* h_in, const void* norm_w, float eps,
                         const void* x_in, void* x_out, const void* w, const void* w_next, int hidden, int n_exp, int k,
-                        int m, void* workspace, uint32_t* ids_out, void* scores_out, int32_t* pred_out, void* sync,
-                        void* stream) {
+                        int m, void* workspace, uint32_t* ids_out, void* scores_out, int32_t* pred_out, void* stream) {
     SlotTable* st = nullptr;
     SlotTable* pt = nullptr;
     uint32_t* slots = nullptr;
@@ -617,8 +584,7 @@ int c_router_tables_dev(int step_layer, int pf_layer, int max_fetch, const float
     unsigned* counter = (unsigned*)((uint8_t*)workspace + (size_t)(2 * n_exp) * sizeof(float));
     return launch_router(h_in, (const __half*)norm_w, eps, (const __half*)x_in, (__half*)x_out,
                          (const __half*)w, (const __half*)w_next, hidden, n_exp, k, m, scratch, counter,
-                         ids_out, (__half*)scores_out, pred_out, st, slots, pt, max_fetch, (hipStream_t)stream,
-                         (StageSync*)sync, pf_layer);
+                         ids_out, (__half*)scores_out, pred_out, st, slots, pt, max_fetch, (hipStream_t)stream);
 }
 
 int moe_f64_to_f16(const double* in, uint16_t* out, int n, void* stream) {

@@ -81,44 +81,6 @@ struct SlotTable {
     int32_t status;                     // 0 ok; nonzero: rejected input (device kernels)
 };
 
-// Device-side handshakes of the staged decode (one per stack of layers; zero-initialised).
-// Flags hold the sequence number of the token that last set them; a token begins by
-// incrementing `seq`.  Indexed by C-ABI layer.
-//   pf_ready[l]  the prefetch copy list of layer l is written (router of the layer before)
-//   pf_done[l]   the prefetch copies of layer l have landed (prefetch staging)
-//   dm_done[l]   the demand copies of layer l have landed (demand staging)
-// Waits are bounded: a wait that gives up sets `err` (the layer | 0x80000000 of the first
-// failure) and continues, so no kernel can hang on a flag.
-struct StageSync {
-    uint32_t seq;
-    uint32_t err;
-    uint32_t pad[30];
-    uint32_t pf_ready[MOE_MAX_LAYERS];
-    uint32_t pf_done[MOE_MAX_LAYERS];
-    uint32_t dm_done[MOE_MAX_LAYERS];
-    uint32_t cnt[2][MOE_MAX_LAYERS];   // completion counters of the staging launches (list 0 / 1)
-};
-enum { SYNC_WAIT_PF_READY = 1, SYNC_WAIT_PREV_DM_DONE = 2, SYNC_WAIT_PF_DONE = 4 };
-
-// Bounded wait (2^18 polls, a fraction of a second) until *flag reaches `want`.  Polls with
-// relaxed agent-scope loads (coherent across XCDs, no cache maintenance) and acquires once when
-// the flag is seen: an acquire per poll would invalidate this XCD's L2 at the polling rate.
-__device__ inline bool sync_wait(const uint32_t* flag, uint32_t want) {
-    for (uint32_t i = 0; i < (1u << 18); ++i) {
-        const uint32_t v = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((int32_t)(v - want) >= 0) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            return true;
-        }
-        __builtin_amdgcn_s_sleep(8);               // ~500 cycles between polls
-    }
-    return false;
-}
-
-__device__ inline void sync_fail(StageSync* s, int layer) {
-    atomicCAS(&s->err, 0u, (uint32_t)layer | 0x80000000u);
-}
-
 // Stats word indices (same order as c_layer_get_stats, expert_io.c:791-812).
 enum {
     ST_DEC_REQ = 0, ST_DEC_LRU_HIT, ST_DEC_PREF_HIT, ST_DEC_MISS, ST_DEC_BYTES, ST_PREF_BYTES,
@@ -164,8 +126,7 @@ int launch_router(const float* h_in, const __half* norm_w, float eps, const __ha
                   __half* x_out, const __half* w, const __half* w_next, int hidden, int n_exp,
                   int k, int m, float* scratch, unsigned* counter, uint32_t* ids_out,
                   __half* scores_out, int32_t* pred_out, SlotTable* step_tab, uint32_t* slot_inds,
-                  SlotTable* pf_tab, int max_fetch, hipStream_t s, StageSync* sync = nullptr,
-                  int pf_layer = -1);
+                  SlotTable* pf_tab, int max_fetch, hipStream_t s);
 int launch_f64_to_f16(const double* in, uint16_t* out, int n, hipStream_t s);
 int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidden, __half* x_out,
                    hipStream_t s);
@@ -181,10 +142,7 @@ int launch_slot_step(SlotTable* t, const uint32_t* ids, int k, uint32_t* slot_in
 int launch_slot_prefetch(SlotTable* t, const int32_t* preds, int m, int max_fetch,
                          hipStream_t s);
 int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t store_stride,
-                 uint8_t* pool, size_t pool_stride, size_t bytes, int ctas, hipStream_t s,
-                 StageSync* sync = nullptr, int layer = -1, int wait_mask = 0,
-                 int max_copies = MOE_MAX_PREFETCH);
-int launch_token_begin(StageSync* sync, hipStream_t s);
+                 uint8_t* pool, size_t pool_stride, size_t bytes, int ctas, hipStream_t s);
 int launch_store_u32(uint32_t* dst, const uint32_t* vals, int n, hipStream_t s);
 int launch_copy_calib(void* dst, const void* src, size_t bytes, hipStream_t s);
 int launch_stream_calib(const void* src, size_t bytes, int grid, float* out, hipStream_t s);

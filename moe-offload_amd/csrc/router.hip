@@ -109,8 +109,7 @@ __global__ __launch_bounds__(kThreads) void k_router(
     int hidden, int n_exp, int k, int m,
     float* __restrict__ scratch, unsigned* __restrict__ counter,
     uint32_t* __restrict__ ids_out, __half* __restrict__ scores_out, int32_t* __restrict__ pred_out,
-    SlotTable* __restrict__ step_tab, uint32_t* __restrict__ slot_inds, SlotTable* __restrict__ pf_tab, int max_fetch,
-    StageSync* __restrict__ sync, int pf_layer) {
+    SlotTable* __restrict__ step_tab, uint32_t* __restrict__ slot_inds, SlotTable* __restrict__ pf_tab, int max_fetch) {
     __shared__ __align__(16) uint16_t xs[kMaxHidden];
     __shared__ double red[kThreads / 64];
     __shared__ int is_last;
@@ -284,15 +283,6 @@ __global__ __launch_bounds__(kThreads) void k_router(
         __syncthreads();
         if (wv == 0 && step_tab) slot_dev::dev_slot_step(step_tab, tabs[0], sel_ids, k, slot_inds, lane);
         if (wv == 1 && pf_tab && w_next && m > 0) slot_dev::dev_slot_prefetch(pf_tab, tabs[1], sel_pred, m, max_fetch, lane);
-        if (sync && pf_tab && pf_layer >= 0) {
-            // the prefetch list of pf_layer is complete: publish it to the staging launch
-            __threadfence();
-            __syncthreads();
-            if (tid == 0)
-                __hip_atomic_store(&sync->pf_ready[pf_layer],
-                                   __hip_atomic_load(&sync->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                                   __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        }
     }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -331,11 +321,7 @@ int launch_router(const float* h_in, const __half* norm_w, float eps, const __ha
                   __half* x_out, const __half* w, const __half* w_next, int hidden, int n_exp,
                   int k, int m, float* scratch, unsigned* counter, uint32_t* ids_out,
                   __half* scores_out, int32_t* pred_out, SlotTable* step_tab, uint32_t* slot_inds,
-                  SlotTable* pf_tab, int max_fetch, hipStream_t s, StageSync* sync, int pf_layer) {
-    if (sync && pf_tab && (pf_layer < 0 || pf_layer >= MOE_MAX_LAYERS)) {
-        moe_set_error("router: pf_layer %d out of range", pf_layer);
-        return -1;
-    }
+                  SlotTable* pf_tab, int max_fetch, hipStream_t s) {
     if (hidden <= 0 || hidden > kMaxHidden || hidden % 8 != 0) {
         moe_set_error("router: hidden=%d unsupported (multiple of 8, <= %d)", hidden, kMaxHidden);
         return -1;
@@ -357,7 +343,7 @@ int launch_router(const float* h_in, const __half* norm_w, float eps, const __ha
     int grid = (rows + kRowsPerBlock - 1) / kRowsPerBlock;      // one row per wave
     MOE_LAUNCH(TK_ROUTER, k_router, dim3(grid), dim3(kThreads), 0, s, h_in, norm_w, eps, x_in, x_out,
                        w, w_next, hidden, n_exp, k, w_next ? m : 0, scratch, counter, ids_out,
-                       scores_out, pred_out, step_tab, slot_inds, pf_tab, max_fetch, sync, pf_layer);
+                       scores_out, pred_out, step_tab, slot_inds, pf_tab, max_fetch);
     HIP_TRY(hipGetLastError());
     return 0;
 }

@@ -25,74 +25,32 @@ __global__ __launch_bounds__(64) void k_slot_prefetch(SlotTable* __restrict__ t,
 // the copy, blockIdx.x strides over its 16-byte units, four in flight per thread; the store is
 // pinned host memory read over PCIe (a kernel copy sustains the link rate with blob-sized
 // pieces, where one DMA request per blob does not).
-//
-// With `sync`, the launch first waits (thread 0 of every block, bounded) for the flags named by
-// wait_mask, and the last block to finish publishes this list's done flag for `layer`, after
-// every block has written its copies back at agent scope.
 __global__ __launch_bounds__(256) void k_stage(const SlotTable* __restrict__ t, int list,
                                                const uint8_t* __restrict__ store, size_t store_stride,
-                                               uint8_t* __restrict__ pool, size_t pool_stride, size_t bytes,
-                                               StageSync* __restrict__ sync, int layer, int wait_mask) {
-    __shared__ uint32_t want_s;
-    uint32_t want = 0;
-    if (sync) {
-        if (threadIdx.x == 0) {
-            want = __hip_atomic_load(&sync->seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            bool ok = true;
-            if (wait_mask & SYNC_WAIT_PF_READY) ok = sync_wait(&sync->pf_ready[layer], want) && ok;
-            if ((wait_mask & SYNC_WAIT_PREV_DM_DONE) && layer > 0) ok = sync_wait(&sync->dm_done[layer - 1], want) && ok;
-            if (wait_mask & SYNC_WAIT_PF_DONE) ok = sync_wait(&sync->pf_done[layer], want) && ok;
-            if (!ok) sync_fail(sync, layer);
-            want_s = want;
-        }
-        __syncthreads();
-        want = want_s;
-    }
+                                               uint8_t* __restrict__ pool, size_t pool_stride, size_t bytes) {
     const int c = blockIdx.y;
     const int n = list ? t->pf_n_copy : t->n_copy;
-    bool active = c < min(n, MOE_MAX_PREFETCH);
-    int eid = 0, slot = 0;
-    if (active) {
-        eid = list ? t->pf_copy_eid[c] : t->copy_eid[c];
-        slot = list ? t->pf_copy_slot[c] : t->copy_slot[c];
-        active = eid >= 0 && eid < MOE_NUM_EXPERTS && slot >= 0 && slot < t->capacity;
+    if (c >= min(n, MOE_MAX_PREFETCH)) return;
+    const int eid = list ? t->pf_copy_eid[c] : t->copy_eid[c];
+    const int slot = list ? t->pf_copy_slot[c] : t->copy_slot[c];
+    if (eid < 0 || eid >= MOE_NUM_EXPERTS || slot < 0 || slot >= t->capacity) return;
+    const uint4* src = reinterpret_cast<const uint4*>(store + (size_t)eid * store_stride);
+    uint4* dst = reinterpret_cast<uint4*>(pool + (size_t)slot * pool_stride);
+    const unsigned units = (unsigned)(bytes / 16);
+    const unsigned step = gridDim.x * blockDim.x;
+    // Four independent 16-byte loads in flight per thread, held in named registers (an array
+    // here gets moved to LDS by the compiler, which serialises the loads behind LDS writes).
+    for (unsigned u = blockIdx.x * blockDim.x + threadIdx.x; u < units; u += 4 * step) {
+        const bool m1 = u + step < units, m2 = u + 2 * step < units, m3 = u + 3 * step < units;
+        uint4 a = src[u], b = {}, c = {}, d = {};
+        if (m1) b = src[u + step];
+        if (m2) c = src[u + 2 * step];
+        if (m3) d = src[u + 3 * step];
+        dst[u] = a;
+        if (m1) dst[u + step] = b;
+        if (m2) dst[u + 2 * step] = c;
+        if (m3) dst[u + 3 * step] = d;
     }
-    if (active) {
-        const uint4* src = reinterpret_cast<const uint4*>(store + (size_t)eid * store_stride);
-        uint4* dst = reinterpret_cast<uint4*>(pool + (size_t)slot * pool_stride);
-        const unsigned units = (unsigned)(bytes / 16);
-        const unsigned step = gridDim.x * blockDim.x;
-        // Four independent 16-byte loads in flight per thread, held in named registers (an array
-        // here gets moved to LDS by the compiler, which serialises the loads behind LDS writes).
-        for (unsigned u = blockIdx.x * blockDim.x + threadIdx.x; u < units; u += 4 * step) {
-            const bool m1 = u + step < units, m2 = u + 2 * step < units, m3 = u + 3 * step < units;
-            uint4 a = src[u], b = {}, c2 = {}, d = {};
-            if (m1) b = src[u + step];
-            if (m2) c2 = src[u + 2 * step];
-            if (m3) d = src[u + 3 * step];
-            dst[u] = a;
-            if (m1) dst[u + step] = b;
-            if (m2) dst[u + 2 * step] = c2;
-            if (m3) dst[u + 3 * step] = d;
-        }
-    }
-    if (sync) {
-        __threadfence();                     // this block's copies visible at agent scope
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t* cnt = &sync->cnt[list ? 1 : 0][layer];
-            const uint32_t total = gridDim.x * gridDim.y;
-            if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1) {
-                __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                uint32_t* done = list ? &sync->pf_done[layer] : &sync->dm_done[layer];
-                __hip_atomic_store(done, want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-    }
-}
-
-__global__ void k_token_begin(StageSync* sync) {
-    if (threadIdx.x == 0) sync->seq = sync->seq + 1u;
 }
 
 // Plain device copy of a known byte count: the reference reading for scaling memory counters
@@ -137,33 +95,19 @@ int launch_slot_prefetch(SlotTable* t, const int32_t* preds, int m, int max_fetc
 }
 
 int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t store_stride, uint8_t* pool,
-                 size_t pool_stride, size_t bytes, int ctas, hipStream_t s, StageSync* sync, int layer, int wait_mask,
-                 int max_copies) {
-    if (max_copies <= 0 || max_copies > MOE_MAX_PREFETCH) {
-        moe_set_error("stage: max_copies %d out of range 1..%d", max_copies, MOE_MAX_PREFETCH);
-        return -1;
-    }
-    if (sync && (layer < 0 || layer >= MOE_MAX_LAYERS)) { moe_set_error("stage: layer %d out of range", layer); return -1; }
+                 size_t pool_stride, size_t bytes, int ctas, hipStream_t s) {
     if (bytes % 16 || store_stride % 16 || pool_stride % 16 || bytes > pool_stride || bytes > store_stride) {
         moe_set_error("stage: bytes=%zu strides=%zu/%zu must be multiples of 16 with bytes <= stride",
                       bytes, store_stride, pool_stride);
         return -1;
     }
     if (bytes / 16 > 0xFFFFFFFFull) { moe_set_error("stage: blob of %zu bytes too large", bytes); return -1; }
-    // ctas = blocks per copy; the grid covers the largest possible copy list (max_copies rows; a
-    // longer list is the caller's error: its tail is not copied), empty rows do nothing.
+    // ctas = blocks per copy; the grid covers the largest possible copy list, empty rows exit.
     // 2 blocks x 256 threads x 4 x 16 B in flight per copy already saturate PCIe; more only
     // crowds other kernels' memory requests.
     if (ctas <= 0) ctas = 2;
-    MOE_LAUNCH(TK_STAGE, k_stage, dim3(ctas, max_copies), dim3(256), 0, s, t, list, store, store_stride,
-               pool, pool_stride, bytes, sync, layer, wait_mask);
-    HIP_TRY(hipGetLastError());
-    return 0;
-}
-
-int launch_token_begin(StageSync* sync, hipStream_t s) {
-    if (!sync) { moe_set_error("token_begin: null sync"); return -1; }
-    hipLaunchKernelGGL(k_token_begin, dim3(1), dim3(64), 0, s, sync);
+    MOE_LAUNCH(TK_STAGE, k_stage, dim3(ctas, MOE_MAX_PREFETCH), dim3(256), 0, s, t, list, store, store_stride,
+               pool, pool_stride, bytes);
     HIP_TRY(hipGetLastError());
     return 0;
 }

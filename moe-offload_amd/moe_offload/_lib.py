@@ -70,10 +70,7 @@ SIGNATURES: dict[str, tuple] = {
     "c_layer_switch_glu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
     "c_layer_mark_read": (_c_int, [_c_int, _c_vp]),
     "c_router_tables_dev": (_c_int, [_c_int, _c_int, _c_int, _c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_vp, _c_vp, _c_int,
-                                     _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
-    "moe_stage_sync_bytes": (_c_u64, []),
-    "c_token_begin": (_c_int, [_c_vp, _c_vp]),
-    "c_layer_stage_dev_sync": (_c_int, [_c_int, _c_int, _c_int, _c_vp, _c_int, _c_int, _c_vp]),
+                                     _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "c_layer_grouped_switch_glu": (_c_int, [_c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_int, _c_vp,
                                             _c_vp, _c_vp]),
     "c_layer_set_device_mode": (_c_int, [_c_int, _c_int]),

@@ -50,15 +50,11 @@ class StackConfig:
     eps: float = 1e-6
     seed: int = 0
     layer_base: int = 0          # first C-ABI layer index used (tables are global to the library)
-    stage_ctas: int = 2          # staging blocks per copied expert for prefetch copies (they run
-                                 # under GEMV and router; more blocks only slow those down)
-    demand_ctas: int = 2         # staging blocks per copied expert for demand copies (nothing
-                                 # else runs while they land)
+    stage_ctas: int = 2          # staging blocks per copied expert (enough to fill PCIe; more
+                                 # only floods the L2 miss queues with slow host reads)
     resident: bool = False       # every layer's experts in HBM (no slot tables, no staging)
     fused_tables: bool = True    # device mode: the router's last block runs the slot-table step
                                  # and the next layer's prefetch (no separate table launches)
-    stage_flags: bool = True     # device mode with fused tables: staging ordered by device-side
-                                 # flags (bounded spins) instead of per-layer cross-stream events
 
 
 def random_blobs(n_exp: int, hidden: int, inter: int, group: int, gen: torch.Generator, device,
@@ -144,8 +140,6 @@ class DecodeStack:
         self.ev_pref = [torch.cuda.Event() for _ in range(c.n_layers)]
         self.ev_copy = [torch.cuda.Event() for _ in range(c.n_layers)]
         self.ev_demand = [torch.cuda.Event() for _ in range(c.n_layers)]
-        self.ev_begin, self.ev_end = torch.cuda.Event(), torch.cuda.Event()
-        self.sync = torch.zeros(int(L.moe_stage_sync_bytes()), dtype=torch.uint8, device=dev)
         self.graph = None
 
     # C-ABI layer index of stack layer l
@@ -171,11 +165,7 @@ class DecodeStack:
         return list(o)
 
     # ---- one token ---------------------------------------------------------------------------
-    def sync_error(self) -> int:
-        """Error word of the staging handshakes (0: every bounded wait succeeded)."""
-        return int(self.sync[4:8].view(torch.int32).item()) & 0xFFFFFFFF
-
-    def _router(self, l: int, tables: bool = False, sync: bool = False):
+    def _router(self, l: int, tables: bool = False):
         c = self.cfg
         wn = self.router_w[l + 1] if (c.prefetch and l + 1 < c.n_layers) else None
         x_in = self.xs[0] if l == 0 else None
@@ -192,7 +182,6 @@ class DecodeStack:
                                             c.hidden, c.n_exp, c.top_k, c.top_m if wn is not None else 0,
                                             self.router_ws[l].data_ptr(), self.ids[l].data_ptr(),
                                             self.scores[l].data_ptr(), self.pred[l].data_ptr(),
-                                            self.sync.data_ptr() if sync else None,
                                             torch.cuda.current_stream().cuda_stream)
             _lib.check(rc, "router_tables")
             return
@@ -240,9 +229,6 @@ class DecodeStack:
         layer wait for its prefetch copies because both may target the same slot."""
         c = self.cfg
         main = torch.cuda.current_stream()
-        if not c.resident and c.fused_tables and c.stage_flags:
-            self._token_flags(main)
-            return
         for l in range(c.n_layers):
             if c.resident:
                 self._router(l)
@@ -277,34 +263,6 @@ class DecodeStack:
             self._glu(l)
         _lib.check(self.L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
                                       c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), main.cuda_stream), "rmsnorm")
-
-    def _token_flags(self, main):
-        """Device-driven token whose staging is ordered by device-side flags: one cross-stream
-        join at each end of the token instead of two per layer.
-        main, layer l: router + step(l) + prefetch table(l+1) [marks list l+1 ready] ->
-          demand copies(l) [wait: prefetch copies(l) landed] -> gate/up -> down;
-        side: prefetch copies(l+1) [wait: list l+1 ready, demand copies(l) landed]."""
-        c, L = self.cfg, self.L
-        sp = self.sync.data_ptr()
-        _lib.check(L.c_token_begin(sp, main.cuda_stream), "token_begin")
-        if c.prefetch:
-            self.ev_begin.record(main)
-            self.side.wait_event(self.ev_begin)
-        for l in range(c.n_layers):
-            self._router(l, tables=True, sync=True)
-            if l >= 1:
-                _lib.check(L.c_layer_stage_dev_sync(self.cidx(l), 0, c.demand_ctas, sp, 4 if c.prefetch else 0,
-                                                    c.top_k, main.cuda_stream), "stage_demand")
-            if c.prefetch and l + 1 < c.n_layers:
-                _lib.check(L.c_layer_stage_dev_sync(self.cidx(l + 1), 1, c.stage_ctas, sp, 1 | (2 if l >= 1 else 0),
-                                                    min(c.prefetch_cap if 0 < c.prefetch_cap < 32 else 32, c.top_m),
-                                                    self.side.cuda_stream), "stage_prefetch")
-            self._glu(l)
-        if c.prefetch:
-            self.ev_end.record(self.side)
-            main.wait_event(self.ev_end)
-        _lib.check(L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
-                                 c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), main.cuda_stream), "rmsnorm")
 
     def _layer_fused(self, l: int, main):
         """One layer of the device-driven token with the table work inside the router:

@@ -22,9 +22,9 @@ pytestmark = pytest.mark.gpu
 N_LAYERS, N_TOK = 6, 12
 
 
-def run_stack(mode, layer_base, graph=False, fused=True, flags=True):
+def run_stack(mode, layer_base, graph=False, fused=True):
     from moe_offload.stack import DecodeStack, StackConfig
-    cfg = StackConfig(n_layers=N_LAYERS, seed=5, layer_base=layer_base, fused_tables=fused, stage_flags=flags)
+    cfg = StackConfig(n_layers=N_LAYERS, seed=5, layer_base=layer_base, fused_tables=fused)
     st = DecodeStack(cfg, mode=mode)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(99)
@@ -40,8 +40,6 @@ def run_stack(mode, layer_base, graph=False, fused=True, flags=True):
                     "hs": st.hs.cpu().numpy().copy(),
                     "slots": {l: st.slot_inds[l][:cfg.top_k].cpu().numpy().copy() for l in range(1, N_LAYERS)}})
     stats = {l: st.layer_stats(l) for l in range(1, N_LAYERS)}
-    if mode == "device":
-        assert st.sync_error() == 0, hex(st.sync_error())
     return st, rec, stats
 
 
@@ -109,12 +107,11 @@ def test_slot_sequence_matches_oracle_lru(runs):
         assert layers[l].stats() == stats[l], l
 
 
-@pytest.mark.parametrize("fused,flags", [(False, False), (True, False)])
-def test_other_device_orderings_match(runs, fused, flags):
-    """Separate step / prefetch kernels with event joins, and the fused router with event joins,
-    take the same decisions and produce the same outputs as the fused router with flag joins."""
+def test_separate_table_launches_match_fused(runs):
+    """The router with the table work in its last block and the separate step / prefetch
+    kernels take identical decisions."""
     (_, d, ds), _ = runs
-    st, u, us = run_stack("device", 0, fused=fused, flags=flags)
+    st, u, us = run_stack("device", 0, fused=False)
     try:
         for t in range(N_TOK):
             assert np.array_equal(u[t]["xs"], d[t]["xs"]), f"token {t}"
