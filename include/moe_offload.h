@@ -77,6 +77,37 @@ void c_layer_get_stats(int layer_idx, uint64_t* out_stats);
 /* expert_io.c:834-852.  out[6] summed over layers 1..num_layers-1. */
 void c_get_decode_totals(int num_layers, uint64_t* out6);
 
+/* Superset ABI of the reference's C++ runner (cpp/src/expert_io.h:8-108, implemented in
+ * cpp/third_party/expert_io.c).  These act on host-driven layers. */
+enum { MOE_SCHED_SYNC_DEMAND = 1, MOE_SCHED_NO_PREFETCH = 2, MOE_SCHED_SPLIT = 4 };
+/* cpp/third_party/expert_io.c:1094-1394.  One call per layer: the decode step of layer_idx
+ * (skipped for layer 0 or null eids; k > 16 is cut to 16) whose victim choice also protects
+ * the experts the layer's last prefetch fetched, then the prefetch of next_layer (only when
+ * next_layer > 0, pred given, n_pred > 0, prefetch_cap > 0 and not NO_PREFETCH) taking each
+ * predicted expert at most once, its copies queued behind the demand copies.  SPLIT records
+ * the hit / miss slot lists when 0 < misses < k; SYNC_DEMAND blocks the host until the layer's
+ * copies land; with no miss the layer's copies are joined on the GPU.  Returns the misses. */
+int c_layer_decode_step_sched(int layer_idx, const int32_t* eids, int k, const int32_t* pred,
+                              int n_pred, int next_layer, int prefetch_cap, int flags);
+/* cpp/third_party/expert_io.c:1062-1092.  The last recorded split of the layer: hit slots,
+ * miss slots (id order) and each id's position in hits ++ misses (kept until the next split). */
+void c_layer_get_split_inds(int layer_idx, uint32_t* out_hit_slots, uint32_t* out_miss_slots,
+                            int32_t* out_inv_order);
+/* cpp/third_party/expert_io.c:1048-1060.  Joins the layer's copies on the GPU side (the
+ * compute stream waits; the host does not block). */
+void c_layer_wait_demand(int layer_idx);
+/* cpp/third_party/expert_io.c:1002-1038.  Per-token accounting over host-driven calls: out10 =
+ * lru hits, demand misses, prefetch loads, prefetch hits, wasted prefetches, demand re-reads
+ * within 16 / 64 tokens, prefetch re-reads within 16 / 64 tokens, bytes staged.  Tokens are
+ * numbered by the library (token_idx is ignored, as in the reference); layer 1's reset
+ * restarts the numbering. */
+void c_set_io_accounting(int enabled);
+void c_begin_decode_token(int token_idx);
+void c_end_decode_token(uint64_t* out10);
+/* cpp/third_party/expert_io.c:1040-1042.  Host bytes held by the library's tables and
+ * buffers. */
+uint64_t c_get_native_buffer_bytes(void);
+
 /* ---- Part 2: compute (MLX built-ins of the reference) ------------------------------------- */
 
 /* loader.py:903-908 + loader.py:237-242,950-958 (cpp/src/layers.cpp:311-341).  Optional
@@ -104,8 +135,9 @@ uint64_t moe_q2_expert_bytes(int hidden, int inter, int group);
 int moe_q2_gate_up(const void* x, const void* pool, uint64_t stride, int n_slots,
                    const uint32_t* slots, int k, int hidden, int inter, int group, void* h_out,
                    void* stream);
-/* gather_qmm down + weighted combine (loader.py:964-965): y_out fp32 [hidden] =
- * residual + sum_j scores[j] * down_j(h_j), or per-expert rows y_out[k][hidden]. */
+/* gather_qmm down + weighted combine (loader.py:964-965).  per_expert 0: y_out fp32 [hidden] =
+ * residual + sum_j scores[j] * down_j(h_j); 1: per-expert rows y_out[k][hidden]; 2: y_out +=
+ * sum_j scores[j] * down_j(h_j) (residual ignored). */
 int moe_q2_down(const void* h, const void* pool, uint64_t stride, int n_slots,
                 const uint32_t* slots, const void* scores, int k, int hidden, int inter, int group,
                 const void* residual, float* y_out, int per_expert, void* stream);
@@ -165,6 +197,16 @@ int c_layer_grouped_switch_glu(int layer_idx, const void* x, int n_tokens, const
                                const int32_t* row_out, int n_rows, int n_out_rows,
                                const int32_t* seg_start, int n_seg, void* h_ws, void* y_out,
                                void* stream);
+/* Split SwitchGLU after c_layer_decode_step_sched with MOE_SCHED_SPLIT (the purpose of the
+ * reference's split lists, cpp/third_party/expert_io.c:1257-1276,1380-1390: hit experts start
+ * before the misses land).  part 0: the hit experts, after the layer's prefetch copies only,
+ * y_out = residual + their sum; part 1: after the demand copies, y_out += the missed experts'
+ * sum.  scores in router order; both parts on one stream, part 0 first. */
+int c_layer_switch_glu_split(int layer_idx, int part, const void* x, const void* scores,
+                             const void* residual, void* h_ws, float* y_out, void* stream);
+/* Device-driven tables follow the scheduler variant's decisions (on != 0) or the published
+ * ones (the default). */
+int c_layer_set_sched(int layer_idx, int on);
 /* Record that work queued on `stream` so far reads the layer's pool (copies into it wait). */
 int c_layer_mark_read(int layer_idx, void* stream);
 /* Move a layer's slot table to device memory (on != 0) or back.  Device-driven layers take

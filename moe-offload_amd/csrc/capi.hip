@@ -54,9 +54,36 @@ struct LayerState {
     int hidden = 0, inter = 0, group = 0;
     uint8_t* bounce = nullptr;                // pinned bounce buffer for file-backed stores
     size_t bounce_bytes = 0;
+    // Prefetch copies (c_layer_start_prefetch, the scheduler's next-layer prefetch) also record
+    // pf_done, so work on the step's hit slots can wait for them alone (split GLU).
+    hipEvent_t pf_done = nullptr;
+    bool pf_pending = false;
+    uint8_t* split_dev = nullptr;             // device copy of the split lists (split GLU)
+    int32_t evicted_at[MOE_NUM_EXPERTS];      // per-token accounting: token of last eviction
 };
 
 LayerState g_layers[MOE_MAX_LAYERS];
+
+// Scheduler split lists, per layer, kept until the next split (c_layer_get_split_inds reads
+// the last one, as cpp/third_party/expert_io.c:1062-1092 does).
+SplitLists g_split[MOE_MAX_LAYERS];
+
+// Per-token accounting (cpp/third_party/expert_io.c:98-111,1002-1038).
+bool g_acct_on = false;
+int32_t g_token_seq = 0, g_cur_token = -1;
+uint64_t g_tok[10] = {0};
+
+slot_host::Acct* acct_for(LayerState& L, slot_host::Acct& a) {
+    if (!g_acct_on) return nullptr;
+    a.cur_token = g_cur_token;
+    a.evicted_at = L.evicted_at;
+    a.tok = g_tok;
+    return &a;
+}
+
+void reset_evictions(LayerState& L) {
+    for (int e = 0; e < MOE_NUM_EXPERTS; ++e) L.evicted_at[e] = -1;
+}
 hipStream_t g_compute = nullptr;             // caller's stream (null stream by default)
 hipStream_t g_copy = nullptr;
 bool g_ready = false;
@@ -75,6 +102,7 @@ int ensure_runtime() {
 int ensure_events(LayerState& L) {
     if (!L.copy_done) HIP_TRY(hipEventCreateWithFlags(&L.copy_done, hipEventDisableTiming));
     if (!L.read_done) HIP_TRY(hipEventCreateWithFlags(&L.read_done, hipEventDisableTiming));
+    if (!L.pf_done) HIP_TRY(hipEventCreateWithFlags(&L.pf_done, hipEventDisableTiming));
     return 0;
 }
 
@@ -114,12 +142,20 @@ int pread_full(int fd, uint8_t* buf, size_t n, uint64_t off) {
     return 0;
 }
 
-// Queue the copies store[eid] -> pool[slot] for every tensor on the copy stream.
-int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* slots, int n) {
+// Queue the copies store[eid] -> pool[slot] for every tensor on the copy stream.  A prefetch's
+// copies also record pf_done.
+int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* slots, int n,
+                 bool prefetch = false) {
     if (n <= 0) return 0;
     bool any = false;
     for (int t = 0; t < MOE_NUM_TENSORS; ++t) any |= (L.row_bytes[t] && L.src[t] && L.dst[t]);
     if (!any) return 0;                       // accounting-only layer
+    if (g_acct_on) {
+        uint64_t b = 0;
+        for (int t = 0; t < MOE_NUM_TENSORS; ++t)
+            if (L.row_bytes[t] && L.src[t] && L.dst[t]) b += L.row_bytes[t];
+        g_tok[slot_host::AC_BYTES] += (uint64_t)n * b;
+    }
     if (ensure_runtime()) return -1;
     if (ensure_events(L)) return -1;
     if (L.read_recorded) HIP_TRY(hipStreamWaitEvent(g_copy, L.read_done, 0));
@@ -158,6 +194,10 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
     }
     HIP_TRY(hipEventRecord(L.copy_done, g_copy));
     L.copy_pending = true;
+    if (prefetch) {
+        HIP_TRY(hipEventRecord(L.pf_done, g_copy));
+        L.pf_pending = true;
+    }
     (void)layer;
     return 0;
 }
@@ -166,6 +206,7 @@ int wait_copies_gpu(LayerState& L, hipStream_t s) {
     if (!L.copy_pending) return 0;
     HIP_TRY(hipStreamWaitEvent(s, L.copy_done, 0));
     L.copy_pending = false;
+    L.pf_pending = false;
     return 0;
 }
 
@@ -176,21 +217,28 @@ int write_slot_inds(LayerState& L, const uint32_t* slots, int k) {
     return 0;
 }
 
-int step_host(int layer, const uint32_t* eids, int k, int async_io) {
-    LayerState& L = g_layers[layer];
-    if (!L.init) { moe_set_error("layer %d not initialised", layer); return -1; }
+// Input checks of a decode step (the reference indexes its tables with the ids unchecked).
+bool check_step_ids(const char* who, const LayerState& L, const uint32_t* eids, int k) {
+    if (!L.init) { moe_set_error("%s: layer not initialised", who); return false; }
     if (k <= 0 || k > MOE_MAX_K || k > L.capacity) {
-        moe_set_error("step: k=%d must be in 1..%d and <= capacity %d", k, MOE_MAX_K, L.capacity);
-        return -1;
+        moe_set_error("%s: k=%d must be in 1..%d and <= capacity %d", who, k, MOE_MAX_K, L.capacity);
+        return false;
     }
     for (int i = 0; i < k; ++i) {
-        if (eids[i] >= MOE_NUM_EXPERTS) { moe_set_error("step: expert id %u out of range", eids[i]); return -1; }
+        if (eids[i] >= MOE_NUM_EXPERTS) { moe_set_error("%s: expert id %u out of range", who, eids[i]); return false; }
         for (int j = 0; j < i; ++j)
-            if (eids[j] == eids[i]) { moe_set_error("step: expert id %u repeated", eids[i]); return -1; }
+            if (eids[j] == eids[i]) { moe_set_error("%s: expert id %u repeated", who, eids[i]); return false; }
     }
+    return true;
+}
+
+int step_host(int layer, const uint32_t* eids, int k, int async_io) {
+    LayerState& L = g_layers[layer];
+    if (!check_step_ids("step", L, eids, k)) return -1;
     if (pull_table(L)) return -1;
     uint32_t out[MOE_MAX_K];
-    int n_miss = slot_host::step(&L.tab, eids, k, out);
+    slot_host::Acct acct;
+    int n_miss = slot_host::step(&L.tab, eids, k, out, nullptr, nullptr, acct_for(L, acct));
     if (push_table(L)) return -1;
     if (write_slot_inds(L, out, k)) return -1;
     if (issue_copies(layer, L, L.tab.copy_eid, L.tab.copy_slot, L.tab.n_copy)) return -1;
@@ -274,6 +322,8 @@ void c_io_shutdown(void) {
         if (L.dtab) (void)hipFree(L.dtab);
         if (L.copy_done) (void)hipEventDestroy(L.copy_done);
         if (L.read_done) (void)hipEventDestroy(L.read_done);
+        if (L.pf_done) (void)hipEventDestroy(L.pf_done);
+        if (L.split_dev) (void)hipFree(L.split_dev);
         L = LayerState();
     }
     (void)hipStreamDestroy(g_copy);
@@ -286,6 +336,11 @@ void c_layer_reset_cache(int layer) {
     LayerState& L = g_layers[layer];
     if (pull_table(L)) return;
     slot_host::reset_cache(&L.tab);
+    reset_evictions(L);
+    if (layer == 1) {                         // layer 1's reset restarts the token numbering
+        g_token_seq = 0;
+        g_cur_token = -1;
+    }
     push_table(L);
 }
 
@@ -308,10 +363,18 @@ void c_layer_init(int layer, int fd, int capacity, const uint64_t* base_offsets,
     if (L.copy_pending) (void)hipEventSynchronize(L.copy_done);
     if (L.bounce) (void)hipHostFree(L.bounce);
     if (L.dtab) (void)hipFree(L.dtab);
-    hipEvent_t cd = L.copy_done, rd = L.read_done;
+    hipEvent_t cd = L.copy_done, rd = L.read_done, pd = L.pf_done;
+    uint8_t* sd = L.split_dev;
     L = LayerState();
     L.copy_done = cd;
     L.read_done = rd;
+    L.pf_done = pd;
+    L.split_dev = sd;
+    reset_evictions(L);
+    if (layer == 1) {
+        g_token_seq = 0;
+        g_cur_token = -1;
+    }
     L.fd = fd;
     L.capacity = capacity;
     for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
@@ -363,9 +426,10 @@ void c_layer_start_prefetch(int layer, const int32_t* preds, int n, int max_fetc
     if (!L.init) { moe_set_error("layer %d not initialised", layer); return; }
     if (n < 0 || n > MOE_MAX_PREFETCH) { moe_set_error("prefetch: %d predictions (max %d)", n, MOE_MAX_PREFETCH); return; }
     if (pull_table(L)) return;
-    slot_host::prefetch(&L.tab, preds, n, max_fetch);
+    slot_host::Acct acct;
+    slot_host::prefetch(&L.tab, preds, n, max_fetch, false, acct_for(L, acct));
     if (push_table(L)) return;
-    issue_copies(layer, L, L.tab.pf_copy_eid, L.tab.pf_copy_slot, L.tab.pf_n_copy);
+    issue_copies(layer, L, L.tab.pf_copy_eid, L.tab.pf_copy_slot, L.tab.pf_n_copy, true);
 }
 
 void c_layer_start_prefetch10(int layer, int max_fetch, int32_t e0, int32_t e1, int32_t e2, int32_t e3,
@@ -425,6 +489,7 @@ void c_layer_set_lru_state(int layer, const int32_t* eids, const int32_t* slots,
         }
     if (pull_table(L)) return;
     slot_host::set_state(&L.tab, eids, slots, n, add_req, add_hits, add_miss);
+    for (int i = 0; i < n; ++i) L.evicted_at[eids[i]] = -1;
     push_table(L);
 }
 
@@ -451,6 +516,110 @@ void c_get_decode_totals(int num_layers, uint64_t* out6) {
         t[5] += st[ST_PREF_BYTES];
     }
     memcpy(out6, t, sizeof(t));
+}
+
+// ---- scheduler variant and per-token accounting (cpp/third_party/expert_io.c) --------------
+
+// GPU-side join of a layer's copies: the compute stream waits for every copy queued for the
+// layer (its prefetch and its demand misses) before later work reads the pool.
+void c_layer_wait_demand(int layer) {
+    if (!valid_layer(layer) || !g_layers[layer].init) return;
+    wait_copies_gpu(g_layers[layer], g_compute);
+}
+
+int c_layer_decode_step_sched(int layer, const int32_t* eids, int k, const int32_t* pred, int n_pred, int next_layer,
+                              int prefetch_cap, int flags) {
+    int n_miss = 0;
+    // 1: the step of `layer` (layer 0 is resident and never stepped)
+    if (layer > 0 && layer < MOE_MAX_LAYERS && eids && k > 0) {
+        if (k > MOE_MAX_K) k = MOE_MAX_K;
+        LayerState& L = g_layers[layer];
+        if (!check_step_ids("decode_step_sched", L, reinterpret_cast<const uint32_t*>(eids), k)) return -1;
+        if (pull_table(L)) return -1;
+        uint64_t extra[8] = {0};
+        if (L.tab.snap_valid) memcpy(extra, L.tab.snap_fetched, sizeof(extra));
+        uint32_t out[MOE_MAX_K];
+        uint8_t hit[MOE_MAX_K];
+        slot_host::Acct acct;
+        n_miss = slot_host::step(&L.tab, reinterpret_cast<const uint32_t*>(eids), k, out, extra, hit,
+                                 acct_for(L, acct));
+        if (push_table(L)) return -1;
+        if (write_slot_inds(L, out, k)) return -1;
+        if ((flags & MOE_SCHED_SPLIT) && n_miss > 0 && n_miss < k) {
+            SplitLists& S = g_split[layer];
+            const int n_hit = k - n_miss;
+            int h = 0, m = 0;
+            for (int i = 0; i < k; ++i) {
+                if (hit[i]) { S.hit[h] = out[i]; S.inv[i] = h++; }
+                else { S.miss[m] = out[i]; S.inv[i] = n_hit + m++; }
+            }
+            S.n_hit = n_hit;
+            S.n_miss = n_miss;
+            S.k = k;
+        }
+        if (issue_copies(layer, L, L.tab.copy_eid, L.tab.copy_slot, L.tab.n_copy)) return -1;
+    }
+    // 2: the prefetch of `next_layer`, queued behind the demand copies
+    if (!(flags & MOE_SCHED_NO_PREFETCH) && next_layer > 0 && next_layer < MOE_MAX_LAYERS && pred && n_pred > 0 &&
+        prefetch_cap > 0) {
+        LayerState& N = g_layers[next_layer];
+        if (!N.init) { moe_set_error("decode_step_sched: next layer %d not initialised", next_layer); return -1; }
+        if (pull_table(N)) return -1;
+        slot_host::Acct acct;
+        slot_host::prefetch(&N.tab, pred, n_pred, prefetch_cap, true, acct_for(N, acct));
+        if (push_table(N)) return -1;
+        if (issue_copies(next_layer, N, N.tab.pf_copy_eid, N.tab.pf_copy_slot, N.tab.pf_n_copy, true)) return -1;
+    }
+    // 3: joins.  SYNC_DEMAND blocks the host until the layer's copies have landed; with no miss
+    // the layer's (prefetch) copies are joined on the GPU so the GEMV needs no further call.
+    if (layer > 0 && layer < MOE_MAX_LAYERS && g_layers[layer].init) {
+        LayerState& L = g_layers[layer];
+        if (flags & MOE_SCHED_SYNC_DEMAND) {
+            if (L.copy_pending) HIP_TRY(hipEventSynchronize(L.copy_done));
+            wait_copies_gpu(L, g_compute);
+        } else if (n_miss == 0) {
+            wait_copies_gpu(L, g_compute);
+        }
+    }
+    return n_miss;
+}
+
+void c_layer_get_split_inds(int layer, uint32_t* out_hit_slots, uint32_t* out_miss_slots, int32_t* out_inv_order) {
+    if (!valid_layer(layer)) return;
+    const SplitLists& S = g_split[layer];
+    if (S.n_hit > 0 && out_hit_slots) memcpy(out_hit_slots, S.hit, (size_t)S.n_hit * sizeof(uint32_t));
+    if (S.n_miss > 0 && out_miss_slots) memcpy(out_miss_slots, S.miss, (size_t)S.n_miss * sizeof(uint32_t));
+    if (S.k > 0 && out_inv_order) memcpy(out_inv_order, S.inv, (size_t)S.k * sizeof(int32_t));
+}
+
+void c_set_io_accounting(int enabled) {
+    g_acct_on = enabled != 0;
+    if (!g_acct_on) g_cur_token = -1;
+}
+
+void c_begin_decode_token(int token_idx) {
+    (void)token_idx;                          // tokens are numbered by the library, as in the reference
+    g_cur_token = g_token_seq++;
+    memset(g_tok, 0, sizeof(g_tok));
+}
+
+void c_end_decode_token(uint64_t* out10) { memcpy(out10, g_tok, sizeof(g_tok)); }
+
+uint64_t c_get_native_buffer_bytes(void) {
+    uint64_t b = sizeof(g_layers) + sizeof(g_split);
+    for (int l = 0; l < MOE_MAX_LAYERS; ++l) {
+        if (g_layers[l].dtab) b += sizeof(SlotTable);
+        b += g_layers[l].bounce_bytes;
+    }
+    return b;
+}
+
+int c_layer_set_sched(int layer, int on) {
+    if (!valid_layer(layer) || !g_layers[layer].init) { moe_set_error("set_sched: bad layer %d", layer); return -1; }
+    LayerState& L = g_layers[layer];
+    if (pull_table(L)) return -1;
+    L.tab.sched = on ? 1 : 0;
+    return push_table(L);
 }
 
 // ---- device-driven slot tables ----------------------------------------------------------------
@@ -651,6 +820,47 @@ int c_layer_switch_glu(int layer, const void* x, const void* scores, const void*
     if (moe_q2_switch_glu(x, (const void*)L.dst[0], L.row_bytes[0], L.capacity, L.slot_inds, scores, k, L.hidden, L.inter,
                           L.group, residual, h_ws, y_out, per_expert, stream))
         return -1;
+    HIP_TRY(hipEventRecord(L.read_done, s));
+    L.read_recorded = true;
+    return 0;
+}
+
+// Half of a split SwitchGLU over the layer's pool after a scheduler step with SPLIT:
+// part 0 runs the step's hit experts as soon as the layer's prefetch copies have landed and
+// writes y = residual + sum over hits; part 1 waits for the demand copies and adds the sum over
+// the missed experts.  Both parts must run on the same stream, part 0 first.
+int c_layer_switch_glu_split(int layer, int part, const void* x, const void* scores, const void* residual,
+                             void* h_ws, float* y_out, void* stream) {
+    if (!valid_layer(layer) || !g_layers[layer].init || !g_layers[layer].hidden) {
+        moe_set_error("layer_switch_glu_split: layer %d has no Q2 format (c_layer_set_format)", layer);
+        return -1;
+    }
+    if (part != 0 && part != 1) { moe_set_error("layer_switch_glu_split: part %d (0 hits, 1 misses)", part); return -1; }
+    LayerState& L = g_layers[layer];
+    const SplitLists& S = g_split[layer];
+    if (S.n_hit <= 0 || S.n_miss <= 0) {
+        moe_set_error("layer_switch_glu_split: layer %d has no split (scheduler step with SPLIT and 0 < misses < k)",
+                      layer);
+        return -1;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    if (ensure_events(L)) return -1;
+    if (!L.split_dev) HIP_TRY(hipMalloc((void**)&L.split_dev, 256));
+    uint32_t* dslots = reinterpret_cast<uint32_t*>(L.split_dev);
+    __half* dscores = reinterpret_cast<__half*>(L.split_dev + 128);
+    int rc;
+    if (part == 0) {
+        if (L.pf_pending) HIP_TRY(hipStreamWaitEvent(s, L.pf_done, 0));
+        if (launch_split_lists(S, (const __half*)scores, dslots, dscores, s)) return -1;
+        rc = moe_q2_switch_glu(x, (const void*)L.dst[0], L.row_bytes[0], L.capacity, dslots, dscores, S.n_hit,
+                               L.hidden, L.inter, L.group, residual, h_ws, y_out, 0, stream);
+    } else {
+        if (wait_copies_gpu(L, s)) return -1;
+        rc = moe_q2_switch_glu(x, (const void*)L.dst[0], L.row_bytes[0], L.capacity, dslots + MOE_MAX_K,
+                               dscores + MOE_MAX_K, S.n_miss, L.hidden, L.inter, L.group, nullptr, h_ws, y_out, 2,
+                               stream);
+    }
+    if (rc) return -1;
     HIP_TRY(hipEventRecord(L.read_done, s));
     L.read_recorded = true;
     return 0;

@@ -79,6 +79,16 @@ struct SlotTable {
     int32_t pf_copy_eid[MOE_MAX_PREFETCH];
     int32_t pf_copy_slot[MOE_MAX_PREFETCH];
     int32_t status;                     // 0 ok; nonzero: rejected input (device kernels)
+    int32_t sched;                      // device-driven ops follow the scheduler variant
+                                        // (cpp/third_party/expert_io.c:1094-1394) when nonzero
+};
+
+// Hit/miss split of one scheduler step (c_layer_get_split_inds): slots of the ids that were
+// resident, slots of the missed ids (both in id order), and each id's position in hits ++ misses.
+struct SplitLists {
+    uint32_t hit[MOE_MAX_K], miss[MOE_MAX_K];
+    int32_t inv[MOE_MAX_K];
+    int32_t n_hit, n_miss, k;
 };
 
 // Stats word indices (same order as c_layer_get_stats, expert_io.c:791-812).
@@ -144,6 +154,10 @@ int launch_slot_prefetch(SlotTable* t, const int32_t* preds, int m, int max_fetc
 int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t store_stride,
                  uint8_t* pool, size_t pool_stride, size_t bytes, int ctas, hipStream_t s);
 int launch_store_u32(uint32_t* dst, const uint32_t* vals, int n, hipStream_t s);
+// slots_out[0..n_hit) / [16..16+n_miss): hit / miss slots; scores_out likewise, gathered from
+// the step's scores (router order) through inv.
+int launch_split_lists(const SplitLists& a, const __half* scores, uint32_t* slots_out, __half* scores_out,
+                       hipStream_t s);
 int launch_copy_calib(void* dst, const void* src, size_t bytes, hipStream_t s);
 int launch_stream_calib(const void* src, size_t bytes, int grid, float* out, hipStream_t s);
 int launch_q2_grouped_gate_up(const __half* x, int n_tokens, const int32_t* row_token, int n_rows,

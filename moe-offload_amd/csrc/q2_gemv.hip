@@ -20,8 +20,9 @@
 //                      GPR = hidden/64 lanes per row.  Writes h = silu(g)*u as fp16 [k][inter].
 //   k_q2_down<GPR>:    8 output rows per block x all k experts (4 waves split the experts);
 //                      h is staged in LDS in dot2 pair order; the block reduces over experts in
-//                      a fixed order and writes y = residual + sum_j s_j y_j (fp32), or the
-//                      per-expert rows when per_expert != 0.
+//                      a fixed order and writes y = residual + sum_j s_j y_j (fp32, mode 0), the
+//                      per-expert rows (mode 1), or adds sum_j s_j y_j to y (mode 2: the second
+//                      half of a hit/miss split).
 #include <hip/hip_fp16.h>
 
 #include "moe_common.h"
@@ -230,7 +231,7 @@ __global__ __launch_bounds__(256) void k_q2_down(
 #pragma unroll
             for (int o = LPR / 2; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
             int rloc = it * RPI + rl;
-            if (per_expert) {
+            if (per_expert == 1) {
                 int row = row0 + rloc;
                 if (g == 0 && rloc < kDownRows && row < hidden) y_out[(size_t)j * hidden + row] = part;
             } else {
@@ -238,7 +239,7 @@ __global__ __launch_bounds__(256) void k_q2_down(
             }
         }
     }
-    if (per_expert) return;
+    if (per_expert == 1) return;
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
         int rloc = it * RPI + rl;
@@ -249,8 +250,12 @@ __global__ __launch_bounds__(256) void k_q2_down(
         int row = row0 + tid;
         if (row < hidden) {
             float y = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
-            if (residual) y += __half2float(residual[row]);
-            y_out[row] = y;
+            if (per_expert == 2) {
+                y_out[row] += y;
+            } else {
+                if (residual) y += __half2float(residual[row]);
+                y_out[row] = y;
+            }
         }
     }
 }
@@ -309,6 +314,7 @@ int launch_q2_down(const __half* h, const uint8_t* pool, size_t stride, int n_sl
                    const __half* scores, int k, int hidden, int inter, int group,
                    const __half* residual, float* y_out, int per_expert, hipStream_t s) {
     if (!check_shape("q2_down", k, hidden, inter, group)) return -1;
+    if (per_expert < 0 || per_expert > 2) { moe_set_error("q2_down: mode %d (0 sum, 1 per expert, 2 add)", per_expert); return -1; }
     if (n_slots <= 0 || !pool || !slots || !h || !y_out) { moe_set_error("q2_down: empty pool or null pointer"); return -1; }
     BlobLayout L = blob_layout(hidden, inter, group);
     if (stride < L.bytes) { moe_set_error("q2_down: expert stride %zu < blob bytes %zu", stride, L.bytes); return -1; }

@@ -78,6 +78,19 @@ __global__ void k_store_u32(uint32_t* dst, U32x16 vals, int n) {
     if (i < n) dst[i] = vals.v[i];
 }
 
+// One thread per id of the step (router order i): its slot and score go to the hit half
+// [0, MOE_MAX_K) or the miss half [MOE_MAX_K, 2 MOE_MAX_K) at its rank there.
+__global__ void k_split_lists(SplitLists a, const __half* __restrict__ scores, uint32_t* __restrict__ slots_out,
+                              __half* __restrict__ scores_out) {
+    const int i = threadIdx.x;
+    if (i >= a.k) return;
+    const int d = a.inv[i];
+    const bool hit = d < a.n_hit;
+    const int dst = hit ? d : MOE_MAX_K + (d - a.n_hit);
+    slots_out[dst] = hit ? a.hit[d] : a.miss[d - a.n_hit];
+    scores_out[dst] = scores[i];
+}
+
 }  // namespace
 
 int launch_slot_step(SlotTable* t, const uint32_t* ids, int k, uint32_t* slot_inds, hipStream_t s) {
@@ -134,6 +147,20 @@ int launch_store_u32(uint32_t* dst, const uint32_t* vals, int n, hipStream_t s) 
     U32x16 v = {};
     for (int i = 0; i < n; ++i) v.v[i] = vals[i];
     hipLaunchKernelGGL(k_store_u32, dim3(1), dim3(64), 0, s, dst, v, n);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int launch_split_lists(const SplitLists& a, const __half* scores, uint32_t* slots_out, __half* scores_out,
+                       hipStream_t s) {
+    if (a.k <= 0 || a.k > MOE_MAX_K || a.n_hit < 0 || a.n_miss < 0 || a.n_hit + a.n_miss != a.k) {
+        moe_set_error("split_lists: inconsistent split (k=%d hits=%d misses=%d)", a.k, a.n_hit, a.n_miss);
+        return -1;
+    }
+    for (int i = 0; i < a.k; ++i)
+        if (a.inv[i] < 0 || a.inv[i] >= a.k) { moe_set_error("split_lists: order entry %d out of range", a.inv[i]); return -1; }
+    if (!scores || !slots_out || !scores_out) { moe_set_error("split_lists: null pointer"); return -1; }
+    hipLaunchKernelGGL(k_split_lists, dim3(1), dim3(64), 0, s, a, scores, slots_out, scores_out);
     HIP_TRY(hipGetLastError());
     return 0;
 }

@@ -8,6 +8,11 @@
 // slot gives it the next clock value.  Each operation copies the table into LDS (~4.5 KB),
 // decides, and writes it back.
 //
+// With t->sched set, the scheduler variant of mlx-qwen38/cpp/third_party/expert_io.c:1094-1394
+// applies: the step's victim choice also protects the experts the last prefetch fetched
+// (1141-1146), the prefetch skips repeated predictions (1311-1322) and does nothing at all when
+// max_fetch <= 0 (1288-1290).
+//
 // All synchronisation is wave-level: a wave's LDS accesses complete in program order, so a
 // compiler fence at wavefront scope is all that separates one step from the next.  That lets
 // two operations on different tables run at once in two waves of one block.
@@ -30,6 +35,7 @@ struct LdsTable {
     uint32_t resident[16];
     uint32_t pred[16];
     uint32_t fetched[16];
+    uint32_t spare[16];        // step: its own ids (never the fallback victim)
     int32_t list_e[MOE_MAX_PREFETCH];
     int32_t list_s[MOE_MAX_PREFETCH];
     int32_t n_list;
@@ -58,6 +64,7 @@ __device__ inline void load_table(const SlotTable* t, LdsTable& L, int lane) {
         L.resident[lane] = 0;
         L.pred[lane] = 0;
         L.fetched[lane] = 0;
+        L.spare[lane] = 0;
     }
     if (lane == 0) L.n_list = 0;
     if (lane < 18) L.stats[lane] = t->stats[lane];
@@ -101,14 +108,17 @@ __device__ inline void renorm(SlotTable* t, LdsTable& L, int lane, uint32_t& clo
     wave_sync();
 }
 
-// One victim for a slot allocation (uniform across the wave). Returns the slot.
-__device__ inline int take_slot(SlotTable* t, LdsTable& L, int lane, int& n_free, const uint32_t* protect) {
+// One victim for a slot allocation (uniform across the wave). Returns the slot.  When every
+// resident expert is protected, the oldest one not in `spare` (may be null) goes before the
+// oldest outright (the host table's rule, slot_table_host.h).
+__device__ inline int take_slot(SlotTable* t, LdsTable& L, int lane, int& n_free, const uint32_t* protect,
+                                const uint32_t* spare = nullptr) {
     if (n_free > 0) {
         --n_free;
         return t->free_stack[n_free];
     }
     const int cap = t->capacity;
-    uint64_t best = ~0ull, oldest = ~0ull;
+    uint64_t best = ~0ull, oldest = ~0ull, spared = ~0ull;
     for (int s = lane; s < cap; s += 64) {
         uint32_t st = L.stamp[s];
         if (!st) continue;
@@ -116,10 +126,12 @@ __device__ inline int take_slot(SlotTable* t, LdsTable& L, int lane, int& n_free
         oldest = key < oldest ? key : oldest;
         int e = L.eid_of[s];
         if (e >= 0 && !bit(protect, e)) best = key < best ? key : best;
+        if (spare && e >= 0 && !bit(spare, e)) spared = key < spared ? key : spared;
     }
     best = wave_min_u64(best);
     oldest = wave_min_u64(oldest);
-    uint64_t pick = (best != ~0ull) ? best : oldest;
+    spared = wave_min_u64(spared);
+    uint64_t pick = (best != ~0ull) ? best : (spared != ~0ull ? spared : oldest);
     int s = (int)(pick & 0xFFFFFFFFu);
     wave_sync();
     if (lane == 0 && pick != ~0ull) {
@@ -191,7 +203,10 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
         if (lane == 0) { t->status = 2; t->n_copy = 0; }
         return;
     }
-    if (e >= 0) atomicOr(&L.protect[e >> 5], 1u << (e & 31));
+    if (e >= 0) {
+        atomicOr(&L.protect[e >> 5], 1u << (e & 31));
+        atomicOr(&L.spare[e >> 5], 1u << (e & 31));
+    }
     wave_sync();
 
     const bool snap = t->snap_valid != 0;
@@ -238,10 +253,13 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
         L.list_e[rank] = e;
     }
     wave_sync();
+    if (t->sched && snap && lane < 16)       // in-flight prefetched experts are protected too
+        L.protect[lane] |= reinterpret_cast<const uint32_t*>(t->snap_fetched)[lane];
+    wave_sync();
 
     for (int r = 0; r < n_miss; ++r) {
         int me = L.list_e[r];
-        int s = take_slot(t, L, lane, n_free, L.protect);
+        int s = take_slot(t, L, lane, n_free, L.protect, L.spare);
         bind(L, lane, me, s, clock);
         if (lane == 0) L.list_s[r] = s;
     }
@@ -277,6 +295,11 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
 // Prefetch of expert_io.c:527-581 for m predictions (one wave).
 __device__ inline void dev_slot_prefetch(SlotTable* __restrict__ t, LdsTable& L, const int32_t* preds, int m, int max_fetch,
                                   int lane) {
+    const bool sched = t->sched != 0;
+    if (sched && max_fetch <= 0) {            // the scheduler variant prefetches nothing
+        if (lane == 0) { t->pf_n_copy = 0; t->status = 0; }
+        return;
+    }
     load_table(t, L, lane);
     uint32_t clock = t->clock;
     int n_free = t->n_free;
@@ -294,7 +317,7 @@ __device__ inline void dev_slot_prefetch(SlotTable* __restrict__ t, LdsTable& L,
             if (e < 0 || e >= MOE_NUM_EXPERTS) continue;
             L.pred[e >> 5] |= 1u << (e & 31);
             L.protect[e >> 5] |= 1u << (e & 31);
-            if (L.slot_of[e] < 0 && np < cap) {
+            if (L.slot_of[e] < 0 && np < cap && !(sched && bit(L.fetched, e))) {
                 L.list_e[np++] = e;
                 L.fetched[e >> 5] |= 1u << (e & 31);
             }

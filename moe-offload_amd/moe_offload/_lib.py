@@ -40,6 +40,14 @@ SIGNATURES: dict[str, tuple] = {
     "c_layer_set_lru_state": (None, [_c_int, _i32p, _i32p, _c_int, _c_u64, _c_u64, _c_u64]),
     "c_layer_get_stats": (None, [_c_int, _u64p]),
     "c_get_decode_totals": (None, [_c_int, _u64p]),
+    # superset ABI of the reference's C++ runner (cpp/src/expert_io.h)
+    "c_layer_decode_step_sched": (_c_int, [_c_int, _i32p, _c_int, _i32p, _c_int, _c_int, _c_int, _c_int]),
+    "c_layer_get_split_inds": (None, [_c_int, _u32p, _u32p, _i32p]),
+    "c_layer_wait_demand": (None, [_c_int]),
+    "c_set_io_accounting": (None, [_c_int]),
+    "c_begin_decode_token": (None, [_c_int]),
+    "c_end_decode_token": (None, [_u64p]),
+    "c_get_native_buffer_bytes": (_c_u64, []),
     # compute
     "moe_router": (_c_int, [_c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int,
                             _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
@@ -74,6 +82,8 @@ SIGNATURES: dict[str, tuple] = {
     "c_layer_grouped_switch_glu": (_c_int, [_c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_int, _c_vp,
                                             _c_vp, _c_vp]),
     "c_layer_set_device_mode": (_c_int, [_c_int, _c_int]),
+    "c_layer_set_sched": (_c_int, [_c_int, _c_int]),
+    "c_layer_switch_glu_split": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "c_layer_step_decode_dev": (_c_int, [_c_int, _c_vp, _c_int, _c_int, _c_vp]),
     "c_layer_start_prefetch_dev": (_c_int, [_c_int, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
     "c_layer_stage_dev": (_c_int, [_c_int, _c_int, _c_int, _c_vp]),

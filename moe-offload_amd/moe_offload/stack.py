@@ -55,6 +55,11 @@ class StackConfig:
     resident: bool = False       # every layer's experts in HBM (no slot tables, no staging)
     fused_tables: bool = True    # device mode: the router's last block runs the slot-table step
                                  # and the next layer's prefetch (no separate table launches)
+    sched: bool = False          # the C++ runner's scheduler variant (cpp/src/engine.cpp:700-730,
+                                 # cpp/third_party/expert_io.c:1094-1394): host mode makes one
+                                 # c_layer_decode_step_sched call per layer; device mode tables
+                                 # take the variant's decisions
+    split: bool = False          # host mode with sched: hit experts run before the misses land
 
 
 def random_blobs(n_exp: int, hidden: int, inter: int, group: int, gen: torch.Generator, device,
@@ -120,6 +125,8 @@ class DecodeStack:
             _lib.check(L.c_layer_set_format(li, c.hidden, c.inter, c.group), "set_format")
             if mode == "device":
                 _lib.check(L.c_layer_set_device_mode(li, 1), "set_device_mode")
+            if c.sched:
+                _lib.check(L.c_layer_set_sched(li, 1), "set_sched")
         _lib.check_error("c_layer_init")
         self._init_buffers()
 
@@ -290,6 +297,8 @@ class DecodeStack:
         L = self.L
         main = torch.cuda.current_stream()
         L.c_set_compute_stream(ctypes.c_void_p(main.cuda_stream))
+        if c.sched:
+            return self._decode_token_sched(main)
         for l in range(c.n_layers):
             self._router(l)
             if l == 0:
@@ -309,6 +318,45 @@ class DecodeStack:
         _lib.check_error("decode_token_host")
         _lib.check(L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
                                  c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), main.cuda_stream), "rmsnorm")
+
+    def _decode_token_sched(self, main):
+        """The runner's decode loop (cpp/src/engine.cpp:545-560,700-730): after the resident
+        layer 0 a prefetch-only call for layer 1, then per cached layer one
+        c_layer_decode_step_sched(l, ids, k, pred(l+1), m, l+1, cap, flags) -- step of l and
+        prefetch of l+1 in one call -- and the layer's SwitchGLU; with split, the hit experts
+        run first and the missed ones after their copies."""
+        c, L = self.cfg, self.L
+        m = c.top_m
+        pf_cap = c.prefetch_cap if c.prefetch else 0
+        stream = main.cuda_stream
+        for l in range(c.n_layers):
+            self._router(l)
+            if l == 0:
+                self._glu(0)
+                if c.prefetch and c.n_layers > 1:
+                    p = self.pred[0, :m].tolist()
+                    _lib.check(L.c_layer_decode_step_sched(0, None, 0, (ctypes.c_int32 * m)(*p), m, self.cidx(1),
+                                                           pf_cap, 0), "sched prefetch")
+                continue
+            sel = torch.cat([self.ids[l], self.pred[l, :m]]).tolist()      # the one sync per layer
+            ids, pred = sel[:c.top_k], sel[c.top_k:]
+            last = l + 1 >= c.n_layers or not c.prefetch
+            flags = (4 if c.split else 0) | (2 if last else 0)
+            n = L.c_layer_decode_step_sched(self.cidx(l), (ctypes.c_int32 * c.top_k)(*ids), c.top_k,
+                                            None if last else (ctypes.c_int32 * m)(*pred), 0 if last else m,
+                                            -1 if last else self.cidx(l + 1), pf_cap, flags)
+            _lib.check(n, "decode_step_sched")
+            if c.split and 0 < n < c.top_k:
+                for part in (0, 1):
+                    _lib.check(L.c_layer_switch_glu_split(self.cidx(l), part, self.xs[l].data_ptr(),
+                                                          self.scores[l].data_ptr(), self.xs[l].data_ptr(),
+                                                          self.h_ws.data_ptr(), self.hs[l].data_ptr(), stream),
+                               "switch_glu_split")
+            else:
+                self._glu(l)
+        _lib.check_error("decode_token_sched")
+        _lib.check(L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
+                                 c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), stream), "rmsnorm")
 
     def decode_token(self, x0: torch.Tensor | None = None) -> torch.Tensor:
         if x0 is not None:

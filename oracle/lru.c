@@ -21,6 +21,23 @@
  *   coalescing        187-276  (counters only) sort misses by eid, count contiguous runs
  * Expert bytes are a per-layer parameter here; the reference hard-codes 1,536,000.
  *
+ * Superset entry points of `mlx-qwen38/cpp/third_party/expert_io.c` (same decisions as above,
+ * plus the scheduler variant and per-token accounting):
+ *   sched step        1094-1394  one call per layer: decode step of `l` (skipped for l <= 0)
+ *                                whose victim choice also protects the experts the last
+ *                                prefetch of `l` fetched; optional split of the step's slots
+ *                                into hit / miss lists with the inverse order; then a prefetch
+ *                                of `next` (only when 0 < next, preds given, cap > 0 and not
+ *                                NO_PREFETCH) that skips repeated predictions
+ *   split lists       1062-1092  kept per layer until the next split (stale otherwise)
+ *   token accounting  1002-1038  10 per-token counters; evictions stamped with the token
+ *                                number (493-525), re-reads within 16 / 64 tokens counted
+ *                                when an evicted expert is loaded again (656-666, 756-768)
+ *   reset             551-574    layer 1's reset also restarts the token numbering
+ * "Bytes read" (out10[9]) is the staged byte count per expert set with
+ * o_layer_set_staged_bytes (0 for accounting-only layers, as the reference reports for
+ * zero-length reads).
+ *
  * Pinned by: golden traces written by the reference's own expert_io.c compiled from source
  * (tests/golden/make_lru_traces.py), the independent OrderedDict restatement in lru.py, and
  * invariants / brute force in tests/test_oracle_lru.py.
@@ -45,9 +62,39 @@ typedef struct {
     int snap_valid;
     uint64_t snap_resident[8], snap_pred[8], snap_fetched[8];
     uint64_t st[18];
+    int32_t evicted_at[O_NUM_EXPERTS];   /* token number of the last eviction, -1 = none */
+    uint64_t staged_bytes;               /* bytes one staged expert reads (accounting) */
 } OLayer;
 
 static OLayer g_o[O_MAX_LAYERS];
+
+/* scheduler split lists (per layer, kept until the next split) */
+static uint32_t g_hit_slots[O_MAX_LAYERS][16], g_miss_slots[O_MAX_LAYERS][16];
+static int32_t g_inv[O_MAX_LAYERS][16];
+static int g_n_hit[O_MAX_LAYERS], g_n_miss[O_MAX_LAYERS], g_split_k[O_MAX_LAYERS];
+
+/* per-token accounting */
+enum { A_LRU_HIT, A_MISS, A_PF_LOADS, A_PF_HITS, A_PF_WASTED, A_DEM_RE16, A_DEM_RE64, A_PF_RE16, A_PF_RE64,
+       A_BYTES };
+static int g_acct_on = 0;
+static int32_t g_token_seq = 0, g_cur_token = -1;
+static uint64_t g_tok[10];
+
+static void note_eviction(OLayer *L, int e) {
+    if (g_acct_on && g_cur_token >= 0) L->evicted_at[e] = g_cur_token;
+}
+
+/* An expert is being loaded again: count it as a re-read when it was evicted recently. */
+static void note_reload(OLayer *L, int e, int re16, int re64) {
+    if (!(g_acct_on && g_cur_token >= 0)) return;
+    int32_t ev = L->evicted_at[e];
+    if (ev >= 0 && g_cur_token >= ev) {
+        int32_t d = g_cur_token - ev;
+        if (d <= 16) g_tok[re16]++;
+        if (d <= 64) g_tok[re64]++;
+    }
+    L->evicted_at[e] = -1;
+}
 
 static int bm_has(const uint64_t *bm, int e) { return (int)((bm[e >> 6] >> (e & 63)) & 1ULL); }
 static void bm_set(uint64_t *bm, int e) { bm[e >> 6] |= 1ULL << (e & 63); }
@@ -77,17 +124,28 @@ static void bind(OLayer *L, int e, int s) {
     push_mru(L, s);
 }
 
-static int take_slot(OLayer *L, const uint64_t *protect) {
+/* `spare` (may be NULL): when every resident expert is protected, the fallback victim is the
+ * oldest one not in `spare` (the step's own ids) rather than the LRU end.  The reference takes
+ * the LRU end; that differs only when the LRU end is one of the step's ids, which the
+ * published step never reaches (k <= capacity) and where the scheduler step's later list
+ * operations index slot -1 (undefined behaviour in the reference). */
+static int take_slot(OLayer *L, const uint64_t *protect, const uint64_t *spare) {
     if (L->n_free > 0) return L->free_stack[--L->n_free];
     int s = L->lru_end;
     for (; s >= 0; s = L->newer[s]) {
         int e = L->eid_of[s];
         if (e >= 0 && !bm_has(protect, e)) break;
     }
+    if (s < 0 && spare) {
+        for (s = L->lru_end; s >= 0; s = L->newer[s]) {
+            int e = L->eid_of[s];
+            if (e >= 0 && !bm_has(spare, e)) break;
+        }
+    }
     if (s < 0) s = L->lru_end;            /* every resident expert is protected */
     int e = L->eid_of[s];
     unlink_slot(L, s);
-    if (e >= 0) L->slot_of[e] = -1;
+    if (e >= 0) { L->slot_of[e] = -1; note_eviction(L, e); }
     L->eid_of[s] = -1;
     return s;
 }
@@ -115,6 +173,12 @@ void o_layer_reset_cache(int l) {
     L->n_free = L->capacity;
     for (int i = 0; i < L->capacity; ++i) L->free_stack[i] = (int16_t)(L->capacity - 1 - i);
     L->snap_valid = 0;
+    for (int i = 0; i < O_NUM_EXPERTS; ++i) L->evicted_at[i] = -1;
+    if (l == 1) { g_token_seq = 0; g_cur_token = -1; }
+}
+
+void o_layer_set_staged_bytes(int l, uint64_t b) {
+    if (l >= 0 && l < O_MAX_LAYERS) g_o[l].staged_bytes = b;
 }
 
 void o_layer_reset_stats(int l) {
@@ -130,16 +194,18 @@ void o_layer_init(int l, int capacity, uint64_t expert_bytes) {
     o_layer_reset_cache(l);
 }
 
-/* Returns the number of misses; out_slots[k] gets every id's slot, miss_eids/miss_slots
- * (<= 16 each) the demand copies in allocation order. */
-int o_layer_step_decode(int l, const uint32_t *eids, int k, uint32_t *out_slots,
-                        int32_t *miss_eids, int32_t *miss_slots) {
-    if (l < 0 || l >= O_MAX_LAYERS) return 0;
-    OLayer *L = &g_o[l];
-    uint64_t want[8] = {0};
+/* Decode step shared by the published entry point and the scheduler variant.  `extra` (may be
+ * NULL) is OR-ed into the victim protection; is_hit[i] (may be NULL) records whether id i was
+ * resident when classified. */
+static int step_core(OLayer *L, const uint32_t *eids, int k, uint32_t *out_slots, int32_t *miss_eids,
+                     int32_t *miss_slots, const uint64_t *extra, uint8_t *is_hit) {
+    uint64_t want[8] = {0}, protect[8];
     int n_miss = 0;
     L->st[0] += (uint64_t)k;
     for (int i = 0; i < k; ++i) bm_set(want, (int)eids[i]);
+    for (int w = 0; w < 8; ++w) protect[w] = want[w] | (extra ? extra[w] : 0);
+    uint64_t fetched_total = 0, lru_h = 0, pref_h = 0;
+    const int had_snap = L->snap_valid;
     if (L->snap_valid) {
         for (int w = 0; w < 8; ++w) {
             uint64_t missing_before = want[w] & ~L->snap_resident[w];
@@ -149,21 +215,33 @@ int o_layer_step_decode(int l, const uint32_t *eids, int k, uint32_t *out_slots,
             L->st[13] += (uint64_t)__builtin_popcountll(missing_before & L->snap_fetched[w]);
             L->st[14] += (uint64_t)__builtin_popcountll(missing_before);
             L->st[15] += (uint64_t)__builtin_popcountll(L->snap_fetched[w]);
+            fetched_total += (uint64_t)__builtin_popcountll(L->snap_fetched[w]);
         }
     }
     for (int i = 0; i < k; ++i) {
         int e = (int)eids[i];
+        if (is_hit) is_hit[i] = L->slot_of[e] >= 0;
         if (L->slot_of[e] >= 0) {
-            if (!L->snap_valid || bm_has(L->snap_resident, e)) L->st[1]++;
-            else L->st[2]++;
+            if (!L->snap_valid || bm_has(L->snap_resident, e)) { L->st[1]++; lru_h++; }
+            else { L->st[2]++; pref_h++; }
         } else {
             L->st[3]++;
             miss_eids[n_miss++] = e;
         }
     }
+    if (g_acct_on) {
+        g_tok[A_LRU_HIT] += lru_h;
+        g_tok[A_MISS] += (uint64_t)n_miss;
+        if (had_snap) {
+            g_tok[A_PF_HITS] += pref_h;
+            if (fetched_total >= pref_h) g_tok[A_PF_WASTED] += fetched_total - pref_h;
+        }
+        g_tok[A_BYTES] += (uint64_t)n_miss * L->staged_bytes;
+    }
     L->snap_valid = 0;
     for (int i = 0; i < n_miss; ++i) {
-        int s = take_slot(L, want);
+        int s = take_slot(L, protect, want);
+        note_reload(L, miss_eids[i], A_DEM_RE16, A_DEM_RE64);
         bind(L, miss_eids[i], s);
         miss_slots[i] = s;
     }
@@ -177,11 +255,17 @@ int o_layer_step_decode(int l, const uint32_t *eids, int k, uint32_t *out_slots,
     return n_miss;
 }
 
-/* Returns the number of experts fetched; fetch_eids/fetch_slots (<= 32) in insertion order. */
-int o_layer_start_prefetch(int l, const int32_t *preds, int n, int max_fetch,
-                           int32_t *fetch_eids, int32_t *fetch_slots) {
+/* Returns the number of misses; out_slots[k] gets every id's slot, miss_eids/miss_slots
+ * (<= 16 each) the demand copies in allocation order. */
+int o_layer_step_decode(int l, const uint32_t *eids, int k, uint32_t *out_slots,
+                        int32_t *miss_eids, int32_t *miss_slots) {
     if (l < 0 || l >= O_MAX_LAYERS) return 0;
-    OLayer *L = &g_o[l];
+    return step_core(&g_o[l], eids, k, out_slots, miss_eids, miss_slots, NULL, NULL);
+}
+
+/* Prefetch shared by both entry points; `dedupe` skips a prediction already taken. */
+static int prefetch_core(OLayer *L, const int32_t *preds, int n, int max_fetch, int dedupe,
+                         int32_t *fetch_eids, int32_t *fetch_slots) {
     memset(L->snap_resident, 0, sizeof(L->snap_resident));
     memset(L->snap_pred, 0, sizeof(L->snap_pred));
     memset(L->snap_fetched, 0, sizeof(L->snap_fetched));
@@ -197,28 +281,94 @@ int o_layer_start_prefetch(int l, const int32_t *preds, int n, int max_fetch,
         if (e < 0 || e >= O_NUM_EXPERTS) continue;
         bm_set(L->snap_pred, e);
         bm_set(protect, e);
-        if (L->slot_of[e] < 0 && np < cap) {
+        if (L->slot_of[e] < 0 && np < cap && !(dedupe && bm_has(L->snap_fetched, e))) {
             pick[np++] = e;
             bm_set(L->snap_fetched, e);
         }
     }
     for (int i = 0; i < np; ++i) {
         int e = pick[np - 1 - i];
-        int s = take_slot(L, protect);
+        int s = take_slot(L, protect, NULL);
+        note_reload(L, e, A_PF_RE16, A_PF_RE64);
         bind(L, e, s);
         fetch_eids[i] = e;
         fetch_slots[i] = s;
+    }
+    if (g_acct_on) {
+        g_tok[A_PF_LOADS] += (uint64_t)np;
+        g_tok[A_BYTES] += (uint64_t)np * L->staged_bytes;
     }
     L->st[5] += (uint64_t)np * L->expert_bytes;
     count_runs(L, fetch_eids, np);
     return np;
 }
 
+/* Returns the number of experts fetched; fetch_eids/fetch_slots (<= 32) in insertion order. */
+int o_layer_start_prefetch(int l, const int32_t *preds, int n, int max_fetch,
+                           int32_t *fetch_eids, int32_t *fetch_slots) {
+    if (l < 0 || l >= O_MAX_LAYERS) return 0;
+    return prefetch_core(&g_o[l], preds, n, max_fetch, 0, fetch_eids, fetch_slots);
+}
+
+/* Scheduler entry point.  Returns the step's miss count (0 when the step is skipped);
+ * *n_fetch gets the prefetch's count (0 when skipped). */
+int o_layer_decode_step_sched(int l, const int32_t *eids, int k, const int32_t *pred, int n_pred, int next,
+                              int prefetch_cap, int flags, uint32_t *out_slots, int32_t *miss_eids,
+                              int32_t *miss_slots, int32_t *fetch_eids, int32_t *fetch_slots, int *n_fetch) {
+    int n_miss = 0;
+    *n_fetch = 0;
+    if (l > 0 && l < O_MAX_LAYERS && eids && k > 0) {
+        if (k > 16) k = 16;
+        OLayer *L = &g_o[l];
+        uint64_t extra[8] = {0};
+        if (L->snap_valid) memcpy(extra, L->snap_fetched, sizeof(extra));
+        uint32_t ids[16];
+        uint8_t hit[16];
+        for (int i = 0; i < k; ++i) ids[i] = (uint32_t)eids[i];
+        n_miss = step_core(L, ids, k, out_slots, miss_eids, miss_slots, extra, hit);
+        if ((flags & 4) && n_miss > 0 && n_miss < k) {
+            int h = 0, m = 0, n_hit = k - n_miss;
+            for (int i = 0; i < k; ++i) {
+                if (hit[i]) { g_hit_slots[l][h] = out_slots[i]; g_inv[l][i] = h++; }
+                else { g_miss_slots[l][m] = out_slots[i]; g_inv[l][i] = n_hit + m++; }
+            }
+            g_n_hit[l] = n_hit;
+            g_n_miss[l] = n_miss;
+            g_split_k[l] = k;
+        }
+    }
+    if (!(flags & 2) && next > 0 && next < O_MAX_LAYERS && pred && n_pred > 0 && prefetch_cap > 0)
+        *n_fetch = prefetch_core(&g_o[next], pred, n_pred, prefetch_cap, 1, fetch_eids, fetch_slots);
+    return n_miss;
+}
+
+/* Counts (n_hit, n_miss, k) of the stored split; lists copied when the pointers are non-null. */
+void o_layer_get_split_inds(int l, uint32_t *hit, uint32_t *miss, int32_t *inv, int *counts3) {
+    if (l < 0 || l >= O_MAX_LAYERS) return;
+    if (hit && g_n_hit[l] > 0) memcpy(hit, g_hit_slots[l], (size_t)g_n_hit[l] * sizeof(uint32_t));
+    if (miss && g_n_miss[l] > 0) memcpy(miss, g_miss_slots[l], (size_t)g_n_miss[l] * sizeof(uint32_t));
+    if (inv && g_split_k[l] > 0) memcpy(inv, g_inv[l], (size_t)g_split_k[l] * sizeof(int32_t));
+    if (counts3) { counts3[0] = g_n_hit[l]; counts3[1] = g_n_miss[l]; counts3[2] = g_split_k[l]; }
+}
+
+void o_set_io_accounting(int on) {
+    g_acct_on = on ? 1 : 0;
+    if (!g_acct_on) g_cur_token = -1;
+}
+
+void o_begin_decode_token(void) {
+    g_cur_token = g_token_seq++;
+    memset(g_tok, 0, sizeof(g_tok));
+}
+
+void o_end_decode_token(uint64_t *out10) { memcpy(out10, g_tok, sizeof(g_tok)); }
+
 void o_layer_load_sync(int l, const int32_t *eids, const int32_t *slots, int n, int is_prefill) {
     (void)slots;
     if (l < 0 || l >= O_MAX_LAYERS || n <= 0) return;
     OLayer *L = &g_o[l];
     if (is_prefill) L->st[9] += (uint64_t)n * L->expert_bytes;
+    if (g_acct_on) g_tok[A_BYTES] += (uint64_t)n * L->staged_bytes;
     count_runs(L, eids, n);
 }
 
@@ -239,7 +389,11 @@ void o_layer_set_lru_state(int l, const int32_t *eids, const int32_t *slots, int
     L->lru_end = L->mru_end = -1;
     L->snap_valid = 0;
     uint8_t used[O_NUM_EXPERTS] = {0};
-    for (int i = 0; i < n; ++i) { used[slots[i]] = 1; bind(L, eids[i], slots[i]); }
+    for (int i = 0; i < n; ++i) {
+        used[slots[i]] = 1;
+        if (eids[i] >= 0 && eids[i] < O_NUM_EXPERTS) L->evicted_at[eids[i]] = -1;
+        bind(L, eids[i], slots[i]);
+    }
     L->n_free = 0;
     for (int s = L->capacity - 1; s >= 0; --s) if (!used[s]) L->free_stack[L->n_free++] = (int16_t)s;
 }

@@ -47,6 +47,15 @@ def _load() -> ctypes.CDLL:
                                           ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64]
     lib.o_layer_get_stats.argtypes = [ctypes.c_int, u64p]
     lib.o_get_decode_totals.argtypes = [ctypes.c_int, u64p]
+    lib.o_layer_decode_step_sched.argtypes = [ctypes.c_int, i32p, ctypes.c_int, i32p, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_int, u32p, i32p, i32p, i32p, i32p,
+                                              ctypes.POINTER(ctypes.c_int)]
+    lib.o_layer_decode_step_sched.restype = ctypes.c_int
+    lib.o_layer_get_split_inds.argtypes = [ctypes.c_int, u32p, u32p, i32p, i32p]
+    lib.o_set_io_accounting.argtypes = [ctypes.c_int]
+    lib.o_begin_decode_token.argtypes = []
+    lib.o_end_decode_token.argtypes = [u64p]
+    lib.o_layer_set_staged_bytes.argtypes = [ctypes.c_int, ctypes.c_uint64]
     return lib
 
 
@@ -113,6 +122,61 @@ def decode_totals(num_layers: int):
     out = (ctypes.c_uint64 * 6)()
     lib().o_get_decode_totals(num_layers, out)
     return list(out)
+
+
+SCHED_SYNC_DEMAND, SCHED_NO_PREFETCH, SCHED_SPLIT = 1, 2, 4
+
+
+def decode_step_sched(layer, eids, pred, next_layer, prefetch_cap, flags):
+    """Scheduler entry point of the C restatement.
+
+    Returns (n_miss, slots of the step's ids, demand (eid, slot) pairs, prefetch (eid, slot) pairs).
+    `eids` / `pred` may be None (skipped step / no prefetch)."""
+    k = len(eids) if eids is not None else 0
+    n_pred = len(pred) if pred is not None else 0
+    ea = (ctypes.c_int32 * max(k, 1))(*(eids or []))
+    pa = (ctypes.c_int32 * max(n_pred, 1))(*(pred or []))
+    out = (ctypes.c_uint32 * 16)()
+    me, ms, fe, fs = ((ctypes.c_int32 * 32)() for _ in range(4))
+    nf = ctypes.c_int(0)
+    n = lib().o_layer_decode_step_sched(layer, ea if eids is not None else None, k,
+                                        pa if pred is not None else None, n_pred, next_layer, prefetch_cap,
+                                        flags, out, me, ms, fe, fs, ctypes.byref(nf))
+    kk = min(k, 16)
+    return n, list(out[:kk]), list(zip(me[:n], ms[:n])), list(zip(fe[:nf.value], fs[:nf.value]))
+
+
+def layer_stats(layer):
+    """The 18 counters of a layer of the C restatement."""
+    out = (ctypes.c_uint64 * 18)()
+    lib().o_layer_get_stats(layer, out)
+    return [int(v) for v in out]
+
+
+def split_inds(layer):
+    """(hit slots, miss slots, inverse order) stored by the last split of `layer`."""
+    h, m = (ctypes.c_uint32 * 16)(), (ctypes.c_uint32 * 16)()
+    inv, c = (ctypes.c_int32 * 16)(), (ctypes.c_int32 * 3)()
+    lib().o_layer_get_split_inds(layer, h, m, inv, c)
+    return list(h[:c[0]]), list(m[:c[1]]), list(inv[:c[2]])
+
+
+def set_io_accounting(on: bool):
+    lib().o_set_io_accounting(1 if on else 0)
+
+
+def begin_decode_token():
+    lib().o_begin_decode_token()
+
+
+def end_decode_token():
+    out = (ctypes.c_uint64 * 10)()
+    lib().o_end_decode_token(out)
+    return list(out)
+
+
+def set_staged_bytes(layer, nbytes):
+    lib().o_layer_set_staged_bytes(layer, nbytes)
 
 
 class PyLru:

@@ -9,6 +9,7 @@ import pytest
 
 from conftest import ROOT
 from moe_offload import _lib
+from sched_replay import TokenMixin, load, replay
 
 HEADER = ROOT / "include" / "moe_offload.h"
 
@@ -160,3 +161,103 @@ def test_stamp_renormalisation_keeps_order():
         assert s1 == s2 and n1 == len(m2)
     assert L.state() == [list(v) for v in O.get_state()]
     assert L.stats()[:16] == O.stats()[:16]
+
+
+class ProductSched(TokenMixin):
+    """The product library's expert-cache ABI (host tables, accounting-only layers) in the shape
+    the scheduler replay expects (tests/sched_replay.py)."""
+
+    def __init__(self):
+        super().__init__()
+        self.L = _lib.lib()
+        self.layers = {}
+
+    def init(self, l, cap):
+        self.layers[l] = CLayer(l, cap)
+
+    def reset_stats(self, l):
+        self.L.c_layer_reset_stats(l)
+
+    def reset_cache(self, l):
+        self.L.c_layer_reset_cache(l)
+
+    def accounting(self, on):
+        self.L.c_set_io_accounting(1 if on else 0)
+
+    def begin(self):
+        self.L.c_begin_decode_token(0)
+
+    def end(self):
+        o = (ctypes.c_uint64 * 10)()
+        self.L.c_end_decode_token(o)
+        return list(o)
+
+    def sched(self, l, ids, preds, nxt, cap, flags):
+        k = len(ids) if ids is not None else 0
+        ia = (ctypes.c_int32 * max(k, 1))(*(ids or []))
+        npred = len(preds) if preds is not None else 0
+        pa = (ctypes.c_int32 * max(npred, 1))(*(preds or []))
+        n = self.L.c_layer_decode_step_sched(l, ia if ids is not None else None, k,
+                                             pa if preds is not None else None, npred, nxt, cap, flags)
+        _lib.check(n, "decode_step_sched")
+        self.L.c_layer_wait_demand(l)
+        slots = list(self.layers[l].slot_buf[:min(k, 16)]) if (l in self.layers and ids is not None) else []
+        return n, slots
+
+    def step(self, l, ids):
+        slots, n = self.layers[l].step(ids)
+        return n, slots
+
+    def prefetch(self, l, preds, cap):
+        self.layers[l].prefetch(preds, cap)
+
+    def stats(self, l):
+        return self.layers[l].stats()
+
+    def state(self, l):
+        return self.layers[l].state()
+
+    def set_state(self, l, e, s, add):
+        self.layers[l].set_state(e, s, *add)
+
+    def split(self, l):
+        h = (ctypes.c_uint32 * 16)(*([0xFFFFFFFF] * 16))
+        m = (ctypes.c_uint32 * 16)(*([0xFFFFFFFF] * 16))
+        inv = (ctypes.c_int32 * 16)(*([-7] * 16))
+        self.L.c_layer_get_split_inds(l, h, m, inv)
+        return [[v for v in h if v != 0xFFFFFFFF], [v for v in m if v != 0xFFFFFFFF], [v for v in inv if v != -7]]
+
+    def totals(self, n_layers):
+        o = (ctypes.c_uint64 * 6)()
+        self.L.c_get_decode_totals(n_layers, o)
+        return list(o)
+
+
+def test_host_scheduler_entry_point_reproduces_reference_traces():
+    """c_layer_decode_step_sched / c_layer_get_split_inds / per-token accounting of the product
+    against the traces of the reference's cpp/third_party/expert_io.c."""
+    for sc in load()["scenarios"]:
+        assert replay(sc, ProductSched()) > 50, sc["name"]
+    assert _lib.last_error() == ""
+
+
+def test_scheduler_entry_point_input_rules():
+    lib = _lib.lib()
+    L = CLayer(43, 16)
+    ids = (ctypes.c_int32 * 10)(*range(10))
+    # layer 0 (resident) is never stepped: only the prefetch of next_layer happens
+    assert lib.c_layer_decode_step_sched(0, ids, 10, ids, 10, 43, 3, 0) == 0
+    assert L.stats()[0] == 0 and L.stats()[5] == 3 * 1_536_000
+    # prefetch_cap 0 prefetches nothing (the published entry point would take 32)
+    before = L.stats()
+    assert lib.c_layer_decode_step_sched(0, None, 0, ids, 10, 43, 0, 0) == 0
+    assert L.stats() == before
+    # a repeated id is rejected and changes nothing
+    bad = (ctypes.c_int32 * 10)(*([1] + list(range(1, 10))))
+    assert lib.c_layer_decode_step_sched(43, bad, 10, None, 0, -1, 0, 0) == -1
+    lib.c_clear_error()
+    assert L.stats() == before
+    # k > 16 is cut to 16, as in the reference
+    many = (ctypes.c_int32 * 20)(*range(100, 120))
+    assert lib.c_layer_decode_step_sched(43, many, 20, None, 0, -1, 0, 0) == 16
+    assert L.stats()[0] == 16

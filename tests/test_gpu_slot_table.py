@@ -79,6 +79,101 @@ def test_device_table_replays_reference_traces(L, lru_traces):
         assert L.c_layer_table_status(layer) == 0
 
 
+class DeviceSched:
+    """Device-driven tables in scheduler mode, driven with the golden scheduler traces: the
+    step and the next layer's prefetch of a c_layer_decode_step_sched call run as the device
+    table kernels (published ops of the mixed scenario with scheduler mode switched off).
+    Miss counts are read as the change of the layer's demand-miss counter."""
+
+    def __init__(self, lib, base):
+        self.L, self.base = lib, base
+        self.slots, self.misses = {}, {}
+        self.stream = torch.cuda.current_stream().cuda_stream
+
+    def begin_if_needed(self):
+        pass
+
+    def token_done(self):
+        pass
+
+    def init(self, l, cap):
+        self.slots[l] = torch.zeros(16, dtype=torch.int32, device="cuda")
+        _init_layer(self.L, self.base + l, cap, slot_ptr=self.slots[l].data_ptr())
+        assert self.L.c_layer_set_device_mode(self.base + l, 1) == 0
+        assert self.L.c_layer_set_sched(self.base + l, 1) == 0
+        self.misses[l] = 0
+
+    def reset_stats(self, l):
+        self.L.c_layer_reset_stats(self.base + l)
+        self.misses[l] = 0
+
+    def reset_cache(self, l):
+        self.L.c_layer_reset_cache(self.base + l)
+
+    def accounting(self, on):
+        pass
+
+    def _step(self, l, ids):
+        t = torch.tensor(ids, dtype=torch.int32, device="cuda")
+        assert self.L.c_layer_step_decode_dev(self.base + l, t.data_ptr(), len(ids), 0, self.stream) == 0
+        _check(self.L)
+        m = self.stats(l)[3]
+        n, self.misses[l] = m - self.misses[l], m
+        return n, self.slots[l][:len(ids)].cpu().tolist()
+
+    def _prefetch(self, l, preds, cap):
+        p = torch.tensor(preds, dtype=torch.int32, device="cuda")
+        assert self.L.c_layer_start_prefetch_dev(self.base + l, p.data_ptr(), len(preds), cap, 0, self.stream) == 0
+        _check(self.L)
+
+    def sched(self, l, ids, preds, nxt, cap, flags):
+        n, slots = (self._step(l, ids) if (l > 0 and ids) else (0, []))
+        if not (flags & 2) and nxt > 0 and preds:
+            self._prefetch(nxt, preds, cap)
+        return n, slots
+
+    def _published(self, l, fn):
+        assert self.L.c_layer_set_sched(self.base + l, 0) == 0
+        out = fn()
+        assert self.L.c_layer_set_sched(self.base + l, 1) == 0
+        return out
+
+    def step(self, l, ids):
+        return self._published(l, lambda: self._step(l, ids))
+
+    def prefetch(self, l, preds, cap):
+        self._published(l, lambda: self._prefetch(l, preds, cap))
+
+    def stats(self, l):
+        return _stats(self.L, self.base + l)
+
+    def state(self, l):
+        return _state(self.L, self.base + l)
+
+    def set_state(self, l, e, s, add):
+        self.L.c_layer_set_lru_state(self.base + l, (ctypes.c_int32 * max(1, len(e)))(*e),
+                                     (ctypes.c_int32 * max(1, len(s)))(*s), len(e), *add)
+
+    def split(self, l):
+        raise AssertionError("split lists are not compared for device tables")
+
+    def totals(self, n_layers):
+        t = [0] * 6
+        for l in range(1, n_layers):
+            st = self.stats(l)
+            for i, w in enumerate((1, 2, 3, 0, 4, 5)):     # c_get_decode_totals' order
+                t[i] += st[w]
+        return t
+
+
+def test_device_tables_replay_reference_scheduler_traces(L):
+    """Scheduler-mode device tables (decisions only: split lists and per-token accounting are
+    host-path features) against the reference's cpp/third_party/expert_io.c traces."""
+    from sched_replay import load, replay
+    for i, sc in enumerate(load()["scenarios"]):
+        assert replay(sc, DeviceSched(L, 10 * i), check_split=False, check_tokens=False) > 50, sc["name"]
+
+
 def test_device_table_rejects_bad_ids(L):
     stream = torch.cuda.current_stream().cuda_stream
     slots = torch.zeros(16, dtype=torch.int32, device="cuda")
