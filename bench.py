@@ -49,6 +49,9 @@ def parse():
     ap.add_argument("--extras", action="store_true", help="add per-kernel and cache details to the JSON line")
     ap.add_argument("--stage-ctas", type=int, default=2, help="staging blocks per copied expert")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill grouped-GEMM pass")
+    ap.add_argument("--sched", action="store_true",
+                    help="the C++ runner's scheduler variant of the expert cache (c_layer_decode_step_sched)")
+    ap.add_argument("--split", action="store_true", help="with --sched --mode host: hit experts before misses land")
     ap.add_argument("--only", choices=["headline", "resident", "prefill", "calib", "floor"], default=None,
                     help="run one pass and print its own JSON line (for sweeps and profiling); "
                          "calib runs the known-size copy kernel used to scale memory counters")
@@ -334,7 +337,7 @@ def main():
 
     # ---- headline: 20% cache, misses staged from the pinned host store ---------------------
     cfg = StackConfig(n_layers=args.layers, budget_pct=args.budget_pct, prefetch=not args.no_prefetch,
-                      stage_ctas=args.stage_ctas)
+                      stage_ctas=args.stage_ctas, sched=args.sched, split=args.split)
     if args.only == "resident":
         res = resident_pass(args, cfg, gen, n_tok)
         print(json.dumps({"resident": {k: v for k, v in res.items() if not k.startswith("_")}}), flush=True)
@@ -354,7 +357,9 @@ def main():
     del st
     torch.cuda.empty_cache()
     if args.only == "headline":
-        print(json.dumps({"value": round(tok_s, 2), "stage_ctas": args.stage_ctas,
+        print(json.dumps({"value": round(tok_s, 2), "driver": args.mode + ("+graph" if use_graph else ""),
+                          "sched": args.sched, "split": args.split, "stage_ctas": args.stage_ctas,
+                          "effective_hit_rate": round((tot1[0] - tot0[0] + tot1[1] - tot0[1]) / req, 4),
                           "staged_gb_per_s": round(staged / elapsed / 1e9, 2),
                           "headline_kernels_us": {k: round(v["avg_us"], 2) for k, v in (head_k or {}).items()
                                                   if v["launches"]}}), flush=True)
