@@ -116,7 +116,8 @@ def timed_tokens(st, xs, warmup, steps, use_graph):
     return elapsed, tot0, st.decode_totals()
 
 
-KINDS = ["router", "gate_up", "down", "stage", "slot_table", "grouped_gate_up", "grouped_down", "pair_combine"]
+KINDS = ["router", "gate_up", "down", "stage", "slot_table", "grouped_gate_up", "grouped_down", "pair_combine",
+         "cb_up", "cb_down"]
 
 
 def timed_kernels(run, calls, launches_per_call):

@@ -175,6 +175,25 @@ int moe_q2_grouped_switch_glu(const void* x, int n_tokens, const int32_t* row_to
 int moe_pair_combine(const void* y, const void* scores, const void* residual, int n_tokens, int k,
                      int hidden, float* out, void* stream);
 
+/* 2-bit codebook experts: the Nemotron model of README.md:37 (IQ2_XXS GGUF, 240 experts, top-9),
+ * run by the reference only inside llama.cpp's Metal backend (llama-moe-cache.patch:1-12 adds the
+ * mul_mm_id map for 9 experts per token; format in csrc/moe_common.h CbLayout): non-gated up ->
+ * squared ReLU -> down.
+ * grid: device uint8 [256][8] magnitudes (the workload's seeded grid holds {1, 3, 5}).
+ * hidden, inter multiples of 256 (hidden <= 4096, inter <= 2048); k * inter * 2 <= 48 KiB. */
+uint64_t moe_cb_expert_bytes(int hidden, int inter);
+/* h_out bf16 [k][inter] = relu(U_j x)^2 for x fp16 [hidden]; a slot id >= n_slots yields 0. */
+int moe_cb_up(const void* x, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots, int k,
+              int hidden, int inter, const void* grid, void* h_out, void* stream);
+/* per_expert 0: y_out fp32 [hidden] = residual + sum_j scores[j] * D_j h_j; 1: rows y_out[k][hidden]. */
+int moe_cb_down(const void* h, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots,
+                const void* scores, int k, int hidden, int inter, const void* grid, const void* residual,
+                float* y_out, int per_expert, void* stream);
+/* Both of the above (h_ws: k*inter bf16 workspace). */
+int moe_cb_moe(const void* x, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots,
+               const void* scores, int k, int hidden, int inter, const void* grid, const void* residual,
+               void* h_ws, float* y_out, int per_expert, void* stream);
+
 /* ---- Part 3: no counterpart in the reference ----------------------------------------------- */
 
 /* Last recorded failure ("" if none) / clear it. */
@@ -240,9 +259,10 @@ int c_layer_table_status(int layer_idx);
 int c_sync_copies(void);
 /* Per-kernel timing: launches between begin and end are dispatched with start/stop events
  * stamped at the kernel's own begin/end; end() sums durations per kind (0 router, 1 gate/up,
- * 2 down, 3 staging, 4 slot table, 5 grouped gate/up, 6 grouped down, 7 pair combine) into
- * out_ms[MOE_TIMING_KINDS] and counts into out_n[MOE_TIMING_KINDS]. */
-#define MOE_TIMING_KINDS 8
+ * 2 down, 3 staging, 4 slot table, 5 grouped gate/up, 6 grouped down, 7 pair combine,
+ * 8 codebook up, 9 codebook down) into out_ms[MOE_TIMING_KINDS] and counts into
+ * out_n[MOE_TIMING_KINDS]. */
+#define MOE_TIMING_KINDS 10
 int c_timing_begin(int capacity);
 int c_timing_end(double* out_ms, int* out_n);
 /* Plain device-to-device copy of `bytes` (multiple of 16): the known-size reference for scaling

@@ -893,6 +893,33 @@ int moe_q2_grouped_switch_glu(const void* x, int n_tokens, const int32_t* row_to
                                hidden, inter, group, y_out, stream);
 }
 
+uint64_t moe_cb_expert_bytes(int hidden, int inter) {
+    if (hidden <= 0 || inter <= 0 || hidden % 256 || inter % 256) return 0;
+    return cb_layout(hidden, inter).bytes;
+}
+
+int moe_cb_up(const void* x, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots, int k, int hidden,
+              int inter, const void* grid, void* h_out, void* stream) {
+    return launch_cb_up((const __half*)x, (const uint8_t*)pool, stride, n_slots, slots, k, hidden, inter,
+                        (const uint8_t*)grid, (uint16_t*)h_out, (hipStream_t)stream);
+}
+
+int moe_cb_down(const void* h, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots,
+                const void* scores, int k, int hidden, int inter, const void* grid, const void* residual, float* y_out,
+                int per_expert, void* stream) {
+    return launch_cb_down((const uint16_t*)h, (const uint8_t*)pool, stride, n_slots, slots, (const __half*)scores, k,
+                          hidden, inter, (const uint8_t*)grid, (const __half*)residual, y_out, per_expert,
+                          (hipStream_t)stream);
+}
+
+int moe_cb_moe(const void* x, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots,
+               const void* scores, int k, int hidden, int inter, const void* grid, const void* residual, void* h_ws,
+               float* y_out, int per_expert, void* stream) {
+    if (moe_cb_up(x, pool, stride, n_slots, slots, k, hidden, inter, grid, h_ws, stream)) return -1;
+    return moe_cb_down(h_ws, pool, stride, n_slots, slots, scores, k, hidden, inter, grid, residual, y_out, per_expert,
+                       stream);
+}
+
 int moe_pair_combine(const void* y, const void* scores, const void* residual, int n_tokens, int k, int hidden,
                      float* out, void* stream) {
     return launch_pair_combine((const __half*)y, (const __half*)scores, (const __half*)residual, n_tokens, k, hidden, out,

@@ -48,6 +48,29 @@ static inline __host__ __device__ BlobLayout blob_layout(int hidden, int inter, 
     return L;
 }
 
+// 2-bit codebook expert blob (IQ2_XXS-style super-blocks of 256 weights, seeded 256-entry grid):
+//   up_qs [I][H/256][8][8 B] | down_qs [H][I/256][8][8 B] | up_d [I][H/256] fp16 | down_d [H][I/256] fp16
+// Each 8-byte sub-block entry (32 weights) = 4 grid indices (one per 8-weight group) and a u32
+// aux = sign7_0 | sign7_1 << 7 | sign7_2 << 14 | sign7_3 << 21 | sub_scale << 28.
+struct CbLayout {
+    int hidden, inter;
+    size_t up_qs, down_qs, up_d, down_d, bytes;
+};
+
+static inline __host__ __device__ CbLayout cb_layout(int hidden, int inter) {
+    CbLayout L;
+    L.hidden = hidden;
+    L.inter = inter;
+    const size_t uq = (size_t)inter * (hidden / 256) * 64, dq = (size_t)hidden * (inter / 256) * 64;
+    const size_t ud = (size_t)inter * (hidden / 256) * 2, dd = (size_t)hidden * (inter / 256) * 2;
+    L.up_qs = 0;
+    L.down_qs = uq;
+    L.up_d = uq + dq;
+    L.down_d = uq + dq + ud;
+    L.bytes = uq + dq + ud + dd;
+    return L;
+}
+
 // Per-layer slot table.  The reference keeps a doubly linked list over slots
 // (mlx-qwen38/expert_io.c:43-91); this keeps the same order as recency stamps: a resident
 // slot carries stamp > 0, the LRU end is the smallest stamp, moving a slot to the MRU end
@@ -117,7 +140,8 @@ void moe_set_error(const char* fmt, ...);
 // Optional per-launch kernel timing: when enabled, launchers dispatch through
 // hipExtLaunchKernelGGL with a start/stop event pair, which the runtime stamps at the kernel's
 // own begin/end; kinds index the accumulated totals.
-enum { TK_ROUTER = 0, TK_GATE_UP, TK_DOWN, TK_STAGE, TK_SLOT, TK_PF_GATE_UP, TK_PF_DOWN, TK_COMBINE, TK_KINDS };
+enum { TK_ROUTER = 0, TK_GATE_UP, TK_DOWN, TK_STAGE, TK_SLOT, TK_PF_GATE_UP, TK_PF_DOWN, TK_COMBINE, TK_CB_UP,
+       TK_CB_DOWN, TK_KINDS };
 bool kt_enabled();
 void kt_events(int kind, hipEvent_t* start, hipEvent_t* stop);   // both null when disabled / full
 
@@ -168,5 +192,10 @@ int launch_q2_grouped_down(const __half* h, int n_rows, const int32_t* row_out, 
                            const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
                            const uint8_t* pool, size_t stride, int n_slots, int hidden, int inter,
                            int group, __half* y_out, hipStream_t s);
+int launch_cb_up(const __half* x, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots, int k,
+                 int hidden, int inter, const uint8_t* grid, uint16_t* h_out, hipStream_t s);
+int launch_cb_down(const uint16_t* h, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots,
+                   const __half* scores, int k, int hidden, int inter, const uint8_t* grid, const __half* residual,
+                   float* y_out, int per_expert, hipStream_t s);
 int launch_pair_combine(const __half* y, const __half* scores, const __half* residual, int n_tokens,
                         int k, int hidden, float* out, hipStream_t s);

@@ -67,6 +67,12 @@ SIGNATURES: dict[str, tuple] = {
                                      _c_int, _c_int, _c_int, _c_vp, _c_vp]),
     "moe_q2_grouped_switch_glu": (_c_int, [_c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_vp,
                                            _c_u64, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    "moe_cb_expert_bytes": (_c_u64, [_c_int, _c_int]),
+    "moe_cb_up": (_c_int, [_c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
+    "moe_cb_down": (_c_int, [_c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
+                             _c_int, _c_vp]),
+    "moe_cb_moe": (_c_int, [_c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
+                            _c_vp, _c_int, _c_vp]),
     "moe_pair_combine": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
     # no reference counterpart
     "c_last_error": (ctypes.c_char_p, []),

@@ -168,3 +168,38 @@ def pair_combine(y, scores, residual=None, out=None):
     rc = _lib.lib().moe_pair_combine(_p(y), _p(scores), _p(residual), n_tok, k, hidden, _p(out), _stream())
     _lib.check(rc, "moe_pair_combine")
     return out
+
+
+# ---- 2-bit codebook experts (non-gated: up -> squared ReLU -> down) ---------------------------
+
+def cb_moe(x: torch.Tensor, pool: torch.Tensor, slots: torch.Tensor, grid: torch.Tensor, hidden: int, inter: int,
+           scores: torch.Tensor | None = None, residual: torch.Tensor | None = None, per_expert: bool = False,
+           h_ws: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """Codebook experts pool[slots[j]] (format of moe_offload.cbformat) for one token.
+
+    Returns fp32 [hidden] = residual + sum_j scores[j] * down_j(relu(up_j x)^2), or fp32
+    [k, hidden] per-expert outputs when per_expert.  grid: device uint8 [256, 8]."""
+    k = slots.numel()
+    assert x.dtype == torch.float16 and x.numel() == hidden and x.is_contiguous()
+    assert pool.dtype == torch.uint8 and pool.dim() == 2 and pool.is_contiguous()
+    assert slots.dtype == torch.int32 and slots.is_contiguous()
+    assert grid.dtype == torch.uint8 and grid.numel() == 256 * 8 and grid.is_cuda
+    dev = x.device
+    if h_ws is None:
+        h_ws = torch.empty(k * inter, dtype=torch.bfloat16, device=dev)
+    if out is None:
+        out = torch.empty((k, hidden) if per_expert else (hidden,), dtype=torch.float32, device=dev)
+    rc = _lib.lib().moe_cb_moe(_p(x), _p(pool), pool.shape[1], pool.shape[0], _p(slots), _p(scores), k, hidden, inter,
+                               _p(grid), _p(residual), _p(h_ws), _p(out), int(per_expert), _stream())
+    _lib.check(rc, "moe_cb_moe")
+    return out
+
+
+def cb_up(x, pool, slots, grid, hidden, inter, h_out=None):
+    """bf16 [k, inter] = relu(up_j x)^2."""
+    k = slots.numel()
+    h_out = h_out if h_out is not None else torch.empty((k, inter), dtype=torch.bfloat16, device=x.device)
+    rc = _lib.lib().moe_cb_up(_p(x), _p(pool), pool.shape[1], pool.shape[0], _p(slots), k, hidden, inter, _p(grid),
+                              _p(h_out), _stream())
+    _lib.check(rc, "moe_cb_up")
+    return h_out
