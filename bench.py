@@ -52,7 +52,7 @@ def parse():
     ap.add_argument("--sched", action="store_true",
                     help="the C++ runner's scheduler variant of the expert cache (c_layer_decode_step_sched)")
     ap.add_argument("--split", action="store_true", help="with --sched --mode host: hit experts before misses land")
-    ap.add_argument("--only", choices=["headline", "resident", "prefill", "calib", "floor"], default=None,
+    ap.add_argument("--only", choices=["headline", "resident", "prefill", "calib", "floor", "nemotron"], default=None,
                     help="run one pass and print its own JSON line (for sweeps and profiling); "
                          "calib runs the known-size copy kernel used to scale memory counters")
     return ap.parse_args()
@@ -302,6 +302,67 @@ def resident_pass(args, cfg, gen, n_tok, xs=None):
             "_routed": routed, "_elapsed": r_elapsed}
 
 
+def nemotron_pass(steps=64, warmup=8, layers=40):
+    """The codebook workload (40 layers, 240 experts, top-9, hidden 3072, inter 1536, Zipf(1.0)
+    routing): every expert resident (the kernels' roofline), then a 4 GiB HBM expert cache fed
+    from the pinned host store."""
+    import torch
+
+    from moe_offload import cbformat
+    from moe_offload.cbstack import CbStackConfig, CodebookStack, zipf_routing
+
+    n_tok = warmup + steps
+    out = {}
+    base = CbStackConfig(n_layers=layers)
+    ids, sc = zipf_routing(n_tok, layers, base.n_exp, base.top_k, base.zipf_s, seed=77)
+    ids_d, sc_d = torch.from_numpy(ids).cuda(), torch.from_numpy(sc).cuda()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4321)
+    xs = torch.randn((n_tok, base.hidden), device="cuda", generator=gen).half()
+    o = cbformat.blob_offsets(base.hidden, base.inter)
+    up_bytes = base.top_k * ((o["down_qs"] - o["up_qs"]) + (o["down_d"] - o["up_d"]))
+    dn_bytes = base.top_k * ((o["up_d"] - o["down_qs"]) + (o["bytes"] - o["down_d"]))
+    for resident in (True, False):
+        t0 = time.perf_counter()
+        st = CodebookStack(CbStackConfig(n_layers=layers, resident=resident))
+        setup = time.perf_counter() - t0
+        st.capture_graph()
+        for i in range(warmup):
+            st.decode_token(xs[i], ids_d[i], sc_d[i])
+        torch.cuda.synchronize()
+        tot0 = st.totals()
+        t0 = time.perf_counter()
+        for i in range(warmup, n_tok):
+            st.decode_token(xs[i], ids_d[i], sc_d[i])
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        tot1 = st.totals()
+        rec = {"tok_s": round(steps / el, 2), "ms_per_token": round(el / steps * 1e3, 3), "setup_s": round(setup, 1)}
+        if resident:
+            st.graph = None
+            k = timed_kernels(lambda i: st.decode_token(xs[warmup + i], ids_d[warmup + i], sc_d[warmup + i]),
+                              min(steps, 16), layers * 4)
+            up_us, dn_us = k["cb_up"]["avg_us"], k["cb_down"]["avg_us"]
+            rec.update({"routed_gb_per_s": round(st.routed_bytes_per_token() * steps / el / 1e9, 1),
+                        "cb_up_us": round(up_us, 3), "cb_up_gb_s": round(up_bytes / up_us / 1e3, 1),
+                        "cb_down_us": round(dn_us, 3), "cb_down_gb_s": round(dn_bytes / dn_us / 1e3, 1),
+                        "cb_up_bytes_per_launch": up_bytes, "cb_down_bytes_per_launch": dn_bytes})
+        else:
+            req = max(1, tot1[3] - tot0[3])
+            staged = (tot1[4] - tot0[4]) + (tot1[5] - tot0[5])
+            rec.update({"slots_per_layer": st.capacity, "hit_rate": round((tot1[0] - tot0[0]) / req, 4),
+                        "staged_mb_per_token": round(staged / steps / 1e6, 1),
+                        "staged_gb_per_s": round(staged / el / 1e9, 2)})
+        out["resident" if resident else "cache_4gib"] = rec
+        st.close()
+        del st
+        torch.cuda.empty_cache()
+    out["workload"] = (f"{layers}-layer codebook-expert decode: {base.n_exp} experts, top-{base.top_k}, hidden "
+                       f"{base.hidden}, non-gated inter {base.inter} (squared ReLU), 2-bit codebook (IQ2_XXS-style, "
+                       f"seeded grid), Zipf({base.zipf_s:g}) routing, batch 1, {steps} tokens")
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -316,6 +377,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.only == "prefill":
         print(json.dumps({"prefill": prefill_pass()}), flush=True)
+        return
+    if args.only == "nemotron":
+        print(json.dumps({"nemotron": nemotron_pass()}), flush=True)
         return
     if args.only == "floor":
         fl = launch_floor([3_276_800, 6_553_600, 9_830_400, 64 << 20])
