@@ -180,7 +180,7 @@ int moe_pair_combine(const void* y, const void* scores, const void* residual, in
  * mul_mm_id map for 9 experts per token; format in csrc/moe_common.h CbLayout): non-gated up ->
  * squared ReLU -> down.
  * grid: device uint8 [256][8] magnitudes (the workload's seeded grid holds {1, 3, 5}).
- * hidden, inter multiples of 256 (hidden <= 4096, inter <= 2048); k * inter * 2 <= 48 KiB. */
+ * hidden, inter multiples of 256 (hidden <= 4096, inter <= 2048), k <= 16. */
 uint64_t moe_cb_expert_bytes(int hidden, int inter);
 /* h_out bf16 [k][inter] = relu(U_j x)^2 for x fp16 [hidden]; a slot id >= n_slots yields 0. */
 int moe_cb_up(const void* x, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots, int k,

@@ -19,8 +19,9 @@
 //                 grid (inter / 32, k).  h = relu(u)^2 is written as bf16 [k][inter] (fp32
 //                 range: a square can exceed fp16).
 //   k_cb_down<T>: 16 lanes per row, 8 output rows per block x all k experts (4 waves split the
-//                 experts); h is staged in LDS; the block reduces over experts in a fixed order
-//                 and writes y = residual + sum_j s_j y_j (fp32) or the per-expert rows.
+//                 experts, the next expert's codes and h slice loaded while the current one is
+//                 multiplied); the block reduces over experts in a fixed order and writes
+//                 y = residual + sum_j s_j y_j (fp32) or the per-expert rows.
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
 
@@ -41,39 +42,50 @@ __device__ __forceinline__ uint32_t mag_bits(uint32_t v, bool bf16) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)v);
 }
 
-// gtab[e] = the 8 magnitudes of grid entry e as halves (fp16 or bf16), in weight order;
+// gtab[e] = the 8 magnitudes of grid entry e as halves (fp16 or bf16), in weight order, built by
+// thread e from its grid entry g (loaded early by the caller: 256 threads, one entry each);
 // stab[s7] = the sign bit (bit 15 of a half) of each of the 8 weights for sign7 = s7.
-__device__ __forceinline__ void build_tables(const uint8_t* __restrict__ grid, uint4* gtab, uint4* stab, int tid,
-                                             bool bf16) {
-    for (int e = tid; e < 256; e += blockDim.x) {
-        const uint2 g = reinterpret_cast<const uint2*>(grid)[e];
-        uint32_t w[4];
+__device__ __forceinline__ void build_tables(uint2 g, uint4* gtab, uint4* stab, int tid, bool bf16) {
+    uint32_t w[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t src = k < 2 ? g.x : g.y;
-            const uint32_t lo = (src >> (16 * (k & 1))) & 0xFF, hi = (src >> (16 * (k & 1) + 8)) & 0xFF;
-            w[k] = mag_bits(lo, bf16) | (mag_bits(hi, bf16) << 16);
-        }
-        gtab[e] = make_uint4(w[0], w[1], w[2], w[3]);
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t src = k < 2 ? g.x : g.y;
+        const uint32_t lo = (src >> (16 * (k & 1))) & 0xFF, hi = (src >> (16 * (k & 1) + 8)) & 0xFF;
+        w[k] = mag_bits(lo, bf16) | (mag_bits(hi, bf16) << 16);
     }
-    for (int s = tid; s < 128; s += blockDim.x) {
-        const uint32_t s8 = (uint32_t)s | ((uint32_t)(__popc(s) & 1) << 7);
+    gtab[tid] = make_uint4(w[0], w[1], w[2], w[3]);
+    if (tid < 128) {
+        const uint32_t s8 = (uint32_t)tid | ((uint32_t)(__popc(tid) & 1) << 7);
         uint32_t m[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) m[k] = (((s8 >> (2 * k)) & 1u) << 15) | (((s8 >> (2 * k + 1)) & 1u) << 31);
-        stab[s] = make_uint4(m[0], m[1], m[2], m[3]);
+        stab[tid] = make_uint4(m[0], m[1], m[2], m[3]);
     }
+}
+
+// The table entries of one sub-block's 4 groups (8 LDS reads, issued together).
+struct SubTab {
+    uint4 m[4], sg[4];
+};
+
+__device__ __forceinline__ SubTab fetch_tab(uint2 q, const uint4* gtab, const uint4* stab) {
+    SubTab r;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        r.m[g] = gtab[(q.x >> (8 * g)) & 0xFF];
+        r.sg[g] = stab[(q.y >> (7 * g)) & 0x7F];
+    }
+    return r;
 }
 
 // Dot of one sub-block (4 groups of 8) with 32 activations xa[0..15] (pairs, natural order):
 // unscaled sum over the sub-block of grid magnitude * sign * x.
 template <bool BF16>
-__device__ __forceinline__ float sub_dot(uint2 q, const uint32_t* xa, const uint4* gtab, const uint4* stab) {
+__device__ __forceinline__ float sub_dot(const SubTab& tb, const uint32_t* xa) {
     float s = 0.f;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        const uint4 m = gtab[(q.x >> (8 * g)) & 0xFF];
-        const uint4 sg = stab[(q.y >> (7 * g)) & 0x7F];
+        const uint4 m = tb.m[g], sg = tb.sg[g];
         const uint32_t w[4] = {m.x ^ sg.x, m.y ^ sg.y, m.z ^ sg.z, m.w ^ sg.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -106,8 +118,8 @@ __global__ __launch_bounds__(256) void k_cb_up(const __half* __restrict__ x, con
                                                uint16_t* __restrict__ h_out) {
     __shared__ uint4 gtab[256];
     __shared__ uint4 stab[128];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    build_tables(grid, gtab, stab, tid, false);
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint2 gentry = reinterpret_cast<const uint2*>(grid)[tid];     // blockDim == 256
 
     const int j = blockIdx.y;
     const uint32_t slot = slots[j];
@@ -115,46 +127,70 @@ __global__ __launch_bounds__(256) void k_cb_up(const __half* __restrict__ x, con
     const int nsub = L.hidden / 32, nsb = L.hidden / 256, inter = L.inter;
     const int li = lane & 31, rsel = lane >> 5;
 
-    // activation slice: sub-blocks li + 32 t, 16 pairs each
+    // All loads are unconditional, from clamped in-range addresses, and masked where the value
+    // is used: a load under a branch makes the compiler wait for it at the join, serialising
+    // the round trips.
+    const uint8_t* blob = pool + (size_t)(ok ? slot : 0) * stride;
+    const uint2* qs = reinterpret_cast<const uint2*>(blob + L.up_qs);
+    const uint16_t* dd = reinterpret_cast<const uint16_t*>(blob + L.up_d);
+    const int row_base = blockIdx.x * kUpRowsPerBlock + wv * 8;
+
+    uint2 q[4][T];
+    uint16_t dr[4][T];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int row = row_base + 2 * it + rsel;
+        const int rc = row < inter ? row : inter - 1;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int sb = li + 32 * t;
+            const int sc = sb < nsub ? sb : nsub - 1;
+            q[it][t] = qs[(size_t)rc * nsub + sc];
+            dr[it][t] = dd[(size_t)rc * nsb + sc / 8];
+        }
+    }
+
+    // activation slice: sub-blocks li + 32 t, 16 pairs each (zeros past the end)
     uint32_t xa[T][16];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const int sb = li + 32 * t;
+        const int sc = sb < nsub ? sb : nsub - 1;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const uint4 u = sb < nsub ? reinterpret_cast<const uint4*>(x + (size_t)sb * 32)[v] : make_uint4(0, 0, 0, 0);
+            const uint4 u = reinterpret_cast<const uint4*>(x + (size_t)sc * 32)[v];
             xa[t][4 * v] = u.x;
             xa[t][4 * v + 1] = u.y;
             xa[t][4 * v + 2] = u.z;
             xa[t][4 * v + 3] = u.w;
         }
     }
-
-    const uint8_t* blob = pool + (size_t)(ok ? slot : 0) * stride;
-    const uint2* qs = reinterpret_cast<const uint2*>(blob + L.up_qs);
-    const __half* dd = reinterpret_cast<const __half*>(blob + L.up_d);
-    const int row_base = blockIdx.x * kUpRowsPerBlock + wv * 8;
-
-    uint2 q[4][T];
+    build_tables(gentry, gtab, stab, tid, false);
+    __syncthreads();                                      // tables built
+    // a lane whose sub-block, row or expert is out of range contributes nothing (scale 0)
     float dv[4][T];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int row = row_base + 2 * it + rsel;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const int sb = li + 32 * t;
-            const bool v = ok && row < inter && sb < nsub;
-            q[it][t] = v ? qs[(size_t)row * nsub + sb] : make_uint2(0, 0);
-            dv[it][t] = v ? __half2float(dd[(size_t)row * nsb + sb / 8]) : 0.f;
+            const bool v = ok && row < inter && li + 32 * t < nsub;
+            dv[it][t] = v ? __half2float(__ushort_as_half(dr[it][t])) : 0.f;
         }
     }
-    __syncthreads();                                      // tables built
 
+    // the next sub-block's table entries are fetched while the current one is multiplied
+    SubTab tb[2];
+    tb[0] = fetch_tab(q[0][0], gtab, stab);
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         float acc = 0.f;
 #pragma unroll
-        for (int t = 0; t < T; ++t) acc += sub_scale(q[it][t], dv[it][t]) * sub_dot<false>(q[it][t], xa[t], gtab, stab);
+        for (int t = 0; t < T; ++t) {
+            const int i = it * T + t;
+            if (i + 1 < 4 * T) tb[(i + 1) & 1] = fetch_tab(q[(i + 1) / T][(i + 1) % T], gtab, stab);
+            acc += sub_scale(q[it][t], dv[it][t]) * sub_dot<false>(tb[i & 1], xa[t]);
+        }
 #pragma unroll
         for (int o = 16; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
         const int row = row_base + 2 * it + rsel;
@@ -166,6 +202,14 @@ __global__ __launch_bounds__(256) void k_cb_up(const __half* __restrict__ x, con
 }
 
 template <int T>
+struct DownLoad {                    // one expert's operands for one lane
+    uint2 q[2][T];                   // sub-block codes of the lane's 2 rows
+    uint16_t dr[2][T];               // their super-block scales (fp16 bits)
+    uint32_t ha[T][16];              // h slice: T sub-blocks x 16 bf16 pairs
+    bool ok;
+};
+
+template <int T>
 __global__ __launch_bounds__(256) void k_cb_down(const uint16_t* __restrict__ h, const uint8_t* __restrict__ pool,
                                                  size_t stride, const uint32_t* __restrict__ slots, int n_slots,
                                                  const __half* __restrict__ scores, int k, CbLayout L,
@@ -173,60 +217,74 @@ __global__ __launch_bounds__(256) void k_cb_down(const uint16_t* __restrict__ h,
                                                  float* __restrict__ y_out, int per_expert) {
     __shared__ uint4 gtab[256];
     __shared__ uint4 stab[128];
-    extern __shared__ uint4 hs[];                         // h [k][inter] bf16
     __shared__ float red[4][kDownRows];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    build_tables(grid, gtab, stab, tid, true);
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int inter = L.inter, hidden = L.hidden, nsub = inter / 32, nsb = inter / 256;
-    const int n16 = k * inter / 8;                        // uint4 units of h
-    for (int i = tid; i < n16; i += 256) hs[i] = reinterpret_cast<const uint4*>(h)[i];
-
     const int li = lane & 15, rsel = lane >> 4;
     const int row0 = blockIdx.x * kDownRows;
-    __syncthreads();
+    const uint2 gentry = reinterpret_cast<const uint2*>(grid)[tid];     // blockDim == 256
 
-    float acc[2] = {0.f, 0.f};
-    for (int jj = wv; jj < k; jj += 4) {
+    // Wave wv takes experts wv, wv + 4, ... (k <= 16: at most 4); the next expert's operands are
+    // loaded while the current one is multiplied.  Loads are unconditional from clamped
+    // addresses (see k_cb_up).
+    auto load = [&](int jj, DownLoad<T>& b) {
         const uint32_t slot = slots[jj];
-        const bool ok = slot < (uint32_t)n_slots;         // an invalid slot reads nothing, yields 0
-        const uint8_t* blob = pool + (size_t)(ok ? slot : 0) * stride;
+        b.ok = slot < (uint32_t)n_slots;
+        const uint8_t* blob = pool + (size_t)(b.ok ? slot : 0) * stride;
         const uint2* qs = reinterpret_cast<const uint2*>(blob + L.down_qs);
-        const __half* dd = reinterpret_cast<const __half*>(blob + L.down_d);
-        uint2 q[2][T];
-        float dv[2][T];
+        const uint16_t* dd = reinterpret_cast<const uint16_t*>(blob + L.down_d);
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
             const int row = row0 + 4 * it + rsel;
+            const int rc = row < hidden ? row : hidden - 1;
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 const int sb = li + 16 * t;
-                const bool v = ok && row < hidden && sb < nsub;
-                q[it][t] = v ? qs[(size_t)row * nsub + sb] : make_uint2(0, 0);
-                dv[it][t] = v ? __half2float(dd[(size_t)row * nsb + sb / 8]) : 0.f;
+                const int sc = sb < nsub ? sb : nsub - 1;
+                b.q[it][t] = qs[(size_t)rc * nsub + sc];
+                b.dr[it][t] = dd[(size_t)rc * nsb + sc / 8];
             }
         }
-        uint32_t ha[T][16];
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const int sb = li + 16 * t;
+            const int sc = li + 16 * t < nsub ? li + 16 * t : nsub - 1;
+            const uint4* hp = reinterpret_cast<const uint4*>(h + (size_t)jj * inter + (size_t)sc * 32);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const uint4 u = sb < nsub ? hs[((size_t)jj * inter + (size_t)sb * 32) / 8 + v] : make_uint4(0, 0, 0, 0);
-                ha[t][4 * v] = u.x;
-                ha[t][4 * v + 1] = u.y;
-                ha[t][4 * v + 2] = u.z;
-                ha[t][4 * v + 3] = u.w;
+                const uint4 u = hp[v];
+                b.ha[t][4 * v] = u.x;
+                b.ha[t][4 * v + 1] = u.y;
+                b.ha[t][4 * v + 2] = u.z;
+                b.ha[t][4 * v + 3] = u.w;
             }
         }
+    };
+
+    DownLoad<T> buf[2];
+    if (wv < k) load(wv, buf[0]);
+    build_tables(gentry, gtab, stab, tid, true);
+    __syncthreads();
+
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int qi = 0; qi < (MOE_MAX_K + 3) / 4; ++qi) {
+        const int jj = wv + 4 * qi;
+        if (jj >= k) break;
+        if (jj + 4 < k) load(jj + 4, buf[(qi + 1) & 1]);
+        const DownLoad<T>& b = buf[qi & 1];
         const float sj = scores ? __half2float(scores[jj]) : 1.0f;
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
+            const int row = row0 + 4 * it + rsel;
             float part = 0.f;
 #pragma unroll
-            for (int t = 0; t < T; ++t) part += sub_scale(q[it][t], dv[it][t]) * sub_dot<true>(q[it][t], ha[t], gtab, stab);
+            for (int t = 0; t < T; ++t) {
+                const bool v = b.ok && row < hidden && li + 16 * t < nsub;
+                const float d = v ? __half2float(__ushort_as_half(b.dr[it][t])) : 0.f;
+                part += sub_scale(b.q[it][t], d) * sub_dot<true>(fetch_tab(b.q[it][t], gtab, stab), b.ha[t]);
+            }
 #pragma unroll
             for (int o = 8; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
-            const int row = row0 + 4 * it + rsel;
             if (per_expert) {
                 if (li == 0 && row < hidden) y_out[(size_t)jj * hidden + row] = part;
             } else {
@@ -276,9 +334,8 @@ template <int T>
 int down_t(const uint16_t* h, const uint8_t* pool, size_t stride, const uint32_t* slots, int n_slots,
            const __half* scores, int k, const CbLayout& L, const uint8_t* grid, const __half* residual, float* y_out,
            int per_expert, hipStream_t s) {
-    const size_t shmem = (size_t)k * L.inter * sizeof(uint16_t);
     dim3 g((L.hidden + kDownRows - 1) / kDownRows);
-    MOE_LAUNCH(TK_CB_DOWN, (k_cb_down<T>), g, dim3(256), shmem, s, h, pool, stride, slots, n_slots, scores, k, L,
+    MOE_LAUNCH(TK_CB_DOWN, (k_cb_down<T>), g, dim3(256), 0, s, h, pool, stride, slots, n_slots, scores, k, L,
                grid, residual, y_out, per_expert);
     HIP_TRY(hipGetLastError());
     return 0;
@@ -303,10 +360,6 @@ int launch_cb_down(const uint16_t* h, const uint8_t* pool, size_t stride, int n_
                    float* y_out, int per_expert, hipStream_t s) {
     if (!check_cb("cb_down", k, hidden, inter, pool, n_slots, stride, slots, grid, h, y_out)) return -1;
     if (per_expert != 0 && per_expert != 1) { moe_set_error("cb_down: mode %d (0 sum, 1 per expert)", per_expert); return -1; }
-    if ((size_t)k * inter * sizeof(uint16_t) > 48 * 1024) {
-        moe_set_error("cb_down: k * inter = %d exceeds the 48 KiB LDS stage of h", k * inter);
-        return -1;
-    }
     const CbLayout L = cb_layout(hidden, inter);
     switch ((inter / 32 + 15) / 16) {
         case 1: return down_t<1>(h, pool, stride, slots, n_slots, scores, k, L, grid, residual, y_out, per_expert, s);
