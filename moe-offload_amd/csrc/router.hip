@@ -80,25 +80,53 @@ __device__ __forceinline__ uint32_t f16_order(uint16_t b) {
 }
 
 // fp64 RMSNorm of h (fp32 [hidden]) into fp16 bits in LDS; every block computes it.
+// Thread tid owns elements 4 (c kThreads + tid) + 0..3 for chunk c (hidden is a multiple of 8).
+// Every load is issued before the first use (unconditional, clamped, masked): a load inside a
+// loop that also consumes it costs one full memory round trip per iteration.
 __device__ void norm_into_lds(const float* __restrict__ h_in, const __half* __restrict__ norm_w, float eps,
                               int hidden, uint16_t* xs, __half* x_out, double* red) {
+    constexpr int kChunks = kMaxHidden / (4 * kThreads);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    float4 hv[kChunks];
+    uint2 wv2[kChunks];
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        const int i = 4 * (c * kThreads + tid);
+        const int ic = i < hidden ? i : hidden - 4;
+        hv[c] = *reinterpret_cast<const float4*>(h_in + ic);
+        wv2[c] = norm_w ? *reinterpret_cast<const uint2*>(norm_w + ic) : make_uint2(0x3C003C00u, 0x3C003C00u);
+    }
     double ss = 0.0;
-    for (int i = tid; i < hidden; i += kThreads) {
-        double v = h_in[i];
-        ss += v * v;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        if (4 * (c * kThreads + tid) >= hidden) continue;
+        const double a = hv[c].x, b = hv[c].y, d = hv[c].z, e = hv[c].w;
+        ss += a * a;
+        ss += b * b;
+        ss += d * d;
+        ss += e * e;
     }
     ss = wave_sum_f64(ss);
     if (lane == 0) red[wv] = ss;
     __syncthreads();
     const double tot = red[0] + red[1] + red[2] + red[3];
     const double denom = sqrt(tot / hidden + (double)eps);
-    for (int i = tid; i < hidden; i += kThreads) {
-        double v = (double)h_in[i] / denom;
-        if (norm_w) v *= (double)__half2float(norm_w[i]);
-        uint16_t b = f64_to_f16_bits(v);
-        xs[i] = b;
-        if (x_out) x_out[i] = __ushort_as_half(b);
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        const int i = 4 * (c * kThreads + tid);
+        if (i >= hidden) continue;
+        const float hh[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
+        const uint32_t ww[2] = {wv2[c].x, wv2[c].y};
+        uint16_t b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            double v = (double)hh[j] / denom;
+            if (norm_w) v *= (double)__half2float(__ushort_as_half((uint16_t)(ww[j >> 1] >> (16 * (j & 1)))));
+            b[j] = f64_to_f16_bits(v);
+        }
+        const uint2 packed = make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
+        *reinterpret_cast<uint2*>(&xs[i]) = packed;
+        if (x_out) *reinterpret_cast<uint2*>(x_out + i) = packed;
     }
 }
 
@@ -311,7 +339,10 @@ int launch_f64_to_f16(const double* in, uint16_t* out, int n, hipStream_t s) {
 }
 
 int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidden, __half* x_out, hipStream_t s) {
-    if (!h_in || !x_out || hidden <= 0) { moe_set_error("rmsnorm: bad arguments"); return -1; }
+    if (!h_in || !x_out || hidden <= 0 || hidden > kMaxHidden || hidden % 8) {
+        moe_set_error("rmsnorm: hidden=%d (multiple of 8, <= %d) or null pointer", hidden, kMaxHidden);
+        return -1;
+    }
     hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, s, h_in, norm_w, eps, hidden, x_out);
     HIP_TRY(hipGetLastError());
     return 0;
