@@ -52,6 +52,7 @@ def parse():
     ap.add_argument("--sched", action="store_true",
                     help="the C++ runner's scheduler variant of the expert cache (c_layer_decode_step_sched)")
     ap.add_argument("--split", action="store_true", help="with --sched --mode host: hit experts before misses land")
+    ap.add_argument("--nemo-layers", type=int, default=40, help="layers of the codebook (Nemotron-style) workload")
     ap.add_argument("--only", choices=["headline", "resident", "prefill", "calib", "floor", "nemotron"], default=None,
                     help="run one pass and print its own JSON line (for sweeps and profiling); "
                          "calib runs the known-size copy kernel used to scale memory counters")
@@ -379,7 +380,8 @@ def main():
         print(json.dumps({"prefill": prefill_pass()}), flush=True)
         return
     if args.only == "nemotron":
-        print(json.dumps({"nemotron": nemotron_pass()}), flush=True)
+        print(json.dumps({"nemotron": nemotron_pass(min(args.steps, 64), min(args.warmup, 8), args.nemo_layers)}),
+              flush=True)
         return
     if args.only == "floor":
         fl = launch_floor([3_276_800, 6_553_600, 9_830_400, 64 << 20])

@@ -89,10 +89,11 @@ struct SlotTable {
     uint64_t snap_fetched[8];
     uint64_t stats[18];
     uint64_t expert_bytes;
-    int16_t slot_of[MOE_NUM_EXPERTS];   // expert id -> slot, -1 when not resident
-    int16_t eid_of[MOE_NUM_EXPERTS];    // slot -> expert id, -1 when empty
-    int16_t free_stack[MOE_NUM_EXPERTS];
-    uint32_t stamp[MOE_NUM_EXPERTS];    // 0 = slot not on the recency list
+    // (16-byte aligned so the device kernels copy them with 128-bit loads)
+    alignas(16) int16_t slot_of[MOE_NUM_EXPERTS];   // expert id -> slot, -1 when not resident
+    alignas(16) int16_t eid_of[MOE_NUM_EXPERTS];    // slot -> expert id, -1 when empty
+    alignas(16) int16_t free_stack[MOE_NUM_EXPERTS];
+    alignas(16) uint32_t stamp[MOE_NUM_EXPERTS];    // 0 = slot not on the recency list
     // Copies the last decode step (list 0) and the last prefetch (list 1) need: (eid, slot).
     // Two lists, so a step may run while the previous prefetch's copies are still queued.
     int32_t n_copy;

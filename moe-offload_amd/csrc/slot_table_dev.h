@@ -28,9 +28,9 @@ __device__ __forceinline__ void wave_sync() {
 
 struct LdsTable {
     uint64_t stats[18];        // the table's counters, written back once at the end
-    int16_t slot_of[MOE_NUM_EXPERTS];
-    int16_t eid_of[MOE_NUM_EXPERTS];
-    uint32_t stamp[MOE_NUM_EXPERTS];
+    alignas(16) int16_t slot_of[MOE_NUM_EXPERTS];
+    alignas(16) int16_t eid_of[MOE_NUM_EXPERTS];
+    alignas(16) uint32_t stamp[MOE_NUM_EXPERTS];
     uint32_t protect[16];      // bitmap over expert ids
     uint32_t resident[16];
     uint32_t pred[16];
@@ -52,13 +52,35 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
     return v;
 }
 
+// One 128-bit load per array per lane (entries 8 lane .. 8 lane + 7), all issued before any is
+// used: a copy loop that stores each value before loading the next waits a full round trip per
+// iteration.  Entries at or past the capacity hold -1 / 0 in every table (reset, state import
+// and store_table keep them so); they are masked anyway.
 __device__ inline void load_table(const SlotTable* t, LdsTable& L, int lane) {
+    static_assert(MOE_NUM_EXPERTS == 64 * 8, "one 8-entry vector per lane");
     const int cap = t->capacity;
-    for (int i = lane; i < MOE_NUM_EXPERTS; i += 64) {
-        L.slot_of[i] = t->slot_of[i];
-        L.eid_of[i] = i < cap ? t->eid_of[i] : (int16_t)-1;
-        L.stamp[i] = i < cap ? t->stamp[i] : 0u;
+    const uint4 so = reinterpret_cast<const uint4*>(t->slot_of)[lane];
+    uint4 eo = reinterpret_cast<const uint4*>(t->eid_of)[lane];
+    uint4 s0 = reinterpret_cast<const uint4*>(t->stamp)[2 * lane];
+    uint4 s1 = reinterpret_cast<const uint4*>(t->stamp)[2 * lane + 1];
+    const int i0 = 8 * lane;
+    if (i0 + 8 > cap) {                        // mask the entries past the capacity
+        uint32_t e[4] = {eo.x, eo.y, eo.z, eo.w};
+        uint32_t st[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (i0 + j < cap) continue;
+            e[j >> 1] |= 0xFFFFu << (16 * (j & 1));
+            st[j] = 0u;
+        }
+        eo = make_uint4(e[0], e[1], e[2], e[3]);
+        s0 = make_uint4(st[0], st[1], st[2], st[3]);
+        s1 = make_uint4(st[4], st[5], st[6], st[7]);
     }
+    reinterpret_cast<uint4*>(L.slot_of)[lane] = so;
+    reinterpret_cast<uint4*>(L.eid_of)[lane] = eo;
+    reinterpret_cast<uint4*>(L.stamp)[2 * lane] = s0;
+    reinterpret_cast<uint4*>(L.stamp)[2 * lane + 1] = s1;
     if (lane < 16) {
         L.protect[lane] = 0;
         L.resident[lane] = 0;
@@ -71,15 +93,13 @@ __device__ inline void load_table(const SlotTable* t, LdsTable& L, int lane) {
     wave_sync();
 }
 
+// Entries past the capacity are -1 / 0 in LDS as well (load_table masks them and no operation
+// touches them), so the whole arrays are written back.
 __device__ inline void store_table(SlotTable* t, const LdsTable& L, int lane) {
-    const int cap = t->capacity;
-    for (int i = lane; i < MOE_NUM_EXPERTS; i += 64) {
-        t->slot_of[i] = L.slot_of[i];
-        if (i < cap) {
-            t->eid_of[i] = L.eid_of[i];
-            t->stamp[i] = L.stamp[i];
-        }
-    }
+    reinterpret_cast<uint4*>(t->slot_of)[lane] = reinterpret_cast<const uint4*>(L.slot_of)[lane];
+    reinterpret_cast<uint4*>(t->eid_of)[lane] = reinterpret_cast<const uint4*>(L.eid_of)[lane];
+    reinterpret_cast<uint4*>(t->stamp)[2 * lane] = reinterpret_cast<const uint4*>(L.stamp)[2 * lane];
+    reinterpret_cast<uint4*>(t->stamp)[2 * lane + 1] = reinterpret_cast<const uint4*>(L.stamp)[2 * lane + 1];
 }
 
 // Relabel stamps by rank when the clock nears wrap-around (order unchanged).
