@@ -8,13 +8,15 @@
 //     y_r = D_u h_r                          (k_q2g_proj<.., kDown>, fp16 out, row row_out[r])
 // with W = scale * q + bias per group of 64 inputs (2-bit codes, 16 per u32, LSB first).
 //
-// Tiling.  The rows of a segment form M tiles of 16 (v_mfma_f32_16x16x32_f16).  A block of 4
-// waves shares the M tile; each wave owns 4 subtiles of 16 weight rows (gate/up: 2 x 16 rows of
-// each projection = 128 intermediate rows per block; down: 4 x 16 = 256 output rows).  Per
-// 256-wide K chunk j a lane (n = lane & 15, kq = lane >> 4) loads group 4j + kq of weight row n
-// (one 16-byte load of 64 codes plus the (scale, bias) word) and the same group of activation
-// row n of the M tile (8 x 16 bytes, from L1/L2).  Nothing is staged in LDS: the next chunk's
-// loads are in flight while the current chunk is multiplied.
+// Tiling.  The rows of a segment form M tiles of 16 (v_mfma_f32_16x16x32_f16), taken in
+// batches of up to 4 tiles.  A block of 4 waves works on one segment and one slice of weight
+// rows; each wave owns 4 subtiles of 16 weight rows (gate/up: 2 x 16 rows of each projection =
+// 128 intermediate rows per block; down: 4 x 16 = 256 output rows).  Per 256-wide K chunk j a
+// lane (n = lane & 15, kq = lane >> 4) loads group 4j + kq of weight row n (one 16-byte load of
+// 64 codes plus the (scale, bias) word), dequantises it once and multiplies it into every tile
+// of the batch; the chunk's activations of the batch's rows are staged in LDS (each thread
+// stages 2 units of 16 bytes per tile).  One chunk is in flight per block; the latency is
+// covered by the other resident blocks of the CU.
 //
 // Dequantisation.  A 2-bit code in the low bits of a nibble is the fp4 (e2m1) value q/2, so
 // w & 0x33333333 (even codes) and (w >> 2) & 0x33333333 (odd codes) are 8 fp4 values each;
@@ -37,6 +39,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMT = 16;          // rows per M tile
 constexpr int kSub = 4;          // 16-row weight subtiles per wave
 constexpr int kMaxChunks = 10;   // K <= 2560
+constexpr int kMaxMT = 4;        // M tiles multiplied per pass over a segment's weights
 constexpr int kGateUp = 0, kDown = 1;
 
 // Block index -> work item, keeping consecutive work items on one XCD (blocks are dealt to the
@@ -90,7 +93,7 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
     const int slot = seg_slot ? seg_slot[seg] : seg;
     if (r1 == r0 || slot < 0 || slot >= n_slots) return;
 
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, kq = lane >> 4;
     const uint8_t* blob = pool + (size_t)slot * stride;
     const size_t code_row = (size_t)K / 4, sb_row = (size_t)kg;   // bytes / words per weight row
@@ -115,128 +118,168 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
             so = L.down_sb;
         }
         col[s] = base + n;
-        rv[s] = base + n < N;
+        // N is a multiple of 64, so a subtile is wholly in range or wholly out; one that is out
+        // reads the last in-range subtile (unconditional loads) and is never written
+        rv[s] = base < N;
+        if (base >= N) base = N - 16;
         codes[s] = blob + co + (size_t)base * code_row;
         sbp[s] = reinterpret_cast<const uint32_t*>(blob + so) + (size_t)base * sb_row;
     }
-    const size_t lane_code = (size_t)n * code_row + (size_t)kq * 16, lane_sb = (size_t)n * sb_row + kq;
+    const uint32_t lane_code0 = (uint32_t)((size_t)n * code_row + (size_t)kq * 16);
+    const uint32_t lane_sb0 = (uint32_t)((size_t)n * sb_row + kq);
 
-    // Activation chunks are staged in LDS, shared by the 4 waves: 16 rows x 32 units of 16 bytes
-    // (256 inputs) per buffer, unit v of row m stored at m * 32 + (v ^ m) so that the 16 lanes
-    // reading one unit column of the tile hit distinct banks.  Each thread stages 2 units.
-    __shared__ uint4 a_lds[2][kMT * 32];
+    // The segment's rows are taken in batches of up to kMaxMT M tiles (64 rows); within a batch
+    // every K chunk's weights are loaded and dequantised once and multiplied into every tile, so
+    // a long segment costs one pass over its weights per batch, not one per tile.
+    //
+    // Activation chunks are staged in LDS, shared by the 4 waves: per tile 16 rows x 32 units of
+    // 16 bytes (256 inputs), unit v of row m stored at m * 32 + (v ^ m) so that the 16 lanes
+    // reading one unit column hit distinct banks.  Each thread stages 2 units per tile.
+    __shared__ uint4 a_lds[kMaxMT][kMT * 32];
     const int t = threadIdx.x;
     const int sm0 = t >> 5, sm1 = sm0 + 8, sv = t & 31;       // the two units this thread stages
 
-    for (int m0 = r0; m0 < r1; m0 += kMT) {
-        const int cnt = (r1 - m0) < kMT ? (r1 - m0) : kMT;
-        // source rows of the two staged units; a row past the tile or naming an out-of-range
+    for (int b0 = r0; b0 < r1; b0 += kMT * kMaxMT) {
+        const int rows = (r1 - b0) < kMT * kMaxMT ? (r1 - b0) : kMT * kMaxMT;
+        const int mts = (rows + kMT - 1) / kMT;                // tiles in this batch (wave-uniform)
+        // The weight loads do not depend on the batch; an opaque copy of the lane offsets keeps
+        // the compiler from hoisting (and holding) a short K's whole weight slice across batches.
+        uint32_t lane_code = lane_code0, lane_sb = lane_sb0;
+        asm volatile("" : "+v"(lane_code), "+v"(lane_sb));
+        // source rows of the staged units; a row past the segment or naming an out-of-range
         // source row is staged as zeros
-        auto src_row = [&](int m) {
-            if (m >= cnt) return -1;
-            const int r = m0 + m;
-            const int sr = row_map ? row_map[r] : r;
-            return (sr < 0 || sr >= n_src_rows) ? -1 : sr;
-        };
-        const int sr0 = src_row(sm0), sr1 = src_row(sm1);
-        const uint4* ar0 = reinterpret_cast<const uint4*>(src + (size_t)(sr0 < 0 ? 0 : sr0) * K);
-        const uint4* ar1 = reinterpret_cast<const uint4*>(src + (size_t)(sr1 < 0 ? 0 : sr1) * K);
-
-        f32x4 acc[kSub];
+        int sr[kMaxMT][2];
 #pragma unroll
-        for (int s = 0; s < kSub; ++s) acc[s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < kMaxMT; ++mt) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int m = mt * kMT + (h ? sm1 : sm0);
+                int v = -1;
+                if (m < rows) {
+                    const int r = b0 + m;
+                    v = row_map ? row_map[r] : r;
+                    if (v < 0 || v >= n_src_rows) v = -1;
+                }
+                sr[mt][h] = v;
+            }
+        }
 
-        uint4 cw[2][kSub];
-        uint32_t sw[2][kSub];
-        uint4 xs0, xs1;                                        // staged activation units in flight
-        auto load = [&](int j, int b) {
+        f32x4 acc[kMaxMT][kSub];
+#pragma unroll
+        for (int mt = 0; mt < kMaxMT; ++mt)
+#pragma unroll
+            for (int s = 0; s < kSub; ++s) acc[mt][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+        uint4 cw[kSub];
+        uint32_t sw[kSub];
+        uint4 xs[kMaxMT][2];                                   // staged activation units in flight
+        // Loads are unconditional from clamped in-range addresses and nothing masks them where
+        // they land: a load whose value is selected right away is sunk into a branch by the
+        // compiler, which then waits for it at the join and serialises a chunk's round trips.
+        // Groups past K (a K that is not a multiple of 256) read group kg - 1: their activations
+        // are staged as zeros, so those finite weights add nothing.  Rows past the segment and
+        // out-of-range source rows are zeroed when staged.
+        auto load = [&](int j) {
             const bool gv = 4 * j + kq < kg;
+            const int gdelta = gv ? 0 : (kg - 1) - (4 * j + kq);      // clamp to group kg - 1
 #pragma unroll
             for (int s = 0; s < kSub; ++s) {
-                const bool ok = rv[s] && gv;
-                cw[b][s] = ok ? *reinterpret_cast<const uint4*>(codes[s] + lane_code + (size_t)j * 64)
-                              : make_uint4(0, 0, 0, 0);
-                sw[b][s] = ok ? sbp[s][lane_sb + 4 * j] : 0u;
+                cw[s] = *reinterpret_cast<const uint4*>(codes[s] + lane_code + (size_t)j * 64 + (ptrdiff_t)gdelta * 16);
+                sw[s] = sbp[s][lane_sb + 4 * j + gdelta];
             }
             const int u = 32 * j + sv;                         // 16-byte unit within the row
-            const bool uv = u * 8 < K;
-            xs0 = (sr0 >= 0 && uv) ? ar0[u] : make_uint4(0, 0, 0, 0);
-            xs1 = (sr1 >= 0 && uv) ? ar1[u] : make_uint4(0, 0, 0, 0);
+            const int uc = u * 8 < K ? u : K / 8 - 1;
+#pragma unroll
+            for (int mt = 0; mt < kMaxMT; ++mt) {
+                if (mt >= mts) break;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int v = sr[mt][h] < 0 ? 0 : sr[mt][h];
+                    xs[mt][h] = reinterpret_cast<const uint4*>(src + (size_t)v * K)[uc];
+                }
+            }
         };
-        auto stage = [&](int b) {
-            a_lds[b][sm0 * 32 + (sv ^ sm0)] = xs0;
-            a_lds[b][sm1 * 32 + (sv ^ sm1)] = xs1;
+        auto stage = [&](int j) {
+            const bool uv = (32 * j + sv) * 8 < K;
+#pragma unroll
+            for (int mt = 0; mt < kMaxMT; ++mt) {
+                if (mt >= mts) break;
+                a_lds[mt][sm0 * 32 + (sv ^ sm0)] = (sr[mt][0] >= 0 && uv) ? xs[mt][0] : make_uint4(0, 0, 0, 0);
+                a_lds[mt][sm1 * 32 + (sv ^ sm1)] = (sr[mt][1] >= 0 && uv) ? xs[mt][1] : make_uint4(0, 0, 0, 0);
+            }
         };
-        auto compute = [&](int b) {
+        // Per 32-bit word q of the lane's group: the activation fragments of every tile, then per
+        // subtile the two dequantised weight fragments, multiplied into every tile.
+        auto compute = [&]() {
             f16x2 s2[kSub], b2[kSub];
 #pragma unroll
             for (int s = 0; s < kSub; ++s) {
-                const f16x2 sb = __builtin_bit_cast(f16x2, sw[b][s]);
+                const f16x2 sb = __builtin_bit_cast(f16x2, sw[s]);
                 const _Float16 two_s = sb.x * (_Float16)2.0f;
                 s2[s] = (f16x2){two_s, two_s};
                 b2[s] = (f16x2){sb.y, sb.y};
             }
-            const uint4* arow = a_lds[b] + n * 32;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int v = 8 * kq + 2 * q;
-                f16x8 a_ev, a_od;
-                split_even_odd(arow[v ^ n], arow[(v + 1) ^ n], a_ev, a_od);
+                f16x8 a_ev[kMaxMT], a_od[kMaxMT];
+#pragma unroll
+                for (int mt = 0; mt < kMaxMT; ++mt) {
+                    if (mt >= mts) break;
+                    const uint4* arow = a_lds[mt] + n * 32;
+                    split_even_odd(arow[v ^ n], arow[(v + 1) ^ n], a_ev[mt], a_od[mt]);
+                }
 #pragma unroll
                 for (int s = 0; s < kSub; ++s) {
-                    const uint32_t w = q == 0 ? cw[b][s].x : q == 1 ? cw[b][s].y : q == 2 ? cw[b][s].z : cw[b][s].w;
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_ev, dequant8(w & 0x33333333u, s2[s], b2[s]),
-                                                                  acc[s], 0, 0, 0);
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_od, dequant8((w >> 2) & 0x33333333u, s2[s], b2[s]),
-                                                                  acc[s], 0, 0, 0);
+                    const uint32_t w = q == 0 ? cw[s].x : q == 1 ? cw[s].y : q == 2 ? cw[s].z : cw[s].w;
+                    const f16x8 b_ev = dequant8(w & 0x33333333u, s2[s], b2[s]);
+                    const f16x8 b_od = dequant8((w >> 2) & 0x33333333u, s2[s], b2[s]);
+#pragma unroll
+                    for (int mt = 0; mt < kMaxMT; ++mt) {
+                        if (mt >= mts) break;
+                        acc[mt][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_ev[mt], b_ev, acc[mt][s], 0, 0, 0);
+                        acc[mt][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_od[mt], b_od, acc[mt][s], 0, 0, 0);
+                    }
                 }
             }
         };
-        // Pipeline: while chunk j is multiplied out of LDS buffer j & 1, chunk j + 1's weights
-        // (registers) and activations (registers, then LDS buffer (j + 1) & 1) are in flight.
-        // One barrier per chunk: the buffer written after compute(j) was last read by
-        // compute(j - 1), which every wave finished before the previous barrier.
-        __syncthreads();                                       // previous tile's reads are done
-        load(0, 0);
-        stage(0);
-        __syncthreads();
+        // Per chunk: issue its loads, then (after every wave is done with the previous chunk's
+        // activations) stage them and multiply.  Latency is hidden by the other resident blocks.
 #pragma unroll 1
-        for (int j = 0; j < NCH; j += 2) {
-            if (j + 1 < NCH) load(j + 1, 1);
-            compute(0);
-            if (j + 1 < NCH) {
-                stage(1);
-                __syncthreads();
-                if (j + 2 < NCH) load(j + 2, 0);
-                compute(1);
-                if (j + 2 < NCH) {
-                    stage(0);
-                    __syncthreads();
-                }
-            }
+        for (int j = 0; j < NCH; ++j) {
+            load(j);
+            __syncthreads();                                   // every wave is done with chunk j - 1
+            stage(j);
+            __syncthreads();
+            compute();
         }
 
-        // Epilogue: lane holds rows 4*kq + i (i = 0..3) of column n of each subtile.
+        // Epilogue: lane holds rows 4*kq + i (i = 0..3) of column n of each subtile of each tile.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 4 * kq + i;
-            if (m >= cnt) continue;
-            const int r = m0 + m;
-            if (MODE == kGateUp) {
+        for (int mt = 0; mt < kMaxMT; ++mt) {
+            if (mt >= mts) break;
 #pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    if (!rv[2 * p]) continue;
-                    const float g = acc[2 * p][i], u = acc[2 * p + 1][i];
-                    out[(size_t)r * N + col[2 * p]] = __float2half_rn(g / (1.0f + __expf(-g)) * u);
+            for (int i = 0; i < 4; ++i) {
+                const int m = mt * kMT + 4 * kq + i;
+                if (m >= rows) continue;
+                const int r = b0 + m;
+                if (MODE == kGateUp) {
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        if (!rv[2 * p]) continue;
+                        const float g = acc[mt][2 * p][i], u = acc[mt][2 * p + 1][i];
+                        out[(size_t)r * N + col[2 * p]] = __float2half_rn(g / (1.0f + __expf(-g)) * u);
+                    }
+                } else {
+                    const int orow = row_out ? row_out[r] : r;
+                    if (orow < 0 || orow >= n_out_rows) continue;
+#pragma unroll
+                    for (int s = 0; s < kSub; ++s)
+                        if (rv[s]) out[(size_t)orow * N + col[s]] = __float2half_rn(acc[mt][s][i]);
                 }
-            } else {
-                const int orow = row_out ? row_out[r] : r;
-                if (orow < 0 || orow >= n_out_rows) continue;
-#pragma unroll
-                for (int s = 0; s < kSub; ++s)
-                    if (rv[s]) out[(size_t)orow * N + col[s]] = __float2half_rn(acc[s][i]);
             }
         }
+        __syncthreads();                                       // a_lds is reused by the next batch
     }
 }
 
@@ -323,6 +366,10 @@ int launch_q2_grouped_gate_up(const __half* x, int n_tokens, const int32_t* row_
                        h_out))
         return -1;
     if (n_seg == 0 || n_rows == 0) return 0;
+    if (n_tokens <= 0) {                      // the kernel reads source row 0 unconditionally
+        moe_set_error("q2_grouped_gate_up: %d rows but no tokens", n_rows);
+        return -1;
+    }
     BlobLayout L = blob_layout(hidden, inter, group);
     return dispatch_proj<kGateUp>(hidden, x, n_tokens, row_token, nullptr, 0, seg_start, seg_slot, n_seg, n_rows, pool,
                                   stride, n_slots, L, h_out, s);
