@@ -39,7 +39,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMT = 16;          // rows per M tile
 constexpr int kSub = 4;          // 16-row weight subtiles per wave
 constexpr int kMaxChunks = 10;   // K <= 2560
-constexpr int kMaxMT = 4;        // M tiles multiplied per pass over a segment's weights
 constexpr int kGateUp = 0, kDown = 1;
 
 // Block index -> work item, keeping consecutive work items on one XCD (blocks are dealt to the
@@ -74,6 +73,12 @@ __device__ __forceinline__ void split_even_odd(uint4 lo, uint4 hi, f16x8& ev, f1
     od = __builtin_bit_cast(f16x8, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
+// M tiles multiplied per pass over a segment's weights: 4 for gate/up (K = hidden: the long
+// contraction pays for the extra accumulators), 1 for down (a short K: registers buy more
+// resident blocks instead).
+template <int MODE>
+constexpr int max_mt() { return MODE == 0 ? 4 : 1; }
+
 template <int NCH, int MODE>
 __global__ __launch_bounds__(256) void k_q2g_proj(
     const __half* __restrict__ src, int n_src_rows, const int32_t* __restrict__ row_map,
@@ -81,6 +86,7 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
     const int32_t* __restrict__ seg_start, const int32_t* __restrict__ seg_slot, int n_seg, int n_rows,
     const uint8_t* __restrict__ pool, size_t stride, int n_slots, BlobLayout L, int tiles_per_seg,
     __half* __restrict__ out) {
+    constexpr int kMaxMT = max_mt<MODE>();
     const int K = MODE == kGateUp ? L.hidden : L.inter;          // contraction length
     const int N = MODE == kGateUp ? L.inter : L.hidden;          // output rows per projection
     const int kg = K / 64;
