@@ -271,16 +271,31 @@ class DecodeStack:
         _lib.check(self.L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
                                       c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), main.cuda_stream), "rmsnorm")
 
+    def demand_overlaps_prefetch(self, l: int) -> bool:
+        """Whether layer l's demand copies may be queued before its prefetch copies have landed.
+
+        A demand miss takes the oldest unprotected slot; the experts the last prefetch fetched
+        are the newest entries of the table (nothing touches it between that prefetch and this
+        step), so they are reached only after every older unprotected entry: at least
+        capacity - prefetch_cap - top_k of them, which covers the at most top_k misses when
+        capacity >= 2 top_k + prefetch_cap.  Then no demand copy targets a slot a prefetch copy
+        is still writing, and the join can move from before the demand copies to before the
+        GEMV that reads the prefetched slots (it then overlaps the demand copies)."""
+        c = self.cfg
+        return self.capacities[l] >= 2 * c.top_k + c.prefetch_cap
+
     def _layer_fused(self, l: int, main):
         """One layer of the device-driven token with the table work inside the router:
-        main: router + step(l) + prefetch table(l+1) -> [join prefetch copies(l)] ->
-        demand copies(l) -> gate/up -> down;  side: prefetch copies(l+1) after the demand
+        main: router + step(l) + prefetch table(l+1) -> demand copies(l) -> [join prefetch
+        copies(l)] -> gate/up -> down (the join goes before the demand copies when the pool is
+        too small for demand_overlaps_prefetch);  side: prefetch copies(l+1) after the demand
         copies of layer l (demand first: they gate this layer's GEMV)."""
         c = self.cfg
         self._router(l, tables=True)
         pf = c.prefetch and l + 1 < c.n_layers
         if l >= 1:
-            if c.prefetch:
+            early = c.prefetch and self.demand_overlaps_prefetch(l)
+            if c.prefetch and not early:
                 main.wait_event(self.ev_copy[l])
             _lib.check(self.L.c_layer_stage_dev(self.cidx(l), 0, c.stage_ctas, main.cuda_stream), "stage_demand")
         if pf:
@@ -289,6 +304,8 @@ class DecodeStack:
             _lib.check(self.L.c_layer_stage_dev(self.cidx(l + 1), 1, c.stage_ctas, self.side.cuda_stream),
                        "stage_prefetch")
             self.ev_copy[l + 1].record(self.side)
+        if l >= 1 and c.prefetch and self.demand_overlaps_prefetch(l):
+            main.wait_event(self.ev_copy[l])           # the GEMV reads the prefetched slots
         self._glu(l)
 
     def decode_token_host(self):
