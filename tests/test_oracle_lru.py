@@ -117,3 +117,29 @@ def test_bruteforce_tiny_capacity():
                     order.pop(0)
             order.append(e)
             assert C.get_state()[0] == order
+
+
+def test_demand_victims_avoid_in_flight_prefetch_slots():
+    """The ordering rule of the device-driven decode (stack.DecodeStack.demand_overlaps_prefetch):
+    with capacity >= 2 k + prefetch cap, no demand miss of a step lands in a slot the preceding
+    prefetch of that layer fetched into, so demand copies may be queued while prefetch copies
+    are still landing.  Checked on the C restatement over random traces at the boundary
+    capacity, and shown necessary by finding a collision below it."""
+    import numpy as np
+    rng = np.random.default_rng(17)
+    k, pcap = 10, 3
+
+    def collisions(cap, steps=400, universe=60):
+        L = olru.CLru(45, cap)
+        hits = 0
+        for _ in range(steps):
+            preds = [int(v) for v in rng.choice(universe, size=12, replace=False)]
+            fetched = {s for _, s in L.prefetch(preds, pcap)}
+            ids = [int(v) for v in rng.choice(universe, size=k, replace=False)]
+            _, misses = L.step(ids)
+            hits += sum(1 for _, s in misses if s in fetched)
+        return hits
+
+    for cap in (2 * k + pcap, 2 * k + pcap + 7, 102):
+        assert collisions(cap) == 0, cap
+    assert collisions(k + 1) > 0
