@@ -25,6 +25,7 @@
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
 
+#include "lane_reduce.h"
 #include "moe_common.h"
 
 namespace {
@@ -191,8 +192,7 @@ __global__ __launch_bounds__(256) void k_cb_up(const __half* __restrict__ x, con
             if (i + 1 < 4 * T) tb[(i + 1) & 1] = fetch_tab(q[(i + 1) / T][(i + 1) % T], gtab, stab);
             acc += sub_scale(q[it][t], dv[it][t]) * sub_dot<false>(tb[i & 1], xa[t]);
         }
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        acc = lanes::group_sum<32>(acc);
         const int row = row_base + 2 * it + rsel;
         if (li == 0 && row < inter) {
             const float r = acc > 0.f ? acc : 0.f;
@@ -283,8 +283,7 @@ __global__ __launch_bounds__(256) void k_cb_down(const uint16_t* __restrict__ h,
                 const float d = v ? __half2float(__ushort_as_half(b.dr[it][t])) : 0.f;
                 part += sub_scale(b.q[it][t], d) * sub_dot<true>(fetch_tab(b.q[it][t], gtab, stab), b.ha[t]);
             }
-#pragma unroll
-            for (int o = 8; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
+            part = lanes::group_sum<16>(part);
             if (per_expert) {
                 if (li == 0 && row < hidden) y_out[(size_t)jj * hidden + row] = part;
             } else {

@@ -25,6 +25,7 @@
 //                      half of a hit/miss split).
 #include <hip/hip_fp16.h>
 
+#include "lane_reduce.h"
 #include "moe_common.h"
 
 namespace {
@@ -64,12 +65,9 @@ __device__ __forceinline__ float pos_weight(int j) {
     return 1.0f / (float)(1 << (2 * cls));
 }
 
-// Build the 32 pairs and the two constants for activation slice a[0..63] (fp16 values,
-// 16-byte aligned).
-__device__ __forceinline__ void build_pairs(const __half* a, h2_t* P, float& cst, float& sum) {
-    uint4 q[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q[i] = reinterpret_cast<const uint4*>(a)[i];
+// Build the 32 pairs and the two constants for an activation slice a[0..63] (fp16 values,
+// held as 8 16-byte words).
+__device__ __forceinline__ void build_pairs(const uint4 (&q)[8], h2_t* P, float& cst, float& sum) {
     const uint16_t* hv = reinterpret_cast<const uint16_t*>(q);
     float c = 0.f, s = 0.f;
 #pragma unroll
@@ -93,7 +91,7 @@ __device__ __forceinline__ float sb_apply(uint32_t sb, float dot, float cst, flo
     return sc * (dot - cst) + bi * sum;
 }
 
-constexpr int kGuRowsPerIter = 4;   // iterations per wave (each covers 32/GPR rows)
+constexpr int kGuRowsPerIter = 2;   // rows per wave (each iteration covers 32/GPR rows)
 
 template <int GPR>
 __global__ __launch_bounds__(256) void k_q2_gate_up(
@@ -101,47 +99,54 @@ __global__ __launch_bounds__(256) void k_q2_gate_up(
     const uint32_t* __restrict__ slots, int n_slots, int inter, BlobLayout L, __half* __restrict__ h_out) {
     constexpr int RPI = 32 / GPR;                       // rows per wave instruction
     constexpr int ROWS_PER_WAVE = RPI * kGuRowsPerIter;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = blockIdx.y;
     const int proj = lane >> 5, sub = lane & 31;
     const int rl = sub / GPR, g = sub % GPR;
     const int row_base = (blockIdx.x * 4 + wv) * ROWS_PER_WAVE;
 
+    // The activation slice first: it comes from L2, and loads complete in issue order, so
+    // building its pairs then overlaps the weight loads' flight instead of following them.
+    uint4 xq[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xq[i] = reinterpret_cast<const uint4*>(x + g * 64)[i];
+
     const uint32_t slot = slots[j];
-    const bool ok = slot < (uint32_t)n_slots;         // an invalid slot reads nothing, yields 0
+    const bool ok = slot < (uint32_t)n_slots;         // an invalid slot yields h = 0
     const uint8_t* blob = pool + (size_t)(ok ? slot : 0) * stride;
     const uint8_t* codes = blob + (proj ? L.up_codes : L.gate_codes);
     const uint32_t* sbv = reinterpret_cast<const uint32_t*>(blob + (proj ? L.up_sb : L.gate_sb));
     const size_t row_bytes = (size_t)GPR * 16;
 
+    // Every load is unconditional from a clamped in-range row; nothing is selected on arrival
+    // (a load whose value is masked right away is sunk into a branch and waited for there).
     uint4 c[kGuRowsPerIter];
     uint32_t sb[kGuRowsPerIter];
 #pragma unroll
     for (int it = 0; it < kGuRowsPerIter; ++it) {
         int row = row_base + it * RPI + rl;
-        if (ok && row < inter) {
-            c[it] = *reinterpret_cast<const uint4*>(codes + (size_t)row * row_bytes + g * 16);
-            sb[it] = sbv[(size_t)row * GPR + g];
-        } else {
-            c[it] = make_uint4(0, 0, 0, 0);
-            sb[it] = 0;
-        }
+        row = row < inter ? row : inter - 1;
+        c[it] = *reinterpret_cast<const uint4*>(codes + (size_t)row * row_bytes + g * 16);
+        sb[it] = sbv[(size_t)row * GPR + g];
     }
 
     h2_t P[32];
     float cst, sum;
-    build_pairs(x + g * 64, P, cst, sum);
+    build_pairs(xq, P, cst, sum);
 
+    float part[kGuRowsPerIter];
+#pragma unroll
+    for (int it = 0; it < kGuRowsPerIter; ++it) part[it] = sb_apply(sb[it], q2_group_dot(c[it], P), cst, sum);
+    // row sums over the GPR lanes of each row (DPP / permlane, no LDS round trips)
+#pragma unroll
+    for (int it = 0; it < kGuRowsPerIter; ++it) part[it] = lanes::group_sum<GPR>(part[it]);
 #pragma unroll
     for (int it = 0; it < kGuRowsPerIter; ++it) {
-        float part = sb_apply(sb[it], q2_group_dot(c[it], P), cst, sum);
-#pragma unroll
-        for (int o = GPR / 2; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
-        float up = __shfl(part, lane + 32, 64);
-        int row = row_base + it * RPI + rl;
+        float gt, up;                                   // gate row (lanes 0-31), up row (32-63)
+        lanes::halves(part[it], gt, up);
+        const int row = row_base + it * RPI + rl;
         if (proj == 0 && g == 0 && row < inter) {
-            float gt = part;
-            float hval = gt / (1.0f + __expf(-gt)) * up;
+            const float hval = ok ? gt / (1.0f + __expf(-gt)) * up : 0.0f;
             h_out[(size_t)j * inter + row] = __float2half_rn(hval);
         }
     }
@@ -158,58 +163,86 @@ __global__ __launch_bounds__(256) void k_q2_down(
     constexpr int RPI = 64 / LPR;                  // rows per wave instruction
     constexpr int ITERS = (kDownRows + RPI - 1) / RPI;
     constexpr int MAXJ = (MOE_MAX_K + 3) / 4;      // experts per wave
-    __shared__ h2_t hp[MOE_MAX_K][GPR][32];
+    constexpr int kUnits = MOE_MAX_K * GPR * 4;    // 16-value units of h at the largest k
+    constexpr int kUnitIters = (kUnits + 255) / 256;
+    __shared__ uint4 hp[MOE_MAX_K][GPR][8];        // per (expert, group): 32 dot2 pairs
     __shared__ float hc[MOE_MAX_K][GPR][2];
     __shared__ float red[4][kDownRows];
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane % LPR, rl = lane / LPR;
     const int row0 = blockIdx.x * kDownRows;
     const int inter = GPR * 64;
 
-    // Issue this wave's weight loads first (experts wv, wv+4, ...).
+    // h[k][inter] -> LDS as dot2 pairs plus the per-(expert, group) constants.  Unit u = 16
+    // values 16w..16w+15 of group gg of expert jj (w = u % 4): two 16-byte loads give its 8
+    // pairs (h[16w + p], h[16w + p + 8]); the 4 units of a group sit on 4 adjacent lanes, which
+    // sum their partial constants with two DPP steps.
+    const int n_units = k * GPR * 4;
+    uint4 hv[kUnitIters][2];
+#pragma unroll
+    for (int ui = 0; ui < kUnitIters; ++ui) {
+        const int u = tid + 256 * ui;
+        const int uc = u < n_units ? u : 0;
+        const __half* src = h + (size_t)uc * 16;          // units are contiguous in h
+        hv[ui][0] = reinterpret_cast<const uint4*>(src)[0];
+        hv[ui][1] = reinterpret_cast<const uint4*>(src)[1];
+    }
+    // This wave's weight loads (experts wv, wv+4, ...), all unconditional from clamped
+    // in-range addresses: a value loaded inside a branch and merged with another value at the
+    // join is waited for in the branch, which would serialise the round trips.  A position past
+    // k re-reads expert k-1's rows, which another wave of the block loads too (an L2 hit); the
+    // scores are one lane load, read out after the staging barrier.
+    uint32_t slot_q[MAXJ];
+#pragma unroll
+    for (int q = 0; q < MAXJ; ++q) {
+        const int j = wv + 4 * q;
+        slot_q[q] = slots[j < k ? j : k - 1];
+    }
     uint4 c[MAXJ][ITERS];
     uint32_t sb[MAXJ][ITERS];
 #pragma unroll
     for (int q = 0; q < MAXJ; ++q) {
-        int j = wv + 4 * q;
+        const uint32_t slot = slot_q[q] < (uint32_t)n_slots ? slot_q[q] : 0u;
+        const uint8_t* blob = pool + (size_t)slot * stride;
 #pragma unroll
         for (int it = 0; it < ITERS; ++it) {
             int row = row0 + it * RPI + rl;
-            const uint32_t slot = j < k ? slots[j] : 0u;
-            if (j < k && slot < (uint32_t)n_slots && row < hidden && it * RPI + rl < kDownRows) {
-                const uint8_t* blob = pool + (size_t)slot * stride;
-                c[q][it] = *reinterpret_cast<const uint4*>(blob + L.down_codes + (size_t)row * GPR * 16 + g * 16);
-                sb[q][it] = reinterpret_cast<const uint32_t*>(blob + L.down_sb)[(size_t)row * GPR + g];
-            } else {
-                c[q][it] = make_uint4(0, 0, 0, 0);
-                sb[q][it] = 0;
+            row = row < hidden ? row : hidden - 1;
+            c[q][it] = *reinterpret_cast<const uint4*>(blob + L.down_codes + (size_t)row * GPR * 16 + g * 16);
+            sb[q][it] = reinterpret_cast<const uint32_t*>(blob + L.down_sb)[(size_t)row * GPR + g];
+        }
+    }
+    const bool weighted = scores != nullptr;
+    const float s_lane = __half2float((weighted ? scores : h)[lane < k ? lane : 0]);
+
+#pragma unroll
+    for (int ui = 0; ui < kUnitIters; ++ui) {
+        const int u = tid + 256 * ui;
+        if (256 * ui >= n_units) break;            // block-uniform: no lane of this pass is valid
+        const uint32_t lo[4] = {hv[ui][0].x, hv[ui][0].y, hv[ui][0].z, hv[ui][0].w};
+        const uint32_t hi[4] = {hv[ui][1].x, hv[ui][1].y, hv[ui][1].z, hv[ui][1].w};
+        uint32_t pr[8];
+        float cc = 0.f, ss = 0.f;
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            pr[p] = __builtin_amdgcn_perm(hi[p >> 1], lo[p >> 1], (p & 1) ? 0x07060302u : 0x05040100u);
+            const h2_t v = as_h2(pr[p]);
+            const float f = (float)v.x + (float)v.y;
+            ss += f;
+            cc += pos_weight(p) * f;
+        }
+        cc = lanes::group_sum<4>(cc);
+        ss = lanes::group_sum<4>(ss);
+        if (u < n_units) {
+            const int jj = u / (GPR * 4), gg = (u >> 2) % GPR, w = u & 3;
+            hp[jj][gg][2 * w] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+            hp[jj][gg][2 * w + 1] = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+            if (w == 0) {
+                hc[jj][gg][0] = 1024.0f * cc;
+                hc[jj][gg][1] = ss;
             }
         }
-    }
-
-    // Stage h[k][inter] into LDS as dot2 pairs and per-(expert, group) constants.
-    for (int t = tid; t < k * GPR * 32; t += 256) {
-        int jj = t / (GPR * 32), rem = t % (GPR * 32), gg = rem / 32, pi = rem % 32;
-        int w = pi >> 3, p = pi & 7;
-        const __half* src = h + (size_t)jj * inter + gg * 64 + 16 * w + p;
-        h2_t pr;
-        pr.x = __builtin_bit_cast(_Float16, src[0]);
-        pr.y = __builtin_bit_cast(_Float16, src[8]);
-        hp[jj][gg][pi] = pr;
-    }
-    __syncthreads();
-    for (int t = tid; t < k * GPR; t += 256) {
-        int jj = t / GPR, gg = t % GPR;
-        float cc = 0.f, ss = 0.f;
-        for (int pi = 0; pi < 32; ++pi) {
-            h2_t pr = hp[jj][gg][pi];
-            float f = (float)pr.x + (float)pr.y;
-            ss += f;
-            cc += pos_weight(pi & 7) * f;
-        }
-        hc[jj][gg][0] = 1024.0f * cc;
-        hc[jj][gg][1] = ss;
     }
     __syncthreads();
 
@@ -218,21 +251,28 @@ __global__ __launch_bounds__(256) void k_q2_down(
     for (int it = 0; it < ITERS; ++it) acc[it] = 0.f;
 #pragma unroll
     for (int q = 0; q < MAXJ; ++q) {
-        int j = wv + 4 * q;
+        const int j = wv + 4 * q;
         if (j >= k) break;
         h2_t P[32];
+        const uint4* src = hp[j][g];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) P[i] = hp[j][g][i];
+        for (int i = 0; i < 8; ++i) {
+            const uint4 v = src[i];
+            P[4 * i] = as_h2(v.x);
+            P[4 * i + 1] = as_h2(v.y);
+            P[4 * i + 2] = as_h2(v.z);
+            P[4 * i + 3] = as_h2(v.w);
+        }
         const float cst = hc[j][g][0], sum = hc[j][g][1];
-        const float sj = scores ? __half2float(scores[j]) : 1.0f;
+        const bool ok = slot_q[q] < (uint32_t)n_slots;  // an invalid slot contributes 0
+        const float sj = weighted ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s_lane), j)) : 1.0f;
 #pragma unroll
         for (int it = 0; it < ITERS; ++it) {
-            float part = sb_apply(sb[q][it], q2_group_dot(c[q][it], P), cst, sum);
-#pragma unroll
-            for (int o = LPR / 2; o >= 1; o >>= 1) part += __shfl_xor(part, o, 64);
-            int rloc = it * RPI + rl;
+            float part = ok ? sb_apply(sb[q][it], q2_group_dot(c[q][it], P), cst, sum) : 0.0f;
+            part = lanes::group_sum<LPR>(part);
+            const int rloc = it * RPI + rl;
             if (per_expert == 1) {
-                int row = row0 + rloc;
+                const int row = row0 + rloc;
                 if (g == 0 && rloc < kDownRows && row < hidden) y_out[(size_t)j * hidden + row] = part;
             } else {
                 acc[it] += sj * part;

@@ -24,6 +24,7 @@
 // needs a launch of its own.
 #include <hip/hip_fp16.h>
 
+#include "lane_reduce.h"
 #include "moe_common.h"
 #include "slot_table_dev.h"
 
@@ -34,17 +35,8 @@ constexpr int kRowsPerBlock = 4;          // one weight row per wave
 constexpr int kMaxHidden = 4096;
 constexpr int kMaxExperts = 1024;
 
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-__device__ __forceinline__ double wave_max_f64(double v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
-    return v;
-}
+using lanes::wave_max_f64;
+using lanes::wave_sum_f64;
 
 // Wave-wide max of a uint32 with DPP inside each 16-lane row, then the four row results.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
@@ -73,6 +65,32 @@ __device__ __forceinline__ float round_f16(double v) {
     return __half2float(__ushort_as_half(f64_to_f16_bits(v)));
 }
 
+// The n largest keys of keys[lo, hi) (LDS; distinct, 0 = empty) by one wave: lane r < n gets
+// the r-th largest (0 once the range runs out).  The range holds at most 8 keys per lane.
+__device__ __forceinline__ uint32_t wave_topn(const uint32_t* keys, int lo, int hi, int n, int lane) {
+    constexpr int kMaxKpl = kMaxExperts / 128;
+    const int kpl = (hi - lo + 63) / 64;                    // wave-uniform
+    uint32_t key[kMaxKpl];
+#pragma unroll
+    for (int i = 0; i < kMaxKpl; ++i) {
+        const int idx = lo + lane + 64 * i;
+        key[i] = (i < kpl && idx < hi) ? keys[idx] : 0u;
+    }
+    uint32_t mine = 0;
+    for (int r = 0; r < n; ++r) {
+        uint32_t best = key[0];
+#pragma unroll
+        for (int i = 1; i < kMaxKpl; ++i)
+            if (i < kpl) best = max(best, key[i]);
+        best = wave_max_u32(best);
+#pragma unroll
+        for (int i = 0; i < kMaxKpl; ++i)
+            if (i < kpl && key[i] == best) key[i] = 0u;
+        if (lane == r) mine = best;
+    }
+    return mine;
+}
+
 // Order-preserving map of an fp16 value to uint16 (signed values; -0 folded onto +0).
 __device__ __forceinline__ uint32_t f16_order(uint16_t b) {
     if (b == 0x8000u) b = 0;
@@ -81,26 +99,22 @@ __device__ __forceinline__ uint32_t f16_order(uint16_t b) {
 
 // fp64 RMSNorm of h (fp32 [hidden]) into fp16 bits in LDS; every block computes it.
 // Thread tid owns elements 4 (c kThreads + tid) + 0..3 for chunk c (hidden is a multiple of 8).
-// Every load is issued before the first use (unconditional, clamped, masked): a load inside a
-// loop that also consumes it costs one full memory round trip per iteration.
-__device__ void norm_into_lds(const float* __restrict__ h_in, const __half* __restrict__ norm_w, float eps,
-                              int hidden, uint16_t* xs, __half* x_out, double* red) {
-    constexpr int kChunks = kMaxHidden / (4 * kThreads);
+// The loads are issued by the caller, all of them before the weight loads (loads retire in
+// issue order), so the normalisation overlaps the weights' flight.
+constexpr int kNormChunks = kMaxHidden / (4 * kThreads);
+struct NormIn {
+    float4 hv[kNormChunks];
+    uint2 w2[kNormChunks];
+};
+
+__device__ void norm_finish(const NormIn& in, bool has_w, float eps, int hidden, uint16_t* xs, __half* x_out,
+                            double* red) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    float4 hv[kChunks];
-    uint2 wv2[kChunks];
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-        const int i = 4 * (c * kThreads + tid);
-        const int ic = i < hidden ? i : hidden - 4;
-        hv[c] = *reinterpret_cast<const float4*>(h_in + ic);
-        wv2[c] = norm_w ? *reinterpret_cast<const uint2*>(norm_w + ic) : make_uint2(0x3C003C00u, 0x3C003C00u);
-    }
     double ss = 0.0;
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
+    for (int c = 0; c < kNormChunks; ++c) {
         if (4 * (c * kThreads + tid) >= hidden) continue;
-        const double a = hv[c].x, b = hv[c].y, d = hv[c].z, e = hv[c].w;
+        const double a = in.hv[c].x, b = in.hv[c].y, d = in.hv[c].z, e = in.hv[c].w;
         ss += a * a;
         ss += b * b;
         ss += d * d;
@@ -112,16 +126,16 @@ __device__ void norm_into_lds(const float* __restrict__ h_in, const __half* __re
     const double tot = red[0] + red[1] + red[2] + red[3];
     const double denom = sqrt(tot / hidden + (double)eps);
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
+    for (int c = 0; c < kNormChunks; ++c) {
         const int i = 4 * (c * kThreads + tid);
         if (i >= hidden) continue;
-        const float hh[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
-        const uint32_t ww[2] = {wv2[c].x, wv2[c].y};
+        const float hh[4] = {in.hv[c].x, in.hv[c].y, in.hv[c].z, in.hv[c].w};
+        const uint32_t ww[2] = {in.w2[c].x, in.w2[c].y};
         uint16_t b[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             double v = (double)hh[j] / denom;
-            if (norm_w) v *= (double)__half2float(__ushort_as_half((uint16_t)(ww[j >> 1] >> (16 * (j & 1)))));
+            if (has_w) v *= (double)__half2float(__ushort_as_half((uint16_t)(ww[j >> 1] >> (16 * (j & 1)))));
             b[j] = f64_to_f16_bits(v);
         }
         const uint2 packed = make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
@@ -130,6 +144,10 @@ __device__ void norm_into_lds(const float* __restrict__ h_in, const __half* __re
     }
 }
 
+// NC = 16-byte weight units per lane and row: hidden <= 512 * NC.  NORM: the input is h (fp32,
+// normalised here) rather than x (fp16); a compile-time choice, so that no branch lets the
+// compiler sink the input loads behind the weight loads.
+template <int NC, bool NORM>
 __global__ __launch_bounds__(kThreads) void k_router(
     const float* __restrict__ h_in, const __half* __restrict__ norm_w, float eps,
     const __half* __restrict__ x_in, __half* __restrict__ x_out,
@@ -147,39 +165,59 @@ __global__ __launch_bounds__(kThreads) void k_router(
     const __half* wr = nullptr;
     if (row < total_rows) wr = (row < n_exp) ? (w + (size_t)row * hidden) : (w_next + (size_t)(row - n_exp) * hidden);
 
-    // Issue this wave's weight loads before anything waits (hidden <= 4096: 4 x 16 B / lane / 2048).
-    constexpr int kMaxChunks = kMaxHidden / 512;
-    uint4 q[kMaxChunks];
-    const int chunks = hidden / 512;
-    const int tail = hidden % 512;                 // hidden is a multiple of 8
+    // Loads first, nothing waits before all are issued: the input (h and the norm weights, or
+    // x), then this wave's weight row.  Every load is unconditional from a clamped in-range
+    // address and masked where it is used (a row past the end reads row 0; a unit past the
+    // row's end reads its last unit).  The input is read as 16-byte units of whichever vector
+    // is given (h: 4 fp32 per unit, x: 8 fp16), so no branch separates the two cases.
+    NormIn nin;
+    {
+        const uint4* src = NORM ? reinterpret_cast<const uint4*>(h_in) : reinterpret_cast<const uint4*>(x_in);
+        const int n_units = NORM ? hidden / 4 : hidden / 8;
+        // without norm weights, read the input again in their place (in range; unused)
+        const __half* wsrc = norm_w ? norm_w : reinterpret_cast<const __half*>(src);
 #pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c)
-        if (wr && c < chunks) q[c] = *reinterpret_cast<const uint4*>(wr + c * 512 + lane * 8);
-    uint4 qt = make_uint4(0, 0, 0, 0);
-    if (wr && tail && lane * 8 < tail) qt = *reinterpret_cast<const uint4*>(wr + chunks * 512 + lane * 8);
+        for (int c = 0; c < kNormChunks; ++c) {
+            const int u = c * kThreads + tid;
+            const uint4 v = src[u < n_units ? u : n_units - 1];
+            nin.hv[c] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+            const int i = 4 * u;
+            nin.w2[c] = *reinterpret_cast<const uint2*>(wsrc + (i < hidden ? i : hidden - 4));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep every input load ahead of the weight loads
+    const __half* wrow = wr ? wr : w;
+    uint4 q[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int off = c * 512 + lane * 8;
+        q[c] = *reinterpret_cast<const uint4*>(wrow + (off < hidden ? off : hidden - 8));
+    }
+    __builtin_amdgcn_sched_barrier(0);   // every weight load issued before anything waits
 
-    if (h_in) {
-        norm_into_lds(h_in, norm_w, eps, hidden, xs, (x_out && blockIdx.x == 0) ? x_out : nullptr, red);
+    if constexpr (NORM) {
+        norm_finish(nin, norm_w != nullptr, eps, hidden, xs, (x_out && blockIdx.x == 0) ? x_out : nullptr, red);
     } else {
-        for (int i = tid * 8; i < hidden; i += kThreads * 8)
-            *reinterpret_cast<uint4*>(&xs[i]) = *reinterpret_cast<const uint4*>(x_in + i);
+#pragma unroll
+        for (int c = 0; c < kNormChunks; ++c) {
+            const int i = 8 * (c * kThreads + tid);
+            if (i < hidden) {
+                const float4 v = nin.hv[c];
+                *reinterpret_cast<uint4*>(&xs[i]) =
+                    make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w));
+            }
+        }
     }
     __syncthreads();
 
     if (wr) {
         double acc = 0.0;
 #pragma unroll
-        for (int c = 0; c <= kMaxChunks; ++c) {
-            uint4 wq, xq;
-            if (c < kMaxChunks) {
-                if (c >= chunks) continue;
-                wq = q[c];
-                xq = *reinterpret_cast<const uint4*>(&xs[c * 512 + lane * 8]);
-            } else {
-                if (!(tail && lane * 8 < tail)) continue;
-                wq = qt;
-                xq = *reinterpret_cast<const uint4*>(&xs[chunks * 512 + lane * 8]);
-            }
+        for (int c = 0; c < NC; ++c) {
+            const int off = c * 512 + lane * 8;
+            if (off >= hidden) continue;
+            const uint4 wq = q[c];
+            const uint4 xq = *reinterpret_cast<const uint4*>(&xs[off]);
             const __half* hw = reinterpret_cast<const __half*>(&wq);
             const __half* hx = reinterpret_cast<const __half*>(&xq);
 #pragma unroll
@@ -203,23 +241,34 @@ __global__ __launch_bounds__(kThreads) void k_router(
 
     __shared__ uint32_t keys[kMaxExperts];
     __shared__ uint32_t pkeys[kMaxExperts];
+    __shared__ uint32_t cand[64], pcand[64];
     __shared__ uint32_t sel_ids[MOE_MAX_K];
     __shared__ int32_t sel_pred[MOE_MAX_PREFETCH];
     __shared__ double redm[kThreads / 64], reds[kThreads / 64];
     const int n_pad = ((n_exp + 63) / 64) * 64;
-    // softmax over the logits in fp64, spread over the whole block
+    const bool predict = w_next && m > 0;
+    // softmax over the logits in fp64, spread over the whole block.  Every logit load is issued
+    // first, unconditionally from a clamped index (scratch holds 2 * n_exp values), and masked
+    // afterwards: a load merged with a default value at a branch join is waited for inside the
+    // branch, one round trip per load.
     constexpr int kPer = kMaxExperts / kThreads;
+    float lraw[kPer], praw[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = tid + kThreads * i;
+        const int ec = e < n_exp ? e : 0;
+        lraw[i] = __hip_atomic_load(&scratch[ec], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        praw[i] = __hip_atomic_load(&scratch[n_exp + ec], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     double lv[kPer];
     double mx = -1e300;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-        int e = tid + kThreads * i;
-        lv[i] = (e < n_exp) ? (double)__hip_atomic_load(&scratch[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -1e300;
+        const int e = tid + kThreads * i;
+        lv[i] = e < n_exp ? (double)lraw[i] : -1e300;
         mx = fmax(mx, lv[i]);
-        if (w_next && m > 0 && e < n_pad) {
-            float v = (e < n_exp) ? __hip_atomic_load(&scratch[n_exp + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
-            pkeys[e] = (e < n_exp) ? ((f16_order(__half_as_ushort(__float2half_rn(v))) << 16) | (uint32_t)e) : 0u;
-        }
+        if (predict && e < n_pad)
+            pkeys[e] = (e < n_exp) ? ((f16_order(__half_as_ushort(__float2half_rn(praw[i]))) << 16) | (uint32_t)e) : 0u;
     }
     mx = wave_max_f64(mx);
     if (lane == 0) redm[wv] = mx;
@@ -243,23 +292,24 @@ __global__ __launch_bounds__(kThreads) void k_router(
         if (e < n_pad) keys[e] = (e < n_exp) ? (((uint32_t)f64_to_f16_bits(lv[i] / sum) << 16) | (uint32_t)e) : 0u;
     }
     __syncthreads();
-    const int per_lane = n_pad / 64;
 
+    // Top-k in two stages: the experts are split into parts, each wave takes the top-k (top-m)
+    // of its part, then one wave takes the top-k of the candidates (one per lane).  The top-k
+    // of the union of the parts' top-k is the top-k of all.  Selection on waves 0-3 (4 parts),
+    // or on waves 0-1 with the predictor on waves 2-3 (2 parts each).
+    const int sel_parts = predict ? 2 : 4;
+    if (wv < sel_parts) {
+        const int span = n_pad / sel_parts;
+        const uint32_t r = wave_topn(keys, wv * span, (wv + 1) * span, k, lane);
+        if (lane < 16) cand[16 * wv + lane] = lane < k ? r : 0u;
+    } else {
+        const int part = wv - 2, span = n_pad / 2;
+        const uint32_t r = wave_topn(pkeys, part * span, (part + 1) * span, m, lane);
+        if (lane < 32) pcand[32 * part + lane] = lane < m ? r : 0u;
+    }
+    __syncthreads();
     if (wv == 0) {
-        uint32_t key[kMaxExperts / 64];
-#pragma unroll
-        for (int i = 0; i < kMaxExperts / 64; ++i) key[i] = (i < per_lane) ? keys[lane + 64 * i] : 0u;
-        uint32_t mine = 0;                        // lane j keeps the j-th largest key
-        for (int r = 0; r < k; ++r) {
-            uint32_t best = 0;
-#pragma unroll
-            for (int i = 0; i < kMaxExperts / 64; ++i) best = max(best, key[i]);
-            best = wave_max_u32(best);
-#pragma unroll
-            for (int i = 0; i < kMaxExperts / 64; ++i)
-                if (key[i] == best) key[i] = 0;
-            if (lane == r) mine = best;
-        }
+        const uint32_t mine = wave_topn(cand, 0, 16 * sel_parts, k, lane);  // lane j: the j-th largest
         // output position of the r-th largest is k-1-r (ascending gate order)
         const int pos = k - 1 - lane;
         const float g = __half2float(__ushort_as_half((uint16_t)(mine >> 16)));
@@ -267,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void k_router(
         // fp16 values in ascending order, so every partial sum is exact in fp32 before rounding
         float s = 0.0f;
         for (int j = 0; j < k; ++j) {
-            float gj = __shfl(g, k - 1 - j, 64);
+            float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), k - 1 - j));
             s = __half2float(__float2half_rn(s + gj));
         }
         if (lane < k) {
@@ -275,27 +325,14 @@ __global__ __launch_bounds__(kThreads) void k_router(
             sel_ids[pos] = mine & 0xFFFFu;
             scores_out[pos] = __float2half_rn(g / s);   // correctly rounded f32 division, then f16
         }
-    } else if (wv == 1 && w_next && m > 0) {
-        uint32_t key[kMaxExperts / 64];
-#pragma unroll
-        for (int i = 0; i < kMaxExperts / 64; ++i) key[i] = (i < per_lane) ? pkeys[lane + 64 * i] : 0u;
-        uint32_t mine = 0;
-        for (int r = 0; r < m; ++r) {
-            uint32_t best = 0;
-#pragma unroll
-            for (int i = 0; i < kMaxExperts / 64; ++i) best = max(best, key[i]);
-            best = wave_max_u32(best);
-#pragma unroll
-            for (int i = 0; i < kMaxExperts / 64; ++i)
-                if (key[i] == best) key[i] = 0;
-            if (lane == r) mine = best;
-        }
+    } else if (wv == 2 && predict) {
+        const uint32_t mine = wave_topn(pcand, 0, 64, m, lane);
         // lanes 0..m-1 hold descending (value, id); equal values must come out in ascending id:
         // within a run of equal values, lane r takes the id of its mirror position in the run
         const uint32_t val = mine >> 16;
         int first = lane, last = lane;
         for (int q2 = 0; q2 < m; ++q2) {
-            uint32_t vq = (uint32_t)__shfl((int)val, q2, 64);
+            uint32_t vq = (uint32_t)__builtin_amdgcn_readlane((int)val, q2);
             if (vq == val && q2 < first) first = q2;
             if (vq == val && q2 > last) last = q2;
         }
@@ -321,7 +358,16 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ 
                                                        float eps, int hidden, __half* __restrict__ x_out) {
     __shared__ __align__(16) uint16_t xs[kMaxHidden];
     __shared__ double red[kThreads / 64];
-    norm_into_lds(h_in, norm_w, eps, hidden, xs, x_out, red);
+    NormIn nin;
+    const __half* wsrc = norm_w ? norm_w : reinterpret_cast<const __half*>(h_in);
+#pragma unroll
+    for (int c = 0; c < kNormChunks; ++c) {
+        const int i = 4 * (c * kThreads + threadIdx.x);
+        const int ic = i < hidden ? i : hidden - 4;
+        nin.hv[c] = *reinterpret_cast<const float4*>(h_in + ic);
+        nin.w2[c] = *reinterpret_cast<const uint2*>(wsrc + ic);
+    }
+    norm_finish(nin, norm_w != nullptr, eps, hidden, xs, x_out, red);
 }
 
 __global__ void k_f64_to_f16(const double* __restrict__ in, uint16_t* __restrict__ out, int n) {
@@ -372,9 +418,22 @@ int launch_router(const float* h_in, const __half* norm_w, float eps, const __ha
     }
     int rows = n_exp * (w_next ? 2 : 1);
     int grid = (rows + kRowsPerBlock - 1) / kRowsPerBlock;      // one row per wave
-    MOE_LAUNCH(TK_ROUTER, k_router, dim3(grid), dim3(kThreads), 0, s, h_in, norm_w, eps, x_in, x_out,
-                       w, w_next, hidden, n_exp, k, w_next ? m : 0, scratch, counter, ids_out,
-                       scores_out, pred_out, step_tab, slot_inds, pf_tab, max_fetch);
+    auto go = [&](auto nc, auto norm) {
+        constexpr int NC = decltype(nc)::value;
+        constexpr bool NORM = decltype(norm)::value;
+        MOE_LAUNCH(TK_ROUTER, (k_router<NC, NORM>), dim3(grid), dim3(kThreads), 0, s, h_in, norm_w, eps, x_in, x_out,
+                           w, w_next, hidden, n_exp, k, w_next ? m : 0, scratch, counter, ids_out,
+                           scores_out, pred_out, step_tab, slot_inds, pf_tab, max_fetch);
+    };
+    using N4 = std::integral_constant<int, 4>;
+    using N8 = std::integral_constant<int, 8>;
+    if (h_in) {
+        if (hidden <= 2048) go(N4(), std::true_type());
+        else go(N8(), std::true_type());
+    } else {
+        if (hidden <= 2048) go(N4(), std::false_type());
+        else go(N8(), std::false_type());
+    }
     HIP_TRY(hipGetLastError());
     return 0;
 }
