@@ -65,30 +65,39 @@ __device__ __forceinline__ float pos_weight(int j) {
     return 1.0f / (float)(1 << (2 * cls));
 }
 
-// Build the 32 pairs and the two constants for an activation slice a[0..63] (fp16 values,
-// held as 8 16-byte words).
-__device__ __forceinline__ void build_pairs(const uint4 (&q)[8], h2_t* P, float& cst, float& sum) {
-    const uint16_t* hv = reinterpret_cast<const uint16_t*>(q);
-    float c = 0.f, s = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            uint16_t lo = hv[16 * w + j], hi = hv[16 * w + j + 8];
-            P[8 * w + j] = as_h2((uint32_t)lo | ((uint32_t)hi << 16));
-            float f = __half2float(__ushort_as_half(lo)) + __half2float(__ushort_as_half(hi));
-            s += f;
-            c += pos_weight(j) * f;
-        }
-    }
-    cst = 1024.0f * c;
-    sum = s;
-}
-
 __device__ __forceinline__ float sb_apply(uint32_t sb, float dot, float cst, float sum) {
     float sc = __half2float(__ushort_as_half((uint16_t)(sb & 0xFFFFu)));
     float bi = __half2float(__ushort_as_half((uint16_t)(sb >> 16)));
     return sc * (dot - cst) + bi * sum;
+}
+
+// Stage one 16-value unit of an fp16 vector (lo = values 0-7, hi = 8-15 of unit w of a group of
+// 64) as its 8 dot2 pairs P[8w + p] = (a[16w + p], a[16w + p + 8]) and add its share of the
+// group's constants.  The 4 units of a group sit on 4 adjacent lanes, which sum the constants
+// with two DPP steps, so every lane of the wave must call this (store masks the writes).
+__device__ __forceinline__ void stage_pairs(uint4 lo4, uint4 hi4, bool store, uint4* grp_pairs, float* grp_c, int w) {
+    const uint32_t lo[4] = {lo4.x, lo4.y, lo4.z, lo4.w};
+    const uint32_t hi[4] = {hi4.x, hi4.y, hi4.z, hi4.w};
+    uint32_t pr[8];
+    float cc = 0.f, ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        pr[p] = __builtin_amdgcn_perm(hi[p >> 1], lo[p >> 1], (p & 1) ? 0x07060302u : 0x05040100u);
+        const h2_t v = as_h2(pr[p]);
+        const float f = (float)v.x + (float)v.y;
+        ss += f;
+        cc += pos_weight(p) * f;
+    }
+    cc = lanes::group_sum<4>(cc);
+    ss = lanes::group_sum<4>(ss);
+    if (store) {
+        grp_pairs[2 * w] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+        grp_pairs[2 * w + 1] = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+        if (w == 0) {
+            grp_c[0] = 1024.0f * cc;
+            grp_c[1] = ss;
+        }
+    }
 }
 
 constexpr int kGuRowsPerIter = 2;   // rows per wave (each iteration covers 32/GPR rows)
@@ -105,11 +114,18 @@ __global__ __launch_bounds__(256) void k_q2_gate_up(
     const int rl = sub / GPR, g = sub % GPR;
     const int row_base = (blockIdx.x * 4 + wv) * ROWS_PER_WAVE;
 
-    // The activation slice first: it comes from L2, and loads complete in issue order, so
-    // building its pairs then overlaps the weight loads' flight instead of following them.
-    uint4 xq[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xq[i] = reinterpret_cast<const uint4*>(x + g * 64)[i];
+    // The activation vector first, one 16-value unit per thread (hidden / 16 <= 256 units): it
+    // comes from L2, and loads complete in issue order, so staging its pairs in LDS overlaps the
+    // weight loads' flight instead of following them.  The block stages x once; every lane then
+    // reads its group's 32 pairs from LDS.
+    __shared__ uint4 xp[32][8];                         // per group of 64: 32 dot2 pairs
+    __shared__ float xc[32][2];
+    const int tid = threadIdx.x;
+    const int n_units = GPR * 4;
+    const int uc = tid < n_units ? tid : 0;
+    const uint4 xlo = reinterpret_cast<const uint4*>(x)[2 * uc];
+    const uint4 xhi = reinterpret_cast<const uint4*>(x)[2 * uc + 1];
+    __builtin_amdgcn_sched_barrier(0);
 
     const uint32_t slot = slots[j];
     const bool ok = slot < (uint32_t)n_slots;         // an invalid slot yields h = 0
@@ -129,10 +145,22 @@ __global__ __launch_bounds__(256) void k_q2_gate_up(
         c[it] = *reinterpret_cast<const uint4*>(codes + (size_t)row * row_bytes + g * 16);
         sb[it] = sbv[(size_t)row * GPR + g];
     }
+    __builtin_amdgcn_sched_barrier(0);
 
+    stage_pairs(xlo, xhi, tid < n_units, xp[uc >> 2], xc[uc >> 2], uc & 3);
+    __builtin_amdgcn_sched_barrier(0);                  // no weight use ahead of the barrier
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
     h2_t P[32];
-    float cst, sum;
-    build_pairs(xq, P, cst, sum);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint4 v = xp[g][i];
+        P[4 * i] = as_h2(v.x);
+        P[4 * i + 1] = as_h2(v.y);
+        P[4 * i + 2] = as_h2(v.z);
+        P[4 * i + 3] = as_h2(v.w);
+    }
+    const float cst = xc[g][0], sum = xc[g][1];
 
     float part[kGuRowsPerIter];
 #pragma unroll
@@ -172,7 +200,6 @@ __global__ __launch_bounds__(256) void k_q2_down(
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane % LPR, rl = lane / LPR;
     const int row0 = blockIdx.x * kDownRows;
-    const int inter = GPR * 64;
 
     // h[k][inter] -> LDS as dot2 pairs plus the per-(expert, group) constants.  Unit u = 16
     // values 16w..16w+15 of group gg of expert jj (w = u % 4): two 16-byte loads give its 8
@@ -220,29 +247,9 @@ __global__ __launch_bounds__(256) void k_q2_down(
     for (int ui = 0; ui < kUnitIters; ++ui) {
         const int u = tid + 256 * ui;
         if (256 * ui >= n_units) break;            // block-uniform: no lane of this pass is valid
-        const uint32_t lo[4] = {hv[ui][0].x, hv[ui][0].y, hv[ui][0].z, hv[ui][0].w};
-        const uint32_t hi[4] = {hv[ui][1].x, hv[ui][1].y, hv[ui][1].z, hv[ui][1].w};
-        uint32_t pr[8];
-        float cc = 0.f, ss = 0.f;
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            pr[p] = __builtin_amdgcn_perm(hi[p >> 1], lo[p >> 1], (p & 1) ? 0x07060302u : 0x05040100u);
-            const h2_t v = as_h2(pr[p]);
-            const float f = (float)v.x + (float)v.y;
-            ss += f;
-            cc += pos_weight(p) * f;
-        }
-        cc = lanes::group_sum<4>(cc);
-        ss = lanes::group_sum<4>(ss);
-        if (u < n_units) {
-            const int jj = u / (GPR * 4), gg = (u >> 2) % GPR, w = u & 3;
-            hp[jj][gg][2 * w] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-            hp[jj][gg][2 * w + 1] = make_uint4(pr[4], pr[5], pr[6], pr[7]);
-            if (w == 0) {
-                hc[jj][gg][0] = 1024.0f * cc;
-                hc[jj][gg][1] = ss;
-            }
-        }
+        const int uc = u < n_units ? u : 0;
+        const int jj = uc / (GPR * 4), gg = (uc >> 2) % GPR;
+        stage_pairs(hv[ui][0], hv[ui][1], u < n_units, hp[jj][gg], hc[jj][gg], uc & 3);
     }
     __syncthreads();
 

@@ -66,29 +66,38 @@ __device__ __forceinline__ float round_f16(double v) {
 }
 
 // The n largest keys of keys[lo, hi) (LDS; distinct, 0 = empty) by one wave: lane r < n gets
-// the r-th largest (0 once the range runs out).  The range holds at most 8 keys per lane.
-__device__ __forceinline__ uint32_t wave_topn(const uint32_t* keys, int lo, int hi, int n, int lane) {
-    constexpr int kMaxKpl = kMaxExperts / 128;
-    const int kpl = (hi - lo + 63) / 64;                    // wave-uniform
-    uint32_t key[kMaxKpl];
+// the r-th largest (0 once the range runs out).  KPL keys per lane cover the range; each round
+// takes the wave maximum and clears it where it sits.
+template <int KPL>
+__device__ __forceinline__ uint32_t wave_topn_k(const uint32_t* keys, int lo, int hi, int n, int lane) {
+    uint32_t key[KPL];
 #pragma unroll
-    for (int i = 0; i < kMaxKpl; ++i) {
+    for (int i = 0; i < KPL; ++i) {
         const int idx = lo + lane + 64 * i;
-        key[i] = (i < kpl && idx < hi) ? keys[idx] : 0u;
+        key[i] = idx < hi ? keys[idx] : 0u;
     }
     uint32_t mine = 0;
     for (int r = 0; r < n; ++r) {
         uint32_t best = key[0];
 #pragma unroll
-        for (int i = 1; i < kMaxKpl; ++i)
-            if (i < kpl) best = max(best, key[i]);
+        for (int i = 1; i < KPL; ++i) best = max(best, key[i]);
         best = wave_max_u32(best);
 #pragma unroll
-        for (int i = 0; i < kMaxKpl; ++i)
-            if (i < kpl && key[i] == best) key[i] = 0u;
+        for (int i = 0; i < KPL; ++i) key[i] = key[i] == best ? 0u : key[i];
         if (lane == r) mine = best;
     }
     return mine;
+}
+
+// wave_topn_k with KPL fixed at compile time for the range size (up to kMaxExperts keys): a
+// runtime bound would turn every key operation into a masked select.
+__device__ __forceinline__ uint32_t wave_topn(const uint32_t* keys, int lo, int hi, int n, int lane) {
+    const int kpl = (hi - lo + 63) / 64;                    // wave-uniform
+    if (kpl <= 1) return wave_topn_k<1>(keys, lo, hi, n, lane);
+    if (kpl <= 2) return wave_topn_k<2>(keys, lo, hi, n, lane);
+    if (kpl <= 4) return wave_topn_k<4>(keys, lo, hi, n, lane);
+    if (kpl <= 8) return wave_topn_k<8>(keys, lo, hi, n, lane);
+    return wave_topn_k<kMaxExperts / 64>(keys, lo, hi, n, lane);
 }
 
 // Order-preserving map of an fp16 value to uint16 (signed values; -0 folded onto +0).
@@ -241,7 +250,6 @@ __global__ __launch_bounds__(kThreads) void k_router(
 
     __shared__ uint32_t keys[kMaxExperts];
     __shared__ uint32_t pkeys[kMaxExperts];
-    __shared__ uint32_t cand[64], pcand[64];
     __shared__ uint32_t sel_ids[MOE_MAX_K];
     __shared__ int32_t sel_pred[MOE_MAX_PREFETCH];
     __shared__ double redm[kThreads / 64], reds[kThreads / 64];
@@ -293,23 +301,12 @@ __global__ __launch_bounds__(kThreads) void k_router(
     }
     __syncthreads();
 
-    // Top-k in two stages: the experts are split into parts, each wave takes the top-k (top-m)
-    // of its part, then one wave takes the top-k of the candidates (one per lane).  The top-k
-    // of the union of the parts' top-k is the top-k of all.  Selection on waves 0-3 (4 parts),
-    // or on waves 0-1 with the predictor on waves 2-3 (2 parts each).
-    const int sel_parts = predict ? 2 : 4;
-    if (wv < sel_parts) {
-        const int span = n_pad / sel_parts;
-        const uint32_t r = wave_topn(keys, wv * span, (wv + 1) * span, k, lane);
-        if (lane < 16) cand[16 * wv + lane] = lane < k ? r : 0u;
-    } else {
-        const int part = wv - 2, span = n_pad / 2;
-        const uint32_t r = wave_topn(pkeys, part * span, (part + 1) * span, m, lane);
-        if (lane < 32) pcand[32 * part + lane] = lane < m ? r : 0u;
-    }
-    __syncthreads();
+    // Top-k by rounds of wave maxima, one wave over all keys (the selection on wave 0, the
+    // predictor on wave 2): a round is a short dependent chain, and splitting the keys over
+    // waves adds a barrier and a second selection over the candidates, which costs more than
+    // it saves.
     if (wv == 0) {
-        const uint32_t mine = wave_topn(cand, 0, 16 * sel_parts, k, lane);  // lane j: the j-th largest
+        const uint32_t mine = wave_topn(keys, 0, n_pad, k, lane);  // lane j: the j-th largest
         // output position of the r-th largest is k-1-r (ascending gate order)
         const int pos = k - 1 - lane;
         const float g = __half2float(__ushort_as_half((uint16_t)(mine >> 16)));
@@ -326,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void k_router(
             scores_out[pos] = __float2half_rn(g / s);   // correctly rounded f32 division, then f16
         }
     } else if (wv == 2 && predict) {
-        const uint32_t mine = wave_topn(pcand, 0, 64, m, lane);
+        const uint32_t mine = wave_topn(pkeys, 0, n_pad, m, lane);
         // lanes 0..m-1 hold descending (value, id); equal values must come out in ascending id:
         // within a run of equal values, lane r takes the id of its mirror position in the run
         const uint32_t val = mine >> 16;

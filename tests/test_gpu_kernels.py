@@ -57,6 +57,36 @@ def test_router_rmsnorm_prologue_exact(dev):
         assert np.array_equal(sc.cpu().numpy().astype(np.float64), want_s[0])
 
 
+@pytest.mark.parametrize("n_exp,hidden,k,m", [(16, 256, 4, 6), (100, 520, 8, 12), (200, 2048, 10, 12),
+                                             (1024, 2048, 16, 32), (512, 4096, 10, 12)])
+def test_router_shapes_exact(dev, n_exp, hidden, k, m):
+    """Expert counts covering 1, 2, 4 and 16 keys per lane in the selection, a hidden size that
+    is not a multiple of 512 and one above 2048; both input kinds (x, and h with RMSNorm)."""
+    from moe_offload import ops, synth
+    w = synth.router_weight(n_exp, hidden, seed=n_exp + hidden)
+    wn = synth.router_weight(n_exp, hidden, seed=n_exp + hidden + 1)
+    wt, wnt = torch.from_numpy(w).to(dev), torch.from_numpy(wn).to(dev)
+    rng = np.random.default_rng(n_exp)
+    nw = (1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float16)
+    for t in range(4):
+        if t % 2 == 0:
+            xn = rng.standard_normal(hidden).astype(np.float16)
+            ids, sc, pred = ops.router(wt, k, x=torch.from_numpy(xn).to(dev), w_next=wnt, m=m)
+            xn = xn.astype(np.float64)
+        else:
+            h = (rng.standard_normal(hidden) * (1 + t)).astype(np.float32)
+            x_out = torch.empty(hidden, dtype=torch.float16, device=dev)
+            ids, sc, pred = ops.router(wt, k, h=torch.from_numpy(h).to(dev), norm_w=torch.from_numpy(nw).to(dev),
+                                       eps=1e-6, x_out=x_out, w_next=wnt, m=m)
+            xn = q2.round_to(q2.rmsnorm(h.astype(np.float64), nw, 1e-6), "f16")
+            assert np.array_equal(x_out.cpu().numpy().astype(np.float64), xn), (n_exp, hidden, t)
+        want_i, want_s, _ = q2.route(q2.router_logits(xn, w, "f16")[None], k, "f16")
+        want_p = q2.predict_topm(q2.router_logits(xn, wn, "f16")[None], m)
+        assert ids.cpu().numpy().astype(np.int64).tolist() == want_i[0].astype(np.int64).tolist(), (n_exp, hidden, t)
+        assert np.array_equal(sc.cpu().numpy().astype(np.float64), want_s[0]), (n_exp, hidden, t)
+        assert pred.cpu().numpy().tolist() == want_p[0].tolist(), (n_exp, hidden, t)
+
+
 def test_router_ties_follow_stable_rule(dev):
     """Hand-built ties: equal gates keep ascending id and the higher id wins the k boundary;
     equal predictor logits come out in ascending id."""
