@@ -118,7 +118,7 @@ def timed_tokens(st, xs, warmup, steps, use_graph):
 
 
 KINDS = ["router", "gate_up", "down", "stage", "slot_table", "grouped_gate_up", "grouped_down", "pair_combine",
-         "cb_up", "cb_down"]
+         "cb_up", "cb_down", "stream_calib"]
 
 
 def timed_kernels(run, calls, launches_per_call):
@@ -243,8 +243,10 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
 
 
 def launch_floor(byte_counts, grids=(320, 640, 1280, 2560), reps=50):
-    """Fastest single launch that only streams B bytes from HBM (moe_calibrate_stream over a
-    512 MiB region, a fresh offset each launch so the reads miss the caches), best grid."""
+    """Shortest kernel that only streams B bytes from HBM: moe_calibrate_stream launched `reps`
+    times back to back (a fresh offset of a 512 MiB region each launch, so the reads miss the
+    caches), each launch timed like the GEMV's -- HIP events stamped at the kernel's own begin and
+    end -- so the two durations compare like with like; best grid."""
     import torch
 
     from moe_offload import _lib
@@ -257,17 +259,13 @@ def launch_floor(byte_counts, grids=(320, 640, 1280, 2560), reps=50):
     for nb in byte_counts:
         best = None
         for grid in grids:
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-            for i in range(reps + 5):
+            def run(i, nb=nb, grid=grid):
                 off = ((i * nb) % (region - nb)) & ~255
-                if i >= 5:
-                    ev[i - 5][0].record(s)
                 _lib.check(L.moe_calibrate_stream(buf.data_ptr() + off, nb, grid, out.data_ptr(), s.cuda_stream),
                            "calibrate_stream")
-                if i >= 5:
-                    ev[i - 5][1].record(s)
-            torch.cuda.synchronize()
-            us = sum(a.elapsed_time(b) for a, b in ev) / reps * 1e3
+            for i in range(5):
+                run(i)
+            us = timed_kernels(run, reps, 1)["stream_calib"]["avg_us"]
             best = us if best is None or us < best else best
         res[nb] = best
     del buf

@@ -260,9 +260,9 @@ int c_sync_copies(void);
 /* Per-kernel timing: launches between begin and end are dispatched with start/stop events
  * stamped at the kernel's own begin/end; end() sums durations per kind (0 router, 1 gate/up,
  * 2 down, 3 staging, 4 slot table, 5 grouped gate/up, 6 grouped down, 7 pair combine,
- * 8 codebook up, 9 codebook down) into out_ms[MOE_TIMING_KINDS] and counts into
- * out_n[MOE_TIMING_KINDS]. */
-#define MOE_TIMING_KINDS 10
+ * 8 codebook up, 9 codebook down, 10 streaming calibration) into out_ms[MOE_TIMING_KINDS] and
+ * counts into out_n[MOE_TIMING_KINDS]. */
+#define MOE_TIMING_KINDS 11
 int c_timing_begin(int capacity);
 int c_timing_end(double* out_ms, int* out_n);
 /* Plain device-to-device copy of `bytes` (multiple of 16): the known-size reference for scaling

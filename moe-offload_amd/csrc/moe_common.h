@@ -142,7 +142,7 @@ void moe_set_error(const char* fmt, ...);
 // hipExtLaunchKernelGGL with a start/stop event pair, which the runtime stamps at the kernel's
 // own begin/end; kinds index the accumulated totals.
 enum { TK_ROUTER = 0, TK_GATE_UP, TK_DOWN, TK_STAGE, TK_SLOT, TK_PF_GATE_UP, TK_PF_DOWN, TK_COMBINE, TK_CB_UP,
-       TK_CB_DOWN, TK_KINDS };
+       TK_CB_DOWN, TK_STREAM_CALIB, TK_KINDS };
 bool kt_enabled();
 void kt_events(int kind, hipEvent_t* start, hipEvent_t* stop);   // both null when disabled / full
 

@@ -137,7 +137,7 @@ int launch_stream_calib(const void* src, size_t bytes, int grid, float* out, hip
         moe_set_error("stream_calib: bytes must be a positive multiple of 16, grid > 0");
         return -1;
     }
-    hipLaunchKernelGGL(k_stream_calib, dim3(grid), dim3(256), 0, s, (const uint4*)src, bytes / 16, out);
+    MOE_LAUNCH(TK_STREAM_CALIB, k_stream_calib, dim3(grid), dim3(256), 0, s, (const uint4*)src, bytes / 16, out);
     HIP_TRY(hipGetLastError());
     return 0;
 }
