@@ -75,7 +75,11 @@ __device__ __forceinline__ float sb_apply(uint32_t sb, float dot, float cst, flo
 // 64) as its 8 dot2 pairs P[8w + p] = (a[16w + p], a[16w + p + 8]) and add its share of the
 // group's constants.  The 4 units of a group sit on 4 adjacent lanes, which sum the constants
 // with two DPP steps, so every lane of the wave must call this (store masks the writes).
-__device__ __forceinline__ void stage_pairs(uint4 lo4, uint4 hi4, bool store, uint4* grp_pairs, float* grp_c, int w) {
+// A group's 8 pair vectors sit at slots i ^ swz (swz = group & 7): lanes reading vector i of
+// different groups then hit different LDS banks instead of all the same ones (a group is 128
+// bytes, a full bank cycle).
+__device__ __forceinline__ void stage_pairs(uint4 lo4, uint4 hi4, bool store, uint4* grp_pairs, float* grp_c, int w,
+                                            int swz) {
     const uint32_t lo[4] = {lo4.x, lo4.y, lo4.z, lo4.w};
     const uint32_t hi[4] = {hi4.x, hi4.y, hi4.z, hi4.w};
     uint32_t pr[8];
@@ -91,8 +95,8 @@ __device__ __forceinline__ void stage_pairs(uint4 lo4, uint4 hi4, bool store, ui
     cc = lanes::group_sum<4>(cc);
     ss = lanes::group_sum<4>(ss);
     if (store) {
-        grp_pairs[2 * w] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-        grp_pairs[2 * w + 1] = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+        grp_pairs[(2 * w) ^ swz] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+        grp_pairs[(2 * w + 1) ^ swz] = make_uint4(pr[4], pr[5], pr[6], pr[7]);
         if (w == 0) {
             grp_c[0] = 1024.0f * cc;
             grp_c[1] = ss;
@@ -147,14 +151,14 @@ __global__ __launch_bounds__(256) void k_q2_gate_up(
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    stage_pairs(xlo, xhi, tid < n_units, xp[uc >> 2], xc[uc >> 2], uc & 3);
+    stage_pairs(xlo, xhi, tid < n_units, xp[uc >> 2], xc[uc >> 2], uc & 3, (uc >> 2) & 7);
     __builtin_amdgcn_sched_barrier(0);                  // no weight use ahead of the barrier
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     h2_t P[32];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const uint4 v = xp[g][i];
+        const uint4 v = xp[g][i ^ (g & 7)];
         P[4 * i] = as_h2(v.x);
         P[4 * i + 1] = as_h2(v.y);
         P[4 * i + 2] = as_h2(v.z);
@@ -249,7 +253,7 @@ __global__ __launch_bounds__(256) void k_q2_down(
         if (256 * ui >= n_units) break;            // block-uniform: no lane of this pass is valid
         const int uc = u < n_units ? u : 0;
         const int jj = uc / (GPR * 4), gg = (uc >> 2) % GPR;
-        stage_pairs(hv[ui][0], hv[ui][1], u < n_units, hp[jj][gg], hc[jj][gg], uc & 3);
+        stage_pairs(hv[ui][0], hv[ui][1], u < n_units, hp[jj][gg], hc[jj][gg], uc & 3, gg & 7);
     }
     __syncthreads();
 
@@ -264,7 +268,7 @@ __global__ __launch_bounds__(256) void k_q2_down(
         const uint4* src = hp[j][g];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint4 v = src[i];
+            const uint4 v = src[i ^ (g & 7)];
             P[4 * i] = as_h2(v.x);
             P[4 * i + 1] = as_h2(v.y);
             P[4 * i + 2] = as_h2(v.z);
