@@ -15,8 +15,8 @@
 // lane (n = lane & 15, kq = lane >> 4) loads group 4j + kq of weight row n (one 16-byte load of
 // 64 codes plus the (scale, bias) word), dequantises it once and multiplies it into every tile
 // of the batch; the chunk's activations of the batch's rows are staged in LDS (each thread
-// stages 2 units of 16 bytes per tile).  One chunk is in flight per block; the latency is
-// covered by the other resident blocks of the CU.
+// stages 2 units of 16 bytes per tile).  The next chunk's weights are loaded while the current
+// chunk is multiplied.
 //
 // Dequantisation.  A 2-bit code in the low bits of a nibble is the fp4 (e2m1) value q/2, so
 // w & 0x33333333 (even codes) and (w >> 2) & 0x33333333 (odd codes) are 8 fp4 values each;
@@ -87,6 +87,7 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
     const uint8_t* __restrict__ pool, size_t stride, int n_slots, BlobLayout L, int tiles_per_seg,
     __half* __restrict__ out) {
     constexpr int kMaxMT = max_mt<MODE>();
+    constexpr bool kPrefetch = MODE == kGateUp;        // a short K (down) gains nothing from it
     const int K = MODE == kGateUp ? L.hidden : L.inter;          // contraction length
     const int N = MODE == kGateUp ? L.inter : L.hidden;          // output rows per projection
     const int kg = K / 64;
@@ -176,8 +177,8 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
 #pragma unroll
             for (int s = 0; s < kSub; ++s) acc[mt][s] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-        uint4 cw[kSub];
-        uint32_t sw[kSub];
+        uint4 cwa[kSub], cwb[kSub];                            // weights of the current / next chunk
+        uint32_t swa[kSub], swb[kSub];
         uint4 xs[kMaxMT][2];                                   // staged activation units in flight
         // Loads are unconditional from clamped in-range addresses and nothing masks them where
         // they land: a load whose value is selected right away is sunk into a branch by the
@@ -185,7 +186,7 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
         // Groups past K (a K that is not a multiple of 256) read group kg - 1: their activations
         // are staged as zeros, so those finite weights add nothing.  Rows past the segment and
         // out-of-range source rows are zeroed when staged.
-        auto load = [&](int j) {
+        auto load_w = [&](int j, uint4 (&cw)[kSub], uint32_t (&sw)[kSub]) {
             const bool gv = 4 * j + kq < kg;
             const int gdelta = gv ? 0 : (kg - 1) - (4 * j + kq);      // clamp to group kg - 1
 #pragma unroll
@@ -193,6 +194,8 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
                 cw[s] = *reinterpret_cast<const uint4*>(codes[s] + lane_code + (size_t)j * 64 + (ptrdiff_t)gdelta * 16);
                 sw[s] = sbp[s][lane_sb + 4 * j + gdelta];
             }
+        };
+        auto load_x = [&](int j) {
             const int u = 32 * j + sv;                         // 16-byte unit within the row
             const int uc = u * 8 < K ? u : K / 8 - 1;
 #pragma unroll
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
         };
         // Per 32-bit word q of the lane's group: the activation fragments of every tile, then per
         // subtile the two dequantised weight fragments, multiplied into every tile.
-        auto compute = [&]() {
+        auto compute = [&](const uint4 (&cw)[kSub], const uint32_t (&sw)[kSub]) {
             f16x2 s2[kSub], b2[kSub];
 #pragma unroll
             for (int s = 0; s < kSub; ++s) {
@@ -249,15 +252,37 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
                 }
             }
         };
-        // Per chunk: issue its loads, then (after every wave is done with the previous chunk's
-        // activations) stage them and multiply.  Latency is hidden by the other resident blocks.
+        // Software pipeline, one chunk deep: chunk j + 1's weights are in flight while chunk j is
+        // multiplied.  Loads retire in issue order, so the activations of chunk j are issued
+        // before the weights of chunk j + 1: staging j then waits for its activations only.  The
+        // last chunk's look-ahead re-reads the last chunk (an L2 hit), so no load is conditional.
+        if constexpr (kPrefetch) {
+            load_x(0);
+            load_w(0, cwa, swa);
 #pragma unroll 1
-        for (int j = 0; j < NCH; ++j) {
-            load(j);
-            __syncthreads();                                   // every wave is done with chunk j - 1
-            stage(j);
-            __syncthreads();
-            compute();
+            for (int j = 0; j < NCH; ++j) {
+                load_w(j + 1 < NCH ? j + 1 : NCH - 1, cwb, swb);
+                __syncthreads();                               // every wave is done with chunk j - 1
+                stage(j);
+                __syncthreads();
+                compute(cwa, swa);
+                load_x(j + 1 < NCH ? j + 1 : NCH - 1);
+#pragma unroll
+                for (int s = 0; s < kSub; ++s) {
+                    cwa[s] = cwb[s];
+                    swa[s] = swb[s];
+                }
+            }
+        } else {
+#pragma unroll 1
+            for (int j = 0; j < NCH; ++j) {
+                load_x(j);
+                load_w(j, cwa, swa);
+                __syncthreads();                               // every wave is done with chunk j - 1
+                stage(j);
+                __syncthreads();
+                compute(cwa, swa);
+            }
         }
 
         // Epilogue: lane holds rows 4*kq + i (i = 0..3) of column n of each subtile of each tile.
