@@ -182,8 +182,24 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
         chunk(i)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / iters
-    kt = timed_kernels(chunk, iters, 3)
-    gu, dn, cb = (kt[n]["avg_us"] * 1e-6 for n in ("grouped_gate_up", "grouped_down", "pair_combine"))
+
+    # each step timed alone, `iters` times back to back, bracketed by two HIP events (per-launch
+    # stamps overlap the kernel queued before; gate/up is two launches: one-tile and longer
+    # segments)
+    def bracketed(fn):
+        s = torch.cuda.current_stream()
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(iters):
+            fn()
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / iters
+    gu = bracketed(lambda: ops.q2_grouped_gate_up(x, row_tok, seg, pool, hidden, inter, seg_slot=slot, h_out=h_ws))
+    dn = bracketed(lambda: ops.q2_grouped_down(h_ws, seg, pool, hidden, inter, row_out=row_out, n_out_rows=m,
+                                               seg_slot=slot, out=y))
+    cb = bracketed(lambda: ops.pair_combine(y, sc, out=out))
     n_used = int(slot.numel())
     blob = q2format.expert_bytes(hidden, inter, 64)
     o = q2format.blob_offsets(hidden, inter, 64)
