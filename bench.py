@@ -552,7 +552,6 @@ def main():
                                     "launches back to back over the 48 layer pools, fresh top-10 draws, bracketed "
                                     "by HIP events on the launch stream",
                      "bytes_per_launch": gu_bytes, "avg_launch_us": round(gu_avg * 1e6, 3),
-                     "avg_launch_us_stamped_in_decode": res["kernels_us"]["gate_up"],
                      "launch_floor_us": round(floor_us, 3),
                      "frac_of_launch_floor": round(floor_us / (gu_avg * 1e6), 4)},
         "cache": {"effective_hit_rate": round((tot1[0] - tot0[0] + tot1[1] - tot0[1]) / req, 4),

@@ -120,6 +120,17 @@ int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_i
                void* workspace, uint32_t* ids_out, void* scores_out, int32_t* pred_out,
                void* stream);
 uint64_t moe_router_workspace_bytes(int n_exp);
+/* moe_router split at the logits, for a pool that holds every expert (the resident path; no
+ * slot table has to run once per layer): moe_router_logits writes logits_out fp32 [n_exp] (each
+ * the fp16-rounded logit moe_router computes), and moe_q2_gate_up_routed's blocks select the
+ * top-k from them with moe_router's rule (same ids, order and scores, bit for bit; ids_out and
+ * scores_out as moe_router's) before their moe_q2_gate_up over pool[id].  Together they replace
+ * moe_router + moe_q2_gate_up without the router's last-block hand-off.  n_exp <= 1024. */
+int moe_router_logits(const float* h_in, const void* norm_w, float eps, const void* x_in, void* x_out,
+                      const void* w, int hidden, int n_exp, float* logits_out, void* stream);
+int moe_q2_gate_up_routed(const void* x, const float* logits, int n_exp, int k, const void* pool,
+                          uint64_t stride, int hidden, int inter, int group, uint32_t* ids_out,
+                          void* scores_out, void* h_out, void* stream);
 /* The single f64 -> f16 rounding every kernel uses (exposed so tests can check it directly). */
 int moe_f64_to_f16(const double* in, uint16_t* out, int n, void* stream);
 /* Builder-defined glue between stacked MoE layers (no reference counterpart: the reference

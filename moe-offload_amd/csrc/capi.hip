@@ -707,6 +707,19 @@ int c_layer_table_status(int layer) {
 
 uint64_t moe_router_workspace_bytes(int n_exp) { return (uint64_t)(2 * n_exp) * sizeof(float) + 256; }
 
+int moe_router_logits(const float* h_in, const void* norm_w, float eps, const void* x_in, void* x_out, const void* w,
+                      int hidden, int n_exp, float* logits_out, void* stream) {
+    return launch_router_logits(h_in, (const __half*)norm_w, eps, (const __half*)x_in, (__half*)x_out,
+                                (const __half*)w, hidden, n_exp, logits_out, (hipStream_t)stream);
+}
+
+int moe_q2_gate_up_routed(const void* x, const float* logits, int n_exp, int k, const void* pool, uint64_t stride,
+                          int hidden, int inter, int group, uint32_t* ids_out, void* scores_out, void* h_out,
+                          void* stream) {
+    return launch_q2_gate_up_routed((const __half*)x, logits, n_exp, k, (const uint8_t*)pool, stride, hidden, inter,
+                                    group, ids_out, (__half*)scores_out, (__half*)h_out, (hipStream_t)stream);
+}
+
 int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_in, void* x_out, const void* w,
                const void* w_next, int hidden, int n_exp, int k, int m, void* workspace, uint32_t* ids_out,
                void* scores_out, int32_t* pred_out, void* stream) {

@@ -162,6 +162,15 @@ int launch_router(const float* h_in, const __half* norm_w, float eps, const __ha
                   int k, int m, float* scratch, unsigned* counter, uint32_t* ids_out,
                   __half* scores_out, int32_t* pred_out, SlotTable* step_tab, uint32_t* slot_inds,
                   SlotTable* pf_tab, int max_fetch, hipStream_t s);
+// The router's [RMSNorm +] GEMV alone: logits_out[n_exp] = fp16-rounded logits (as floats).
+int launch_router_logits(const float* h_in, const __half* norm_w, float eps, const __half* x_in, __half* x_out,
+                         const __half* w, int hidden, int n_exp, float* logits_out, hipStream_t s);
+// Gate/up whose blocks first select the top-k experts from the logits (the router's rule, bit
+// for bit) over a pool holding every expert (slot = id); ids/scores also go to ids_out /
+// scores_out for the down product.
+int launch_q2_gate_up_routed(const __half* x, const float* logits, int n_exp, int k, const uint8_t* pool,
+                             size_t expert_stride, int hidden, int inter, int group, uint32_t* ids_out,
+                             __half* scores_out, __half* h_out, hipStream_t s);
 int launch_f64_to_f16(const double* in, uint16_t* out, int n, hipStream_t s);
 int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidden, __half* x_out,
                    hipStream_t s);

@@ -27,6 +27,7 @@
 
 #include "lane_reduce.h"
 #include "moe_common.h"
+#include "route_select.h"
 
 namespace {
 
@@ -106,10 +107,16 @@ __device__ __forceinline__ void stage_pairs(uint4 lo4, uint4 hi4, bool store, ui
 
 constexpr int kGuRowsPerIter = 2;   // rows per wave (each iteration covers 32/GPR rows)
 
-template <int GPR>
-__global__ __launch_bounds__(256) void k_q2_gate_up(
+// Rows of gate and up for one selected expert.  ROUTED: the block first selects the top-k
+// experts from the router's logits itself (the router's rule, bit for bit) over a pool holding
+// every expert (slot = id); block (0, 0) also writes the ids and scores.  The selection runs
+// while the activation loads are in flight; it replaces the router's last-block hand-off
+// (a device-scope counter and a second read of every logit) on the resident path.
+template <int GPR, bool ROUTED>
+__device__ __forceinline__ void gate_up_body(
     const __half* __restrict__ x, const uint8_t* __restrict__ pool, size_t stride,
-    const uint32_t* __restrict__ slots, int n_slots, int inter, BlobLayout L, __half* __restrict__ h_out) {
+    const uint32_t* __restrict__ slots, int n_slots, int inter, const BlobLayout& L, __half* __restrict__ h_out,
+    const float* __restrict__ logits, int k, uint32_t* __restrict__ ids_out, __half* __restrict__ scores_out) {
     constexpr int RPI = 32 / GPR;                       // rows per wave instruction
     constexpr int ROWS_PER_WAVE = RPI * kGuRowsPerIter;
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -131,7 +138,35 @@ __global__ __launch_bounds__(256) void k_q2_gate_up(
     const uint4 xhi = reinterpret_cast<const uint4*>(x)[2 * uc + 1];
     __builtin_amdgcn_sched_barrier(0);
 
-    const uint32_t slot = slots[j];
+    uint32_t slot;
+    if constexpr (ROUTED) {
+        __shared__ uint32_t keys[route::kMaxExperts];
+        __shared__ double redm[4], reds[4];
+        __shared__ uint32_t sel[MOE_MAX_K];
+        float lraw[route::kPer];
+#pragma unroll
+        for (int i = 0; i < route::kPer; ++i) {
+            const int e = tid + route::kThreads * i;
+            lraw[i] = logits[e < n_slots ? e : 0];
+        }
+        route::gate_keys(lraw, n_slots, keys, redm, reds);
+        if (wv == 0) {
+            uint32_t id;
+            __half sc;
+            const int pos = route::select_topk(keys, ((n_slots + 63) / 64) * 64, k, lane, id, sc);
+            if (pos >= 0) {
+                sel[pos] = id;
+                if (blockIdx.x == 0 && blockIdx.y == 0) {
+                    ids_out[pos] = id;
+                    scores_out[pos] = sc;
+                }
+            }
+        }
+        __syncthreads();
+        slot = sel[j];
+    } else {
+        slot = slots[j];
+    }
     const bool ok = slot < (uint32_t)n_slots;         // an invalid slot yields h = 0
     const uint8_t* blob = pool + (size_t)(ok ? slot : 0) * stride;
     const uint8_t* codes = blob + (proj ? L.up_codes : L.gate_codes);
@@ -182,6 +217,21 @@ __global__ __launch_bounds__(256) void k_q2_gate_up(
             h_out[(size_t)j * inter + row] = __float2half_rn(hval);
         }
     }
+}
+
+template <int GPR>
+__global__ __launch_bounds__(256) void k_q2_gate_up(
+    const __half* __restrict__ x, const uint8_t* __restrict__ pool, size_t stride,
+    const uint32_t* __restrict__ slots, int n_slots, int inter, BlobLayout L, __half* __restrict__ h_out) {
+    gate_up_body<GPR, false>(x, pool, stride, slots, n_slots, inter, L, h_out, nullptr, 0, nullptr, nullptr);
+}
+
+template <int GPR>
+__global__ __launch_bounds__(256) void k_q2_gate_up_routed(
+    const __half* __restrict__ x, const float* __restrict__ logits, int n_exp, int k, const uint8_t* __restrict__ pool,
+    size_t stride, int inter, BlobLayout L, uint32_t* __restrict__ ids_out, __half* __restrict__ scores_out,
+    __half* __restrict__ h_out) {
+    gate_up_body<GPR, true>(x, pool, stride, nullptr, n_exp, inter, L, h_out, logits, k, ids_out, scores_out);
 }
 
 constexpr int kDownRows = 8;      // output rows per block (one wave instruction at GPR = 8)
@@ -322,6 +372,17 @@ int gate_up_t(const __half* x, const uint8_t* pool, size_t stride, const uint32_
 }
 
 template <int GPR>
+int gate_up_routed_t(const __half* x, const float* logits, int n_exp, int k, const uint8_t* pool, size_t stride,
+                     int inter, BlobLayout L, uint32_t* ids_out, __half* scores_out, __half* h_out, hipStream_t s) {
+    constexpr int rows_per_block = 4 * (32 / GPR) * kGuRowsPerIter;
+    dim3 grid((inter + rows_per_block - 1) / rows_per_block, k);
+    MOE_LAUNCH(TK_GATE_UP, (k_q2_gate_up_routed<GPR>), grid, dim3(256), 0, s, x, logits, n_exp, k, pool, stride, inter, L,
+               ids_out, scores_out, h_out);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+template <int GPR>
 int down_t(const __half* h, const uint8_t* pool, size_t stride, const uint32_t* slots, int n_slots,
            const __half* scores, int k, int hidden, BlobLayout L, const __half* residual,
            float* y_out, int per_expert, hipStream_t s) {
@@ -358,6 +419,28 @@ int launch_q2_gate_up(const __half* x, const uint8_t* pool, size_t stride, int n
         case 16: return gate_up_t<16>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
         case 32: return gate_up_t<32>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
         default: moe_set_error("q2_gate_up: hidden=%d unsupported (64*{1,2,4,8,16,32})", hidden); return -1;
+    }
+}
+
+int launch_q2_gate_up_routed(const __half* x, const float* logits, int n_exp, int k, const uint8_t* pool,
+                             size_t stride, int hidden, int inter, int group, uint32_t* ids_out, __half* scores_out,
+                             __half* h_out, hipStream_t s) {
+    if (!check_shape("q2_gate_up_routed", k, hidden, inter, group)) return -1;
+    if (n_exp <= 0 || n_exp > route::kMaxExperts || k > n_exp) {
+        moe_set_error("q2_gate_up_routed: n_exp=%d (<= %d, >= k=%d)", n_exp, route::kMaxExperts, k);
+        return -1;
+    }
+    if (!pool || !x || !logits || !ids_out || !scores_out || !h_out) { moe_set_error("q2_gate_up_routed: null pointer"); return -1; }
+    BlobLayout L = blob_layout(hidden, inter, group);
+    if (stride < L.bytes) { moe_set_error("q2_gate_up_routed: expert stride %zu < blob bytes %zu", stride, L.bytes); return -1; }
+    switch (hidden / 64) {
+        case 1: return gate_up_routed_t<1>(x, logits, n_exp, k, pool, stride, inter, L, ids_out, scores_out, h_out, s);
+        case 2: return gate_up_routed_t<2>(x, logits, n_exp, k, pool, stride, inter, L, ids_out, scores_out, h_out, s);
+        case 4: return gate_up_routed_t<4>(x, logits, n_exp, k, pool, stride, inter, L, ids_out, scores_out, h_out, s);
+        case 8: return gate_up_routed_t<8>(x, logits, n_exp, k, pool, stride, inter, L, ids_out, scores_out, h_out, s);
+        case 16: return gate_up_routed_t<16>(x, logits, n_exp, k, pool, stride, inter, L, ids_out, scores_out, h_out, s);
+        case 32: return gate_up_routed_t<32>(x, logits, n_exp, k, pool, stride, inter, L, ids_out, scores_out, h_out, s);
+        default: moe_set_error("q2_gate_up_routed: hidden=%d unsupported (64*{1,2,4,8,16,32})", hidden); return -1;
     }
 }
 

@@ -1,0 +1,144 @@
+// Expert selection of the router (loader.py:903-908; cpp/src/layers.cpp:311-325), shared by the
+// router's last block and the resident-path gate/up kernel, which therefore select bit for bit
+// alike.  Input: the n_exp logits, already rounded to fp16 (held as floats).
+//   gates = fp16(softmax in fp64), keys = (gate bits << 16 | id): gates are >= 0, so the bit
+//   pattern orders like the value and equal gates order by id (the higher id wins at the k
+//   boundary); the top k keys in ascending order are the selected ids; scores = fp16(g / s) with
+//   s the left-to-right fp16-rounded sum over that order.
+#pragma once
+#include <hip/hip_fp16.h>
+
+#include "lane_reduce.h"
+#include "moe_common.h"
+
+namespace route {
+
+constexpr int kThreads = 256;                  // the selection runs on a block of 256 threads
+constexpr int kMaxExperts = 1024;
+constexpr int kPer = kMaxExperts / kThreads;   // logits per thread
+
+// Wave-wide max of a uint32 with DPP inside each 16-lane row, then the four row results.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+    uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
+}
+
+
+// f64 -> f16 with a single round-to-nearest-even: truncate to f32, set the sticky bit when
+// inexact (round-to-odd with 24 >= 11 + 2 bits), then let the f32 -> f16 conversion round.
+__device__ __forceinline__ uint16_t f64_to_f16_bits(double d) {
+    float f = __double2float_rz(d);
+    if ((double)f != d) f = __uint_as_float(__float_as_uint(f) | 1u);
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+__device__ __forceinline__ float round_f16(double v) {
+    return __half2float(__ushort_as_half(f64_to_f16_bits(v)));
+}
+
+// The n largest keys of keys[lo, hi) (LDS; distinct, 0 = empty) by one wave: lane r < n gets
+// the r-th largest (0 once the range runs out).  KPL keys per lane cover the range; each round
+// takes the wave maximum and clears it where it sits.
+template <int KPL>
+__device__ __forceinline__ uint32_t wave_topn_k(const uint32_t* keys, int lo, int hi, int n, int lane) {
+    uint32_t key[KPL];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+        const int idx = lo + lane + 64 * i;
+        key[i] = idx < hi ? keys[idx] : 0u;
+    }
+    uint32_t mine = 0;
+    for (int r = 0; r < n; ++r) {
+        uint32_t best = key[0];
+#pragma unroll
+        for (int i = 1; i < KPL; ++i) best = max(best, key[i]);
+        best = wave_max_u32(best);
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) key[i] = key[i] == best ? 0u : key[i];
+        if (lane == r) mine = best;
+    }
+    return mine;
+}
+
+// wave_topn_k with KPL fixed at compile time for the range size (up to kMaxExperts keys): a
+// runtime bound would turn every key operation into a masked select.
+__device__ __forceinline__ uint32_t wave_topn(const uint32_t* keys, int lo, int hi, int n, int lane) {
+    const int kpl = (hi - lo + 63) / 64;                    // wave-uniform
+    if (kpl <= 1) return wave_topn_k<1>(keys, lo, hi, n, lane);
+    if (kpl <= 2) return wave_topn_k<2>(keys, lo, hi, n, lane);
+    if (kpl <= 4) return wave_topn_k<4>(keys, lo, hi, n, lane);
+    if (kpl <= 8) return wave_topn_k<8>(keys, lo, hi, n, lane);
+    return wave_topn_k<kMaxExperts / 64>(keys, lo, hi, n, lane);
+}
+
+// Order-preserving map of an fp16 value to uint16 (signed values; -0 folded onto +0).
+__device__ __forceinline__ uint32_t f16_order(uint16_t b) {
+    if (b == 0x8000u) b = 0;
+    return (b & 0x8000u) ? (uint32_t)(~b & 0xFFFFu) : (uint32_t)(b | 0x8000u);
+}
+
+// Block-wide: the gate keys of the logits this thread holds (lraw[i] = logit tid + kThreads i,
+// any value where that index is >= n_exp) into keys[0, n_pad) (n_pad = n_exp rounded up to 64;
+// padding keys 0).  Ends with a barrier.
+__device__ __forceinline__ void gate_keys(const float (&lraw)[kPer], int n_exp, uint32_t* keys, double* redm,
+                                          double* reds) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n_pad = ((n_exp + 63) / 64) * 64;
+    double lv[kPer];
+    double mx = -1e300;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = tid + kThreads * i;
+        lv[i] = e < n_exp ? (double)lraw[i] : -1e300;
+        mx = fmax(mx, lv[i]);
+    }
+    mx = lanes::wave_max_f64(mx);
+    if (lane == 0) redm[wv] = mx;
+    __syncthreads();
+    mx = fmax(fmax(redm[0], redm[1]), fmax(redm[2], redm[3]));
+    double sum = 0.0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        int e = tid + kThreads * i;
+        lv[i] = (e < n_exp) ? exp(lv[i] - mx) : 0.0;
+        sum += lv[i];
+    }
+    sum = lanes::wave_sum_f64(sum);
+    if (lane == 0) reds[wv] = sum;
+    __syncthreads();
+    sum = (reds[0] + reds[1]) + (reds[2] + reds[3]);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        int e = tid + kThreads * i;
+        if (e < n_pad) keys[e] = (e < n_exp) ? (((uint32_t)f64_to_f16_bits(lv[i] / sum) << 16) | (uint32_t)e) : 0u;
+    }
+    __syncthreads();
+}
+
+// One wave: the selection from the keys.  Lane r < k returns the id and score that go to output
+// position k - 1 - r (ascending gate order); other lanes return position -1.
+__device__ __forceinline__ int select_topk(const uint32_t* keys, int n_pad, int k, int lane, uint32_t& id,
+                                           __half& score) {
+    // Top-k by rounds of wave maxima, one wave over all keys: a round is a short dependent chain,
+    // and splitting the keys over waves adds a barrier and a second selection over the
+    // candidates, which costs more than it saves.
+    const uint32_t mine = wave_topn(keys, 0, n_pad, k, lane);  // lane j: the j-th largest
+    const float g = __half2float(__ushort_as_half((uint16_t)(mine >> 16)));
+    // left-to-right sum over ascending order, each partial rounded to fp16; the gates are fp16
+    // values in ascending order, so every partial sum is exact in fp32 before rounding
+    float s = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), k - 1 - j));
+        s = __half2float(__float2half_rn(s + gj));
+    }
+    id = mine & 0xFFFFu;
+    score = __float2half_rn(g / s);                    // correctly rounded f32 division, then f16
+    return lane < k ? k - 1 - lane : -1;
+}
+
+}  // namespace route

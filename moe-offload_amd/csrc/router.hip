@@ -26,85 +26,20 @@
 
 #include "lane_reduce.h"
 #include "moe_common.h"
+#include "route_select.h"
 #include "slot_table_dev.h"
 
 namespace {
 
-constexpr int kThreads = 256;
+using route::kMaxExperts;
+using route::kThreads;
+using route::f16_order;
+using route::f64_to_f16_bits;
+using route::round_f16;
+using route::wave_topn;
+using lanes::wave_sum_f64;
 constexpr int kRowsPerBlock = 4;          // one weight row per wave
 constexpr int kMaxHidden = 4096;
-constexpr int kMaxExperts = 1024;
-
-using lanes::wave_max_f64;
-using lanes::wave_sum_f64;
-
-// Wave-wide max of a uint32 with DPP inside each 16-lane row, then the four row results.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
-    uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-    uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-    return max(max(a, b), max(c, d));
-}
-
-}  // namespace
-
-// f64 -> f16 with a single round-to-nearest-even: truncate to f32, set the sticky bit when
-// inexact (round-to-odd with 24 >= 11 + 2 bits), then let the f32 -> f16 conversion round.
-static __device__ __forceinline__ uint16_t f64_to_f16_bits(double d) {
-    float f = __double2float_rz(d);
-    if ((double)f != d) f = __uint_as_float(__float_as_uint(f) | 1u);
-    return __half_as_ushort(__float2half_rn(f));
-}
-
-namespace {
-
-__device__ __forceinline__ float round_f16(double v) {
-    return __half2float(__ushort_as_half(f64_to_f16_bits(v)));
-}
-
-// The n largest keys of keys[lo, hi) (LDS; distinct, 0 = empty) by one wave: lane r < n gets
-// the r-th largest (0 once the range runs out).  KPL keys per lane cover the range; each round
-// takes the wave maximum and clears it where it sits.
-template <int KPL>
-__device__ __forceinline__ uint32_t wave_topn_k(const uint32_t* keys, int lo, int hi, int n, int lane) {
-    uint32_t key[KPL];
-#pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-        const int idx = lo + lane + 64 * i;
-        key[i] = idx < hi ? keys[idx] : 0u;
-    }
-    uint32_t mine = 0;
-    for (int r = 0; r < n; ++r) {
-        uint32_t best = key[0];
-#pragma unroll
-        for (int i = 1; i < KPL; ++i) best = max(best, key[i]);
-        best = wave_max_u32(best);
-#pragma unroll
-        for (int i = 0; i < KPL; ++i) key[i] = key[i] == best ? 0u : key[i];
-        if (lane == r) mine = best;
-    }
-    return mine;
-}
-
-// wave_topn_k with KPL fixed at compile time for the range size (up to kMaxExperts keys): a
-// runtime bound would turn every key operation into a masked select.
-__device__ __forceinline__ uint32_t wave_topn(const uint32_t* keys, int lo, int hi, int n, int lane) {
-    const int kpl = (hi - lo + 63) / 64;                    // wave-uniform
-    if (kpl <= 1) return wave_topn_k<1>(keys, lo, hi, n, lane);
-    if (kpl <= 2) return wave_topn_k<2>(keys, lo, hi, n, lane);
-    if (kpl <= 4) return wave_topn_k<4>(keys, lo, hi, n, lane);
-    if (kpl <= 8) return wave_topn_k<8>(keys, lo, hi, n, lane);
-    return wave_topn_k<kMaxExperts / 64>(keys, lo, hi, n, lane);
-}
-
-// Order-preserving map of an fp16 value to uint16 (signed values; -0 folded onto +0).
-__device__ __forceinline__ uint32_t f16_order(uint16_t b) {
-    if (b == 0x8000u) b = 0;
-    return (b & 0x8000u) ? (uint32_t)(~b & 0xFFFFu) : (uint32_t)(b | 0x8000u);
-}
 
 // fp64 RMSNorm of h (fp32 [hidden]) into fp16 bits in LDS; every block computes it.
 // Thread tid owns elements 4 (c kThreads + tid) + 0..3 for chunk c (hidden is a multiple of 8).
@@ -234,9 +169,14 @@ __global__ __launch_bounds__(kThreads) void k_router(
         }
         acc = wave_sum_f64(acc);
         // publish with an agent-scope atomic store (written through to the device coherence
-        // point), so the only ordering needed before counting in is this wave's store completion
-        if (lane == 0) __hip_atomic_store(&scratch[row], round_f16(acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // point), so the only ordering needed before counting in is this wave's store completion;
+        // without a counter the logits are the output (read by a later kernel: a plain store)
+        if (lane == 0) {
+            if (counter) __hip_atomic_store(&scratch[row], round_f16(acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else scratch[row] = round_f16(acc);
+        }
     }
+    if (!counter) return;                 // logits only: the consumer selects
 
     // ---- the last block to finish selects ---------------------------------------------------
     // Every logit store of this block has completed (vmcnt(0)) before the block counts itself
@@ -259,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void k_router(
     // first, unconditionally from a clamped index (scratch holds 2 * n_exp values), and masked
     // afterwards: a load merged with a default value at a branch join is waited for inside the
     // branch, one round trip per load.
-    constexpr int kPer = kMaxExperts / kThreads;
+    constexpr int kPer = route::kPer;
     float lraw[kPer], praw[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
@@ -268,59 +208,25 @@ __global__ __launch_bounds__(kThreads) void k_router(
         lraw[i] = __hip_atomic_load(&scratch[ec], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         praw[i] = __hip_atomic_load(&scratch[n_exp + ec], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    double lv[kPer];
-    double mx = -1e300;
+    if (predict) {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int e = tid + kThreads * i;
-        lv[i] = e < n_exp ? (double)lraw[i] : -1e300;
-        mx = fmax(mx, lv[i]);
-        if (predict && e < n_pad)
-            pkeys[e] = (e < n_exp) ? ((f16_order(__half_as_ushort(__float2half_rn(praw[i]))) << 16) | (uint32_t)e) : 0u;
-    }
-    mx = wave_max_f64(mx);
-    if (lane == 0) redm[wv] = mx;
-    __syncthreads();
-    mx = fmax(fmax(redm[0], redm[1]), fmax(redm[2], redm[3]));
-    double sum = 0.0;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        int e = tid + kThreads * i;
-        lv[i] = (e < n_exp) ? exp(lv[i] - mx) : 0.0;
-        sum += lv[i];
-    }
-    sum = wave_sum_f64(sum);
-    if (lane == 0) reds[wv] = sum;
-    __syncthreads();
-    sum = (reds[0] + reds[1]) + (reds[2] + reds[3]);
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        int e = tid + kThreads * i;
-        // gates are >= 0, so fp16 bit patterns order like the values; id breaks ties upward
-        if (e < n_pad) keys[e] = (e < n_exp) ? (((uint32_t)f64_to_f16_bits(lv[i] / sum) << 16) | (uint32_t)e) : 0u;
-    }
-    __syncthreads();
-
-    // Top-k by rounds of wave maxima, one wave over all keys (the selection on wave 0, the
-    // predictor on wave 2): a round is a short dependent chain, and splitting the keys over
-    // waves adds a barrier and a second selection over the candidates, which costs more than
-    // it saves.
-    if (wv == 0) {
-        const uint32_t mine = wave_topn(keys, 0, n_pad, k, lane);  // lane j: the j-th largest
-        // output position of the r-th largest is k-1-r (ascending gate order)
-        const int pos = k - 1 - lane;
-        const float g = __half2float(__ushort_as_half((uint16_t)(mine >> 16)));
-        // left-to-right sum over ascending order, each partial rounded to fp16; the gates are
-        // fp16 values in ascending order, so every partial sum is exact in fp32 before rounding
-        float s = 0.0f;
-        for (int j = 0; j < k; ++j) {
-            float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), k - 1 - j));
-            s = __half2float(__float2half_rn(s + gj));
+        for (int i = 0; i < kPer; ++i) {
+            const int e = tid + kThreads * i;
+            if (e < n_pad)
+                pkeys[e] = (e < n_exp) ? ((f16_order(__half_as_ushort(__float2half_rn(praw[i]))) << 16) | (uint32_t)e) : 0u;
         }
-        if (lane < k) {
-            ids_out[pos] = mine & 0xFFFFu;
-            sel_ids[pos] = mine & 0xFFFFu;
-            scores_out[pos] = __float2half_rn(g / s);   // correctly rounded f32 division, then f16
+    }
+    route::gate_keys(lraw, n_exp, keys, redm, reds);
+
+    // the selection on wave 0, the predictor on wave 2
+    if (wv == 0) {
+        uint32_t id;
+        __half sc;
+        const int pos = route::select_topk(keys, n_pad, k, lane, id, sc);
+        if (pos >= 0) {
+            ids_out[pos] = id;
+            sel_ids[pos] = id;
+            scores_out[pos] = sc;
         }
     } else if (wv == 2 && predict) {
         const uint32_t mine = wave_topn(pkeys, 0, n_pad, m, lane);
@@ -387,6 +293,35 @@ int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidde
         return -1;
     }
     hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, s, h_in, norm_w, eps, hidden, x_out);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int launch_router_logits(const float* h_in, const __half* norm_w, float eps, const __half* x_in, __half* x_out,
+                         const __half* w, int hidden, int n_exp, float* logits_out, hipStream_t s) {
+    if (hidden <= 0 || hidden > kMaxHidden || hidden % 8 != 0) {
+        moe_set_error("router_logits: hidden=%d unsupported (multiple of 8, <= %d)", hidden, kMaxHidden);
+        return -1;
+    }
+    if (n_exp <= 0 || n_exp > kMaxExperts) { moe_set_error("router_logits: n_exp=%d unsupported", n_exp); return -1; }
+    if (!w || !logits_out || (!h_in && !x_in)) { moe_set_error("router_logits: null pointer argument"); return -1; }
+    const int grid = (n_exp + kRowsPerBlock - 1) / kRowsPerBlock;
+    auto go = [&](auto nc, auto norm) {
+        constexpr int NC = decltype(nc)::value;
+        constexpr bool NORM = decltype(norm)::value;
+        MOE_LAUNCH(TK_ROUTER, (k_router<NC, NORM>), dim3(grid), dim3(kThreads), 0, s, h_in, norm_w, eps, x_in, x_out, w,
+                   nullptr, hidden, n_exp, 1, 0, logits_out, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                   nullptr, 0);
+    };
+    using N4 = std::integral_constant<int, 4>;
+    using N8 = std::integral_constant<int, 8>;
+    if (h_in) {
+        if (hidden <= 2048) go(N4(), std::true_type());
+        else go(N8(), std::true_type());
+    } else {
+        if (hidden <= 2048) go(N4(), std::false_type());
+        else go(N8(), std::false_type());
+    }
     HIP_TRY(hipGetLastError());
     return 0;
 }

@@ -53,6 +53,7 @@ class StackConfig:
     stage_ctas: int = 2          # staging blocks per copied expert (enough to fill PCIe; more
                                  # only floods the L2 miss queues with slow host reads)
     resident: bool = False       # every layer's experts in HBM (no slot tables, no staging)
+    routed_glu: bool = True      # resident: the router writes logits, gate/up selects (no hand-off)
     fused_tables: bool = True    # device mode: the router's last block runs the slot-table step
                                  # and the next layer's prefetch (no separate table launches)
     sched: bool = False          # the C++ runner's scheduler variant (cpp/src/engine.cpp:700-730,
@@ -135,6 +136,7 @@ class DecodeStack:
         c, L, dev = self.cfg, self.L, self.device
         k = c.top_k
         self.ids = torch.zeros((c.n_layers, k), dtype=torch.int32, device=dev)
+        self.logits = torch.zeros((c.n_layers, c.n_exp), dtype=torch.float32, device=dev)
         self.scores = torch.zeros((c.n_layers, k), dtype=torch.float16, device=dev)
         self.pred = torch.zeros((c.n_layers, max(c.top_m, 1)), dtype=torch.int32, device=dev)
         self.xs = torch.zeros((c.n_layers + 1, c.hidden), dtype=torch.float16, device=dev)
@@ -202,6 +204,27 @@ class DecodeStack:
                                self.pred[l].data_ptr(), torch.cuda.current_stream().cuda_stream)
         _lib.check(rc, "router")
 
+    def _layer_routed(self, l: int):
+        """Resident layer with the selection inside gate/up: logits -> gate/up (selects the
+        top-k itself, writes ids/scores) -> down."""
+        c = self.cfg
+        stream = torch.cuda.current_stream().cuda_stream
+        x_in = self.xs[0] if l == 0 else None
+        h_in = None if l == 0 else self.hs[l - 1]
+        _lib.check(self.L.moe_router_logits(h_in.data_ptr() if h_in is not None else None,
+                                            self.norm_w[l - 1].data_ptr() if l > 0 else None, c.eps,
+                                            x_in.data_ptr() if x_in is not None else None,
+                                            self.xs[l].data_ptr() if l > 0 else None, self.router_w[l].data_ptr(),
+                                            c.hidden, c.n_exp, self.logits[l].data_ptr(), stream), "router_logits")
+        pool = self.full_pools[l].data_ptr()
+        _lib.check(self.L.moe_q2_gate_up_routed(self.xs[l].data_ptr(), self.logits[l].data_ptr(), c.n_exp, c.top_k,
+                                                pool, self.blob_bytes, c.hidden, c.inter, c.group,
+                                                self.ids[l].data_ptr(), self.scores[l].data_ptr(),
+                                                self.h_ws.data_ptr(), stream), "gate_up_routed")
+        _lib.check(self.L.moe_q2_down(self.h_ws.data_ptr(), pool, self.blob_bytes, c.n_exp, self.ids[l].data_ptr(),
+                                      self.scores[l].data_ptr(), c.top_k, c.hidden, c.inter, c.group,
+                                      self.xs[l].data_ptr(), self.hs[l].data_ptr(), 0, stream), "down")
+
     def _glu(self, l: int):
         c = self.cfg
         stream = torch.cuda.current_stream().cuda_stream
@@ -238,8 +261,11 @@ class DecodeStack:
         main = torch.cuda.current_stream()
         for l in range(c.n_layers):
             if c.resident:
-                self._router(l)
-                self._glu(l)
+                if c.routed_glu:
+                    self._layer_routed(l)
+                else:
+                    self._router(l)
+                    self._glu(l)
                 continue
             if c.fused_tables:
                 self._layer_fused(l, main)
