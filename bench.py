@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--extras", action="store_true", help="add per-kernel and cache details to the JSON line")
     ap.add_argument("--stage-ctas", type=int, default=2, help="staging blocks per copied expert")
+    ap.add_argument("--pf-stage-ctas", type=int, default=3,
+                    help="staging blocks per prefetched expert (0: --stage-ctas)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill grouped-GEMM pass")
     ap.add_argument("--sched", action="store_true",
                     help="the C++ runner's scheduler variant of the expert cache (c_layer_decode_step_sched)")
@@ -479,7 +481,8 @@ def main():
 
     # ---- headline: 20% cache, misses staged from the pinned host store ---------------------
     cfg = StackConfig(n_layers=args.layers, budget_pct=args.budget_pct, prefetch=not args.no_prefetch,
-                      stage_ctas=args.stage_ctas, sched=args.sched, split=args.split)
+                      stage_ctas=args.stage_ctas, pf_stage_ctas=args.pf_stage_ctas, sched=args.sched,
+                      split=args.split)
     if args.only == "roofline":
         # the roofline kernel's timing pass alone (the profile command for the rocprof summary)
         rst = DecodeStack(StackConfig(n_layers=args.layers, prefetch=False, resident=True), mode="device")
@@ -511,6 +514,7 @@ def main():
     if args.only == "headline":
         print(json.dumps({"value": round(tok_s, 2), "driver": args.mode + ("+graph" if use_graph else ""),
                           "sched": args.sched, "split": args.split, "stage_ctas": args.stage_ctas,
+                          "pf_stage_ctas": args.pf_stage_ctas or args.stage_ctas,
                           "effective_hit_rate": round((tot1[0] - tot0[0] + tot1[1] - tot0[1]) / req, 4),
                           "staged_gb_per_s": round(staged / elapsed / 1e9, 2),
                           "headline_kernels_us": {k: round(v["avg_us"], 2) for k, v in (head_k or {}).items()

@@ -762,6 +762,10 @@ int c_router_tables_dev(int step_layer, int pf_layer, int max_fetch, const float
         if (!w_next || m <= 0) { moe_set_error("router_tables_dev: prefetch needs the next router and m > 0"); return -1; }
         pt = g_layers[pf_layer].dtab;
     }
+    if (st && st == pt) {                  // two waves would race on one table
+        moe_set_error("router_tables_dev: step and prefetch name the same layer %d", step_layer);
+        return -1;
+    }
     float* scratch = (float*)workspace;
     unsigned* counter = (unsigned*)((uint8_t*)workspace + (size_t)(2 * n_exp) * sizeof(float));
     return launch_router(h_in, (const __half*)norm_w, eps, (const __half*)x_in, (__half*)x_out,

@@ -41,6 +41,9 @@ using lanes::wave_sum_f64;
 constexpr int kRowsPerBlock = 4;          // one weight row per wave
 constexpr int kMaxHidden = 4096;
 
+// A zeroed table, read (never written) by the last block in place of a missing one.
+__device__ SlotTable g_no_table;
+
 // fp64 RMSNorm of h (fp32 [hidden]) into fp16 bits in LDS; every block computes it.
 // Thread tid owns elements 4 (c kThreads + tid) + 0..3 for chunk c (hidden is a multiple of 8).
 // The loads are issued by the caller, all of them before the weight loads (loads retire in
@@ -208,6 +211,12 @@ __global__ __launch_bounds__(kThreads) void k_router(
         lraw[i] = __hip_atomic_load(&scratch[ec], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         praw[i] = __hip_atomic_load(&scratch[n_exp + ec], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // The slot tables, in the same round trip: wave 0 reads the step's table, wave 1 the
+    // prefetch's; the other waves read one of them again (unused), so that the address is
+    // chosen without a branch and no wait lands inside one.
+    const SlotTable* any_tab = step_tab ? step_tab : (pf_tab ? pf_tab : &g_no_table);
+    const SlotTable* my_tab = (wv == 1 && pf_tab) ? pf_tab : ((wv == 0 && step_tab) ? step_tab : any_tab);
+    const slot_dev::TabRegs tab = slot_dev::fetch_table(my_tab, lane);
     if (predict) {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
@@ -249,8 +258,9 @@ __global__ __launch_bounds__(kThreads) void k_router(
     if (step_tab || pf_tab) {
         __shared__ slot_dev::LdsTable tabs[2];
         __syncthreads();
-        if (wv == 0 && step_tab) slot_dev::dev_slot_step(step_tab, tabs[0], sel_ids, k, slot_inds, lane);
-        if (wv == 1 && pf_tab && w_next && m > 0) slot_dev::dev_slot_prefetch(pf_tab, tabs[1], sel_pred, m, max_fetch, lane);
+        if (wv == 0 && step_tab)
+            slot_dev::dev_slot_step(step_tab, tabs[0], tab, lane < k ? sel_ids[lane] : 0u, k, slot_inds, lane);
+        if (wv == 1 && pf_tab && predict) slot_dev::dev_slot_prefetch(pf_tab, tabs[1], tab, sel_pred, m, max_fetch, lane);
     }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

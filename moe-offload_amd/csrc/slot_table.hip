@@ -9,16 +9,26 @@
 
 namespace {
 
+// The ids / predictions are loaded with the table, in the same round trip.
 __global__ __launch_bounds__(64) void k_slot_step(SlotTable* __restrict__ t, const uint32_t* __restrict__ ids,
                                                   int k, uint32_t* __restrict__ slot_inds) {
     __shared__ slot_dev::LdsTable L;
-    slot_dev::dev_slot_step(t, L, ids, k, slot_inds, threadIdx.x);
+    const int lane = threadIdx.x;
+    const slot_dev::TabRegs r = slot_dev::fetch_table(t, lane);
+    const uint32_t id = ids[lane < k ? lane : 0];
+    slot_dev::dev_slot_step(t, L, r, id, k, slot_inds, lane);
 }
 
 __global__ __launch_bounds__(64) void k_slot_prefetch(SlotTable* __restrict__ t, const int32_t* __restrict__ preds,
                                                       int m, int max_fetch) {
     __shared__ slot_dev::LdsTable L;
-    slot_dev::dev_slot_prefetch(t, L, preds, m, max_fetch, threadIdx.x);
+    __shared__ int32_t p[MOE_MAX_PREFETCH];
+    const int lane = threadIdx.x;
+    const slot_dev::TabRegs r = slot_dev::fetch_table(t, lane);
+    const int32_t v = m > 0 ? preds[lane < m ? lane : 0] : 0;     // m = 0 may come with no list
+    if (lane < m) p[lane] = v;
+    slot_dev::wave_sync();
+    slot_dev::dev_slot_prefetch(t, L, r, p, m, max_fetch, lane);
 }
 
 // Copy the blobs listed in the table's copy list: store[eid] -> pool[slot].  blockIdx.y picks

@@ -5,8 +5,8 @@
 // victim choice 404-426 (free stack first, else the oldest resident slot whose expert is not
 // protected, else the oldest resident slot).  The table is held in recency-stamp form
 // (SlotTable): the oldest resident slot is the one with the smallest stamp, and refreshing a
-// slot gives it the next clock value.  Each operation copies the table into LDS (~4.5 KB),
-// decides, and writes it back.
+// slot gives it the next clock value.  Each operation takes the table as fetch_table read it
+// (one round trip for all of it), decides on a copy in LDS (~4.5 KB), and writes it back.
 //
 // With t->sched set, the scheduler variant of mlx-qwen38/cpp/third_party/expert_io.c:1094-1394
 // applies: the step's victim choice also protects the experts the last prefetch fetched
@@ -36,6 +36,7 @@ struct LdsTable {
     uint32_t pred[16];
     uint32_t fetched[16];
     uint32_t spare[16];        // step: its own ids (never the fallback victim)
+    uint32_t snap_r[16];       // step: the residency snapshot of the last prefetch
     int32_t list_e[MOE_MAX_PREFETCH];
     int32_t list_s[MOE_MAX_PREFETCH];
     int32_t n_list;
@@ -52,17 +53,46 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
     return v;
 }
 
-// One 128-bit load per array per lane (entries 8 lane .. 8 lane + 7), all issued before any is
-// used: a copy loop that stores each value before loading the next waits a full round trip per
-// iteration.  Entries at or past the capacity hold -1 / 0 in every table (reset, state import
-// and store_table keep them so); they are masked anyway.
-__device__ inline void load_table(const SlotTable* t, LdsTable& L, int lane) {
+// Everything an operation reads from its table, in one wave's registers: the three arrays
+// (entries 8 lane .. 8 lane + 7, one 128-bit load per array and lane), the header, the counters
+// and the snapshot bitmaps.  fetch_table issues every load before any is used, so the whole
+// table arrives in one round trip; a caller with other work to do (the router's last block)
+// fetches early and lets the loads fly meanwhile.  Only the free stack is read later, by the
+// allocations that pop it (while the pool is still filling).
+struct TabRegs {
+    uint4 so, eo, s0, s1;
+    int4 hdr;                  // capacity, n_free, clock, snap_valid
+    int32_t sched;
+    uint64_t ebytes;
+    uint64_t stat;             // stats[lane] for lane < 18
+    uint32_t sr, sp, sf;       // snapshot bitmap words [lane & 15]
+};
+
+__device__ __forceinline__ TabRegs fetch_table(const SlotTable* t, int lane) {
     static_assert(MOE_NUM_EXPERTS == 64 * 8, "one 8-entry vector per lane");
-    const int cap = t->capacity;
-    const uint4 so = reinterpret_cast<const uint4*>(t->slot_of)[lane];
-    uint4 eo = reinterpret_cast<const uint4*>(t->eid_of)[lane];
-    uint4 s0 = reinterpret_cast<const uint4*>(t->stamp)[2 * lane];
-    uint4 s1 = reinterpret_cast<const uint4*>(t->stamp)[2 * lane + 1];
+    static_assert(offsetof(SlotTable, capacity) == 0 && offsetof(SlotTable, n_free) == 4 &&
+                      offsetof(SlotTable, clock) == 8 && offsetof(SlotTable, snap_valid) == 12,
+                  "header read as one int4");
+    TabRegs r;
+    r.hdr = *reinterpret_cast<const int4*>(t);
+    r.so = reinterpret_cast<const uint4*>(t->slot_of)[lane];
+    r.eo = reinterpret_cast<const uint4*>(t->eid_of)[lane];
+    r.s0 = reinterpret_cast<const uint4*>(t->stamp)[2 * lane];
+    r.s1 = reinterpret_cast<const uint4*>(t->stamp)[2 * lane + 1];
+    r.sched = t->sched;
+    r.ebytes = t->expert_bytes;
+    r.stat = t->stats[lane < 18 ? lane : 0];
+    r.sr = reinterpret_cast<const uint32_t*>(t->snap_resident)[lane & 15];
+    r.sp = reinterpret_cast<const uint32_t*>(t->snap_pred)[lane & 15];
+    r.sf = reinterpret_cast<const uint32_t*>(t->snap_fetched)[lane & 15];
+    return r;
+}
+
+// Write the fetched table into LDS.  Entries at or past the capacity hold -1 / 0 in every table
+// (reset, state import and store_table keep them so); they are masked here anyway.
+__device__ inline void commit_table(const TabRegs& r, LdsTable& L, int lane) {
+    const int cap = r.hdr.x;
+    uint4 eo = r.eo, s0 = r.s0, s1 = r.s1;
     const int i0 = 8 * lane;
     if (i0 + 8 > cap) {                        // mask the entries past the capacity
         uint32_t e[4] = {eo.x, eo.y, eo.z, eo.w};
@@ -77,7 +107,7 @@ __device__ inline void load_table(const SlotTable* t, LdsTable& L, int lane) {
         s0 = make_uint4(st[0], st[1], st[2], st[3]);
         s1 = make_uint4(st[4], st[5], st[6], st[7]);
     }
-    reinterpret_cast<uint4*>(L.slot_of)[lane] = so;
+    reinterpret_cast<uint4*>(L.slot_of)[lane] = r.so;
     reinterpret_cast<uint4*>(L.eid_of)[lane] = eo;
     reinterpret_cast<uint4*>(L.stamp)[2 * lane] = s0;
     reinterpret_cast<uint4*>(L.stamp)[2 * lane + 1] = s1;
@@ -87,13 +117,14 @@ __device__ inline void load_table(const SlotTable* t, LdsTable& L, int lane) {
         L.pred[lane] = 0;
         L.fetched[lane] = 0;
         L.spare[lane] = 0;
+        L.snap_r[lane] = r.sr;
     }
     if (lane == 0) L.n_list = 0;
-    if (lane < 18) L.stats[lane] = t->stats[lane];
+    if (lane < 18) L.stats[lane] = r.stat;
     wave_sync();
 }
 
-// Entries past the capacity are -1 / 0 in LDS as well (load_table masks them and no operation
+// Entries past the capacity are -1 / 0 in LDS as well (commit_table masks them and no operation
 // touches them), so the whole arrays are written back.
 __device__ inline void store_table(SlotTable* t, const LdsTable& L, int lane) {
     reinterpret_cast<uint4*>(t->slot_of)[lane] = reinterpret_cast<const uint4*>(L.slot_of)[lane];
@@ -103,9 +134,8 @@ __device__ inline void store_table(SlotTable* t, const LdsTable& L, int lane) {
 }
 
 // Relabel stamps by rank when the clock nears wrap-around (order unchanged).
-__device__ inline void renorm(SlotTable* t, LdsTable& L, int lane, uint32_t& clock) {
+__device__ inline void renorm(int cap, LdsTable& L, int lane, uint32_t& clock) {
     if (clock < STAMP_RENORM_AT) return;
-    const int cap = t->capacity;
     uint32_t newst[MOE_NUM_EXPERTS / 64];
     for (int i = 0; i < MOE_NUM_EXPERTS / 64; ++i) {
         int s = lane + 64 * i;
@@ -131,13 +161,12 @@ __device__ inline void renorm(SlotTable* t, LdsTable& L, int lane, uint32_t& clo
 // One victim for a slot allocation (uniform across the wave). Returns the slot.  When every
 // resident expert is protected, the oldest one not in `spare` (may be null) goes before the
 // oldest outright (the host table's rule, slot_table_host.h).
-__device__ inline int take_slot(SlotTable* t, LdsTable& L, int lane, int& n_free, const uint32_t* protect,
-                                const uint32_t* spare = nullptr) {
+__device__ inline int take_slot(const SlotTable* t, int cap, LdsTable& L, int lane, int& n_free,
+                                const uint32_t* protect, const uint32_t* spare = nullptr) {
     if (n_free > 0) {
         --n_free;
         return t->free_stack[n_free];
     }
-    const int cap = t->capacity;
     uint64_t best = ~0ull, oldest = ~0ull, spared = ~0ull;
     for (int s = lane; s < cap; s += 64) {
         uint32_t st = L.stamp[s];
@@ -196,20 +225,21 @@ __device__ inline void count_runs(LdsTable& L, const int32_t* e, int n) {
     L.stats[ST_COAL] += (uint64_t)runs * MOE_NUM_TENSORS;
 }
 
-// Decode step of expert_io.c:583-685 for k ids (one wave; ids may live in LDS or global memory).
-__device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, const uint32_t* ids, int k,
-                              uint32_t* __restrict__ slot_inds, int lane) {
-    load_table(t, L, lane);
-    uint32_t clock = t->clock;
-    int n_free = t->n_free;
-    renorm(t, L, lane, clock);
+// Decode step of expert_io.c:583-685 for k ids (one wave).  r holds the table as fetch_table
+// read it; lane i < k holds the i-th id in id_lane.
+__device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, const TabRegs& r, uint32_t id_lane,
+                                     int k, uint32_t* __restrict__ slot_inds, int lane) {
+    commit_table(r, L, lane);
+    const int cap = r.hdr.x;
+    int n_free = r.hdr.y;
+    uint32_t clock = (uint32_t)r.hdr.z;
+    renorm(cap, L, lane, clock);
 
     int e = -1;
     bool bad = false;
     if (lane < k) {
-        uint32_t v = ids[lane];
-        bad = v >= MOE_NUM_EXPERTS;
-        e = bad ? -1 : (int)v;
+        bad = id_lane >= MOE_NUM_EXPERTS;
+        e = bad ? -1 : (int)id_lane;
     }
     if (__any(bad)) {                      // reject: leave the table untouched
         if (lane == 0) { t->status = 1; t->n_copy = 0; }
@@ -229,16 +259,14 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
     }
     wave_sync();
 
-    const bool snap = t->snap_valid != 0;
+    const bool snap = r.hdr.w != 0;
     if (lane == 0) L.stats[ST_DEC_REQ] += (uint64_t)k;
     if (snap && lane < 16) {
-        // per 32-bit word of the bitmaps (the counters are sums of popcounts)
-        const uint32_t* sr = reinterpret_cast<const uint32_t*>(t->snap_resident);
-        const uint32_t* sp = reinterpret_cast<const uint32_t*>(t->snap_pred);
-        const uint32_t* sf = reinterpret_cast<const uint32_t*>(t->snap_fetched);
-        uint32_t want = L.protect[lane], before_missing = want & ~sr[lane];
-        uint32_t c0 = __popc(want & sp[lane]), c1 = __popc(want), c2 = __popc(sp[lane]);
-        uint32_t c3 = __popc(before_missing & sf[lane]), c4 = __popc(before_missing), c5 = __popc(sf[lane]);
+        // per 32-bit word of the bitmaps (the counters are sums of popcounts); lane < 16 holds
+        // word `lane` of each snapshot bitmap
+        uint32_t want = L.protect[lane], before_missing = want & ~r.sr;
+        uint32_t c0 = __popc(want & r.sp), c1 = __popc(want), c2 = __popc(r.sp);
+        uint32_t c3 = __popc(before_missing & r.sf), c4 = __popc(before_missing), c5 = __popc(r.sf);
 #pragma unroll
         for (int o = 8; o >= 1; o >>= 1) {
             c0 += __shfl_xor(c0, o, 16); c1 += __shfl_xor(c1, o, 16); c2 += __shfl_xor(c2, o, 16);
@@ -254,10 +282,7 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
     const bool resident = (e >= 0) && L.slot_of[e] >= 0;
     const bool miss = (e >= 0) && !resident;
     bool lru_hit = false;
-    if (resident) {
-        const uint32_t* sr = reinterpret_cast<const uint32_t*>(t->snap_resident);
-        lru_hit = !snap || ((sr[e >> 5] >> (e & 31)) & 1u);
-    }
+    if (resident) lru_hit = !snap || bit(L.snap_r, e);
     const uint64_t miss_mask = __ballot(miss);
     const int n_miss = __popcll(miss_mask);
     const int n_lru = __popcll(__ballot(lru_hit));
@@ -273,13 +298,13 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
         L.list_e[rank] = e;
     }
     wave_sync();
-    if (t->sched && snap && lane < 16)       // in-flight prefetched experts are protected too
-        L.protect[lane] |= reinterpret_cast<const uint32_t*>(t->snap_fetched)[lane];
+    if (r.sched && snap && lane < 16)        // in-flight prefetched experts are protected too
+        L.protect[lane] |= r.sf;
     wave_sync();
 
     for (int r = 0; r < n_miss; ++r) {
         int me = L.list_e[r];
-        int s = take_slot(t, L, lane, n_free, L.protect, L.spare);
+        int s = take_slot(t, cap, L, lane, n_free, L.protect, L.spare);
         bind(L, lane, me, s, clock);
         if (lane == 0) L.list_s[r] = s;
     }
@@ -305,25 +330,27 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
         t->clock = clock;
         t->n_free = n_free;
         t->status = 0;
-        L.stats[ST_DEC_BYTES] += (uint64_t)n_miss * t->expert_bytes;
+        L.stats[ST_DEC_BYTES] += (uint64_t)n_miss * r.ebytes;
         count_runs(L, L.list_e, n_miss);
     }
     wave_sync();
     if (lane < 18) t->stats[lane] = L.stats[lane];
 }
 
-// Prefetch of expert_io.c:527-581 for m predictions (one wave).
-__device__ inline void dev_slot_prefetch(SlotTable* __restrict__ t, LdsTable& L, const int32_t* preds, int m, int max_fetch,
-                                  int lane) {
-    const bool sched = t->sched != 0;
+// Prefetch of expert_io.c:527-581 for m predictions (one wave).  r holds the table as
+// fetch_table read it; preds is in LDS.
+__device__ inline void dev_slot_prefetch(SlotTable* __restrict__ t, LdsTable& L, const TabRegs& r, const int32_t* preds,
+                                         int m, int max_fetch, int lane) {
+    const bool sched = r.sched != 0;
     if (sched && max_fetch <= 0) {            // the scheduler variant prefetches nothing
         if (lane == 0) { t->pf_n_copy = 0; t->status = 0; }
         return;
     }
-    load_table(t, L, lane);
-    uint32_t clock = t->clock;
-    int n_free = t->n_free;
-    renorm(t, L, lane, clock);
+    commit_table(r, L, lane);
+    const int cap = r.hdr.x;
+    int n_free = r.hdr.y;
+    uint32_t clock = (uint32_t)r.hdr.z;
+    renorm(cap, L, lane, clock);
 
     // residency snapshot
     for (int e = lane; e < MOE_NUM_EXPERTS; e += 64)
@@ -355,7 +382,7 @@ __device__ inline void dev_slot_prefetch(SlotTable* __restrict__ t, LdsTable& L,
     for (int i = 0; i < np; ++i) order_e[i] = L.list_e[np - 1 - i];   // reverse rank order
     wave_sync();
     for (int i = 0; i < np; ++i) {
-        int s = take_slot(t, L, lane, n_free, L.protect);
+        int s = take_slot(t, cap, L, lane, n_free, L.protect);
         bind(L, lane, order_e[i], s, clock);
         if (lane == 0) { L.list_e[i] = order_e[i]; L.list_s[i] = s; }
     }
@@ -371,7 +398,7 @@ __device__ inline void dev_slot_prefetch(SlotTable* __restrict__ t, LdsTable& L,
         t->clock = clock;
         t->n_free = n_free;
         t->status = 0;
-        L.stats[ST_PREF_BYTES] += (uint64_t)np * t->expert_bytes;
+        L.stats[ST_PREF_BYTES] += (uint64_t)np * r.ebytes;
         count_runs(L, L.list_e, np);
     }
     wave_sync();

@@ -52,6 +52,8 @@ class StackConfig:
     layer_base: int = 0          # first C-ABI layer index used (tables are global to the library)
     stage_ctas: int = 2          # staging blocks per copied expert (enough to fill PCIe; more
                                  # only floods the L2 miss queues with slow host reads)
+    pf_stage_ctas: int = 3       # the same for the prefetch copies (0: stage_ctas); they run
+                                 # alone on the link more often than the demand copies do
     resident: bool = False       # every layer's experts in HBM (no slot tables, no staging)
     routed_glu: bool = True      # resident: the router writes logits, gate/up selects (no hand-off)
     fused_tables: bool = True    # device mode: the router's last block runs the slot-table step
@@ -290,8 +292,8 @@ class DecodeStack:
             if c.prefetch and l + 1 < c.n_layers:
                 self.ev_demand[l].record(main)
                 self.side.wait_event(self.ev_demand[l])
-                _lib.check(self.L.c_layer_stage_dev(self.cidx(l + 1), 1, c.stage_ctas, self.side.cuda_stream),
-                           "stage_prefetch")
+                _lib.check(self.L.c_layer_stage_dev(self.cidx(l + 1), 1, c.pf_stage_ctas or c.stage_ctas,
+                                                    self.side.cuda_stream), "stage_prefetch")
                 self.ev_copy[l + 1].record(self.side)
             self._glu(l)
         _lib.check(self.L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
@@ -327,8 +329,8 @@ class DecodeStack:
         if pf:
             self.ev_demand[l].record(main)
             self.side.wait_event(self.ev_demand[l])
-            _lib.check(self.L.c_layer_stage_dev(self.cidx(l + 1), 1, c.stage_ctas, self.side.cuda_stream),
-                       "stage_prefetch")
+            _lib.check(self.L.c_layer_stage_dev(self.cidx(l + 1), 1, c.pf_stage_ctas or c.stage_ctas,
+                                                self.side.cuda_stream), "stage_prefetch")
             self.ev_copy[l + 1].record(self.side)
         if l >= 1 and c.prefetch and self.demand_overlaps_prefetch(l):
             main.wait_event(self.ev_copy[l])           # the GEMV reads the prefetched slots

@@ -132,3 +132,19 @@ def test_graph_replay_matches_eager(runs):
                 assert np.array_equal(g[t]["slots"][l], d[t]["slots"][l]), (t, l)
     finally:
         st.close()
+
+
+def test_router_tables_reject_one_layer_for_step_and_prefetch(runs):
+    """The step and the prefetch run in two waves at once; naming one table for both is refused
+    before anything is launched."""
+    from moe_offload import _lib
+    (st, _, _), _ = runs
+    c, l = st.cfg, 2
+    rc = st.L.c_router_tables_dev(st.cidx(l), st.cidx(l), c.prefetch_cap, st.hs[l - 1].data_ptr(),
+                                  st.norm_w[l - 1].data_ptr(), c.eps, None, st.xs[l].data_ptr(),
+                                  st.router_w[l].data_ptr(), st.router_w[l + 1].data_ptr(), c.hidden, c.n_exp,
+                                  c.top_k, c.top_m, st.router_ws[l].data_ptr(), st.ids[l].data_ptr(),
+                                  st.scores[l].data_ptr(), st.pred[l].data_ptr(),
+                                  torch.cuda.current_stream().cuda_stream)
+    with pytest.raises(_lib.NativeError, match="same layer"):
+        _lib.check(rc, "router_tables")
