@@ -73,14 +73,23 @@ __device__ __forceinline__ void split_even_odd(uint4 lo, uint4 hi, f16x8& ev, f1
     od = __builtin_bit_cast(f16x8, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
+// Block barrier ordering LDS only (the loop shares nothing else between waves): the fences
+// are limited to the local address space, so a wait at the barrier covers LDS accesses and
+// not the global loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // M tiles multiplied per pass over a segment's weights: 4 for gate/up (K = hidden: the long
 // contraction pays for the extra accumulators), 1 for down (a short K: registers buy more
 // resident blocks instead).
 template <int MODE>
 constexpr int max_mt() { return MODE == 0 ? 4 : 1; }
 
-template <int NCH, int MODE>
-__global__ __launch_bounds__(256) void k_q2g_proj(
+template <int NCH, int MODE, bool SBL>
+__global__ __launch_bounds__(256, 2) void k_q2g_proj(
     const __half* __restrict__ src, int n_src_rows, const int32_t* __restrict__ row_map,
     const int32_t* __restrict__ row_out, int n_out_rows,
     const int32_t* __restrict__ seg_start, const int32_t* __restrict__ seg_slot, int n_seg, int n_rows,
@@ -134,6 +143,35 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
     }
     const uint32_t lane_code0 = (uint32_t)((size_t)n * code_row + (size_t)kq * 16);
     const uint32_t lane_sb0 = (uint32_t)((size_t)n * sb_row + kq);
+
+    // Scale/bias words.  With SBL (gate/up, K a multiple of 256 and at least 512: rows of 4 k
+    // words, so every 16-byte piece below is aligned) each wave loads them four chunks at a time
+    // into its own LDS area, one 16-byte piece per lane and subtile: lane (n, q) loads groups
+    // 16 jj + 4 q .. + 3 of its row n (a piece past the row's end is moved back to its last 4
+    // groups), and chunk j = 4 jj + c reads group 4 j + kq from the piece of lane (n, c).  One
+    // such load touches as many cache lines as one of the per-chunk 4-byte loads it replaces,
+    // and there are four times fewer of them.  The pieces of block jj + 1 are loaded after chunk
+    // 4 jj is multiplied and written to LDS by the staging of chunk 4 jj + 1 (the compiler moves
+    // that write up to the loads, so they are waited for once per block); two buffers, so block
+    // jj + 1 lands while block jj is read.  Without SBL the words are loaded with the codes.
+    constexpr bool kSbLds = SBL;
+    static_assert(!SBL || NCH >= 2, "the LDS path needs K >= 512");
+    __shared__ uint32_t sb_lds[kSbLds ? 2 : 1][4][kSub][kSbLds ? 256 : 1];
+    const uint32_t lane_row_sb = (uint32_t)((size_t)n * sb_row);
+    auto sb_piece = [&](int jj, int q) {                       // first group of lane (., q)'s piece
+        const int g0 = 16 * jj + 4 * q;
+        return g0 + 4 <= kg ? g0 : kg - 4;
+    };
+    uint4 sbn[kSub];                                           // a block's pieces on their way to LDS
+    auto fetch_sb = [&](int jj) {
+        const int gs = sb_piece(jj, kq);
+#pragma unroll
+        for (int s = 0; s < kSub; ++s) sbn[s] = *reinterpret_cast<const uint4*>(sbp[s] + lane_row_sb + gs);
+    };
+    auto put_sb = [&](int jj) {
+#pragma unroll
+        for (int s = 0; s < kSub; ++s) reinterpret_cast<uint4*>(&sb_lds[jj & 1][wv][s][0])[lane] = sbn[s];
+    };
 
     // The segment's rows are taken in batches of up to kMaxMT M tiles (64 rows); within a batch
     // every K chunk's weights are loaded and dequantised once and multiplied into every tile, so
@@ -192,7 +230,22 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
 #pragma unroll
             for (int s = 0; s < kSub; ++s) {
                 cw[s] = *reinterpret_cast<const uint4*>(codes[s] + lane_code + (size_t)j * 64 + (ptrdiff_t)gdelta * 16);
-                sw[s] = sbp[s][lane_sb + 4 * j + gdelta];
+                if constexpr (!kSbLds) sw[s] = sbp[s][lane_sb + 4 * j + gdelta];
+            }
+        };
+        // After chunk j's multiply: the loads of the next block's words (needed from chunk
+        // 4 jj + 4 on), issued before the next activation loads, so that staging those waits for
+        // these too; staging chunk j writes them to the buffer of block jj - 1, which the wave's
+        // reads have left.
+        auto next_sb_block = [&](int j) {
+            if constexpr (kSbLds) {
+                if ((j & 3) == 0 && 4 * ((j >> 2) + 1) < NCH) fetch_sb((j >> 2) + 1);
+            }
+        };
+        auto stage_sb = [&](int j) {
+            if constexpr (kSbLds) {
+                if (j == 0) put_sb(0);
+                else if ((j & 3) == 1 && 4 * ((j >> 2) + 1) < NCH) put_sb((j >> 2) + 1);
             }
         };
         auto load_x = [&](int j) {
@@ -219,11 +272,21 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
         };
         // Per 32-bit word q of the lane's group: the activation fragments of every tile, then per
         // subtile the two dequantised weight fragments, multiplied into every tile.
-        auto compute = [&](const uint4 (&cw)[kSub], const uint32_t (&sw)[kSub]) {
+        auto compute = [&](int j, const uint4 (&cw)[kSub], const uint32_t (&sw)[kSub]) {
+            uint32_t swv[kSub];
+#pragma unroll
+            for (int s = 0; s < kSub; ++s) swv[s] = sw[s];
+            if constexpr (kSbLds) {
+                const int c = j & 3, jj = j >> 2;
+                int e = 16 * jj + 4 * c + kq - sb_piece(jj, c);       // > 3 only for a group past K
+                e = e > 3 ? 3 : e;
+#pragma unroll
+                for (int s = 0; s < kSub; ++s) swv[s] = sb_lds[jj & 1][wv][s][(16 * c + n) * 4 + e];
+            }
             f16x2 s2[kSub], b2[kSub];
 #pragma unroll
             for (int s = 0; s < kSub; ++s) {
-                const f16x2 sb = __builtin_bit_cast(f16x2, sw[s]);
+                const f16x2 sb = __builtin_bit_cast(f16x2, swv[s]);
                 const _Float16 two_s = sb.x * (_Float16)2.0f;
                 s2[s] = (f16x2){two_s, two_s};
                 b2[s] = (f16x2){sb.y, sb.y};
@@ -256,16 +319,19 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
         // multiplied.  Loads retire in issue order, so the activations of chunk j are issued
         // before the weights of chunk j + 1: staging j then waits for its activations only.  The
         // last chunk's look-ahead re-reads the last chunk (an L2 hit), so no load is conditional.
+        if constexpr (kSbLds) fetch_sb(0);
         if constexpr (kPrefetch) {
             load_x(0);
             load_w(0, cwa, swa);
 #pragma unroll 1
             for (int j = 0; j < NCH; ++j) {
                 load_w(j + 1 < NCH ? j + 1 : NCH - 1, cwb, swb);
-                __syncthreads();                               // every wave is done with chunk j - 1
+                lds_barrier();                                 // every wave is done with chunk j - 1
                 stage(j);
-                __syncthreads();
-                compute(cwa, swa);
+                stage_sb(j);
+                lds_barrier();
+                compute(j, cwa, swa);
+                next_sb_block(j);
                 load_x(j + 1 < NCH ? j + 1 : NCH - 1);
 #pragma unroll
                 for (int s = 0; s < kSub; ++s) {
@@ -278,10 +344,12 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
             for (int j = 0; j < NCH; ++j) {
                 load_x(j);
                 load_w(j, cwa, swa);
-                __syncthreads();                               // every wave is done with chunk j - 1
+                lds_barrier();                                 // every wave is done with chunk j - 1
                 stage(j);
-                __syncthreads();
-                compute(cwa, swa);
+                stage_sb(j);
+                lds_barrier();
+                compute(j, cwa, swa);
+                next_sb_block(j);
             }
         }
 
@@ -314,7 +382,7 @@ __global__ __launch_bounds__(256) void k_q2g_proj(
     }
 }
 
-template <int NCH, int MODE>
+template <int NCH, int MODE, bool SBL>
 int launch_proj(const __half* src, int n_src_rows, const int32_t* row_map, const int32_t* row_out, int n_out_rows,
                 const int32_t* seg_start, const int32_t* seg_slot, int n_seg, int n_rows, const uint8_t* pool,
                 size_t stride, int n_slots, const BlobLayout& L, __half* out, hipStream_t s) {
@@ -324,7 +392,7 @@ int launch_proj(const __half* src, int n_src_rows, const int32_t* row_map, const
     const long long nb = (long long)n_seg * tiles;
     if (nb <= 0) return 0;
     if (nb > 0x7FFFFFFFLL) { moe_set_error("grouped q2: grid too large"); return -1; }
-    MOE_LAUNCH(MODE == kGateUp ? TK_PF_GATE_UP : TK_PF_DOWN, (k_q2g_proj<NCH, MODE>), dim3((unsigned)nb), dim3(256),
+    MOE_LAUNCH(MODE == kGateUp ? TK_PF_GATE_UP : TK_PF_DOWN, (k_q2g_proj<NCH, MODE, SBL>), dim3((unsigned)nb), dim3(256),
                0, s, src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg, n_rows, pool, stride,
                n_slots, L, tiles, out);
     HIP_TRY(hipGetLastError());
@@ -335,10 +403,18 @@ template <int MODE>
 int dispatch_proj(int K, const __half* src, int n_src_rows, const int32_t* row_map, const int32_t* row_out,
                   int n_out_rows, const int32_t* seg_start, const int32_t* seg_slot, int n_seg, int n_rows,
                   const uint8_t* pool, size_t stride, int n_slots, const BlobLayout& L, __half* out, hipStream_t s) {
+    // the four-chunk scale/bias blocks pay on gate/up's long K; down (K = inter, often 2 chunks)
+    // is faster with the per-chunk loads
+    const bool sbl = MODE == kGateUp && K % 256 == 0 && K >= 512;
     switch ((K + 255) / 256) {
 #define PF_CASE(c) \
-    case c: return launch_proj<c, MODE>(src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg, \
-                                        n_rows, pool, stride, n_slots, L, out, s);
+    case c: \
+        if (sbl) \
+            return launch_proj<c, MODE, (c >= 2 && MODE == kGateUp)>(src, n_src_rows, row_map, row_out, n_out_rows, \
+                                                                     seg_start, seg_slot, n_seg, n_rows, pool, stride, \
+                                                                     n_slots, L, out, s); \
+        return launch_proj<c, MODE, false>(src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg, \
+                                           n_rows, pool, stride, n_slots, L, out, s);
         PF_CASE(1) PF_CASE(2) PF_CASE(3) PF_CASE(4) PF_CASE(5)
         PF_CASE(6) PF_CASE(7) PF_CASE(8) PF_CASE(9) PF_CASE(10)
 #undef PF_CASE

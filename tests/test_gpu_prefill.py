@@ -182,3 +182,36 @@ def test_cached_layer_prefill(dev, experts, n_tok):
     finally:
         mod.close()
         store.close()
+
+
+@pytest.mark.parametrize("hidden,inter", [(384, 192), (1024, 320), (128, 768), (2560, 64)])
+def test_grouped_gate_up_and_down_odd_contractions(dev, hidden, inter):
+    """Contraction lengths off the 256-wide chunk grid (K = 384, 192, 320, 128, 64) take the
+    per-chunk scale/bias loads; multiples of 256 from 512 up (1024, 768, 2560) take the
+    four-chunk blocks; both against the fp64 oracle."""
+    from moe_offload import ops, q2format, synth
+    n_exp, rows_per = 6, [1, 17, 40, 3, 64, 9]
+    gate, up, down = synth.q2_experts(n_exp, hidden, inter, seed=hidden + inter, scale_std=0.05)
+    pool = torch.from_numpy(q2format.to_blobs(gate, up, down, hidden, inter)).to(dev)
+    rng = np.random.default_rng(hidden)
+    n_rows = sum(rows_per)
+    x = rng.standard_normal((n_rows, hidden)).astype(np.float16)
+    seg = np.concatenate([[0], np.cumsum(rows_per)]).astype(np.int32)
+    row_tok = np.arange(n_rows, dtype=np.int32)
+    h = ops.q2_grouped_gate_up(torch.from_numpy(x).to(dev), torch.from_numpy(row_tok).to(dev),
+                               torch.from_numpy(seg).to(dev), pool, hidden, inter)
+    y = ops.q2_grouped_down(h, torch.from_numpy(seg).to(dev), pool, hidden, inter)
+    h_got, y_got = h.cpu().numpy().astype(np.float64), y.cpu().numpy().astype(np.float64)
+    for u in range(n_exp):
+        r0, r1 = seg[u], seg[u + 1]
+        xg = x[r0:r1].astype(np.float64)
+        g = q2.qmatvec(xg, gate[0][u], gate[1][u], gate[2][u], 2, 64)
+        v = q2.qmatvec(xg, up[0][u], up[1][u], up[2][u], 2, 64)
+        want_h = g / (1.0 + np.exp(-g)) * v
+        # h is stored in fp16: one ulp at the largest |h| on top of the 1% of RMS
+        bound = 1e-2 * np.sqrt(np.mean(want_h ** 2)) + np.abs(want_h).max() * 2.0 ** -10
+        err = np.abs(h_got[r0:r1] - want_h).max()
+        assert err <= bound, f"gate/up expert {u} K={hidden}: max|err| {err:.3e} > {bound:.3e}"
+        want_y = q2.qmatvec(h_got[r0:r1].astype(np.float16).astype(np.float64), down[0][u], down[1][u],
+                            down[2][u], 2, 64)
+        assert_close_rms(y_got[r0:r1], want_y, 1e-2, f"down expert {u} K={inter}")
