@@ -86,11 +86,13 @@ void reset_evictions(LayerState& L) {
 }
 hipStream_t g_compute = nullptr;             // caller's stream (null stream by default)
 hipStream_t g_copy = nullptr;
-// A second copy stream: blob copies from the pinned store alternate between the two (one stream
-// of blob-sized hipMemcpyAsync copies moves ~37 GB/s, two ~49 GB/s), and each batch joins the
-// second into the first, so every event recorded on g_copy after a batch covers all of it.
-hipStream_t g_copy2 = nullptr;
-hipEvent_t g_copy2_done = nullptr;
+// More copy streams: blob copies from the pinned store go round robin over g_copy and these (one
+// stream of blob-sized hipMemcpyAsync copies moves ~37 GB/s, two ~49 GB/s; three or four are
+// slower, sharing the process's 4 hardware queues), and each batch joins them into g_copy, so
+// every event recorded on g_copy after a batch covers all of it.
+constexpr int kCopyStreams = 2;
+hipStream_t g_copy_more[kCopyStreams - 1] = {};
+hipEvent_t g_copy_more_done[kCopyStreams - 1] = {};
 bool g_ready = false;
 std::mutex g_err_mu;
 char g_err[1024] = {0};
@@ -100,8 +102,10 @@ bool valid_layer(int l) { return l >= 0 && l < MOE_MAX_LAYERS; }
 int ensure_runtime() {
     if (g_ready) return 0;
     HIP_TRY(hipStreamCreateWithFlags(&g_copy, hipStreamNonBlocking));
-    HIP_TRY(hipStreamCreateWithFlags(&g_copy2, hipStreamNonBlocking));
-    HIP_TRY(hipEventCreateWithFlags(&g_copy2_done, hipEventDisableTiming));
+    for (int i = 0; i < kCopyStreams - 1; ++i) {
+        HIP_TRY(hipStreamCreateWithFlags(&g_copy_more[i], hipStreamNonBlocking));
+        HIP_TRY(hipEventCreateWithFlags(&g_copy_more_done[i], hipEventDisableTiming));
+    }
     g_ready = true;
     return 0;
 }
@@ -190,7 +194,8 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
             }
         }
     } else {
-        if (L.read_recorded) HIP_TRY(hipStreamWaitEvent(g_copy2, L.read_done, 0));
+        if (L.read_recorded)
+            for (int i = 0; i < kCopyStreams - 1; ++i) HIP_TRY(hipStreamWaitEvent(g_copy_more[i], L.read_done, 0));
         int c = 0;
         for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
             uint64_t rb = L.row_bytes[t];
@@ -198,11 +203,12 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
             for (int i = 0; i < n; ++i, ++c)
                 HIP_TRY(hipMemcpyAsync((void*)(L.dst[t] + (uint64_t)slots[i] * rb),
                                        (const void*)(L.src[t] + (uint64_t)eids[i] * rb), rb,
-                                       hipMemcpyHostToDevice, (c & 1) ? g_copy2 : g_copy));
+                                       hipMemcpyHostToDevice,
+                                       c % kCopyStreams ? g_copy_more[c % kCopyStreams - 1] : g_copy));
         }
-        if (c > 1) {
-            HIP_TRY(hipEventRecord(g_copy2_done, g_copy2));
-            HIP_TRY(hipStreamWaitEvent(g_copy, g_copy2_done, 0));
+        for (int i = 0; i < kCopyStreams - 1 && i + 1 < c; ++i) {
+            HIP_TRY(hipEventRecord(g_copy_more_done[i], g_copy_more[i]));
+            HIP_TRY(hipStreamWaitEvent(g_copy, g_copy_more_done[i], 0));
         }
     }
     HIP_TRY(hipEventRecord(L.copy_done, g_copy));
@@ -339,13 +345,15 @@ void c_io_shutdown(void) {
         if (L.split_dev) (void)hipFree(L.split_dev);
         L = LayerState();
     }
-    (void)hipStreamSynchronize(g_copy2);
+    for (int i = 0; i < kCopyStreams - 1; ++i) {
+        (void)hipStreamSynchronize(g_copy_more[i]);
+        (void)hipStreamDestroy(g_copy_more[i]);
+        (void)hipEventDestroy(g_copy_more_done[i]);
+        g_copy_more[i] = nullptr;
+        g_copy_more_done[i] = nullptr;
+    }
     (void)hipStreamDestroy(g_copy);
-    (void)hipStreamDestroy(g_copy2);
-    (void)hipEventDestroy(g_copy2_done);
     g_copy = nullptr;
-    g_copy2 = nullptr;
-    g_copy2_done = nullptr;
     g_ready = false;
 }
 
