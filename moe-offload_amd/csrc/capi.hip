@@ -196,15 +196,22 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
     } else {
         if (L.read_recorded)
             for (int i = 0; i < kCopyStreams - 1; ++i) HIP_TRY(hipStreamWaitEvent(g_copy_more[i], L.read_done, 0));
+        // Consecutive pairs whose expert ids and slots both step by one are contiguous in the
+        // store and in the pool: one copy each run (a prefill chunk's ranked load list is mostly
+        // such runs; one large copy moves ~57 GB/s).
         int c = 0;
         for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
             uint64_t rb = L.row_bytes[t];
             if (!rb || !L.src[t] || !L.dst[t]) continue;
-            for (int i = 0; i < n; ++i, ++c)
+            for (int i = 0; i < n; ++c) {
+                int r = 1;
+                while (i + r < n && eids[i + r] == eids[i] + r && slots[i + r] == slots[i] + r) ++r;
                 HIP_TRY(hipMemcpyAsync((void*)(L.dst[t] + (uint64_t)slots[i] * rb),
-                                       (const void*)(L.src[t] + (uint64_t)eids[i] * rb), rb,
+                                       (const void*)(L.src[t] + (uint64_t)eids[i] * rb), (uint64_t)r * rb,
                                        hipMemcpyHostToDevice,
                                        c % kCopyStreams ? g_copy_more[c % kCopyStreams - 1] : g_copy));
+                i += r;
+            }
         }
         for (int i = 0; i < kCopyStreams - 1 && i + 1 < c; ++i) {
             HIP_TRY(hipEventRecord(g_copy_more_done[i], g_copy_more[i]));
