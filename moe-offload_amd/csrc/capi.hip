@@ -49,7 +49,13 @@ struct LayerState {
     SlotTable* dtab = nullptr;                // authoritative for device-driven layers
     bool device_mode = false;
     hipEvent_t copy_done = nullptr, read_done = nullptr;
+    // copy_pending: copies the compute stream has not been made to wait for yet.  inflight:
+    // copies that may still be running on the copy streams (a GPU-side wait does not end them);
+    // cleared only once copy_done is known to have completed.  inflight_slots: the slots those
+    // copies write; bounce_busy: they read the bounce buffer.
     bool copy_pending = false, read_recorded = false;
+    bool inflight = false, bounce_busy = false;
+    uint64_t inflight_slots[MOE_NUM_EXPERTS / 64] = {};
     // Q2 blob format of tensor 0 (for c_layer_switch_glu)
     int hidden = 0, inter = 0, group = 0;
     uint8_t* bounce = nullptr;                // pinned bounce buffer for file-backed stores
@@ -153,8 +159,36 @@ int pread_full(int fd, uint8_t* buf, size_t n, uint64_t off) {
     return 0;
 }
 
+// Forget the layer's in-flight copies once its last copy event has completed (non-blocking).
+void settle_copies(LayerState& L) {
+    if (!L.inflight) return;
+    hipError_t e = hipEventQuery(L.copy_done);
+    if (e == hipErrorNotReady) {
+        (void)hipGetLastError();
+        return;
+    }
+    L.inflight = false;
+    L.bounce_busy = false;
+    memset(L.inflight_slots, 0, sizeof(L.inflight_slots));
+}
+
+// Block the host until every copy queued for the layer has landed.
+int drain_copies(LayerState& L) {
+    if (L.inflight) HIP_TRY(hipEventSynchronize(L.copy_done));
+    L.inflight = false;
+    L.bounce_busy = false;
+    memset(L.inflight_slots, 0, sizeof(L.inflight_slots));
+    return 0;
+}
+
 // Queue the copies store[eid] -> pool[slot] for every tensor on the copy stream.  A prefetch's
 // copies also record pf_done.
+//
+// Ordering between batches of one layer: copies on g_copy run in queue order, and each batch
+// joins its g_copy_more copies into g_copy before copy_done is recorded.  A copy on g_copy_more
+// is ordered after nothing on g_copy, so when this batch writes a slot that an earlier batch's
+// copy may still be writing (a demand victim that a prefetch is filling, or a prefill chunk's
+// load after an in-flight prefetch), the g_copy_more streams first wait for that batch.
 int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* slots, int n,
                  bool prefetch = false) {
     if (n <= 0) return 0;
@@ -169,6 +203,10 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
     }
     if (ensure_runtime()) return -1;
     if (ensure_events(L)) return -1;
+    settle_copies(L);
+    bool overlap = false;
+    if (L.inflight)
+        for (int i = 0; i < n && !overlap; ++i) overlap = (L.inflight_slots[slots[i] >> 6] >> (slots[i] & 63)) & 1u;
     if (L.read_recorded) HIP_TRY(hipStreamWaitEvent(g_copy, L.read_done, 0));
     if (L.fd >= 0) {
         size_t need = (size_t)n * expert_bytes_of(L);
@@ -178,10 +216,12 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
             L.bounce = nullptr;
             HIP_TRY(hipHostMalloc((void**)&L.bounce, need, hipHostMallocDefault));
             L.bounce_bytes = need;
-        } else if (L.copy_pending) {
-            // the bounce buffer is reused: earlier copies out of it must have finished
-            HIP_TRY(hipEventSynchronize(L.copy_done));
+        } else if (L.bounce_busy) {
+            // the bounce buffer is reused: earlier copies out of it must have finished (a GPU-side
+            // join of those copies says nothing about the host buffer they read)
+            if (drain_copies(L)) return -1;
         }
+        L.bounce_busy = true;
         size_t off = 0;
         for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
             uint64_t rb = L.row_bytes[t];
@@ -194,8 +234,10 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
             }
         }
     } else {
-        if (L.read_recorded)
-            for (int i = 0; i < kCopyStreams - 1; ++i) HIP_TRY(hipStreamWaitEvent(g_copy_more[i], L.read_done, 0));
+        for (int i = 0; i < kCopyStreams - 1; ++i) {
+            if (L.read_recorded) HIP_TRY(hipStreamWaitEvent(g_copy_more[i], L.read_done, 0));
+            if (overlap) HIP_TRY(hipStreamWaitEvent(g_copy_more[i], L.copy_done, 0));
+        }
         // Consecutive pairs whose expert ids and slots both step by one are contiguous in the
         // store and in the pool: one copy each run (a prefill chunk's ranked load list is mostly
         // such runs; one large copy moves ~57 GB/s).
@@ -220,6 +262,8 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
     }
     HIP_TRY(hipEventRecord(L.copy_done, g_copy));
     L.copy_pending = true;
+    L.inflight = true;
+    for (int i = 0; i < n; ++i) L.inflight_slots[slots[i] >> 6] |= 1ull << (slots[i] & 63);
     if (prefetch) {
         HIP_TRY(hipEventRecord(L.pf_done, g_copy));
         L.pf_pending = true;
@@ -268,7 +312,7 @@ int step_host(int layer, const uint32_t* eids, int k, int async_io) {
     if (push_table(L)) return -1;
     if (write_slot_inds(L, out, k)) return -1;
     if (issue_copies(layer, L, L.tab.copy_eid, L.tab.copy_slot, L.tab.n_copy)) return -1;
-    if (!async_io && L.copy_pending) HIP_TRY(hipEventSynchronize(L.copy_done));
+    if (!async_io && drain_copies(L)) return -1;
     return n_miss;
 }
 
@@ -393,7 +437,7 @@ void c_layer_init(int layer, int fd, int capacity, const uint64_t* base_offsets,
         return;
     }
     LayerState& L = g_layers[layer];
-    if (L.copy_pending) (void)hipEventSynchronize(L.copy_done);
+    if (L.inflight) (void)hipEventSynchronize(L.copy_done);
     if (L.bounce) (void)hipHostFree(L.bounce);
     if (L.dtab) (void)hipFree(L.dtab);
     hipEvent_t cd = L.copy_done, rd = L.read_done, pd = L.pf_done;
@@ -498,10 +542,8 @@ void c_layer_load_sync(int layer, const int32_t* eids, const int32_t* slots, int
     slot_host::count_runs(&L.tab, eids, n);
     if (push_table(L)) return;
     if (issue_copies(layer, L, eids, slots, n)) return;
-    if (L.copy_pending) {
-        (void)hipEventSynchronize(L.copy_done);
-        wait_copies_gpu(L, g_compute);
-    }
+    if (drain_copies(L)) return;
+    wait_copies_gpu(L, g_compute);
 }
 
 void c_layer_get_lru_state(int layer, int32_t* out_eids, int32_t* out_slots, int* out_count) {
@@ -608,7 +650,7 @@ int c_layer_decode_step_sched(int layer, const int32_t* eids, int k, const int32
     if (layer > 0 && layer < MOE_MAX_LAYERS && g_layers[layer].init) {
         LayerState& L = g_layers[layer];
         if (flags & MOE_SCHED_SYNC_DEMAND) {
-            if (L.copy_pending) HIP_TRY(hipEventSynchronize(L.copy_done));
+            if (drain_copies(L)) return -1;
             wait_copies_gpu(L, g_compute);
         } else if (n_miss == 0) {
             wait_copies_gpu(L, g_compute);

@@ -65,6 +65,13 @@ class StackConfig:
     split: bool = False          # host mode with sched: hit experts run before the misses land
 
 
+def effective_fetch_cap(prefetch_cap: int, top_m: int) -> int:
+    """Most experts one prefetch call fetches: cap if 0 < cap < 32 else 32
+    (expert_io.c:545), bounded by the number of predictions."""
+    cap = prefetch_cap if 0 < prefetch_cap < 32 else 32
+    return min(cap, top_m)
+
+
 def random_blobs(n_exp: int, hidden: int, inter: int, group: int, gen: torch.Generator, device,
                  scale_std: float = 0.02) -> torch.Tensor:
     """Synthetic Q2 experts as blobs, generated on the GPU: codes ~ U{0..3} (uniform random
@@ -305,12 +312,14 @@ class DecodeStack:
         A demand miss takes the oldest unprotected slot; the experts the last prefetch fetched
         are the newest entries of the table (nothing touches it between that prefetch and this
         step), so they are reached only after every older unprotected entry: at least
-        capacity - prefetch_cap - top_k of them, which covers the at most top_k misses when
-        capacity >= 2 top_k + prefetch_cap.  Then no demand copy targets a slot a prefetch copy
+        capacity - fetched - top_k of them, which covers the at most top_k misses when
+        capacity >= 2 top_k + fetched.  Then no demand copy targets a slot a prefetch copy
         is still writing, and the join can move from before the demand copies to before the
-        GEMV that reads the prefetched slots (it then overlaps the demand copies)."""
+        GEMV that reads the prefetched slots (it then overlaps the demand copies).  `fetched`
+        is the most one prefetch can fetch: the cap as the table applies it (a cap outside
+        1..31 means 32, expert_io.c:545), and never more than the predictions it is given."""
         c = self.cfg
-        return self.capacities[l] >= 2 * c.top_k + c.prefetch_cap
+        return self.capacities[l] >= 2 * c.top_k + effective_fetch_cap(c.prefetch_cap, c.top_m)
 
     def _layer_fused(self, l: int, main):
         """One layer of the device-driven token with the table work inside the router:

@@ -233,6 +233,59 @@ def test_staging_fills_slots_with_the_right_experts(L, mode):
         L.c_host_free(ptr)
 
 
+def test_host_staging_small_pool_victims_of_inflight_prefetch(L):
+    """Host-driven staging at the 16-slot floor with prefetch cap 8: a demand miss then takes a
+    slot that the prefetch just before it is still filling, and the two copies must land in
+    order (the later one wins).  After every step the step's slots hold its experts; a
+    load_sync right after a prefetch (the prefill chunk's pattern) must win over it too."""
+    from moe_offload import q2format
+    blob = q2format.expert_bytes(256, 128)
+    n_exp, cap, layer = 512, 16, 63
+    ptr = L.c_host_alloc(n_exp * blob)
+    assert ptr
+    try:
+        store = np.ctypeslib.as_array(ctypes.cast(ptr, ctypes.POINTER(ctypes.c_uint8)), shape=(n_exp, blob))
+        store[:] = np.random.default_rng(5).integers(0, 256, size=store.shape, dtype=np.uint8)
+        store_dev = torch.from_numpy(store.copy()).to("cuda")
+        pool = torch.zeros((cap, blob), dtype=torch.uint8, device="cuda")
+        slots = torch.zeros(16, dtype=torch.int32, device="cuda")
+        _init_layer(L, layer, cap, store_ptr=ptr, blob=blob, pool_ptr=pool.data_ptr(), slot_ptr=slots.data_ptr())
+        rng = np.random.default_rng(6)
+        collisions = 0
+        for t in range(60):
+            preds = rng.choice(200, size=12, replace=False).astype(np.int32)
+            ids = rng.choice(200, size=K, replace=False).astype(np.uint32)
+            before = set(_state(L, layer)[0])
+            L.c_layer_start_prefetch12(layer, 8, *[int(v) for v in preds])
+            e0, s0 = _state(L, layer)
+            pf_slots = {sl for e, sl in zip(e0, s0) if e not in before}      # being filled now
+            L.c_layer_step_decode10_async(layer, *[int(v) for v in ids])
+            L.c_layer_wait_prefetch(layer)
+            _check(L)
+            got = slots[:K].cpu().tolist()
+            collisions += len(pf_slots & {sl for sl, e in zip(got, ids) if int(e) not in set(e0)})
+            sl = slots[:K].long()
+            assert torch.equal(pool[sl], store_dev[torch.from_numpy(ids.astype(np.int64)).to("cuda")]), f"step {t}"
+            if t % 10 == 9:
+                # a blocking load right behind a prefetch into the same slots
+                L.c_layer_start_prefetch12(layer, 8, *[int(v) for v in rng.choice(200, size=12, replace=False)])
+                le = rng.choice(np.arange(300, 512), size=cap, replace=False).astype(np.int32)
+                ls = np.arange(cap, dtype=np.int32)
+                L.c_layer_load_sync(layer, le.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                    ls.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), cap, 1)
+                _check(L)
+                assert torch.equal(pool, store_dev[torch.from_numpy(le.astype(np.int64)).to("cuda")]), f"load {t}"
+                L.c_layer_reset_cache(layer)
+        assert collisions > 0, "the id stream never made a demand miss take an in-flight prefetch slot"
+        torch.cuda.synchronize()
+        L.c_sync_copies()
+    finally:
+        torch.cuda.synchronize()
+        L.c_sync_copies()
+        L.c_layer_init(layer, -1, 16, None, None, None, 0)
+        L.c_host_free(ptr)
+
+
 @pytest.fixture(scope="module")
 def config2_store(L):
     """512 experts at H=2048, I=512 in a pinned host store (503 MB)."""
