@@ -120,6 +120,15 @@ int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_i
                void* workspace, uint32_t* ids_out, void* scores_out, int32_t* pred_out,
                void* stream);
 uint64_t moe_router_workspace_bytes(int n_exp);
+/* No counterpart in the reference.  moe_router for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): no workspace argument;
+ * the logits and the arrival counter live in a static device array of the library (8,448 bytes
+ * per GPU, held until the process ends).  Allocates nothing.  n_exp <= 1024 (larger is rejected
+ * with an error).  Every call on one GPU shares that array: calls that overlap on one GPU (other
+ * streams, other threads) race. */
+int moe_router_noalloc(const float* h_in, const void* norm_w, float eps, const void* x_in, void* x_out,
+                       const void* w, const void* w_next, int hidden, int n_exp, int k, int m,
+                       uint32_t* ids_out, void* scores_out, int32_t* pred_out, void* stream);
 /* moe_router split at the logits, for a pool that holds every expert (the resident path; no
  * slot table has to run once per layer): moe_router_logits writes logits_out fp32 [n_exp] (each
  * the fp16-rounded logit moe_router computes), and moe_q2_gate_up_routed's blocks select the

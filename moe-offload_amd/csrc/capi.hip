@@ -805,6 +805,14 @@ int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_i
                          ids_out, (__half*)scores_out, pred_out, nullptr, nullptr, nullptr, 0, (hipStream_t)stream);
 }
 
+int moe_router_noalloc(const float* h_in, const void* norm_w, float eps, const void* x_in, void* x_out, const void* w,
+                       const void* w_next, int hidden, int n_exp, int k, int m, uint32_t* ids_out, void* scores_out,
+                       int32_t* pred_out, void* stream) {
+    return launch_router_noalloc(h_in, (const __half*)norm_w, eps, (const __half*)x_in, (__half*)x_out,
+                                 (const __half*)w, (const __half*)w_next, hidden, n_exp, k, m, ids_out,
+                                 (__half*)scores_out, pred_out, (hipStream_t)stream);
+}
+
 // Router whose last block also runs the decode step of layer step_layer (its selected ids, slot
 // ids into that layer's slot_inds) and the prefetch of layer pf_layer (the prediction); either
 // layer may be -1.  Both must be device-driven layers.  Same decisions as

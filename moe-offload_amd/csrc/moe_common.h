@@ -162,6 +162,11 @@ int launch_router(const float* h_in, const __half* norm_w, float eps, const __ha
                   int k, int m, float* scratch, unsigned* counter, uint32_t* ids_out,
                   __half* scores_out, int32_t* pred_out, SlotTable* step_tab, uint32_t* slot_inds,
                   SlotTable* pf_tab, int max_fetch, hipStream_t s);
+// launch_router with its scratch and arrival counter in a static device array of the library
+// (no allocation, no caller workspace); n_exp <= 1024.  Overlapping calls on one GPU race.
+int launch_router_noalloc(const float* h_in, const __half* norm_w, float eps, const __half* x_in, __half* x_out,
+                          const __half* w, const __half* w_next, int hidden, int n_exp, int k, int m, uint32_t* ids_out,
+                          __half* scores_out, int32_t* pred_out, hipStream_t s);
 // The router's [RMSNorm +] GEMV alone: logits_out[n_exp] = fp16-rounded logits (as floats).
 int launch_router_logits(const float* h_in, const __half* norm_w, float eps, const __half* x_in, __half* x_out,
                          const __half* w, int hidden, int n_exp, float* logits_out, hipStream_t s);

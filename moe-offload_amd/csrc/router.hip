@@ -24,6 +24,8 @@
 // needs a launch of its own.
 #include <hip/hip_fp16.h>
 
+#include <mutex>
+
 #include "lane_reduce.h"
 #include "moe_common.h"
 #include "route_select.h"
@@ -288,7 +290,66 @@ __global__ void k_f64_to_f16(const double* __restrict__ in, uint16_t* __restrict
     if (i < n) out[i] = f64_to_f16_bits(in[i]);
 }
 
+__global__ void k_zero_u32(uint32_t* __restrict__ p, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// ---- the router without a caller workspace ------------------------------------------------------
+// Logits of the router and the predictor (2 * kMaxExperts floats), then the arrival counter on a
+// 256-byte line of its own.  Fixed offsets, so calls with different expert counts share one
+// counter.  Each GPU the library runs on holds its own copy until the process ends.
+constexpr size_t kStaticLogitBytes = 2 * (size_t)kMaxExperts * sizeof(float);
+constexpr size_t kStaticScratchBytes = kStaticLogitBytes + 256;
+constexpr int kMaxDevices = 64;
+
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
 }  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+// Device address of this device's copy of `scratch`, resolved once per device with that device
+// current.  The counter is cleared then (a fill kernel on the caller's stream, not a memset: the
+// first call may be under graph capture); every router launch leaves it at zero again.
+static int static_scratch(hipStream_t s, uint8_t** out) {
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) {
+        moe_set_error("router_noalloc: device %d beyond the %d devices the library tracks", dev, kMaxDevices);
+        return -1;
+    }
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) {
+            moe_set_error("router_noalloc: no device address for the static scratch on device %d", dev);
+            return -1;
+        }
+        hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, s, (uint32_t*)((uint8_t*)p + kStaticLogitBytes), 64);
+        HIP_TRY(hipGetLastError());
+        g_scratch_ptr[dev] = (uint8_t*)p;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+int launch_router_noalloc(const float* h_in, const __half* norm_w, float eps, const __half* x_in, __half* x_out,
+                          const __half* w, const __half* w_next, int hidden, int n_exp, int k, int m, uint32_t* ids_out,
+                          __half* scores_out, int32_t* pred_out, hipStream_t s) {
+    if (n_exp <= 0 || n_exp > kMaxExperts) {
+        moe_set_error("router_noalloc: n_exp=%d exceeds the static scratch (at most %d experts, %zu bytes)", n_exp,
+                      kMaxExperts, kStaticScratchBytes);
+        return -1;
+    }
+    uint8_t* base = nullptr;
+    if (static_scratch(s, &base)) return -1;
+    return launch_router(h_in, norm_w, eps, x_in, x_out, w, w_next, hidden, n_exp, k, m, (float*)base,
+                         (unsigned*)(base + kStaticLogitBytes), ids_out, scores_out, pred_out, nullptr, nullptr,
+                         nullptr, 0, s);
+}
 
 int launch_f64_to_f16(const double* in, uint16_t* out, int n, hipStream_t s) {
     if (n <= 0 || !in || !out) { moe_set_error("f64_to_f16: bad arguments"); return -1; }

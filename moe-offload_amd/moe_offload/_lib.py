@@ -52,6 +52,8 @@ SIGNATURES: dict[str, tuple] = {
     "moe_router": (_c_int, [_c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int,
                             _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     "moe_router_workspace_bytes": (_c_u64, [_c_int]),
+    "moe_router_noalloc": (_c_int, [_c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int,
+                                    _c_int, _c_vp, _c_vp, _c_vp, _c_vp]),
     "moe_router_logits": (_c_int, [_c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp]),
     "moe_q2_gate_up_routed": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_u64, _c_int, _c_int, _c_int, _c_vp,
                                        _c_vp, _c_vp, _c_vp]),
