@@ -62,42 +62,157 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(budget_s: float):
-    """The oracle (numpy, fp64) on one token-layer of the same workload: router, 10-expert
-    dequantise + SwitchGLU + combine, slot-table step.  Scaled to tokens/s of the 48-layer stack."""
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def oracle_fp64_step(budget_s: float = 3.0):
+    """The oracle (numpy, fp64) on one token-layer: router, dequantise + SwitchGLU of 10 experts,
+    slot-table step (median ms; an extra key beside the fp32 baseline)."""
     import numpy as np
-    from threadpoolctl import threadpool_info
 
     from moe_offload import synth
     from oracle import lru as olru
     from oracle import q2
     H, E, K, I = 2048, 512, 10, 512
-    n_exp = 64                                     # the sample draws from 64 experts (memory bound)
-    gate, up, down = synth.q2_experts(n_exp, H, I, seed=1)
+    gate, up, down = synth.q2_experts(32, H, I, seed=1)
     w = synth.router_weight(E, H, seed=3)
-    xs = synth.hidden_states(64, H, seed=4)
-    f = lambda e: ((gate[0][e], gate[1][e], gate[2][e]), (up[0][e], up[1][e], up[2][e]),
-                   (down[0][e], down[1][e], down[2][e]))
+    xs = synth.hidden_states(16, H, seed=4)
+    f = lambda e: ((gate[0][e % 32], gate[1][e % 32], gate[2][e % 32]), (up[0][e % 32], up[1][e % 32], up[2][e % 32]),
+                   (down[0][e % 32], down[1][e % 32], down[2][e % 32]))
     lru = olru.PyLru(0, 102)
-    rng = np.random.default_rng(0)
     times = []
     t_start = time.perf_counter()
-    i = 0
     while time.perf_counter() - t_start < budget_s or len(times) < 2:
-        x = xs[i % len(xs)]
+        x = xs[len(times) % len(xs)]
         t0 = time.perf_counter()
-        logits = q2.router_logits(x, w, "f16")
-        ids, sc, _ = q2.route(logits[None], K, "f16")
+        ids, sc, _ = q2.route(q2.router_logits(x, w, "f16")[None], K, "f16")
         lru.step([int(e) for e in ids[0]])
-        sel = rng.choice(n_exp, size=K, replace=False)
-        q2.moe_combine(x.astype(np.float64), sel, sc[0], f, bits=2, group=64)
+        q2.moe_combine(x.astype(np.float64), ids[0], sc[0], f, bits=2, group=64)
         times.append(time.perf_counter() - t0)
-        i += 1
-    per_layer = float(np.median(times))
-    threads = max([t.get("num_threads", 1) for t in threadpool_info()] + [1])
-    return {"value": round(1.0 / (48 * per_layer), 5), "unit": "tok/s", "cores": int(threads), "kind": "port",
-            "sample": f"{len(times)} token-layers of the oracle (fp64 numpy: router + dequantise/SwitchGLU of 10 "
-                      f"experts + slot-table step), median {per_layer * 1e3:.1f} ms, scaled to 48 layers"}
+    return float(np.median(times)) * 1e3, len(times)
+
+
+def cpu_baseline(budget_s: float):
+    """The reference's CPU path for one token-layer of the workload (hidden 2048, 512 experts,
+    top-10, inter 512, Q2 g64), restated in fp32 PyTorch on the host cores as
+    mlx-qwen38/test_prefill_qproj.py:53,64 does (dequantise, then fp32 matmul):
+      router: logits = W_r x (fp32), softmax, top-10, renormalise (loader.py:903-908);
+      experts: y = sum_j s_j down_j(silu(gate_j x) * up_j x) over the router's own ids
+               (loader.py:964-965), W = scale * q + bias per group of 64, codes LSB first.
+    Variants: (a) dequantise the 10 selected experts each step (what the GPU kernels do),
+    (b) pre-dequantised fp32 weights (the CPU's best case), each with every core and with one;
+    (c) the slot-table step of the oracle's restatement of expert_io.c per token-layer.
+    Median and p90 over >= 50 steps after 5 warm-up steps; value = variant (a) with every core,
+    scaled to the 48-layer token."""
+    import numpy as np
+    import torch
+
+    from moe_offload import synth
+    from oracle import lru as olru
+    H, E, K, I, G = 2048, 512, 10, 512, 64
+    cores = len(os.sched_getaffinity(0))
+    threads0 = torch.get_num_threads()
+    gate, up, down = synth.q2_experts(E, H, I, seed=1)
+    proj = {name: (torch.from_numpy(w.view(np.int32)), torch.from_numpy(sc).float(), torch.from_numpy(b).float())
+            for name, (w, sc, b) in (("gate", gate), ("up", up), ("down", down))}
+    w_r = torch.from_numpy(synth.router_weight(E, H, seed=3)).float()
+    n_steps, n_warm = 50, 5
+    xs = torch.from_numpy(synth.hidden_states(n_steps + n_warm, H, seed=4)).float()
+    shifts = torch.arange(0, 32, 2, dtype=torch.int32)
+
+    def dequant(name, e):
+        w, sc, b = proj[name]
+        q = ((w[e].unsqueeze(-1) >> shifts) & 3).float()               # [out, in/16, 16]
+        rows = q.shape[0]
+        q = q.view(rows, -1, G)                                        # [out, in/64, 64]
+        return (q * sc[e].unsqueeze(-1) + b[e].unsqueeze(-1)).view(rows, -1)
+
+    def route(x):
+        gates = torch.softmax(w_r @ x, dim=-1)
+        top = torch.topk(gates, K)
+        return top.indices, top.values / top.values.sum()
+
+    def step_deq(x):
+        ids, sc = route(x)
+        y = torch.zeros(H)
+        for j in range(K):
+            e = int(ids[j])
+            g = dequant("gate", e) @ x
+            u = dequant("up", e) @ x
+            y += sc[j] * (dequant("down", e) @ (torch.nn.functional.silu(g) * u))
+        return y
+
+    cache = {}
+
+    def step_pre(x):
+        ids, sc = route(x)
+        y = torch.zeros(H)
+        for j in range(K):
+            wg, wu, wd = cache[int(ids[j])]
+            y += sc[j] * (wd @ (torch.nn.functional.silu(wg @ x) * (wu @ x)))
+        return y
+
+    def timed(fn, threads):
+        torch.set_num_threads(threads)
+        ts = []
+        with torch.no_grad():
+            for i in range(n_warm + n_steps):
+                t0 = time.perf_counter()
+                fn(xs[i])
+                if i >= n_warm:
+                    ts.append(time.perf_counter() - t0)
+        ts = np.array(ts)
+        return {"median_ms": round(float(np.median(ts)) * 1e3, 3), "p90_ms": round(float(np.percentile(ts, 90)) * 1e3, 3),
+                "steps": int(ts.size), "threads": threads}
+
+    t_all0 = time.perf_counter()
+    out = {"deq_all": timed(step_deq, cores)}
+    out["deq_1"] = timed(step_deq, 1) if time.perf_counter() - t_all0 < budget_s else None
+    torch.set_num_threads(cores)
+    with torch.no_grad():
+        for i in range(n_warm + n_steps):                             # the experts these steps use
+            for e in route(xs[i])[0].tolist():
+                if e not in cache:
+                    cache[e] = (dequant("gate", e), dequant("up", e), dequant("down", e))
+    out["pre_all"] = timed(step_pre, cores)
+    out["pre_1"] = timed(step_pre, 1)
+    torch.set_num_threads(threads0)
+    # (c) the slot-table step of the oracle's expert_io.c restatement, on the router's ids
+    with torch.no_grad():
+        id_stream = [route(xs[i])[0].tolist() for i in range(n_warm + n_steps)]
+    try:
+        lru, lru_kind = olru.CLru(0, 102), "C restatement of expert_io.c"
+    except Exception:                                                 # noqa: BLE001 (no C oracle build)
+        lru, lru_kind = olru.PyLru(0, 102), "Python restatement of expert_io.c"
+    ts = []
+    for rep in range(20):
+        lru.reset_cache()
+        for ids in id_stream:
+            t0 = time.perf_counter()
+            lru.step(ids)
+            ts.append(time.perf_counter() - t0)
+    lru_us = float(np.median(ts)) * 1e6
+    fp64_ms, fp64_n = oracle_fp64_step(min(3.0, budget_s / 5))
+    per_layer = out["deq_all"]["median_ms"] / 1e3
+    layer_bytes = K * 983_040
+    variants = {k: dict(v, gb_s=round(layer_bytes / (v["median_ms"] / 1e3) / 1e9, 3), tok_s_48l=round(
+        1.0 / (48 * v["median_ms"] / 1e3), 4)) for k, v in out.items() if v is not None}
+    return {"value": round(1.0 / (48 * per_layer), 4), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"one token-layer of the workload in fp32 PyTorch on the host ({_cpu_model()}, {cores} threads): "
+                      f"router + dequantise and SwitchGLU of the router's 10 experts + combine, median of "
+                      f"{out['deq_all']['steps']} steps after {n_warm} warm-up ({out['deq_all']['median_ms']} ms), "
+                      f"scaled to 48 layers",
+            "cpu_model": _cpu_model(), "variants": variants,
+            "slot_step_us": round(lru_us, 2), "slot_step_impl": lru_kind,
+            "oracle_fp64_ms_per_layer": round(fp64_ms, 2), "oracle_fp64_steps": fp64_n,
+            "wall_s": round(time.perf_counter() - t_all0, 1)}
 
 
 def timed_tokens(st, xs, warmup, steps, use_graph):
