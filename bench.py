@@ -236,7 +236,7 @@ def timed_tokens(st, xs, warmup, steps, use_graph):
 
 
 KINDS = ["router", "gate_up", "down", "stage", "slot_table", "grouped_gate_up", "grouped_down", "pair_combine",
-         "cb_up", "cb_down", "stream_calib", "resident_token"]
+         "cb_up", "cb_down", "stream_calib"]
 
 
 def timed_kernels(run, calls, launches_per_call):

@@ -190,24 +190,6 @@ int moe_q2_grouped_switch_glu(const void* x, int n_tokens, const int32_t* row_to
                               const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
                               const void* pool, uint64_t stride, int n_slots, int hidden,
                               int inter, int group, void* h_ws, void* y_out, void* stream);
-/* The whole decode token of a stack whose experts are all resident (loader.py:948-992 over every
- * layer: router, top-k, SwitchGLU + combine, then the stack's RMSNorm into the next layer) in one
- * cooperative launch; ids, scores, xs and hs as moe_router / moe_q2_switch_glu / moe_rmsnorm
- * would write them layer by layer, bit for bit.  x0 fp16 [hidden]; router_w fp16
- * [n_layers][n_exp][hidden]; norm_w fp16 [n_layers][hidden] (the norm after layer l); pool_ptrs:
- * device array of n_layers pool addresses, each pool holding every expert blob (slot = id) at
- * `stride` bytes.  Outputs: ids_out [n_layers][k], scores_out fp16 [n_layers][k], xs_out fp16
- * [n_layers + 1][hidden] (xs_out[n_layers] = the normed output), hs_out fp32 [n_layers][hidden].
- * workspace: moe_resident_workspace_bytes(n_layers) bytes, zeroed once before first use; one
- * token at a time per workspace.  hidden 2048, inter 512, group 64, k <= 16, n_exp <= 1024. */
-uint64_t moe_resident_workspace_bytes(int n_layers);
-int moe_resident_decode(const void* x0, const void* router_w, const void* norm_w, const uint64_t* pool_ptrs,
-                        uint64_t stride, int n_layers, int hidden, int n_exp, int k, int inter, int group,
-                        float eps, uint32_t* ids_out, void* scores_out, void* xs_out, float* hs_out,
-                        void* workspace, void* stream);
-/* Status word of the last resident token on `workspace` (blocks): 0, or 0x80000000 | layer << 8
- * | phase when a wait timed out (phase 1 input, 2 logits, 3 h). */
-int moe_resident_status(const void* workspace, void* stream);
 /* Score-weighted sum of per-(token, k) rows (loader.py:964-965): out fp32 [n_tokens][hidden] =
  * residual + sum_j scores[t][j] * y[t*k + j] (fp16 y, scores, residual; residual may be null). */
 int moe_pair_combine(const void* y, const void* scores, const void* residual, int n_tokens, int k,
@@ -298,9 +280,9 @@ int c_sync_copies(void);
 /* Per-kernel timing: launches between begin and end are dispatched with start/stop events
  * stamped at the kernel's own begin/end; end() sums durations per kind (0 router, 1 gate/up,
  * 2 down, 3 staging, 4 slot table, 5 grouped gate/up, 6 grouped down, 7 pair combine,
- * 8 codebook up, 9 codebook down, 10 streaming calibration, 11 resident token) into
- * out_ms[MOE_TIMING_KINDS] and counts into out_n[MOE_TIMING_KINDS]. */
-#define MOE_TIMING_KINDS 12
+ * 8 codebook up, 9 codebook down, 10 streaming calibration) into out_ms[MOE_TIMING_KINDS] and
+ * counts into out_n[MOE_TIMING_KINDS]. */
+#define MOE_TIMING_KINDS 11
 int c_timing_begin(int capacity);
 int c_timing_end(double* out_ms, int* out_n);
 /* Plain device-to-device copy of `bytes` (multiple of 16): the known-size reference for scaling

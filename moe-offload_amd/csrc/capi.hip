@@ -1020,25 +1020,6 @@ int moe_cb_moe(const void* x, const void* pool, uint64_t stride, int n_slots, co
                        stream);
 }
 
-uint64_t moe_resident_workspace_bytes(int n_layers) { return resident_workspace_bytes(n_layers); }
-
-int moe_resident_decode(const void* x0, const void* router_w, const void* norm_w, const uint64_t* pool_ptrs,
-                        uint64_t stride, int n_layers, int hidden, int n_exp, int k, int inter, int group, float eps,
-                        uint32_t* ids_out, void* scores_out, void* xs_out, float* hs_out, void* workspace,
-                        void* stream) {
-    return launch_resident_token((const __half*)x0, (const __half*)router_w, (const __half*)norm_w, pool_ptrs,
-                                 (size_t)stride, n_layers, hidden, n_exp, k, inter, group, eps, ids_out,
-                                 (__half*)scores_out, (__half*)xs_out, hs_out, (uint32_t*)workspace,
-                                 (hipStream_t)stream);
-}
-
-int moe_resident_status(const void* workspace, void* stream) {
-    uint32_t st = 0;
-    if (!workspace) { moe_set_error("resident_status: null workspace"); return -1; }
-    if (read_resident_status((const uint32_t*)workspace, (hipStream_t)stream, &st)) return -1;
-    return (int)st;
-}
-
 int moe_pair_combine(const void* y, const void* scores, const void* residual, int n_tokens, int k, int hidden,
                      float* out, void* stream) {
     return launch_pair_combine((const __half*)y, (const __half*)scores, (const __half*)residual, n_tokens, k, hidden, out,

@@ -142,7 +142,7 @@ void moe_set_error(const char* fmt, ...);
 // hipExtLaunchKernelGGL with a start/stop event pair, which the runtime stamps at the kernel's
 // own begin/end; kinds index the accumulated totals.
 enum { TK_ROUTER = 0, TK_GATE_UP, TK_DOWN, TK_STAGE, TK_SLOT, TK_PF_GATE_UP, TK_PF_DOWN, TK_COMBINE, TK_CB_UP,
-       TK_CB_DOWN, TK_STREAM_CALIB, TK_RESIDENT, TK_KINDS };
+       TK_CB_DOWN, TK_STREAM_CALIB, TK_KINDS };
 bool kt_enabled();
 void kt_events(int kind, hipEvent_t* start, hipEvent_t* stop);   // both null when disabled / full
 
@@ -212,13 +212,5 @@ int launch_cb_up(const __half* x, const uint8_t* pool, size_t stride, int n_slot
 int launch_cb_down(const uint16_t* h, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots,
                    const __half* scores, int k, int hidden, int inter, const uint8_t* grid, const __half* residual,
                    float* y_out, int per_expert, hipStream_t s);
-// One token through every layer of a fully resident stack in one cooperative launch
-// (resident_decode.hip); ws: resident_workspace_bytes(n_layers) bytes, zeroed once.
-uint64_t resident_workspace_bytes(int n_layers);
-int launch_resident_token(const __half* x0, const __half* router_w, const __half* norm_w, const uint64_t* pools,
-                          size_t stride, int n_layers, int hidden, int n_exp, int k, int inter, int group, float eps,
-                          uint32_t* ids_out, __half* scores_out, __half* xs_out, float* hs_out, uint32_t* ws,
-                          hipStream_t s);
-int read_resident_status(const uint32_t* ws, hipStream_t s, uint32_t* out);
 int launch_pair_combine(const __half* y, const __half* scores, const __half* residual, int n_tokens,
                         int k, int hidden, float* out, hipStream_t s);

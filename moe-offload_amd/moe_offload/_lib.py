@@ -79,10 +79,6 @@ SIGNATURES: dict[str, tuple] = {
     "moe_cb_moe": (_c_int, [_c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
                             _c_vp, _c_int, _c_vp]),
     "moe_pair_combine": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
-    "moe_resident_workspace_bytes": (_c_u64, [_c_int]),
-    "moe_resident_decode": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_u64, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                     _c_int, _c_f, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
-    "moe_resident_status": (_c_int, [_c_vp, _c_vp]),
     # no reference counterpart
     "c_last_error": (ctypes.c_char_p, []),
     "c_clear_error": (None, []),

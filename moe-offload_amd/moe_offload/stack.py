@@ -56,8 +56,6 @@ class StackConfig:
                                  # alone on the link more often than the demand copies do
     resident: bool = False       # every layer's experts in HBM (no slot tables, no staging)
     routed_glu: bool = True      # resident: the router writes logits, gate/up selects (no hand-off)
-    persistent: bool = False     # resident: the whole token in one cooperative launch
-                                 # (moe_resident_decode) instead of three launches per layer
     fused_tables: bool = True    # device mode: the router's last block runs the slot-table step
                                  # and the next layer's prefetch (no separate table launches)
     sched: bool = False          # the C++ runner's scheduler variant (cpp/src/engine.cpp:700-730,
@@ -156,10 +154,6 @@ class DecodeStack:
         self.router_ws = [torch.zeros(int(L.moe_router_workspace_bytes(c.n_exp)), dtype=torch.uint8, device=dev)
                           for _ in range(c.n_layers)]
         self.side = torch.cuda.Stream(device=dev)
-        if c.resident and c.persistent:
-            self.pool_ptrs = torch.tensor([p.data_ptr() for p in self.full_pools], dtype=torch.int64, device=dev)
-            self.resident_ws = torch.zeros(int(L.moe_resident_workspace_bytes(c.n_layers)), dtype=torch.uint8,
-                                           device=dev)
         self.ev_pred = [torch.cuda.Event() for _ in range(c.n_layers)]
         self.ev_pref = [torch.cuda.Event() for _ in range(c.n_layers)]
         self.ev_copy = [torch.cuda.Event() for _ in range(c.n_layers)]
@@ -274,14 +268,6 @@ class DecodeStack:
         layer wait for its prefetch copies because both may target the same slot."""
         c = self.cfg
         main = torch.cuda.current_stream()
-        if c.resident and c.persistent:
-            _lib.check(self.L.moe_resident_decode(self.xs[0].data_ptr(), self.router_w.data_ptr(),
-                                                  self.norm_w.data_ptr(), self.pool_ptrs.data_ptr(), self.blob_bytes,
-                                                  c.n_layers, c.hidden, c.n_exp, c.top_k, c.inter, c.group, c.eps,
-                                                  self.ids.data_ptr(), self.scores.data_ptr(), self.xs.data_ptr(),
-                                                  self.hs.data_ptr(), self.resident_ws.data_ptr(), main.cuda_stream),
-                       "resident_decode")
-            return
         for l in range(c.n_layers):
             if c.resident:
                 if c.routed_glu:
@@ -439,12 +425,8 @@ class DecodeStack:
         return self.xs[self.cfg.n_layers]
 
     def capture_graph(self):
-        """Capture one device-driven token into a HIP graph (replayed by decode_token).  The
-        persistent resident token is one launch already: nothing to capture."""
+        """Capture one device-driven token into a HIP graph (replayed by decode_token)."""
         assert self.mode == "device"
-        if self.cfg.resident and self.cfg.persistent:
-            self.graph = None
-            return
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream(device=self.device)
@@ -455,12 +437,6 @@ class DecodeStack:
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         self.graph = g
-
-    def resident_status(self) -> int:
-        """0, or the (layer, phase) of a wait that timed out in the persistent token (blocks)."""
-        if not (self.cfg.resident and self.cfg.persistent):
-            return 0
-        return int(self.L.moe_resident_status(self.resident_ws.data_ptr(), torch.cuda.current_stream().cuda_stream))
 
     def decode_totals(self) -> list[int]:
         if self.cfg.resident:
