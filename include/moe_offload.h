@@ -151,7 +151,8 @@ int moe_rmsnorm(const float* h_in, const void* norm_w, float eps, int hidden, vo
 uint64_t moe_q2_expert_bytes(int hidden, int inter, int group);
 /* gather_qmm gate+up + SwiGLU (loader.py:564, kernels.cpp:1027-1040,1090-1094):
  * h_out[k][inter] fp16 from x fp16 [hidden] over pool blobs selected by slots[k]; pool holds
- * n_slots blobs of `stride` bytes (a slot id >= n_slots contributes zeros). */
+ * n_slots blobs of `stride` bytes (a slot id >= n_slots contributes zeros).  hidden, inter:
+ * multiples of 64, hidden <= 4096, inter <= 1024. */
 int moe_q2_gate_up(const void* x, const void* pool, uint64_t stride, int n_slots,
                    const uint32_t* slots, int k, int hidden, int inter, int group, void* h_out,
                    void* stream);
@@ -166,6 +167,23 @@ int moe_q2_switch_glu(const void* x, const void* pool, uint64_t stride, int n_sl
                       const uint32_t* slots, const void* scores, int k, int hidden, int inter,
                       int group, const void* residual, void* h_ws, float* y_out, int per_expert,
                       void* stream);
+
+/* The same SwitchGLU over experts held as the reference's 9 tensors (loader.py:332-406: per
+ * projection a code pool [slots][out][in/16] u32 and scale and bias pools [slots][out][in/64]),
+ * each tensor at its own base address with its own bytes per slot.  ptrs / slot_bytes: 9 entries
+ * in role order -- gate weight, scales, biases, up weight, scales, biases, down weight, scales,
+ * biases; scale_bf16 != 0: scales and biases are bf16 (the reference's checkpoints), else fp16.
+ * Any hidden <= 4096 and inter <= 1024 that are multiples of 64 (the real model: 2560 / 640);
+ * other arguments as moe_q2_gate_up / moe_q2_down / moe_q2_switch_glu, which also take these
+ * shapes for blob pools. */
+int moe_q2t_gate_up(const void* x, const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots,
+                    const uint32_t* slots, int k, int hidden, int inter, int group, void* h_out, void* stream);
+int moe_q2t_down(const void* h, const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots,
+                 const uint32_t* slots, const void* scores, int k, int hidden, int inter, int group,
+                 const void* residual, float* y_out, int per_expert, void* stream);
+int moe_q2t_switch_glu(const void* x, const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots,
+                       const uint32_t* slots, const void* scores, int k, int hidden, int inter, int group,
+                       const void* residual, void* h_ws, float* y_out, int per_expert, void* stream);
 
 /* Prefill grouped GEMM (loader.py:566-699 sorted gather_qmm via prefill_qproj.py:18-40;
  * cpp/src/layers.cpp:364-600).  The n_rows (token, k) rows are sorted by expert; segment u
@@ -226,6 +244,13 @@ void* c_host_alloc(uint64_t bytes);
 int c_host_free(void* p);
 /* Declare tensor 0 of a layer as a Q2 blob pool (row_bytes[0] == moe_q2_expert_bytes). */
 int c_layer_set_format(int layer_idx, int hidden, int inter, int group);
+/* Declare the layer's 9 tensors, as loader.py:332-406 passes them to c_layer_init (sorted by file
+ * offset), to be the Q2 projections: roles[t] is the role of tensor t (MOE_Q2T_*); each tensor's
+ * row_bytes must be its size per expert; scale_bf16 as moe_q2t_switch_glu.  c_layer_switch_glu and
+ * c_layer_switch_glu_split then read the 9 pools in place. */
+enum { MOE_Q2T_GATE_W = 0, MOE_Q2T_GATE_S, MOE_Q2T_GATE_B, MOE_Q2T_UP_W, MOE_Q2T_UP_S, MOE_Q2T_UP_B,
+       MOE_Q2T_DOWN_W, MOE_Q2T_DOWN_S, MOE_Q2T_DOWN_B };
+int c_layer_set_format9(int layer_idx, int hidden, int inter, int group, const int32_t* roles, int scale_bf16);
 /* SwitchGLU over the layer's pool with its current slot ids; orders after pending copies. */
 int c_layer_switch_glu(int layer_idx, const void* x, const void* scores, const void* residual,
                        void* h_ws, float* y_out, int per_expert, int k, void* stream);

@@ -56,8 +56,11 @@ struct LayerState {
     bool copy_pending = false, read_recorded = false;
     bool inflight = false, bounce_busy = false;
     uint64_t inflight_slots[MOE_NUM_EXPERTS / 64] = {};
-    // Q2 blob format of tensor 0 (for c_layer_switch_glu)
+    // Q2 format for the layer's GEMV: a blob pool in tensor 0 (c_layer_set_format) or the
+    // reference's 9 tensors (c_layer_set_format9: fmt9, with E9 built from the pools)
     int hidden = 0, inter = 0, group = 0;
+    bool fmt9 = false;
+    Q2Experts E9 = {};
     uint8_t* bounce = nullptr;                // pinned bounce buffer for file-backed stores
     size_t bounce_bytes = 0;
     // Prefetch copies (c_layer_start_prefetch, the scheduler's next-layer prefetch) also record
@@ -278,6 +281,18 @@ int wait_copies_gpu(LayerState& L, hipStream_t s) {
     L.copy_pending = false;
     L.pf_pending = false;
     return 0;
+}
+
+// SwitchGLU over a layer's pool in its format (blob or 9 tensors).
+int layer_glu(const LayerState& L, const void* x, const uint32_t* slots, const void* scores, int k,
+              const void* residual, void* h_ws, float* y_out, int per_expert, hipStream_t s) {
+    if (L.fmt9) {
+        if (launch_q2t_gate_up((const __half*)x, L.E9, L.capacity, slots, k, L.hidden, L.inter, (__half*)h_ws, s)) return -1;
+        return launch_q2t_down((const __half*)h_ws, L.E9, L.capacity, slots, (const __half*)scores, k, L.hidden, L.inter,
+                               (const __half*)residual, y_out, per_expert, s);
+    }
+    return moe_q2_switch_glu(x, (const void*)L.dst[0], L.row_bytes[0], L.capacity, slots, scores, k, L.hidden, L.inter,
+                             L.group, residual, h_ws, y_out, per_expert, s);
 }
 
 int write_slot_inds(LayerState& L, const uint32_t* slots, int k) {
@@ -901,7 +916,105 @@ int c_layer_set_format(int layer, int hidden, int inter, int group) {
     L.hidden = hidden;
     L.inter = inter;
     L.group = group;
+    L.fmt9 = false;
     return 0;
+}
+
+// The layer's 9 tensors (c_layer_init order, which the reference sorts by file offset,
+// loader.py:381-385) are the Q2 projections: roles[t] names tensor t (Q2T_* in moe_offload.h).
+int c_layer_set_format9(int layer, int hidden, int inter, int group, const int32_t* roles, int scale_bf16) {
+    if (!valid_layer(layer) || !g_layers[layer].init) { moe_set_error("set_format9: bad layer %d", layer); return -1; }
+    if (!q2t_shape_ok("set_format9", 1, hidden, inter, group)) return -1;
+    if (!roles) { moe_set_error("set_format9: null roles"); return -1; }
+    LayerState& L = g_layers[layer];
+    int tensor_of[9];
+    for (int r = 0; r < 9; ++r) tensor_of[r] = -1;
+    for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
+        if (roles[t] < 0 || roles[t] >= 9 || tensor_of[roles[t]] >= 0) {
+            moe_set_error("set_format9: roles must name each of the 9 tensors once (tensor %d: %d)", t, roles[t]);
+            return -1;
+        }
+        tensor_of[roles[t]] = t;
+    }
+    Q2Experts E = {};
+    for (int p = 0; p < 3; ++p) {
+        const uint64_t out = p == 2 ? hidden : inter, in = p == 2 ? inter : hidden;
+        const uint64_t want[3] = {out * in / 4, out * (in / 64) * 2, out * (in / 64) * 2};
+        for (int c = 0; c < 3; ++c) {
+            const int t = tensor_of[3 * p + c];
+            if (L.row_bytes[t] != want[c] || !L.dst[t]) {
+                moe_set_error("set_format9: tensor %d (role %d) has %llu bytes per expert, expected %llu", t, 3 * p + c,
+                              (unsigned long long)L.row_bytes[t], (unsigned long long)want[c]);
+                return -1;
+            }
+        }
+        E.p[p].w = (const uint8_t*)L.dst[tensor_of[3 * p]];
+        E.p[p].s = (const uint8_t*)L.dst[tensor_of[3 * p + 1]];
+        E.p[p].b = (const uint8_t*)L.dst[tensor_of[3 * p + 2]];
+        E.p[p].w_stride = L.row_bytes[tensor_of[3 * p]];
+        E.p[p].s_stride = L.row_bytes[tensor_of[3 * p + 1]];
+        E.p[p].b_stride = L.row_bytes[tensor_of[3 * p + 2]];
+        E.p[p].sb_step = 2;
+    }
+    E.bf16 = scale_bf16 ? 1 : 0;
+    L.hidden = hidden;
+    L.inter = inter;
+    L.group = group;
+    L.E9 = E;
+    L.fmt9 = true;
+    return 0;
+}
+
+// The 9 tensors as plain arguments: ptrs / slot_bytes in role order (gate w, s, b, up w, s, b,
+// down w, s, b).
+static bool experts9(const char* who, const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int hidden,
+                     int inter, Q2Experts& E) {
+    if (!ptrs || !slot_bytes) { moe_set_error("%s: null tensor arrays", who); return false; }
+    for (int p = 0; p < 3; ++p) {
+        const uint64_t out = p == 2 ? hidden : inter, in = p == 2 ? inter : hidden;
+        const uint64_t want[3] = {out * in / 4, out * (in / 64) * 2, out * (in / 64) * 2};
+        for (int c = 0; c < 3; ++c)
+            if (!ptrs[3 * p + c] || slot_bytes[3 * p + c] < want[c]) {
+                moe_set_error("%s: tensor %d: %llu bytes per expert < %llu", who, 3 * p + c,
+                              (unsigned long long)slot_bytes[3 * p + c], (unsigned long long)want[c]);
+                return false;
+            }
+        E.p[p].w = (const uint8_t*)ptrs[3 * p];
+        E.p[p].s = (const uint8_t*)ptrs[3 * p + 1];
+        E.p[p].b = (const uint8_t*)ptrs[3 * p + 2];
+        E.p[p].w_stride = slot_bytes[3 * p];
+        E.p[p].s_stride = slot_bytes[3 * p + 1];
+        E.p[p].b_stride = slot_bytes[3 * p + 2];
+        E.p[p].sb_step = 2;
+    }
+    E.bf16 = scale_bf16 ? 1 : 0;
+    return true;
+}
+
+int moe_q2t_gate_up(const void* x, const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots,
+                    const uint32_t* slots, int k, int hidden, int inter, int group, void* h_out, void* stream) {
+    Q2Experts E;
+    if (!q2t_shape_ok("q2t_gate_up", k, hidden, inter, group)) return -1;
+    if (!experts9("q2t_gate_up", ptrs, slot_bytes, scale_bf16, hidden, inter, E)) return -1;
+    return launch_q2t_gate_up((const __half*)x, E, n_slots, slots, k, hidden, inter, (__half*)h_out, (hipStream_t)stream);
+}
+
+int moe_q2t_down(const void* h, const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots,
+                 const uint32_t* slots, const void* scores, int k, int hidden, int inter, int group,
+                 const void* residual, float* y_out, int per_expert, void* stream) {
+    Q2Experts E;
+    if (!q2t_shape_ok("q2t_down", k, hidden, inter, group)) return -1;
+    if (!experts9("q2t_down", ptrs, slot_bytes, scale_bf16, hidden, inter, E)) return -1;
+    return launch_q2t_down((const __half*)h, E, n_slots, slots, (const __half*)scores, k, hidden, inter,
+                           (const __half*)residual, y_out, per_expert, (hipStream_t)stream);
+}
+
+int moe_q2t_switch_glu(const void* x, const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots,
+                       const uint32_t* slots, const void* scores, int k, int hidden, int inter, int group,
+                       const void* residual, void* h_ws, float* y_out, int per_expert, void* stream) {
+    if (moe_q2t_gate_up(x, ptrs, slot_bytes, scale_bf16, n_slots, slots, k, hidden, inter, group, h_ws, stream)) return -1;
+    return moe_q2t_down(h_ws, ptrs, slot_bytes, scale_bf16, n_slots, slots, scores, k, hidden, inter, group, residual,
+                        y_out, per_expert, stream);
 }
 
 // SwitchGLU over the layer's slot pool with the slot ids of its last decode step.  Orders the
@@ -917,9 +1030,7 @@ int c_layer_switch_glu(int layer, const void* x, const void* scores, const void*
     hipStream_t s = (hipStream_t)stream;
     if (wait_copies_gpu(L, s)) return -1;
     if (ensure_events(L)) return -1;
-    if (moe_q2_switch_glu(x, (const void*)L.dst[0], L.row_bytes[0], L.capacity, L.slot_inds, scores, k, L.hidden, L.inter,
-                          L.group, residual, h_ws, y_out, per_expert, stream))
-        return -1;
+    if (layer_glu(L, x, L.slot_inds, scores, k, residual, h_ws, y_out, per_expert, s)) return -1;
     HIP_TRY(hipEventRecord(L.read_done, s));
     L.read_recorded = true;
     return 0;
@@ -952,13 +1063,10 @@ int c_layer_switch_glu_split(int layer, int part, const void* x, const void* sco
     if (part == 0) {
         if (L.pf_pending) HIP_TRY(hipStreamWaitEvent(s, L.pf_done, 0));
         if (launch_split_lists(S, (const __half*)scores, dslots, dscores, s)) return -1;
-        rc = moe_q2_switch_glu(x, (const void*)L.dst[0], L.row_bytes[0], L.capacity, dslots, dscores, S.n_hit,
-                               L.hidden, L.inter, L.group, residual, h_ws, y_out, 0, stream);
+        rc = layer_glu(L, x, dslots, dscores, S.n_hit, residual, h_ws, y_out, 0, s);
     } else {
         if (wait_copies_gpu(L, s)) return -1;
-        rc = moe_q2_switch_glu(x, (const void*)L.dst[0], L.row_bytes[0], L.capacity, dslots + MOE_MAX_K,
-                               dscores + MOE_MAX_K, S.n_miss, L.hidden, L.inter, L.group, nullptr, h_ws, y_out, 2,
-                               stream);
+        rc = layer_glu(L, x, dslots + MOE_MAX_K, dscores + MOE_MAX_K, S.n_miss, nullptr, h_ws, y_out, 2, s);
     }
     if (rc) return -1;
     HIP_TRY(hipEventRecord(L.read_done, s));
@@ -1038,6 +1146,7 @@ int c_layer_grouped_switch_glu(int layer, const void* x, int n_tokens, const int
     }
     LayerState& L = g_layers[layer];
     if (!L.dst[0]) { moe_set_error("layer_grouped_switch_glu: layer %d has no pool", layer); return -1; }
+    if (L.fmt9) { moe_set_error("layer_grouped_switch_glu: layer %d holds 9 tensors (the grouped GEMM takes blob pools)", layer); return -1; }
     if (n_seg > L.capacity) {
         moe_set_error("layer_grouped_switch_glu: %d segments > capacity %d", n_seg, L.capacity);
         return -1;

@@ -48,6 +48,26 @@ static inline __host__ __device__ BlobLayout blob_layout(int hidden, int inter, 
     return L;
 }
 
+// The Q2 experts of a pool addressed per projection (gate, up, down): code rows [out][in/16] u32 at
+// w + slot * w_stride, scales and biases at s / b + slot * s_stride / b_stride with sb_step bytes
+// between consecutive (row, group) entries -- 2 for separate scale and bias arrays (the
+// reference's 9 pools, loader.py:332-406), 4 for the interleaved (scale, bias) words of a blob.
+// bf16 != 0: scales and biases are bf16, else fp16.
+struct Q2Proj {
+    const uint8_t* w;
+    const uint8_t* s;
+    const uint8_t* b;
+    uint64_t w_stride, s_stride, b_stride;
+    int sb_step;
+};
+struct Q2Experts {
+    Q2Proj p[3];
+    int bf16;
+};
+
+// Roles of the 9 tensors of a reference layer (c_layer_set_format9).
+enum { Q2T_GATE_W = 0, Q2T_GATE_S, Q2T_GATE_B, Q2T_UP_W, Q2T_UP_S, Q2T_UP_B, Q2T_DOWN_W, Q2T_DOWN_S, Q2T_DOWN_B };
+
 // 2-bit codebook expert blob (IQ2_XXS-style super-blocks of 256 weights, seeded 256-entry grid):
 //   up_qs [I][H/256][8][8 B] | down_qs [H][I/256][8][8 B] | up_d [I][H/256] fp16 | down_d [H][I/256] fp16
 // Each 8-byte sub-block entry (32 weights) = 4 grid indices (one per 8-weight group) and a u32
@@ -186,6 +206,13 @@ int launch_q2_down(const __half* h, const uint8_t* pool, size_t expert_stride, i
                    const uint32_t* slots, const __half* scores, int k, int hidden, int inter,
                    int group, const __half* residual, float* y_out, int per_expert,
                    hipStream_t s);
+// Tensor-form Q2 GEMV (q2_gemv_t.hip): any hidden <= 4096 / inter <= 1024, multiples of 64.
+bool q2t_shape_ok(const char* who, int k, int hidden, int inter, int group);
+Q2Experts q2_experts_from_blob(const uint8_t* pool, size_t stride, const BlobLayout& L);
+int launch_q2t_gate_up(const __half* x, const Q2Experts& E, int n_slots, const uint32_t* slots, int k, int hidden,
+                       int inter, __half* h_out, hipStream_t s);
+int launch_q2t_down(const __half* h, const Q2Experts& E, int n_slots, const uint32_t* slots, const __half* scores,
+                    int k, int hidden, int inter, const __half* residual, float* y_out, int per_expert, hipStream_t s);
 int launch_slot_step(SlotTable* t, const uint32_t* ids, int k, uint32_t* slot_inds,
                      hipStream_t s);
 int launch_slot_prefetch(SlotTable* t, const int32_t* preds, int m, int max_fetch,

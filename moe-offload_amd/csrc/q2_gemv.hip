@@ -347,7 +347,8 @@ int launch_q2_gate_up(const __half* x, const uint8_t* pool, size_t stride, int n
         case 8: return gate_up_t<8>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
         case 16: return gate_up_t<16>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
         case 32: return gate_up_t<32>(x, pool, stride, slots, n_slots, k, inter, L, h_out, s);
-        default: moe_set_error("q2_gate_up: hidden=%d unsupported (64*{1,2,4,8,16,32})", hidden); return -1;
+        default:   // other multiples of 64: the tensor-form kernel over the blob's tensors
+            return launch_q2t_gate_up(x, q2_experts_from_blob(pool, stride, L), n_slots, slots, k, hidden, inter, h_out, s);
     }
 }
 
@@ -387,6 +388,8 @@ int launch_q2_down(const __half* h, const uint8_t* pool, size_t stride, int n_sl
         case 4: return down_t<4>(h, pool, stride, slots, n_slots, scores, k, hidden, L, residual, y_out, per_expert, s);
         case 8: return down_t<8>(h, pool, stride, slots, n_slots, scores, k, hidden, L, residual, y_out, per_expert, s);
         case 16: return down_t<16>(h, pool, stride, slots, n_slots, scores, k, hidden, L, residual, y_out, per_expert, s);
-        default: moe_set_error("q2_down: inter=%d unsupported (64*{1,2,4,8,16})", inter); return -1;
+        default:   // other multiples of 64: the tensor-form kernel over the blob's tensors
+            return launch_q2t_down(h, q2_experts_from_blob(pool, stride, L), n_slots, slots, scores, k, hidden, inter,
+                                   residual, y_out, per_expert, s);
     }
 }

@@ -1,0 +1,283 @@
+// Q2 gather-GEMV (SwitchGLU decode) over experts addressed as tensors, at any hidden / intermediate
+// size that is a multiple of 64 (gfx950).
+//
+// Reference semantics: mlx-qwen38/loader.py:557-564,964-965 (gather_qmm x3 + SwiGLU + the
+// score-weighted sum), cpp/src/layers.cpp:343-362.  The reference keeps a layer's slot pool as 9
+// tensors (loader.py:332-406): per projection (gate, up, down) a code pool [cap][out][in/16] u32 and
+// scale and bias pools [cap][out][in/64] (bf16 in its checkpoints).  Here each projection is
+// addressed by three base addresses with their own bytes per slot, and scale/bias by an element
+// step (2: separate arrays, 4: the interleaved (scale, bias) words of a blob), so the same kernels
+// read the reference's 9 pools in place, bf16 or fp16, and blob pools of any shape.  The real
+// model's layer (hidden 2560, intermediate 640: 40 and 10 groups per row) runs here.
+//
+// Arithmetic: the Q2 dot of q2_dot.h (codes expanded by the fp16 1024-offset trick, v_dot2 against
+// activation pairs staged in LDS), fp32 accumulation, W = scale * q + bias per group of 64.
+//   k_q2t_gate_up: 8 lanes per row, each lane looping over the row's groups g = l8, l8 + 8, ...;
+//                  gate rows on lanes 0-31, up rows on lanes 32-63 (4 rows per wave).
+//   k_q2t_down:    16 lanes per output row (one group each: intermediate <= 1024), 8 rows per
+//                  block, the block's 4 waves split the experts; fixed-order cross-wave sum.
+#include <hip/hip_fp16.h>
+
+#include "lane_reduce.h"
+#include "moe_common.h"
+#include "q2_dot.h"
+
+namespace {
+
+using namespace q2dot;
+
+constexpr int kTMaxGroups = 64;         // hidden <= 4096
+constexpr int kTMaxPasses = 8;          // groups per lane of a gate/up row
+constexpr int kTDownRows = 8;           // output rows per down block
+constexpr int kTDownLanes = 16;         // lanes per down row: intermediate <= 1024
+
+template <bool BF16>
+__device__ __forceinline__ float half_bits(uint16_t v) {
+    if constexpr (BF16) return __uint_as_float((uint32_t)v << 16);
+    else return __half2float(__ushort_as_half(v));
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_q2t_gate_up(const __half* __restrict__ x, Q2Experts E,
+                                                     const uint32_t* __restrict__ slots, int n_slots, int hidden,
+                                                     int inter, __half* __restrict__ h_out) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = blockIdx.y;
+    const int GPR = hidden >> 6;
+    const int passes = (GPR + 7) >> 3;
+    const int proj = lane >> 5, rl = (lane >> 3) & 3, l8 = lane & 7;
+    const int row = (blockIdx.x * 4 + wv) * 4 + rl;
+    __shared__ uint4 xp[kTMaxGroups][8];
+    __shared__ float xc[kTMaxGroups][2];
+
+    // the activation units first (one 16-value unit per thread), then every weight load
+    const int n_units = hidden >> 4;
+    const int uc = tid < n_units ? tid : 0;
+    const uint4 xlo = reinterpret_cast<const uint4*>(x)[2 * uc];
+    const uint4 xhi = reinterpret_cast<const uint4*>(x)[2 * uc + 1];
+    const uint32_t slot = slots[j];
+    const bool ok = slot < (uint32_t)n_slots;             // an invalid slot yields h = 0
+    const size_t s = ok ? slot : 0;
+    const int rowc = row < inter ? row : inter - 1;
+    const Q2Proj& Pg = E.p[0];
+    const Q2Proj& Pu = E.p[1];
+    const uint8_t* wb = proj ? Pu.w + s * Pu.w_stride : Pg.w + s * Pg.w_stride;
+    const uint8_t* sb = proj ? Pu.s + s * Pu.s_stride : Pg.s + s * Pg.s_stride;
+    const uint8_t* bb = proj ? Pu.b + s * Pu.b_stride : Pg.b + s * Pg.b_stride;
+    const int step = proj ? Pu.sb_step : Pg.sb_step;
+    wb += (size_t)rowc * (hidden >> 2);
+    sb += (size_t)rowc * GPR * step;
+    bb += (size_t)rowc * GPR * step;
+    uint4 c[kTMaxPasses];
+    uint16_t sc[kTMaxPasses], bi[kTMaxPasses];
+#pragma unroll
+    for (int t = 0; t < kTMaxPasses; ++t) {
+        if (t >= passes) break;                           // wave-uniform
+        int g = l8 + 8 * t;
+        g = g < GPR ? g : GPR - 1;
+        c[t] = *reinterpret_cast<const uint4*>(wb + (size_t)g * 16);
+        sc[t] = *reinterpret_cast<const uint16_t*>(sb + (size_t)g * step);
+        bi[t] = *reinterpret_cast<const uint16_t*>(bb + (size_t)g * step);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    stage_pairs(xlo, xhi, tid < n_units, xp[uc >> 2], xc[uc >> 2], uc & 3, (uc >> 2) & 7);
+    __syncthreads();
+
+    float acc = 0.f;
+#pragma unroll
+    for (int t = 0; t < kTMaxPasses; ++t) {
+        if (t >= passes) break;
+        const int g = l8 + 8 * t;
+        if (g < GPR) {
+            h2_t P[32];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint4 v = xp[g][i ^ (g & 7)];
+                P[4 * i] = as_h2(v.x);
+                P[4 * i + 1] = as_h2(v.y);
+                P[4 * i + 2] = as_h2(v.z);
+                P[4 * i + 3] = as_h2(v.w);
+            }
+            const float dot = q2_group_dot(c[t], P);
+            acc += half_bits<BF16>(sc[t]) * (dot - xc[g][0]) + half_bits<BF16>(bi[t]) * xc[g][1];
+        }
+    }
+    acc = lanes::group_sum<8>(acc);
+    float gt, up;
+    lanes::halves(acc, gt, up);
+    if (proj == 0 && l8 == 0 && row < inter) {
+        const float hval = ok ? gt / (1.0f + __expf(-gt)) * up : 0.0f;
+        h_out[(size_t)j * inter + row] = __float2half_rn(hval);
+    }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_q2t_down(const __half* __restrict__ h, Q2Experts E,
+                                                  const uint32_t* __restrict__ slots, int n_slots,
+                                                  const __half* __restrict__ scores, int k, int hidden, int inter,
+                                                  const __half* __restrict__ residual, float* __restrict__ y_out,
+                                                  int per_expert) {
+    constexpr int RPI = 64 / kTDownLanes;                 // rows per wave instruction
+    constexpr int ITERS = kTDownRows / RPI;
+    constexpr int MAXJ = (MOE_MAX_K + 3) / 4;
+    constexpr int kUnitIters = (MOE_MAX_K * 1024 / 16 + 255) / 256;
+    __shared__ uint4 hp[MOE_MAX_K][kTDownLanes][8];
+    __shared__ float hc[MOE_MAX_K][kTDownLanes][2];
+    __shared__ float red[4][kTDownRows];
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int IPR = inter >> 6;
+    const int g = lane & (kTDownLanes - 1), rl = lane / kTDownLanes;
+    const int gc = g < IPR ? g : IPR - 1;
+    const int row0 = blockIdx.x * kTDownRows;
+
+    const int n_units = k * IPR * 4;
+    uint4 hv[kUnitIters][2];
+#pragma unroll
+    for (int ui = 0; ui < kUnitIters; ++ui) {
+        const int u = tid + 256 * ui;
+        const int uc = u < n_units ? u : 0;
+        hv[ui][0] = reinterpret_cast<const uint4*>(h + (size_t)uc * 16)[0];
+        hv[ui][1] = reinterpret_cast<const uint4*>(h + (size_t)uc * 16)[1];
+    }
+    const Q2Proj& Pd = E.p[2];
+    uint32_t slot_q[MAXJ];
+    uint4 c[MAXJ][ITERS];
+    uint16_t sc[MAXJ][ITERS], bi[MAXJ][ITERS];
+#pragma unroll
+    for (int q = 0; q < MAXJ; ++q) {
+        const int jq = wv + 4 * q;
+        slot_q[q] = slots[jq < k ? jq : k - 1];
+        const size_t s = slot_q[q] < (uint32_t)n_slots ? slot_q[q] : 0u;
+        const uint8_t* wb = Pd.w + s * Pd.w_stride;
+        const uint8_t* sb = Pd.s + s * Pd.s_stride;
+        const uint8_t* bb = Pd.b + s * Pd.b_stride;
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            int row = row0 + it * RPI + rl;
+            row = row < hidden ? row : hidden - 1;
+            c[q][it] = *reinterpret_cast<const uint4*>(wb + (size_t)row * (inter >> 2) + (size_t)gc * 16);
+            sc[q][it] = *reinterpret_cast<const uint16_t*>(sb + ((size_t)row * IPR + gc) * Pd.sb_step);
+            bi[q][it] = *reinterpret_cast<const uint16_t*>(bb + ((size_t)row * IPR + gc) * Pd.sb_step);
+        }
+    }
+    const bool weighted = scores != nullptr;
+    const float s_lane = __half2float((weighted ? scores : h)[lane < k ? lane : 0]);
+
+#pragma unroll
+    for (int ui = 0; ui < kUnitIters; ++ui) {
+        const int u = tid + 256 * ui;
+        if (256 * ui >= n_units) break;                   // block-uniform
+        const int uc = u < n_units ? u : 0;
+        const int jj = uc / (IPR * 4), gg = (uc >> 2) % IPR;
+        stage_pairs(hv[ui][0], hv[ui][1], u < n_units, hp[jj][gg], hc[jj][gg], uc & 3, gg & 7);
+    }
+    __syncthreads();
+
+    float acc[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) acc[it] = 0.f;
+#pragma unroll
+    for (int q = 0; q < MAXJ; ++q) {
+        const int jq = wv + 4 * q;
+        if (jq >= k) break;
+        h2_t P[32];
+        const uint4* src = hp[jq][gc];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint4 v = src[i ^ (gc & 7)];
+            P[4 * i] = as_h2(v.x);
+            P[4 * i + 1] = as_h2(v.y);
+            P[4 * i + 2] = as_h2(v.z);
+            P[4 * i + 3] = as_h2(v.w);
+        }
+        const float cst = hc[jq][gc][0], sum = hc[jq][gc][1];
+        const bool ok = slot_q[q] < (uint32_t)n_slots && g < IPR;
+        const float sj = weighted ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s_lane), jq)) : 1.0f;
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            float part = ok ? half_bits<BF16>(sc[q][it]) * (q2_group_dot(c[q][it], P) - cst) +
+                                  half_bits<BF16>(bi[q][it]) * sum
+                            : 0.0f;
+            part = lanes::group_sum<kTDownLanes>(part);
+            const int rloc = it * RPI + rl;
+            if (per_expert == 1) {
+                const int row = row0 + rloc;
+                if (g == 0 && row < hidden) y_out[(size_t)jq * hidden + row] = part;
+            } else {
+                acc[it] += sj * part;
+            }
+        }
+    }
+    if (per_expert == 1) return;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it)
+        if (g == 0) red[wv][it * RPI + rl] = acc[it];
+    __syncthreads();
+    if (tid < kTDownRows) {
+        const int row = row0 + tid;
+        if (row < hidden) {
+            float y = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+            if (per_expert == 2) {
+                y_out[row] += y;
+            } else {
+                if (residual) y += __half2float(residual[row]);
+                y_out[row] = y;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool q2t_shape_ok(const char* who, int k, int hidden, int inter, int group) {
+    if (group != 64) { moe_set_error("%s: group=%d unsupported (kernels take group 64)", who, group); return false; }
+    if (k <= 0 || k > MOE_MAX_K) { moe_set_error("%s: k=%d out of range 1..%d", who, k, MOE_MAX_K); return false; }
+    if (hidden <= 0 || inter <= 0 || hidden % 64 || inter % 64 || hidden > 64 * kTMaxGroups || inter > 64 * kTDownLanes) {
+        moe_set_error("%s: hidden=%d inter=%d (multiples of 64, hidden <= %d, inter <= %d)", who, hidden, inter,
+                      64 * kTMaxGroups, 64 * kTDownLanes);
+        return false;
+    }
+    return true;
+}
+
+Q2Experts q2_experts_from_blob(const uint8_t* pool, size_t stride, const BlobLayout& L) {
+    Q2Experts E;
+    const size_t w_off[3] = {L.gate_codes, L.up_codes, L.down_codes};
+    const size_t sb_off[3] = {L.gate_sb, L.up_sb, L.down_sb};
+    for (int p = 0; p < 3; ++p) {
+        E.p[p].w = pool + w_off[p];
+        E.p[p].s = pool + sb_off[p];
+        E.p[p].b = pool + sb_off[p] + 2;
+        E.p[p].w_stride = E.p[p].s_stride = E.p[p].b_stride = stride;
+        E.p[p].sb_step = 4;
+    }
+    E.bf16 = 0;
+    return E;
+}
+
+int launch_q2t_gate_up(const __half* x, const Q2Experts& E, int n_slots, const uint32_t* slots, int k, int hidden,
+                       int inter, __half* h_out, hipStream_t s) {
+    if (!q2t_shape_ok("q2t_gate_up", k, hidden, inter, 64)) return -1;
+    if (n_slots <= 0 || !slots || !x || !h_out) { moe_set_error("q2t_gate_up: empty pool or null pointer"); return -1; }
+    dim3 grid((inter + 15) / 16, k);
+    if (E.bf16) MOE_LAUNCH(TK_GATE_UP, (k_q2t_gate_up<true>), grid, dim3(256), 0, s, x, E, slots, n_slots, hidden, inter, h_out);
+    else MOE_LAUNCH(TK_GATE_UP, (k_q2t_gate_up<false>), grid, dim3(256), 0, s, x, E, slots, n_slots, hidden, inter, h_out);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int launch_q2t_down(const __half* h, const Q2Experts& E, int n_slots, const uint32_t* slots, const __half* scores,
+                    int k, int hidden, int inter, const __half* residual, float* y_out, int per_expert, hipStream_t s) {
+    if (!q2t_shape_ok("q2t_down", k, hidden, inter, 64)) return -1;
+    if (per_expert < 0 || per_expert > 2) { moe_set_error("q2t_down: mode %d (0 sum, 1 per expert, 2 add)", per_expert); return -1; }
+    if (n_slots <= 0 || !slots || !h || !y_out) { moe_set_error("q2t_down: empty pool or null pointer"); return -1; }
+    dim3 grid((hidden + kTDownRows - 1) / kTDownRows);
+    if (E.bf16)
+        MOE_LAUNCH(TK_DOWN, (k_q2t_down<true>), grid, dim3(256), 0, s, h, E, slots, n_slots, scores, k, hidden, inter,
+                   residual, y_out, per_expert);
+    else
+        MOE_LAUNCH(TK_DOWN, (k_q2t_down<false>), grid, dim3(256), 0, s, h, E, slots, n_slots, scores, k, hidden, inter,
+                   residual, y_out, per_expert);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}

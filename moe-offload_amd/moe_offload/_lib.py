@@ -66,6 +66,12 @@ SIGNATURES: dict[str, tuple] = {
                              _c_vp, _c_vp, _c_int, _c_vp]),
     "moe_q2_switch_glu": (_c_int, [_c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
                                    _c_vp, _c_vp, _c_vp, _c_int, _c_vp]),
+    "moe_q2t_gate_up": (_c_int, [_c_vp, _u64p, _u64p, _c_int, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp,
+                                 _c_vp]),
+    "moe_q2t_down": (_c_int, [_c_vp, _u64p, _u64p, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp,
+                              _c_vp, _c_int, _c_vp]),
+    "moe_q2t_switch_glu": (_c_int, [_c_vp, _u64p, _u64p, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
+                                    _c_vp, _c_vp, _c_vp, _c_int, _c_vp]),
     "moe_q2_grouped_gate_up": (_c_int, [_c_vp, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_u64, _c_int,
                                         _c_int, _c_int, _c_int, _c_vp, _c_vp]),
     "moe_q2_grouped_down": (_c_int, [_c_vp, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_u64, _c_int,
@@ -86,6 +92,7 @@ SIGNATURES: dict[str, tuple] = {
     "c_host_alloc": (_c_vp, [_c_u64]),
     "c_host_free": (_c_int, [_c_vp]),
     "c_layer_set_format": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
+    "c_layer_set_format9": (_c_int, [_c_int, _c_int, _c_int, _c_int, _i32p, _c_int]),
     "c_layer_switch_glu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
     "c_layer_mark_read": (_c_int, [_c_int, _c_vp]),
     "c_router_tables_dev": (_c_int, [_c_int, _c_int, _c_int, _c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_vp, _c_vp, _c_int,

@@ -39,3 +39,17 @@ def assert_close_rms(got, want, tol=1e-2, what=""):
     err = np.abs(got - want).max()
     assert err <= tol * rms, f"{what}: max|err| {err:.3e} > {tol} x RMS {rms:.3e}"
     return err / rms
+
+
+def experts_bf16(n_exp, hidden, inter, seed=1, scale_std=0.02):
+    """MLX-layout experts with bf16 scales and biases, as the reference's checkpoints hold them:
+    per projection (w uint32 [E, out, in/16], scales / biases bf16 bits uint16 [E, out, in/64])."""
+    rng = np.random.default_rng(seed)
+
+    def proj(out_f, in_f):
+        w = rng.integers(0, 2**32, size=(n_exp, out_f, in_f // 16), dtype=np.uint32)
+        s = q2.f32_to_bf16_bits((rng.standard_normal((n_exp, out_f, in_f // 64)) * scale_std).astype(np.float32))
+        b = q2.f32_to_bf16_bits(-1.5 * q2.bf16_bits_to_f32(s))
+        return w, s, b
+
+    return proj(inter, hidden), proj(inter, hidden), proj(hidden, inter)

@@ -261,3 +261,36 @@ def test_scheduler_entry_point_input_rules():
     many = (ctypes.c_int32 * 20)(*range(100, 120))
     assert lib.c_layer_decode_step_sched(43, many, 20, None, 0, -1, 0, 0) == 16
     assert L.stats()[0] == 16
+
+
+def test_set_format9_validates_roles_and_sizes():
+    """c_layer_set_format9 accepts the reference's 9 tensors in any order given their roles, and
+    rejects a missing / repeated role or a tensor whose bytes per expert do not fit its role (host
+    logic only: the pool addresses are never dereferenced)."""
+    from moe_offload import _lib
+    L = _lib.lib()
+    H, I = 2560, 640
+    size = {0: I * H // 4, 1: I * H // 64 * 2, 2: I * H // 64 * 2}         # per projection: w, s, b
+    order = [6, 0, 3, 7, 8, 1, 2, 4, 5]
+    rb = [size[r % 3] for r in order]
+    u64 = ctypes.c_uint64 * 9
+    layer = 60
+    L.c_layer_init(layer, -1, 16, u64(*[0] * 9), u64(*rb), u64(*[0x10000 * (t + 1) for t in range(9)]), 0)
+    L.c_clear_error()
+    try:
+        assert L.c_layer_set_format9(layer, H, I, 64, (ctypes.c_int32 * 9)(*order), 1) == 0
+        bad = list(order)
+        bad[1] = bad[0]                                                  # a role named twice
+        assert L.c_layer_set_format9(layer, H, I, 64, (ctypes.c_int32 * 9)(*bad), 1) == -1
+        assert "each of the 9 tensors once" in _lib.last_error()
+        L.c_clear_error()
+        swapped = list(order)
+        swapped[0], swapped[5] = swapped[5], swapped[0]                  # a weight where a scale belongs
+        assert L.c_layer_set_format9(layer, H, I, 64, (ctypes.c_int32 * 9)(*swapped), 1) == -1
+        assert "bytes per expert" in _lib.last_error()
+        L.c_clear_error()
+        assert L.c_layer_set_format9(layer, H, 600, 64, (ctypes.c_int32 * 9)(*order), 1) == -1   # not 64k
+        L.c_clear_error()
+    finally:
+        L.c_layer_init(layer, -1, 16, None, None, None, 0)
+        L.c_clear_error()
