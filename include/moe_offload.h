@@ -22,14 +22,30 @@ extern "C" {
 
 /* ---- Part 1: expert cache (expert_io.c) -------------------------------------------------- */
 
-/* expert_io.c:430-448.  Creates the copy stream; num_threads is accepted and unused (copies go
- * to the DMA engines). */
+/* expert_io.c:430-448.  num_threads: reader threads of file-backed layers (<= 0: 8), started on
+ * the first file batch; copies from host memory go to the DMA engines. */
 void c_io_init(int num_threads);
-/* cpp/src/expert_io.h:15 (superset ABI).  Drains copies and releases every layer. */
+/* cpp/src/expert_io.h:15 (superset ABI).  Joins file batches, stops the reader threads, drains
+ * copies and releases every layer. */
 void c_io_shutdown(void);
+/* No counterpart in the reference (its files are read through the page cache).  on != 0: file-backed
+ * layers initialised from now on also open their file with O_DIRECT, reading 4 KiB-aligned ranges
+ * that bypass the page cache; a file system that refuses it leaves the layer on the page cache
+ * (c_layer_io_direct says which). */
+void c_io_set_direct(int on);
+/* 1 when the layer reads its file with O_DIRECT, else 0. */
+int c_layer_io_direct(int layer_idx);
+/* Reader threads the file tier uses (c_io_init). */
+int c_io_threads(void);
+/* No counterpart in the reference (loader.py reads a shard through mx.load).  Reads n ranges of
+ * the file (lens[i] bytes at offs[i] into host address dsts[i]) with the reader threads and
+ * returns when all are done: 0, or -1 on a failed or short read (c_last_error).  Host only. */
+int c_io_read_ranges(int fd, const uint64_t* offs, const uint64_t* lens, const uint64_t* dsts, int n);
 /* expert_io.c:497-520.  fd == -1: base_offsets[t] are host addresses of tensor t's expert store
  * (pinned via c_host_alloc for overlap / device staging); fd >= 0: file offsets as in the
- * reference.  base_ptrs[t] are device slot pools; slot_inds_ptr receives slot ids (device or
+ * reference, each batch of misses read by the reader threads as one read per (tensor, run of
+ * consecutive experts) and joined where its slots are used (host-driven staging only; the caller
+ * keeps fd open until the layer is re-initialised or c_io_shutdown).  base_ptrs[t] are device slot pools; slot_inds_ptr receives slot ids (device or
  * host memory).  capacity in 1..512. */
 void c_layer_init(int layer_idx, int fd, int capacity, const uint64_t* base_offsets,
                   const uint64_t* row_bytes, const uint64_t* base_ptrs, uint64_t slot_inds_ptr);

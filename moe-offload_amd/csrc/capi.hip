@@ -9,8 +9,11 @@
 //   fd == -1 : base_offsets[t] are host addresses of tensor t's store (expert e at
 //              base_offsets[t] + e * row_bytes[t]); pinned memory (c_host_alloc) is required
 //              for overlap and for device-driven staging.
-//   fd >= 0  : base_offsets[t] are file offsets, as in the reference; reads go through a
-//              pinned bounce buffer (host-driven staging only).
+//   fd >= 0  : base_offsets[t] are file offsets, as in the reference; a batch of misses is read
+//              by the reader-thread pool (file_io.h) as one read per (tensor, run of consecutive
+//              experts) into one of four shared pinned bounce buffers, and the worker finishing the batch queues
+//              the copies to the slots; the batch is joined where its copies are needed
+//              (host-driven staging only).
 //   base_ptrs[t] : device address of tensor t's slot pool (slot s at + s * row_bytes[t]).
 //   A tensor with row_bytes > 0 but a zero source or destination is accounting-only.
 //
@@ -29,6 +32,14 @@
 #include <mutex>
 #include <vector>
 
+#include <fcntl.h>
+
+#include <algorithm>
+#include <memory>
+#include <numeric>
+#include <string>
+
+#include "file_io.h"
 #include "moe_common.h"
 #include "moe_offload.h"
 #include "slot_table_host.h"
@@ -52,17 +63,20 @@ struct LayerState {
     // copy_pending: copies the compute stream has not been made to wait for yet.  inflight:
     // copies that may still be running on the copy streams (a GPU-side wait does not end them);
     // cleared only once copy_done is known to have completed.  inflight_slots: the slots those
-    // copies write; bounce_busy: they read the bounce buffer.
+    // copies write.
     bool copy_pending = false, read_recorded = false;
-    bool inflight = false, bounce_busy = false;
+    bool inflight = false;
     uint64_t inflight_slots[MOE_NUM_EXPERTS / 64] = {};
     // Q2 format for the layer's GEMV: a blob pool in tensor 0 (c_layer_set_format) or the
     // reference's 9 tensors (c_layer_set_format9: fmt9, with E9 built from the pools)
     int hidden = 0, inter = 0, group = 0;
     bool fmt9 = false;
     Q2Experts E9 = {};
-    uint8_t* bounce = nullptr;                // pinned bounce buffer for file-backed stores
-    size_t bounce_bytes = 0;
+    // File-backed stores: the in-flight batch of reads, and an O_DIRECT descriptor of the same
+    // file when direct reads are on (-1 otherwise).
+    std::shared_ptr<fileio::Batch> fbatch;
+    bool fbatch_pf = false;                   // the in-flight batch is a prefetch (records pf_done)
+    int fd_direct = -1;
     // Prefetch copies (c_layer_start_prefetch, the scheduler's next-layer prefetch) also record
     // pf_done, so work on the step's hit slots can wait for them alone (split GLU).
     hipEvent_t pf_done = nullptr;
@@ -103,6 +117,21 @@ constexpr int kCopyStreams = 2;
 hipStream_t g_copy_more[kCopyStreams - 1] = {};
 hipEvent_t g_copy_more_done[kCopyStreams - 1] = {};
 bool g_ready = false;
+int g_dev = 0;                              // device of the copy streams (the reader threads set it)
+bool g_direct = false;                      // file-backed layers read with O_DIRECT when possible
+
+// Pinned bounce buffers of the file tier, shared by every layer and used in turn.  A buffer is
+// reused once its last batch (`user`) has queued its copies and they have run (`free_ev`, recorded
+// after them); it grows to the largest batch it has held.
+struct Bounce {
+    uint8_t* p = nullptr;
+    size_t bytes = 0;
+    hipEvent_t free_ev = nullptr;
+    std::shared_ptr<fileio::Batch> user;
+};
+constexpr int kBounceBufs = 4;
+Bounce g_bounce[kBounceBufs];
+int g_bounce_next = 0;
 std::mutex g_err_mu;
 char g_err[1024] = {0};
 
@@ -110,6 +139,7 @@ bool valid_layer(int l) { return l >= 0 && l < MOE_MAX_LAYERS; }
 
 int ensure_runtime() {
     if (g_ready) return 0;
+    HIP_TRY(hipGetDevice(&g_dev));
     HIP_TRY(hipStreamCreateWithFlags(&g_copy, hipStreamNonBlocking));
     for (int i = 0; i < kCopyStreams - 1; ++i) {
         HIP_TRY(hipStreamCreateWithFlags(&g_copy_more[i], hipStreamNonBlocking));
@@ -147,40 +177,148 @@ int push_table(LayerState& L) {
     return 0;
 }
 
-// Read `n` bytes of a file at `off` fully (short reads retried; errors reported).
-int pread_full(int fd, uint8_t* buf, size_t n, uint64_t off) {
-    while (n > 0) {
-        ssize_t r = pread(fd, buf, n, (off_t)off);
-        if (r <= 0) {
-            moe_set_error("pread(fd=%d, off=%llu) failed or hit end of file", fd, (unsigned long long)off);
-            return -1;
-        }
-        buf += r;
-        n -= (size_t)r;
-        off += (uint64_t)r;
+// Host join of the layer's in-flight file batch: its reads are done and its copies queued.
+int join_file(LayerState& L) {
+    if (!L.fbatch) return 0;
+    std::string msg;
+    const int rc = fileio::wait(L.fbatch, msg);
+    L.fbatch.reset();
+    if (rc) {
+        moe_set_error("expert file read: %s", msg.c_str());
+        return -1;
     }
     return 0;
 }
 
+// Wait until bounce buffer b may be overwritten: its last batch has queued its copies (a failed
+// batch may have queued part of them: the copy stream is drained) and they have run.
+int bounce_idle(Bounce& b) {
+    if (!b.user) return 0;
+    std::string msg;                              // an error is reported by the owning layer's join
+    const bool failed = fileio::wait(b.user, msg) != 0;
+    b.user.reset();
+    if (failed) HIP_TRY(hipStreamSynchronize(g_copy));
+    else HIP_TRY(hipEventSynchronize(b.free_ev));
+    return 0;
+}
+
+// Release the bounce buffers (every layer's batch joined first).
+void release_bounce() {
+    for (Bounce& b : g_bounce) {
+        (void)bounce_idle(b);
+        if (b.p) (void)hipHostFree(b.p);
+        if (b.free_ev) (void)hipEventDestroy(b.free_ev);
+        b = Bounce();
+    }
+}
+
+// Free a layer's file-tier resources (after joining its batch).
+void release_file(LayerState& L) {
+    (void)join_file(L);
+    if (L.fd_direct >= 0) close(L.fd_direct);
+    L.fd_direct = -1;
+}
+
 // Forget the layer's in-flight copies once its last copy event has completed (non-blocking).
 void settle_copies(LayerState& L) {
-    if (!L.inflight) return;
+    if (!L.inflight || L.fbatch) return;             // a file batch records copy_done when it ends
     hipError_t e = hipEventQuery(L.copy_done);
     if (e == hipErrorNotReady) {
         (void)hipGetLastError();
         return;
     }
     L.inflight = false;
-    L.bounce_busy = false;
     memset(L.inflight_slots, 0, sizeof(L.inflight_slots));
 }
 
 // Block the host until every copy queued for the layer has landed.
 int drain_copies(LayerState& L) {
+    if (join_file(L)) return -1;
     if (L.inflight) HIP_TRY(hipEventSynchronize(L.copy_done));
     L.inflight = false;
-    L.bounce_busy = false;
     memset(L.inflight_slots, 0, sizeof(L.inflight_slots));
+    return 0;
+}
+
+// A batch of misses of a file-backed layer: the (eid, slot) pairs sorted by expert id, each run of
+// consecutive ids read as one contiguous range per tensor (expert_io.c:187-276) into a bounce
+// buffer, longest reads first, by the reader threads; the worker finishing the last read queues the
+// copies (one per run of consecutive slots) and records copy_done (and pf_done for a prefetch).
+// With O_DIRECT each read covers the 4 KiB-aligned range around its bytes (through the reader's
+// own staging buffer: see fileio::Read::direct).
+int issue_file_batch(LayerState& L, const int32_t* eids, const int32_t* slots, int n, bool prefetch) {
+    constexpr uint64_t kAlign = 4096;
+    const bool direct = L.fd_direct >= 0;
+    std::vector<int> ord(n);
+    std::iota(ord.begin(), ord.end(), 0);
+    std::sort(ord.begin(), ord.end(), [&](int a, int b) { return eids[a] < eids[b]; });
+    std::vector<std::pair<int, int>> runs;            // (first position in ord, length)
+    for (int i = 0; i < n;) {
+        int r = 1;
+        while (i + r < n && eids[ord[i + r]] == eids[ord[i]] + r) ++r;
+        runs.emplace_back(i, r);
+        i += r;
+    }
+    struct Piece { int t, run; uint64_t boff, skip; };  // a tensor's run in the bounce buffer
+    std::vector<Piece> pieces;
+    std::vector<fileio::Read> reads;
+    uint64_t total = 0;
+    for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
+        const uint64_t rb = L.row_bytes[t];
+        if (!rb || !L.dst[t]) continue;
+        for (size_t q = 0; q < runs.size(); ++q) {
+            const uint64_t off = L.src[t] + (uint64_t)eids[ord[runs[q].first]] * rb, len = (uint64_t)runs[q].second * rb;
+            const uint64_t a = direct ? off & ~(kAlign - 1) : off;
+            const uint64_t end = direct ? (off + len + kAlign - 1) & ~(kAlign - 1) : off + len;
+            pieces.push_back(Piece{t, (int)q, total, off - a});
+            reads.push_back(fileio::Read{direct ? L.fd_direct : L.fd, a, end - a, off - a + len, nullptr, direct});
+            total += (end - a + kAlign - 1) & ~(kAlign - 1);
+        }
+    }
+    Bounce& B = g_bounce[g_bounce_next];
+    g_bounce_next = (g_bounce_next + 1) % kBounceBufs;
+    if (bounce_idle(B)) return -1;
+    if (total > B.bytes) {
+        if (B.p) HIP_TRY(hipHostFree(B.p));
+        B.p = nullptr;
+        B.bytes = 0;
+        HIP_TRY(hipHostMalloc((void**)&B.p, total, hipHostMallocDefault));
+        B.bytes = total;
+    }
+    if (!B.free_ev) HIP_TRY(hipEventCreateWithFlags(&B.free_ev, hipEventDisableTiming));
+    for (size_t i = 0; i < reads.size(); ++i) reads[i].dst = B.p + pieces[i].boff;
+    auto b = std::make_shared<fileio::Batch>();
+    b->reads = std::move(reads);
+    uint8_t* bounce = B.p;
+    hipEvent_t copy_done = L.copy_done, pf_done = L.pf_done, free_ev = B.free_ev;
+    std::vector<std::pair<int32_t, int32_t>> sorted(n);
+    for (int i = 0; i < n; ++i) sorted[i] = {eids[ord[i]], slots[ord[i]]};
+    const std::vector<uint64_t> rbv(L.row_bytes, L.row_bytes + MOE_NUM_TENSORS), dstv(L.dst, L.dst + MOE_NUM_TENSORS);
+    const int dev = g_dev;
+    b->finish = [=]() -> int {
+        if (hipSetDevice(dev) != hipSuccess) return -1;
+        for (const Piece& pc : pieces) {
+            const uint64_t rb = rbv[pc.t];
+            const int first = runs[pc.run].first, len = runs[pc.run].second;
+            for (int i = 0; i < len;) {                 // one copy per run of consecutive slots
+                int r = 1;
+                while (i + r < len && sorted[first + i + r].second == sorted[first + i].second + r) ++r;
+                if (hipMemcpyAsync((void*)(dstv[pc.t] + (uint64_t)sorted[first + i].second * rb),
+                                   bounce + pc.boff + pc.skip + (uint64_t)i * rb, (uint64_t)r * rb,
+                                   hipMemcpyHostToDevice, g_copy) != hipSuccess)
+                    return -1;
+                i += r;
+            }
+        }
+        if (hipEventRecord(copy_done, g_copy) != hipSuccess) return -1;
+        if (hipEventRecord(free_ev, g_copy) != hipSuccess) return -1;
+        if (prefetch && hipEventRecord(pf_done, g_copy) != hipSuccess) return -1;
+        return 0;
+    };
+    B.user = b;
+    L.fbatch = b;
+    L.fbatch_pf = prefetch;
+    fileio::submit(b);
     return 0;
 }
 
@@ -206,36 +344,14 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
     }
     if (ensure_runtime()) return -1;
     if (ensure_events(L)) return -1;
+    if (join_file(L)) return -1;              // a file batch's copies are queued before this batch's waits
     settle_copies(L);
     bool overlap = false;
     if (L.inflight)
         for (int i = 0; i < n && !overlap; ++i) overlap = (L.inflight_slots[slots[i] >> 6] >> (slots[i] & 63)) & 1u;
     if (L.read_recorded) HIP_TRY(hipStreamWaitEvent(g_copy, L.read_done, 0));
     if (L.fd >= 0) {
-        size_t need = (size_t)n * expert_bytes_of(L);
-        if (need > L.bounce_bytes) {
-            HIP_TRY(hipStreamSynchronize(g_copy));
-            if (L.bounce) HIP_TRY(hipHostFree(L.bounce));
-            L.bounce = nullptr;
-            HIP_TRY(hipHostMalloc((void**)&L.bounce, need, hipHostMallocDefault));
-            L.bounce_bytes = need;
-        } else if (L.bounce_busy) {
-            // the bounce buffer is reused: earlier copies out of it must have finished (a GPU-side
-            // join of those copies says nothing about the host buffer they read)
-            if (drain_copies(L)) return -1;
-        }
-        L.bounce_busy = true;
-        size_t off = 0;
-        for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
-            uint64_t rb = L.row_bytes[t];
-            if (!rb || !L.dst[t]) continue;
-            for (int i = 0; i < n; ++i) {
-                if (pread_full(L.fd, L.bounce + off, rb, L.src[t] + (uint64_t)eids[i] * rb)) return -1;
-                HIP_TRY(hipMemcpyAsync((void*)(L.dst[t] + (uint64_t)slots[i] * rb), L.bounce + off, rb,
-                                       hipMemcpyHostToDevice, g_copy));
-                off += rb;
-            }
-        }
+        if (issue_file_batch(L, eids, slots, n, prefetch)) return -1;
     } else {
         for (int i = 0; i < kCopyStreams - 1; ++i) {
             if (L.read_recorded) HIP_TRY(hipStreamWaitEvent(g_copy_more[i], L.read_done, 0));
@@ -263,20 +379,21 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
             HIP_TRY(hipStreamWaitEvent(g_copy, g_copy_more_done[i], 0));
         }
     }
-    HIP_TRY(hipEventRecord(L.copy_done, g_copy));
+    if (L.fd < 0) {
+        HIP_TRY(hipEventRecord(L.copy_done, g_copy));
+        if (prefetch) HIP_TRY(hipEventRecord(L.pf_done, g_copy));
+    }
     L.copy_pending = true;
     L.inflight = true;
     for (int i = 0; i < n; ++i) L.inflight_slots[slots[i] >> 6] |= 1ull << (slots[i] & 63);
-    if (prefetch) {
-        HIP_TRY(hipEventRecord(L.pf_done, g_copy));
-        L.pf_pending = true;
-    }
+    if (prefetch) L.pf_pending = true;
     (void)layer;
     return 0;
 }
 
 int wait_copies_gpu(LayerState& L, hipStream_t s) {
     if (!L.copy_pending) return 0;
+    if (join_file(L)) return -1;
     HIP_TRY(hipStreamWaitEvent(s, L.copy_done, 0));
     L.copy_pending = false;
     L.pf_pending = false;
@@ -393,17 +510,45 @@ int c_host_free(void* p) {
 // ---- expert_io.c entry points ---------------------------------------------------------------
 
 void c_io_init(int num_threads) {
-    // Copies are queued to the DMA engines, not worker threads; the copy stream is created on
-    // first use so that accounting-only tables work without a GPU.
-    (void)num_threads;
+    // Reader threads of file-backed layers (<= 0: 8); copies from host memory are queued to the DMA
+    // engines.  The copy streams are created on first use so that accounting-only tables work
+    // without a GPU.
+    fileio::set_threads(num_threads);
+}
+
+// Read file-backed layers initialised from now on with O_DIRECT (on != 0) or through the page
+// cache (0, the default).  A file system that refuses O_DIRECT leaves the layer on the page cache.
+void c_io_set_direct(int on) { g_direct = on != 0; }
+
+// 1 when the layer reads its file with O_DIRECT.
+int c_layer_io_direct(int layer) { return valid_layer(layer) && g_layers[layer].fd_direct >= 0 ? 1 : 0; }
+
+// Reader threads of the file tier.
+int c_io_threads(void) { return fileio::threads(); }
+
+// Read n ranges of a file into host memory with the reader threads (blocking): range i is
+// lens[i] bytes at offs[i] into the address dsts[i].  Host code only (no GPU needed); used to fill
+// host expert stores from a shard.  0, or -1 on a failed or short read.
+int c_io_read_ranges(int fd, const uint64_t* offs, const uint64_t* lens, const uint64_t* dsts, int n) {
+    if (n < 0 || (n > 0 && (!offs || !lens || !dsts))) { moe_set_error("io_read_ranges: bad arguments"); return -1; }
+    auto b = std::make_shared<fileio::Batch>();
+    for (int i = 0; i < n; ++i)
+        if (lens[i]) b->reads.push_back(fileio::Read{fd, offs[i], lens[i], lens[i], (uint8_t*)dsts[i]});
+    fileio::submit(b);
+    std::string msg;
+    if (fileio::wait(b, msg)) { moe_set_error("io_read_ranges: %s", msg.c_str()); return -1; }
+    return 0;
 }
 
 void c_io_shutdown(void) {
+    for (int l = 0; l < MOE_MAX_LAYERS; ++l) (void)join_file(g_layers[l]);
+    fileio::shutdown();
     if (!g_ready) return;
     (void)hipStreamSynchronize(g_copy);
+    release_bounce();
     for (int l = 0; l < MOE_MAX_LAYERS; ++l) {
         LayerState& L = g_layers[l];
-        if (L.bounce) (void)hipHostFree(L.bounce);
+        release_file(L);
         if (L.dtab) (void)hipFree(L.dtab);
         if (L.copy_done) (void)hipEventDestroy(L.copy_done);
         if (L.read_done) (void)hipEventDestroy(L.read_done);
@@ -452,8 +597,9 @@ void c_layer_init(int layer, int fd, int capacity, const uint64_t* base_offsets,
         return;
     }
     LayerState& L = g_layers[layer];
+    (void)join_file(L);
     if (L.inflight) (void)hipEventSynchronize(L.copy_done);
-    if (L.bounce) (void)hipHostFree(L.bounce);
+    release_file(L);
     if (L.dtab) (void)hipFree(L.dtab);
     hipEvent_t cd = L.copy_done, rd = L.read_done, pd = L.pf_done;
     uint8_t* sd = L.split_dev;
@@ -468,6 +614,11 @@ void c_layer_init(int layer, int fd, int capacity, const uint64_t* base_offsets,
         g_cur_token = -1;
     }
     L.fd = fd;
+    if (fd >= 0 && g_direct) {                // a second descriptor of the same file, page cache bypassed
+        char path[64];
+        snprintf(path, sizeof(path), "/proc/self/fd/%d", fd);
+        L.fd_direct = open(path, O_RDONLY | O_DIRECT | O_CLOEXEC);
+    }
     L.capacity = capacity;
     for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
         L.src[t] = base_offsets ? base_offsets[t] : 0;
@@ -699,8 +850,8 @@ uint64_t c_get_native_buffer_bytes(void) {
     uint64_t b = sizeof(g_layers) + sizeof(g_split);
     for (int l = 0; l < MOE_MAX_LAYERS; ++l) {
         if (g_layers[l].dtab) b += sizeof(SlotTable);
-        b += g_layers[l].bounce_bytes;
     }
+    for (const Bounce& bb : g_bounce) b += bb.bytes;
     return b;
 }
 
@@ -1061,6 +1212,7 @@ int c_layer_switch_glu_split(int layer, int part, const void* x, const void* sco
     __half* dscores = reinterpret_cast<__half*>(L.split_dev + 128);
     int rc;
     if (part == 0) {
+        if (L.pf_pending && L.fbatch && L.fbatch_pf && join_file(L)) return -1;
         if (L.pf_pending) HIP_TRY(hipStreamWaitEvent(s, L.pf_done, 0));
         if (launch_split_lists(S, (const __half*)scores, dslots, dscores, s)) return -1;
         rc = layer_glu(L, x, dslots, dscores, S.n_hit, residual, h_ws, y_out, 0, s);
@@ -1175,6 +1327,8 @@ int c_layer_mark_read(int layer, void* stream) {
 
 // Host-blocking join of every copy queued so far.
 int c_sync_copies(void) {
+    for (int l = 0; l < MOE_MAX_LAYERS; ++l)
+        if (join_file(g_layers[l])) return -1;
     if (!g_ready) return 0;
     HIP_TRY(hipStreamSynchronize(g_copy));
     return 0;

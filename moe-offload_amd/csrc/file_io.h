@@ -1,0 +1,56 @@
+// Reads of the on-disk expert tier: a pool of reader threads (host code).
+//
+// The reference reads its experts-XX.safetensors shard with a pthread pool and one preadv per
+// (tensor, run of consecutive experts), longest reads first (mlx-qwen38/expert_io.c:95-276); a
+// batch runs in the background and every later entry point joins it first (:312-356).  Here a
+// batch is a list of contiguous reads into pinned host memory plus a `finish` step that runs on
+// the worker completing the batch's last read (it queues the host-to-device copies); `wait` is the
+// join.
+#pragma once
+#include <stdint.h>
+
+#include <atomic>
+#include <condition_variable>
+#include <functional>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace fileio {
+
+struct Read {
+    int fd;
+    uint64_t off;        // file offset
+    uint64_t len;        // bytes to read (len >= need; the tail may lie past the end of the file)
+    uint64_t need;       // bytes that must be read
+    uint8_t* dst;
+    // fd was opened with O_DIRECT (off and len 4 KiB multiples): the kernel cannot read straight
+    // into pinned GPU-visible host memory (its pages cannot be pinned again: EFAULT), so the read
+    // goes through the worker's own aligned buffer, 8 MiB at a time, and is copied to dst.
+    bool direct = false;
+};
+
+struct Batch {
+    std::vector<Read> reads;
+    std::function<int()> finish;          // 0 or -1 (then `error` says why)
+    std::atomic<int> left{0};
+    std::mutex mu;
+    std::condition_variable cv;
+    bool done = false;
+    bool failed = false;
+    std::string error;
+};
+
+// Reader threads (<= 0: 8, the reference's default, loader.py:219-223); takes effect for later
+// batches (the pool drains first).
+void set_threads(int n);
+int threads();
+// Start the batch's reads (largest first); returns at once.
+void submit(const std::shared_ptr<Batch>& b);
+// Block until the batch's reads and its finish step are done; 0, or -1 with the error in `msg`.
+int wait(const std::shared_ptr<Batch>& b, std::string& msg);
+// Stop the reader threads (after the queued work).
+void shutdown();
+
+}  // namespace fileio

@@ -24,6 +24,10 @@ SIGNATURES: dict[str, tuple] = {
     # expert_io.c entry points
     "c_io_init": (None, [_c_int]),
     "c_io_shutdown": (None, []),
+    "c_io_set_direct": (None, [_c_int]),
+    "c_layer_io_direct": (_c_int, [_c_int]),
+    "c_io_threads": (_c_int, []),
+    "c_io_read_ranges": (_c_int, [_c_int, _u64p, _u64p, _u64p, _c_int]),
     "c_layer_init": (None, [_c_int, _c_int, _c_int, _u64p, _u64p, _u64p, _c_u64]),
     "c_layer_reset_cache": (None, [_c_int]),
     "c_layer_reset_stats": (None, [_c_int]),

@@ -4,9 +4,10 @@ Names, arguments and return values follow the reference:
   compute_layer_capacities  loader.py:245-303
   CachedSwitchGLU           loader.py:306-749   (per-layer slot cache + SwitchGLU)
   OffloadEngine             loader.py:1004-1343 (capacities, stats, greedy decode loop)
-Storage differs by design: the slot pool is HBM (a torch uint8 tensor of Q2 blobs) and the
-"SSD" tier is a pinned host expert store (HostExpertStore) or, for file-backed layers, a
-file read through the library's pinned bounce buffers.  The cache decisions, counters and
+Storage differs by design: the slot pool is HBM and the "SSD" tier is a pinned host expert
+store (HostExpertStore), a blob file per layer (FileExpertStore) or the reference's own
+experts-XX.safetensors shards read in place (ShardExpertStore: the 9 tensors of each layer, 9
+HBM slot pools); file-backed layers are read by the library's reader threads.  The cache decisions, counters and
 slot ids come from libmoe_offload.so (the expert_io.c ABI); the compute is its HIP kernels.
 """
 from __future__ import annotations
@@ -133,38 +134,139 @@ class FileExpertStore:
         self.fds.clear()
 
 
+def read_safetensors_header(fd: int) -> tuple[dict, int]:
+    """(header, data_start) of a safetensors file: an 8-byte little-endian header length, the JSON
+    header, then the data (loader.py:318-320 reads it the same way)."""
+    import os
+    import struct
+    n = struct.unpack("<Q", os.pread(fd, 8, 0))[0]
+    if n > (1 << 28):
+        raise ValueError(f"safetensors header of {n} bytes")
+    raw = os.pread(fd, n, 8)
+    if len(raw) != n:
+        raise ValueError("truncated safetensors header")
+    return json.loads(raw), 8 + n
+
+
+SHARD_ROLES = [(proj, suffix) for proj in ("gate_proj", "up_proj", "down_proj")
+               for suffix in ("weight", "scales", "biases")]
+
+
+class ShardExpertStore:
+    """The reference's on-disk tier read in place: layer l's experts live in
+    `experts-{l:02d}.safetensors` as 9 tensors `language_model.model.layers.{l}.mlp.switch_mlp.
+    {gate,up,down}_proj.{weight,scales,biases}` (U32 codes [E, out, in/16]; BF16 or F16 scales and
+    biases [E, out, in/group]).  Per layer the 9 (file offset, bytes per expert) pairs are listed in
+    ascending file offset, as loader.py:336-395 hands them to c_layer_init, with each tensor's role
+    (MOE_Q2T_* order: gate w/s/b, up w/s/b, down w/s/b) for c_layer_set_format9."""
+
+    def __init__(self, shards: "dict[int, str] | str | Path", layers=None):
+        import os
+        if not isinstance(shards, dict):
+            root = Path(shards)
+            shards = {l: str(root / f"experts-{l:02d}.safetensors") for l in (layers or range(1, NUM_LAYERS))}
+        self.paths = dict(shards)
+        self.fds: dict[int, int] = {}
+        self.layout: dict[int, dict] = {}
+        try:
+            for l, path in self.paths.items():
+                fd = os.open(path, os.O_RDONLY)
+                self.fds[l] = fd
+                self.layout[l] = self._layer_layout(fd, l, os.fstat(fd).st_size)
+        except Exception:
+            self.close()
+            raise
+        dims = {(v["n_exp"], v["hidden"], v["inter"], v["group"]) for v in self.layout.values()}
+        if len(dims) != 1:
+            raise ValueError(f"shards disagree on (experts, hidden, inter, group): {sorted(dims)}")
+        self.n_exp, self.hidden, self.inter, self.group = dims.pop()
+        self.blob_bytes = sum(next(iter(self.layout.values()))["row_bytes"])
+
+    @staticmethod
+    def _layer_layout(fd: int, layer: int, file_size: int) -> dict:
+        hdr, data_start = read_safetensors_header(fd)
+        pre = f"language_model.model.layers.{layer}.mlp.switch_mlp"
+        specs, sdt = [], set()
+        for role, (proj, suffix) in enumerate(SHARD_ROLES):
+            name = f"{pre}.{proj}.{suffix}"
+            if name not in hdr:
+                raise KeyError(f"{name} missing from the layer {layer} shard")
+            info = hdr[name]
+            shape, (a, b) = info["shape"], info["data_offsets"]
+            want = "U32" if suffix == "weight" else ("BF16", "F16")
+            if info["dtype"] not in (want if isinstance(want, tuple) else (want,)) or len(shape) != 3:
+                raise ValueError(f"{name}: dtype {info['dtype']} shape {shape}")
+            if suffix != "weight":
+                sdt.add(info["dtype"])
+            if (b - a) % shape[0] or data_start + b > file_size:
+                raise ValueError(f"{name}: data range {a}..{b} does not fit the file")
+            specs.append((data_start + a, (b - a) // shape[0], role, tuple(shape)))
+        if len(sdt) != 1:
+            raise ValueError(f"layer {layer}: mixed scale dtypes {sorted(sdt)}")
+        gw = specs[0][3]
+        n_exp, inter, hidden = gw[0], gw[1], gw[2] * 16
+        group = hidden // specs[1][3][2]
+        specs.sort(key=lambda t: t[0])                 # ascending file offset (loader.py:395)
+        return {"offsets": [t[0] for t in specs], "row_bytes": [t[1] for t in specs],
+                "roles": [t[2] for t in specs], "scale_bf16": sdt.pop() == "BF16",
+                "n_exp": n_exp, "hidden": hidden, "inter": inter, "group": group}
+
+    def close(self):
+        import os
+        for fd in self.fds.values():
+            os.close(fd)
+        self.fds.clear()
+
+
 class CachedSwitchGLU:
     """Per-layer slot cache over an HBM pool + Q2 SwitchGLU (loader.py:306-749).
 
-    `store` is a HostExpertStore (pinned host memory, fd == -1) or a FileExpertStore (the on-disk
-    tier, fd >= 0); the pool holds `capacity` blobs.
+    `store` is a HostExpertStore (pinned host memory, fd == -1), a FileExpertStore (a blob file,
+    fd >= 0; the pool holds `capacity` blobs) or a ShardExpertStore (the reference's shard read in
+    place, fd >= 0; `pools` are the 9 tensors' slot pools, each [capacity, bytes per expert], as
+    loader.py:336-366 allocates them, and hidden/inter/group come from the shard).
     decode: __call__(x [1,1,H] fp16, indices [1,1,k]) -> per-expert outputs [1,1,k,H], exactly
     like SwitchGLU; forward_combined() returns the score-weighted sum directly.
     """
 
-    def __init__(self, store: "HostExpertStore | FileExpertStore", layer_idx: int, capacity: int, hidden: int = 2048,
-                 inter: int = 512, group: int = 64, device: str | torch.device = "cuda"):
+    def __init__(self, store: "HostExpertStore | FileExpertStore | ShardExpertStore", layer_idx: int, capacity: int,
+                 hidden: int = 2048, inter: int = 512, group: int = 64, device: str | torch.device = "cuda"):
+        shard = isinstance(store, ShardExpertStore)
+        if shard:
+            hidden, inter, group = store.hidden, store.inter, store.group
         self.layer_idx, self.capacity = layer_idx, capacity
         self.hidden, self.inter, self.group = hidden, inter, group
         self.store = store
-        self.blob_bytes = q2format.expert_bytes(hidden, inter, group)
-        assert store.blob_bytes == self.blob_bytes
         dev = torch.device(device)
-        self.pool = torch.zeros((capacity, self.blob_bytes), dtype=torch.uint8, device=dev)
-        self._slot_inds_buf = torch.zeros(MAX_K, dtype=torch.int32, device=dev)
-        self._h_ws = torch.zeros(MAX_K * inter, dtype=torch.float16, device=dev)
+        u64 = ctypes.c_uint64 * 9
         L = _lib.lib()
         L.c_set_compute_stream(ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
-        u64 = ctypes.c_uint64 * 9
-        if isinstance(store, FileExpertStore):
-            fd, base = store.fds[layer_idx], store.headers[layer_idx]["data_offset"]
+        self._slot_inds_buf = torch.zeros(MAX_K, dtype=torch.int32, device=dev)
+        self._h_ws = torch.zeros(MAX_K * inter, dtype=torch.float16, device=dev)
+        if shard:
+            lay = store.layout[layer_idx]
+            self.blob_bytes = sum(lay["row_bytes"])
+            self.pool = None
+            self.pools = [torch.zeros((capacity, rb), dtype=torch.uint8, device=dev) for rb in lay["row_bytes"]]
+            L.c_layer_init(layer_idx, store.fds[layer_idx], capacity, u64(*lay["offsets"]), u64(*lay["row_bytes"]),
+                           u64(*[p.data_ptr() for p in self.pools]), self._slot_inds_buf.data_ptr())
+            _lib.check_error("c_layer_init")
+            _lib.check(L.c_layer_set_format9(layer_idx, hidden, inter, group, (ctypes.c_int32 * 9)(*lay["roles"]),
+                                             int(lay["scale_bf16"])), "c_layer_set_format9")
         else:
-            fd, base = -1, store.layer_ptr(layer_idx)
-        L.c_layer_init(layer_idx, fd, capacity, u64(base, *[0] * 8),
-                       u64(self.blob_bytes, *[0] * 8), u64(self.pool.data_ptr(), *[0] * 8),
-                       self._slot_inds_buf.data_ptr())
-        _lib.check_error("c_layer_init")
-        _lib.check(L.c_layer_set_format(layer_idx, hidden, inter, group), "c_layer_set_format")
+            self.blob_bytes = q2format.expert_bytes(hidden, inter, group)
+            assert store.blob_bytes == self.blob_bytes
+            self.pool = torch.zeros((capacity, self.blob_bytes), dtype=torch.uint8, device=dev)
+            self.pools = [self.pool]
+            if isinstance(store, FileExpertStore):
+                fd, base = store.fds[layer_idx], store.headers[layer_idx]["data_offset"]
+            else:
+                fd, base = -1, store.layer_ptr(layer_idx)
+            L.c_layer_init(layer_idx, fd, capacity, u64(base, *[0] * 8),
+                           u64(self.blob_bytes, *[0] * 8), u64(self.pool.data_ptr(), *[0] * 8),
+                           self._slot_inds_buf.data_ptr())
+            _lib.check_error("c_layer_init")
+            _lib.check(L.c_layer_set_format(layer_idx, hidden, inter, group), "c_layer_set_format")
         self._c_stats_buf = (ctypes.c_uint64 * 18)()
         self.reset_stats()
 
@@ -229,6 +331,9 @@ class CachedSwitchGLU:
                                                out.data_ptr(), 1, K, torch.cuda.current_stream().cuda_stream)
             _lib.check(rc, "c_layer_switch_glu")
             return out.to(x.dtype).reshape(1, 1, K, self.hidden)
+        if self.pool is None:
+            raise NotImplementedError("prefill over a layer bound to the shard's 9 tensors: the grouped kernels "
+                                      "read the blob layout (FileExpertStore / HostExpertStore)")
         from .prefill import cached_prefill
         return cached_prefill(self, x, indices)
 

@@ -53,3 +53,33 @@ def experts_bf16(n_exp, hidden, inter, seed=1, scale_std=0.02):
         return w, s, b
 
     return proj(inter, hidden), proj(inter, hidden), proj(hidden, inter)
+
+
+ROLE_NAMES = [(p, s) for p in ("gate_proj", "up_proj", "down_proj") for s in ("weight", "scales", "biases")]
+
+
+def role_arrays(mlx):
+    """The 9 tensors of MLX-layout experts in role order, each as uint8 [E, bytes per expert]."""
+    out = []
+    for w, s, b in mlx:
+        n = w.shape[0]
+        out += [np.ascontiguousarray(a).view(np.uint8).reshape(n, -1) for a in (w, s, b)]
+    return out
+
+
+def write_reference_shard(path, layer, mlx, scale_dtype="bf16"):
+    """An experts-XX.safetensors shard in the reference checkpoint's form (U32 codes; BF16 or F16
+    scales and biases, given as their 16-bit patterns), written by the safetensors library."""
+    import torch
+    from safetensors.torch import save_file
+    half = torch.bfloat16 if scale_dtype == "bf16" else torch.float16
+    pre = f"language_model.model.layers.{layer}.mlp.switch_mlp"
+    tensors = {}
+    for (proj, suffix), a in zip(ROLE_NAMES, [t for p in mlx for t in p]):
+        a = np.ascontiguousarray(a)
+        if suffix == "weight":
+            tensors[f"{pre}.{proj}.{suffix}"] = torch.from_numpy(a.view(np.int32)).view(torch.uint32)
+        else:
+            tensors[f"{pre}.{proj}.{suffix}"] = torch.from_numpy(a.view(np.int16)).view(half)
+    save_file(tensors, str(path))
+    return path

@@ -1,17 +1,20 @@
-"""On-disk tier on the GPU: a cached layer whose misses are read from an expert blob file with
-pread into a pinned bounce buffer and copied to the HBM slot pool (the reference reads its shard
-the same way, `mlx-qwen38/expert_io.c:113-185`).
+"""On-disk tier on the GPU: cached layers whose misses are read from a file by the reader threads
+(one read per tensor and run of consecutive experts, into pinned bounce buffers) and copied to the
+HBM slot pools (the reference reads its shard the same way, `mlx-qwen38/expert_io.c:113-276`).
 
-40 decode steps (capacity 16 over 64 experts) then an 8-token prefill: slot decisions and
-counters match the oracle LRU, every slot holds the expert the table names, outputs match the
-fp64 oracle within 1e-2 x RMS.
+Blob file: 40 decode steps (capacity 16 over 64 experts) then an 8-token prefill.  Reference
+shard read in place (9 tensors, bf16 scales, hidden 2560 / inter 640): decode steps with
+prefetches, 1 and 8 reader threads, page cache and O_DIRECT.  Slot decisions and counters match
+the oracle LRU, every slot holds the expert the table names, outputs match the fp64 oracle within
+1e-2 x RMS.
 """
 import ctypes
 
 import numpy as np
 import pytest
 
-from helpers import H, I, K, assert_close_rms, expert_fn, experts_np, oracle_moe
+from helpers import (H, I, K, assert_close_rms, expert_fn, experts_bf16, experts_np, oracle_moe, role_arrays,
+                     write_reference_shard)
 from oracle import lru as olru
 from oracle import q2
 
@@ -82,4 +85,63 @@ def test_file_backed_layer(tmp_path):
         assert _lib.last_error() == ""
     finally:
         mod.close()
+        store.close()
+
+
+@pytest.mark.parametrize("threads,direct", [(1, 0), (8, 0), (8, 1)])
+def test_reference_shard_read_in_place(tmp_path, threads, direct):
+    from moe_offload import _lib
+    from moe_offload.loader import CachedSwitchGLU, ShardExpertStore
+    Hs, Is, Es, cap, layer = 2560, 640, 40, 12, 35
+    print(f"shard in place: threads={threads} direct={direct}", flush=True)
+    mlx = experts_bf16(Es, Hs, Is, seed=31)
+    write_reference_shard(tmp_path / f"experts-{layer:02d}.safetensors", layer, mlx)
+    want_rows = role_arrays(mlx)
+    dev = torch.device("cuda:0")
+    L = _lib.lib()
+    L.c_io_init(threads)
+    L.c_io_set_direct(direct)
+    store = ShardExpertStore(tmp_path, layers=[layer])
+    mod = None
+    try:
+        mod = CachedSwitchGLU(store, layer, cap)
+        assert (mod.hidden, mod.inter) == (Hs, Is)
+        assert L.c_io_threads() == threads
+        print(f"O_DIRECT in use: {L.c_layer_io_direct(layer)}", flush=True)
+        if not direct:
+            assert L.c_layer_io_direct(layer) == 0
+        lay = store.layout[layer]
+        ora = olru.CLru(layer, cap, expert_bytes=mod.blob_bytes)
+        ora.reset_stats()
+        rng = np.random.default_rng(32)
+        f = lambda e: tuple((p[0][e], p[1][e], p[2][e]) for p in mlx)
+        for t in range(16):
+            ids = [int(v) for v in rng.choice(Es, K, replace=False)]
+            x = rng.standard_normal(Hs).astype(np.float16)
+            sc = rng.dirichlet(np.ones(K)).astype(np.float16)
+            out = mod.forward_combined(torch.from_numpy(x).to(dev), ids, torch.from_numpy(sc).to(dev))
+            slots, _ = ora.step(ids)
+            assert mod._slot_inds_buf[:K].cpu().tolist() == slots, t
+            if t in (0, 9, 15):
+                want = q2.moe_combine(x.astype(np.float64), np.array(ids), sc.astype(np.float64), f, bits=2, group=64,
+                                      sdtype="bf16")
+                assert_close_rms(out.cpu().numpy(), want, 1e-2, f"step {t}")
+            if t % 3 == 1:                       # prefetch 3 of 12 predicted experts for the next step
+                pred = [int(v) for v in rng.choice(Es, 12, replace=False)]
+                mod.start_prefetch(pred, 3)
+                ora.prefetch(pred, 3)
+        mod.wait_prefetch()
+        torch.cuda.synchronize()
+        L.c_sync_copies()
+        mod.sync_stats_from_c()
+        assert [int(v) for v in mod._c_stats_buf] == ora.stats()
+        for e, sl in zip(*ora.get_state()):
+            for t, r in enumerate(lay["roles"]):
+                assert np.array_equal(mod.pools[t][sl].cpu().numpy(), want_rows[r][e]), (e, sl, t)
+        assert _lib.last_error() == ""
+    finally:
+        if mod is not None:
+            mod.close()
+        L.c_io_set_direct(0)
+        L.c_io_init(8)
         store.close()
