@@ -52,11 +52,13 @@ def parse():
     ap.add_argument("--pf-stage-ctas", type=int, default=3,
                     help="staging blocks per prefetched expert (0: --stage-ctas)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill grouped-GEMM pass")
+    ap.add_argument("--no-file-tier", action="store_true", help="skip the on-disk tier pass")
+    ap.add_argument("--io-threads", type=int, default=8, help="reader threads of the on-disk tier pass")
     ap.add_argument("--sched", action="store_true",
                     help="the C++ runner's scheduler variant of the expert cache (c_layer_decode_step_sched)")
     ap.add_argument("--split", action="store_true", help="with --sched --mode host: hit experts before misses land")
     ap.add_argument("--nemo-layers", type=int, default=40, help="layers of the codebook (Nemotron-style) workload")
-    ap.add_argument("--only", choices=["headline", "resident", "roofline", "prefill", "calib", "floor", "nemotron"], default=None,
+    ap.add_argument("--only", choices=["headline", "resident", "roofline", "prefill", "calib", "floor", "nemotron", "filetier"], default=None,
                     help="run one pass and print its own JSON line (for sweeps and profiling); "
                          "calib runs the known-size copy kernel used to scale memory counters")
     return ap.parse_args()
@@ -376,6 +378,55 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
     return res
 
 
+def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8):
+    """The decode stack with the on-disk tier: every cached layer reads its misses from one blob
+    file of 512 experts (q2format.write_blob_file, 503 MB, shared by the 47 cached layers) with the
+    reader threads, host-driven tables (one device->host read of ids per layer).  Timed through
+    the page cache (the file is cached after the warm-up) and with O_DIRECT (every read goes to the
+    device), beside the same host driver over the pinned host store."""
+    import shutil
+    import tempfile
+
+    import torch
+
+    from moe_offload import _lib, q2format
+    from moe_offload.stack import DecodeStack, StackConfig, random_blobs
+    base = StackConfig(n_layers=n_layers)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4321)
+    d = tempfile.mkdtemp(prefix="moe_file_tier_")
+    out = {"workload": f"{n_layers}-layer decode as the headline, misses read by {threads} reader threads from one "
+                       f"512-expert blob file shared by the cached layers, host-driven tables, {steps} tokens",
+           "threads": threads}
+    try:
+        path = os.path.join(d, "experts.q2blob")
+        blobs = random_blobs(base.n_exp, base.hidden, base.inter, base.group, gen, "cuda").cpu().numpy()
+        q2format.write_blob_file(path, blobs, base.hidden, base.inter)
+        del blobs
+        xs = torch.randn((warmup + steps, base.hidden), device="cuda", generator=gen).half()
+        for name, kw in (("host_store", {}), ("page_cache", {"store_file": path}),
+                         ("o_direct", {"store_file": path, "io_direct": True})):
+            cfg = StackConfig(n_layers=n_layers, io_threads=threads, **kw)
+            st = DecodeStack(cfg, mode="host")
+            try:
+                direct = bool(_lib.lib().c_layer_io_direct(st.cidx(1))) if kw else None
+                elapsed, tot0, tot1 = timed_tokens(st, xs, warmup, steps, False)
+                _lib.check_error("file tier decode")
+                read = (tot1[4] - tot0[4]) + (tot1[5] - tot0[5])
+                out[name] = {"tok_s": round(steps / elapsed, 2), "ms_per_token": round(elapsed / steps * 1e3, 3),
+                             "read_mb_per_token": round(read / steps / 1e6, 2),
+                             "read_gb_s": round(read / elapsed / 1e9, 2)}
+                if direct is not None:
+                    out[name]["o_direct_in_use"] = direct
+            finally:
+                st.close()
+                del st
+                torch.cuda.empty_cache()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return out
+
+
 def launch_floor(byte_counts, grids=(320, 640, 1280, 2560), reps=50):
     """Shortest kernel that only streams B bytes from HBM: moe_calibrate_stream launched `reps`
     times back to back (a fresh offset of a 512 MiB region each launch, so the reads miss the
@@ -575,6 +626,9 @@ def main():
         print(json.dumps({"nemotron": nemotron_pass(min(args.steps, 64), min(args.warmup, 8), args.nemo_layers)}),
               flush=True)
         return
+    if args.only == "filetier":
+        print(json.dumps({"file_tier": file_tier_pass(args.layers, threads=args.io_threads)}), flush=True)
+        return
     if args.only == "floor":
         fl = launch_floor([3_276_800, 6_553_600, 9_830_400, 64 << 20])
         print(json.dumps({"launch_floor_us": {str(k): round(v, 2) for k, v in fl.items()}}), flush=True)
@@ -689,6 +743,8 @@ def main():
                           "routed_bytes_per_token": routed}
     if not args.no_prefill:
         line["prefill"] = prefill_pass()
+    if not args.no_file_tier:
+        line["file_tier"] = file_tier_pass(args.layers, threads=args.io_threads)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_sample_s)
     print(json.dumps(line), flush=True)

@@ -11,8 +11,8 @@
 //              for overlap and for device-driven staging.
 //   fd >= 0  : base_offsets[t] are file offsets, as in the reference; a batch of misses is read
 //              by the reader-thread pool (file_io.h) as one read per (tensor, run of consecutive
-//              experts) into one of four shared pinned bounce buffers, and the worker finishing the batch queues
-//              the copies to the slots; the batch is joined where its copies are needed
+//              experts) into a shared pinned bounce buffer, each read's copies to the slots are
+//              queued as soon as it lands, and the batch is joined where its slots are needed
 //              (host-driven staging only).
 //   base_ptrs[t] : device address of tensor t's slot pool (slot s at + s * row_bytes[t]).
 //   A tensor with row_bytes > 0 but a zero source or destination is accounting-only.
@@ -74,8 +74,9 @@ struct LayerState {
     Q2Experts E9 = {};
     // File-backed stores: the in-flight batch of reads, and an O_DIRECT descriptor of the same
     // file when direct reads are on (-1 otherwise).
-    std::shared_ptr<fileio::Batch> fbatch;
-    bool fbatch_pf = false;                   // the in-flight batch is a prefetch (records pf_done)
+    // fbatch: the layer's latest batch (each batch is queued after the one before it, so this one
+    // being done means all are); fpf: its latest prefetch batch (records pf_done) until joined.
+    std::shared_ptr<fileio::Batch> fbatch, fpf;
     int fd_direct = -1;
     // Prefetch copies (c_layer_start_prefetch, the scheduler's next-layer prefetch) also record
     // pf_done, so work on the step's hit slots can wait for them alone (split GLU).
@@ -129,7 +130,7 @@ struct Bounce {
     hipEvent_t free_ev = nullptr;
     std::shared_ptr<fileio::Batch> user;
 };
-constexpr int kBounceBufs = 4;
+constexpr int kBounceBufs = 8;
 Bounce g_bounce[kBounceBufs];
 int g_bounce_next = 0;
 std::mutex g_err_mu;
@@ -183,6 +184,20 @@ int join_file(LayerState& L) {
     std::string msg;
     const int rc = fileio::wait(L.fbatch, msg);
     L.fbatch.reset();
+    L.fpf.reset();
+    if (rc) {
+        moe_set_error("expert file read: %s", msg.c_str());
+        return -1;
+    }
+    return 0;
+}
+
+// Host join of the layer's latest prefetch batch only (pf_done recorded).
+int join_prefetch_file(LayerState& L) {
+    if (!L.fpf) return 0;
+    std::string msg;
+    const int rc = fileio::wait(L.fpf, msg);
+    L.fpf.reset();
     if (rc) {
         moe_set_error("expert file read: %s", msg.c_str());
         return -1;
@@ -221,7 +236,11 @@ void release_file(LayerState& L) {
 
 // Forget the layer's in-flight copies once its last copy event has completed (non-blocking).
 void settle_copies(LayerState& L) {
-    if (!L.inflight || L.fbatch) return;             // a file batch records copy_done when it ends
+    if (!L.inflight) return;
+    if (L.fbatch) {                                  // a file batch records copy_done when it ends
+        std::lock_guard<std::mutex> g(L.fbatch->mu);
+        if (!L.fbatch->done) return;
+    }
     hipError_t e = hipEventQuery(L.copy_done);
     if (e == hipErrorNotReady) {
         (void)hipGetLastError();
@@ -242,8 +261,11 @@ int drain_copies(LayerState& L) {
 
 // A batch of misses of a file-backed layer: the (eid, slot) pairs sorted by expert id, each run of
 // consecutive ids read as one contiguous range per tensor (expert_io.c:187-276) into a bounce
-// buffer, longest reads first, by the reader threads; the worker finishing the last read queues the
-// copies (one per run of consecutive slots) and records copy_done (and pf_done for a prefetch).
+// buffer, longest reads first, by the reader threads.  The worker that completes a read queues its
+// copies (one per run of consecutive slots) at once, so the copy engine works while the other
+// reads run; the batch is queued after the layer's previous one (its copies go first: a demand
+// miss may take a slot an in-flight prefetch is filling), and the worker completing the batch
+// records copy_done (and pf_done for a prefetch).
 // With O_DIRECT each read covers the 4 KiB-aligned range around its bytes (through the reader's
 // own staging buffer: see fileio::Read::direct).
 int issue_file_batch(LayerState& L, const int32_t* eids, const int32_t* slots, int n, bool prefetch) {
@@ -295,29 +317,34 @@ int issue_file_batch(LayerState& L, const int32_t* eids, const int32_t* slots, i
     for (int i = 0; i < n; ++i) sorted[i] = {eids[ord[i]], slots[ord[i]]};
     const std::vector<uint64_t> rbv(L.row_bytes, L.row_bytes + MOE_NUM_TENSORS), dstv(L.dst, L.dst + MOE_NUM_TENSORS);
     const int dev = g_dev;
+    for (size_t i = 0; i < b->reads.size(); ++i) b->reads[i].tag = (int)i;   // tag = piece index
+    b->on_read = [=](int tag) -> int {
+        if (hipSetDevice(dev) != hipSuccess) return -1;
+        const Piece& pc = pieces[tag];
+        const uint64_t rb = rbv[pc.t];
+        const int first = runs[pc.run].first, len = runs[pc.run].second;
+        for (int i = 0; i < len;) {                     // one copy per run of consecutive slots
+            int r = 1;
+            while (i + r < len && sorted[first + i + r].second == sorted[first + i].second + r) ++r;
+            if (hipMemcpyAsync((void*)(dstv[pc.t] + (uint64_t)sorted[first + i].second * rb),
+                               bounce + pc.boff + pc.skip + (uint64_t)i * rb, (uint64_t)r * rb,
+                               hipMemcpyHostToDevice, g_copy) != hipSuccess)
+                return -1;
+            i += r;
+        }
+        return 0;
+    };
     b->finish = [=]() -> int {
         if (hipSetDevice(dev) != hipSuccess) return -1;
-        for (const Piece& pc : pieces) {
-            const uint64_t rb = rbv[pc.t];
-            const int first = runs[pc.run].first, len = runs[pc.run].second;
-            for (int i = 0; i < len;) {                 // one copy per run of consecutive slots
-                int r = 1;
-                while (i + r < len && sorted[first + i + r].second == sorted[first + i].second + r) ++r;
-                if (hipMemcpyAsync((void*)(dstv[pc.t] + (uint64_t)sorted[first + i].second * rb),
-                                   bounce + pc.boff + pc.skip + (uint64_t)i * rb, (uint64_t)r * rb,
-                                   hipMemcpyHostToDevice, g_copy) != hipSuccess)
-                    return -1;
-                i += r;
-            }
-        }
         if (hipEventRecord(copy_done, g_copy) != hipSuccess) return -1;
         if (hipEventRecord(free_ev, g_copy) != hipSuccess) return -1;
         if (prefetch && hipEventRecord(pf_done, g_copy) != hipSuccess) return -1;
         return 0;
     };
     B.user = b;
+    b->after = L.fbatch;
     L.fbatch = b;
-    L.fbatch_pf = prefetch;
+    if (prefetch) L.fpf = b;
     fileio::submit(b);
     return 0;
 }
@@ -344,7 +371,6 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
     }
     if (ensure_runtime()) return -1;
     if (ensure_events(L)) return -1;
-    if (join_file(L)) return -1;              // a file batch's copies are queued before this batch's waits
     settle_copies(L);
     bool overlap = false;
     if (L.inflight)
@@ -1212,7 +1238,7 @@ int c_layer_switch_glu_split(int layer, int part, const void* x, const void* sco
     __half* dscores = reinterpret_cast<__half*>(L.split_dev + 128);
     int rc;
     if (part == 0) {
-        if (L.pf_pending && L.fbatch && L.fbatch_pf && join_file(L)) return -1;
+        if (L.pf_pending && join_prefetch_file(L)) return -1;
         if (L.pf_pending) HIP_TRY(hipStreamWaitEvent(s, L.pf_done, 0));
         if (launch_split_lists(S, (const __half*)scores, dslots, dscores, s)) return -1;
         rc = layer_glu(L, x, dslots, dscores, S.n_hit, residual, h_ws, y_out, 0, s);

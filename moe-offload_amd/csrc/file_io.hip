@@ -35,14 +35,32 @@ Pool& P() {
     return *p;
 }
 
-void complete(Batch& b) {
-    int rc = 0;
-    if (!b.failed && b.finish) rc = b.finish();
+void fail(Batch& b, const std::string& why) {
     std::lock_guard<std::mutex> g(b.mu);
-    if (rc && !b.failed) {
+    if (!b.failed) {
         b.failed = true;
-        if (b.error.empty()) b.error = "copy issue failed";
+        b.error = why;
     }
+}
+
+bool failed(Batch& b) {
+    std::lock_guard<std::mutex> g(b.mu);
+    return b.failed;
+}
+
+// Wait for the batch this one is queued after; its failure becomes this batch's.
+void wait_after(Batch& b) {
+    if (!b.after) return;
+    std::string msg;
+    if (wait(b.after, msg)) fail(b, "an earlier batch of the layer failed: " + msg);
+}
+
+void complete(Batch& b) {
+    wait_after(b);
+    b.after.reset();                                  // every on_read step has run: nothing else reads it
+    const int rc = (!failed(b) && b.finish) ? b.finish() : 0;
+    if (rc) fail(b, "copy issue failed");
+    std::lock_guard<std::mutex> g(b.mu);
     b.done = true;
     b.cv.notify_all();
 }
@@ -104,8 +122,14 @@ void worker() {
             it = std::move(p.queue.front());
             p.queue.pop_front();
         }
-        do_read(*it.batch, it.batch->reads[it.idx]);
-        if (it.batch->left.fetch_sub(1) == 1) complete(*it.batch);
+        Batch& b = *it.batch;
+        const Read& r = b.reads[it.idx];
+        do_read(b, r);
+        if (b.on_read && !failed(b)) {
+            wait_after(b);
+            if (!failed(b) && b.on_read(r.tag)) fail(b, "copy issue failed");
+        }
+        if (b.left.fetch_sub(1) == 1) complete(b);
     }
 }
 

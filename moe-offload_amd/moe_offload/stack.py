@@ -31,7 +31,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib, q2format
-from .loader import HostExpertStore, compute_layer_capacities
+from .loader import FileExpertStore, HostExpertStore, compute_layer_capacities
 
 
 @dataclass
@@ -63,6 +63,10 @@ class StackConfig:
                                  # c_layer_decode_step_sched call per layer; device mode tables
                                  # take the variant's decisions
     split: bool = False          # host mode with sched: hit experts run before the misses land
+    store_file: str | None = None  # host mode: layers 1.. read their misses from this blob file
+                                 # (q2format.write_blob_file) instead of a pinned host store
+    io_threads: int = 8          # reader threads of the file tier
+    io_direct: bool = False      # file tier: O_DIRECT reads (page cache bypassed)
 
 
 def effective_fetch_cap(prefetch_cap: int, top_m: int) -> int:
@@ -117,12 +121,23 @@ class DecodeStack:
             self._init_buffers()
             return
         self.full_pools = None
-        # layers 1..: pinned host store + HBM slot pools
-        self.store = HostExpertStore(c.n_layers, c.n_exp, self.blob_bytes, first_layer=1)
+        if c.store_file is not None:
+            # layers 1..: misses read from a blob file by the reader threads
+            if mode != "host":
+                raise ValueError("a file-backed stack is host-driven (mode='host')")
+            L.c_io_init(c.io_threads)
+            L.c_io_set_direct(int(c.io_direct))
+            self.store = FileExpertStore({l: c.store_file for l in range(1, c.n_layers)})
+            if self.store.blob_bytes != self.blob_bytes:
+                raise ValueError(f"{c.store_file}: blobs of {self.store.blob_bytes} bytes, the stack's are {self.blob_bytes}")
+        else:
+            # layers 1..: pinned host store
+            self.store = HostExpertStore(c.n_layers, c.n_exp, self.blob_bytes, first_layer=1)
         for l in range(1, c.n_layers):
-            blobs = random_blobs(c.n_exp, c.hidden, c.inter, c.group, gen, dev)
-            self.store.tensor(l).copy_(blobs)
-            del blobs
+            if c.store_file is None:
+                blobs = random_blobs(c.n_exp, c.hidden, c.inter, c.group, gen, dev)
+                self.store.tensor(l).copy_(blobs)
+                del blobs
             self.pools[l] = torch.zeros((caps[l], self.blob_bytes), dtype=torch.uint8, device=dev)
             self.slot_inds[l] = torch.zeros(16, dtype=torch.int32, device=dev)
         torch.cuda.synchronize()
@@ -130,7 +145,11 @@ class DecodeStack:
         u64 = ctypes.c_uint64 * 9
         for l in range(1, c.n_layers):
             li = self.cidx(l)
-            L.c_layer_init(li, -1, caps[l], u64(self.store.layer_ptr(l), *[0] * 8), u64(self.blob_bytes, *[0] * 8),
+            if c.store_file is not None:
+                fd, base = self.store.fds[l], self.store.headers[l]["data_offset"]
+            else:
+                fd, base = -1, self.store.layer_ptr(l)
+            L.c_layer_init(li, fd, caps[l], u64(base, *[0] * 8), u64(self.blob_bytes, *[0] * 8),
                            u64(self.pools[l].data_ptr(), *[0] * 8), self.slot_inds[l].data_ptr())
             _lib.check(L.c_layer_set_format(li, c.hidden, c.inter, c.group), "set_format")
             if mode == "device":
@@ -455,6 +474,8 @@ class DecodeStack:
         for l in range(1, self.cfg.n_layers):
             self.L.c_layer_init(self.cidx(l), -1, 16, None, None, None, 0)
         self.store.close()
+        if self.cfg.store_file is not None:
+            self.L.c_io_set_direct(0)
 
     # algorithmic bytes of the routed experts touched per token (the roofline numerator)
     def routed_bytes_per_token(self) -> int:

@@ -1,0 +1,102 @@
+"""GPU parity of the stacked decode with the on-disk tier: 6 layers at the full per-layer shapes
+whose misses are read from a blob file by the reader threads (host-driven tables).
+
+* every layer matches the oracle given the GPU's own input to that layer (teacher forcing), with
+  the experts taken from the file;
+* the id/prediction stream replayed through the oracle LRU in the reference's call order
+  (loader.py:920-977) gives the same slots and counters;
+* 1 reader thread with O_DIRECT and 8 threads through the page cache give bit-identical tokens.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from helpers import assert_close_rms
+from oracle import lru as olru
+from oracle import q2
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+N_LAYERS, N_TOK = 6, 10
+
+
+def _run(path, layer_base, threads, direct):
+    from moe_offload.stack import DecodeStack, StackConfig
+    print(f"file stack: threads={threads} direct={direct}", flush=True)
+    cfg = StackConfig(n_layers=N_LAYERS, seed=6, layer_base=layer_base, store_file=str(path), io_threads=threads,
+                      io_direct=direct)
+    st = DecodeStack(cfg, mode="host")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(98)
+    xs = torch.randn((N_TOK, cfg.hidden), device="cuda", generator=gen).half()
+    rec = []
+    for t in range(N_TOK):
+        st.decode_token(xs[t])
+        torch.cuda.synchronize()
+        rec.append({"ids": st.ids.cpu().numpy().copy(), "scores": st.scores.cpu().numpy().copy(),
+                    "pred": st.pred.cpu().numpy().copy(), "xs": st.xs.cpu().numpy().copy(),
+                    "hs": st.hs.cpu().numpy().copy(),
+                    "slots": {l: st.slot_inds[l][:cfg.top_k].cpu().numpy().copy() for l in range(1, N_LAYERS)}})
+    stats = {l: st.layer_stats(l) for l in range(1, N_LAYERS)}
+    return st, rec, stats
+
+
+def test_file_backed_stack(tmp_path):
+    from moe_offload import q2format
+    from moe_offload.stack import StackConfig, random_blobs
+    c = StackConfig()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    blobs = random_blobs(c.n_exp, c.hidden, c.inter, c.group, gen, "cuda").cpu().numpy()
+    path = tmp_path / "layer.q2blob"
+    q2format.write_blob_file(path, blobs, c.hidden, c.inter)
+    st, rec, stats = _run(path, 50, 8, False)
+    try:
+        W = st.router_w.float().cpu().numpy().astype(np.float16)
+        NW = st.norm_w.cpu().numpy()
+        pool0 = st.pool0.cpu().numpy()
+        for t in (0, N_TOK - 1):
+            r = rec[t]
+            for l in range(N_LAYERS):
+                x = r["xs"][l]
+                if l > 0:
+                    want_x = q2.round_to(q2.rmsnorm(r["hs"][l - 1].astype(np.float64), NW[l - 1], c.eps), "f16")
+                    assert np.array_equal(x.astype(np.float64), want_x), (t, l)
+                ids, sc, _ = q2.route(q2.router_logits(x, W[l], "f16")[None], c.top_k, "f16")
+                assert r["ids"][l].tolist() == ids[0].astype(np.int64).tolist(), (t, l)
+                src = pool0 if l == 0 else blobs
+                experts = lambda e: q2format.from_blob(src[e], c.hidden, c.inter, c.group)
+                want = q2.moe_combine(x.astype(np.float64), ids[0], sc[0], experts, bits=2, group=64)
+                assert_close_rms(r["hs"][l].astype(np.float64) - x.astype(np.float64), want, 1e-2, f"t{t} l{l}")
+        layers = {l: olru.CLru(30 + l, st.capacities[l], expert_bytes=st.blob_bytes) for l in range(1, N_LAYERS)}
+        for L in layers.values():
+            L.reset_stats()
+        for t in range(N_TOK):
+            r = rec[t]
+            layers[1].prefetch(r["pred"][0].tolist(), c.prefetch_cap)
+            for l in range(1, N_LAYERS):
+                slots, _ = layers[l].step(r["ids"][l].tolist())
+                assert slots == r["slots"][l].tolist(), (t, l)
+                if l + 1 < N_LAYERS:
+                    layers[l + 1].prefetch(r["pred"][l].tolist(), c.prefetch_cap)
+        for l in range(1, N_LAYERS):
+            assert layers[l].stats() == stats[l], l
+        for l in range(1, N_LAYERS):                  # every slot holds the expert its table names
+            e, s, n = (ctypes.c_int32 * 512)(), (ctypes.c_int32 * 512)(), ctypes.c_int(0)
+            st.L.c_layer_get_lru_state(st.cidx(l), e, s, ctypes.byref(n))
+            pool = st.pools[l].cpu().numpy()
+            for i in range(n.value):
+                assert np.array_equal(pool[s[i]], blobs[e[i]]), (l, e[i], s[i])
+    finally:
+        st.close()
+    st2, rec2, stats2 = _run(path, 56, 1, True)
+    try:
+        for t in range(N_TOK):
+            assert np.array_equal(rec2[t]["xs"], rec[t]["xs"]), t
+            for l in range(1, N_LAYERS):
+                assert np.array_equal(rec2[t]["slots"][l], rec[t]["slots"][l]), (t, l)
+        assert stats2 == stats
+    finally:
+        st2.close()
