@@ -334,6 +334,80 @@ int moe_calibrate_copy(void* dst, const void* src, uint64_t bytes, void* stream)
 int moe_calibrate_stream(const void* src, uint64_t bytes, int grid, float* out, void* stream);
 int c_abi_version(void);
 
+/* ---- Part 4: P1 I/O scheduler (mlx-qwen38/cpp/src/io_sched.h:46-245) ---------------------- */
+/* The C++ runner's `--io p1` cache: urgent and prefetch read queues served by reader threads,
+ * cancel / promote of queued prefetches, slots pinned while a GPU reader uses them, resize and
+ * forced invalidation.  One handle per scheduler (the reference's class instance); each function
+ * below is the method of the same name (include/moe_io_sched.hpp wraps them in that class).
+ * Slot pools may be HBM (reads are staged in pinned memory and copied by DMA; a read is done once
+ * its copy has completed) or host memory (read into directly).  Counters: 16 values in the order of
+ * P1LayerStats (io_sched.h:23-44). */
+typedef struct moe_p1 moe_p1;
+typedef void (*moe_p1_reader_fn)(int layer_idx, void* user);
+typedef double (*moe_p1_uniform_fn)(void* user);
+/* io_sched.h:48-49 (constructor, destructor: shuts the readers down) */
+moe_p1* moe_p1_create(void);
+void moe_p1_destroy(moe_p1* p);
+/* io_sched.h:54.  num_threads in 0..32; 0 runs every read inside the waits (the reference
+ * clamps to at least 1 thread). */
+void moe_p1_init(moe_p1* p, int num_threads);
+/* io_sched.h:55 */
+void moe_p1_shutdown(moe_p1* p);
+/* io_sched.h:146 */
+int moe_p1_num_threads(moe_p1* p);
+/* io_sched.h:57.  Called (without the scheduler's lock) when an allocation meets slots pinned by
+ * a GPU reader; it must end that reader and unpin (moe_p1_unpin_layer_slots).  fn == NULL: the
+ * scheduler waits for the layer's moe_p1_mark_read event and unpins the layer's slots itself. */
+void moe_p1_set_wait_reader_callback(moe_p1* p, moe_p1_reader_fn fn, void* user);
+/* No counterpart: the stream on which slot ids are written to device memory (default: null
+ * stream), and the event marking the end of layer l's GPU reader (recorded on `stream`). */
+void moe_p1_set_compute_stream(moe_p1* p, void* stream);
+int moe_p1_mark_read(moe_p1* p, int layer_idx, void* stream);
+/* io_sched.h:59-67 */
+void moe_p1_layer_init(moe_p1* p, int layer_idx, int fd, int capacity, int num_tensors,
+                       const uint64_t* base_offsets, const uint64_t* row_bytes, const uint64_t* base_ptrs,
+                       uint64_t slot_inds_ptr);
+/* io_sched.h:69-76 */
+void moe_p1_resize_layer(moe_p1* p, int layer_idx, int new_capacity, const uint64_t* new_base_ptrs,
+                         uint64_t slot_inds_ptr, const int32_t* ordered_eids, const int32_t* ordered_slots,
+                         int count);
+/* io_sched.h:78-79 */
+void moe_p1_reset_cache(moe_p1* p, int layer_idx);
+void moe_p1_reset_stats(moe_p1* p, int layer_idx);
+/* io_sched.h:82-86 */
+void moe_p1_start_prefetch(moe_p1* p, int layer_idx, const int32_t* pred_eids, int pred_count, int max_fetch);
+/* io_sched.h:88-98.  Pending reads the GPU must wait for (moe_p1_wait_layer_urgent); -1 with an
+ * error for an expert id >= 512 or when no slot can be freed. */
+int moe_p1_step_decode(moe_p1* p, int layer_idx, const uint32_t* eids, int k, uint32_t* out_slots);
+/* io_sched.h:100-106 */
+void moe_p1_wait_layer_urgent(moe_p1* p, int layer_idx);
+void moe_p1_wait_layer_all(moe_p1* p, int layer_idx);
+void moe_p1_wait_all(moe_p1* p);
+/* io_sched.h:108-114 */
+void moe_p1_unpin_layer_slots(moe_p1* p, int layer_idx);
+void moe_p1_pin_slots(moe_p1* p, int layer_idx, const uint32_t* slots, int count);
+void moe_p1_unpin_slots(moe_p1* p, int layer_idx, const uint32_t* slots, int count);
+int moe_p1_get_slot_pin_count(moe_p1* p, int layer_idx, int slot);
+/* io_sched.h:116-117.  The reference takes a std::mt19937_64&; here `draw(user)` returns one
+ * uniform [0, 1) value per candidate slot (moe_p1_mt64_uniform over a moe_p1_mt64_create handle
+ * draws exactly what std::uniform_real_distribution<double>(0, 1) does over that generator). */
+int moe_p1_force_invalidate(moe_p1* p, int layer_idx, double rate, moe_p1_uniform_fn draw, void* user);
+void* moe_p1_mt64_create(uint64_t seed);
+void moe_p1_mt64_destroy(void* rng);
+uint64_t moe_p1_mt64_next(void* rng);
+double moe_p1_mt64_uniform(void* rng);
+/* io_sched.h:119-125 */
+void moe_p1_load_sync(moe_p1* p, int layer_idx, const int32_t* eids, const int32_t* slots, int count,
+                      int is_prefill);
+/* io_sched.h:127-140 */
+void moe_p1_get_lru_state(moe_p1* p, int layer_idx, int32_t* out_eids, int32_t* out_slots, int* out_count);
+void moe_p1_set_lru_state(moe_p1* p, int layer_idx, const int32_t* ordered_eids, const int32_t* ordered_slots,
+                          int count, uint64_t add_prefill_requests, uint64_t add_prefill_hits,
+                          uint64_t add_prefill_misses);
+/* io_sched.h:142-143 */
+void moe_p1_get_layer_stats(moe_p1* p, int layer_idx, uint64_t* out16);
+void moe_p1_get_total_stats(moe_p1* p, int num_layers, uint64_t* out16);
+
 #ifdef __cplusplus
 }
 #endif

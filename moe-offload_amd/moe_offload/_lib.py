@@ -117,6 +117,38 @@ SIGNATURES: dict[str, tuple] = {
     "moe_calibrate_copy": (_c_int, [_c_vp, _c_vp, _c_u64, _c_vp]),
     "moe_calibrate_stream": (_c_int, [_c_vp, _c_u64, _c_int, _c_vp, _c_vp]),
     "c_abi_version": (_c_int, []),
+    # P1 I/O scheduler (cpp/src/io_sched.h)
+    "moe_p1_create": (_c_vp, []),
+    "moe_p1_destroy": (None, [_c_vp]),
+    "moe_p1_init": (None, [_c_vp, _c_int]),
+    "moe_p1_shutdown": (None, [_c_vp]),
+    "moe_p1_num_threads": (_c_int, [_c_vp]),
+    "moe_p1_set_wait_reader_callback": (None, [_c_vp, _c_vp, _c_vp]),
+    "moe_p1_set_compute_stream": (None, [_c_vp, _c_vp]),
+    "moe_p1_mark_read": (_c_int, [_c_vp, _c_int, _c_vp]),
+    "moe_p1_layer_init": (None, [_c_vp, _c_int, _c_int, _c_int, _c_int, _u64p, _u64p, _u64p, _c_u64]),
+    "moe_p1_resize_layer": (None, [_c_vp, _c_int, _c_int, _u64p, _c_u64, _i32p, _i32p, _c_int]),
+    "moe_p1_reset_cache": (None, [_c_vp, _c_int]),
+    "moe_p1_reset_stats": (None, [_c_vp, _c_int]),
+    "moe_p1_start_prefetch": (None, [_c_vp, _c_int, _i32p, _c_int, _c_int]),
+    "moe_p1_step_decode": (_c_int, [_c_vp, _c_int, _u32p, _c_int, _u32p]),
+    "moe_p1_wait_layer_urgent": (None, [_c_vp, _c_int]),
+    "moe_p1_wait_layer_all": (None, [_c_vp, _c_int]),
+    "moe_p1_wait_all": (None, [_c_vp]),
+    "moe_p1_unpin_layer_slots": (None, [_c_vp, _c_int]),
+    "moe_p1_pin_slots": (None, [_c_vp, _c_int, _u32p, _c_int]),
+    "moe_p1_unpin_slots": (None, [_c_vp, _c_int, _u32p, _c_int]),
+    "moe_p1_get_slot_pin_count": (_c_int, [_c_vp, _c_int, _c_int]),
+    "moe_p1_force_invalidate": (_c_int, [_c_vp, _c_int, ctypes.c_double, _c_vp, _c_vp]),
+    "moe_p1_mt64_create": (_c_vp, [_c_u64]),
+    "moe_p1_mt64_destroy": (None, [_c_vp]),
+    "moe_p1_mt64_next": (_c_u64, [_c_vp]),
+    "moe_p1_mt64_uniform": (ctypes.c_double, [_c_vp]),
+    "moe_p1_load_sync": (None, [_c_vp, _c_int, _i32p, _i32p, _c_int, _c_int]),
+    "moe_p1_get_lru_state": (None, [_c_vp, _c_int, _i32p, _i32p, ctypes.POINTER(ctypes.c_int)]),
+    "moe_p1_set_lru_state": (None, [_c_vp, _c_int, _i32p, _i32p, _c_int, _c_u64, _c_u64, _c_u64]),
+    "moe_p1_get_layer_stats": (None, [_c_vp, _c_int, _u64p]),
+    "moe_p1_get_total_stats": (None, [_c_vp, _c_int, _u64p]),
 }
 
 
