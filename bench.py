@@ -383,7 +383,8 @@ def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8):
     file of 512 experts (q2format.write_blob_file, 503 MB, shared by the 47 cached layers) with the
     reader threads, host-driven tables (one device->host read of ids per layer).  Timed through
     the page cache (the file is cached after the warm-up) and with O_DIRECT (every read goes to the
-    device), beside the same host driver over the pinned host store."""
+    device), beside the same host driver over the pinned host store; and the same file through the
+    P1 I/O scheduler (the C++ runner's `--io p1`: its own slot decisions, reads staged per reader)."""
     import shutil
     import tempfile
 
@@ -405,11 +406,12 @@ def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8):
         del blobs
         xs = torch.randn((warmup + steps, base.hidden), device="cuda", generator=gen).half()
         for name, kw in (("host_store", {}), ("page_cache", {"store_file": path}),
-                         ("o_direct", {"store_file": path, "io_direct": True})):
+                         ("o_direct", {"store_file": path, "io_direct": True}),
+                         ("p1_page_cache", {"store_file": path, "io": "p1"})):
             cfg = StackConfig(n_layers=n_layers, io_threads=threads, **kw)
             st = DecodeStack(cfg, mode="host")
             try:
-                direct = bool(_lib.lib().c_layer_io_direct(st.cidx(1))) if kw else None
+                direct = bool(_lib.lib().c_layer_io_direct(st.cidx(1))) if kw and st.p1 is None else None
                 elapsed, tot0, tot1 = timed_tokens(st, xs, warmup, steps, False)
                 _lib.check_error("file tier decode")
                 read = (tot1[4] - tot0[4]) + (tot1[5] - tot0[5])

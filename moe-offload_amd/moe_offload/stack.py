@@ -67,6 +67,8 @@ class StackConfig:
                                  # (q2format.write_blob_file) instead of a pinned host store
     io_threads: int = 8          # reader threads of the file tier
     io_direct: bool = False      # file tier: O_DIRECT reads (page cache bypassed)
+    io: str = "exact"            # file tier cache: "exact" (expert_io.c's, c_layer_*) or "p1" (the
+                                 # C++ runner's P1 I/O scheduler, moe_p1_*: cancel/promote, pins)
 
 
 def effective_fetch_cap(prefetch_cap: int, top_m: int) -> int:
@@ -121,6 +123,11 @@ class DecodeStack:
             self._init_buffers()
             return
         self.full_pools = None
+        self.p1 = None
+        if c.io not in ("exact", "p1"):
+            raise ValueError(f"io={c.io!r}: 'exact' or 'p1'")
+        if c.io == "p1" and c.store_file is None:
+            raise ValueError("io='p1' reads from a file: set store_file")
         if c.store_file is not None:
             # layers 1..: misses read from a blob file by the reader threads
             if mode != "host":
@@ -143,6 +150,17 @@ class DecodeStack:
         torch.cuda.synchronize()
         L.c_set_compute_stream(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         u64 = ctypes.c_uint64 * 9
+        if c.io == "p1":
+            self.p1 = L.moe_p1_create()
+            L.moe_p1_init(self.p1, c.io_threads)
+            L.moe_p1_set_compute_stream(self.p1, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            for l in range(1, c.n_layers):
+                L.moe_p1_layer_init(self.p1, self.cidx(l), self.store.fds[l], caps[l], 1,
+                                    u64(self.store.headers[l]["data_offset"], *[0] * 8), u64(self.blob_bytes, *[0] * 8),
+                                    u64(self.pools[l].data_ptr(), *[0] * 8), self.slot_inds[l].data_ptr())
+            _lib.check_error("moe_p1_layer_init")
+            self._init_buffers()
+            return
         for l in range(1, c.n_layers):
             li = self.cidx(l)
             if c.store_file is not None:
@@ -186,6 +204,12 @@ class DecodeStack:
     def reset_caches(self):
         if self.cfg.resident:
             return
+        if self.p1 is not None:
+            for l in range(1, self.cfg.n_layers):
+                self.L.moe_p1_unpin_layer_slots(self.p1, self.cidx(l))
+                self.L.moe_p1_reset_cache(self.p1, self.cidx(l))
+            _lib.check_error("p1 reset_cache")
+            return
         for l in range(1, self.cfg.n_layers):
             self.L.c_layer_reset_cache(self.cidx(l))
         _lib.check_error("reset_cache")
@@ -193,10 +217,18 @@ class DecodeStack:
     def reset_stats(self):
         if self.cfg.resident:
             return
+        if self.p1 is not None:
+            for l in range(1, self.cfg.n_layers):
+                self.L.moe_p1_reset_stats(self.p1, self.cidx(l))
+            return
         for l in range(1, self.cfg.n_layers):
             self.L.c_layer_reset_stats(self.cidx(l))
 
     def layer_stats(self, l: int) -> list[int]:
+        if self.p1 is not None:                      # the 16 P1LayerStats fields (io_sched.h:23-44)
+            o = (ctypes.c_uint64 * 16)()
+            self.L.moe_p1_get_layer_stats(self.p1, self.cidx(l), o)
+            return list(o)
         o = (ctypes.c_uint64 * 18)()
         self.L.c_layer_get_stats(self.cidx(l), o)
         return list(o)
@@ -392,6 +424,43 @@ class DecodeStack:
         _lib.check(L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
                                  c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), main.cuda_stream), "rmsnorm")
 
+    def decode_token_p1(self):
+        """The C++ runner's `--io p1` token (cpp/src/engine.cpp:572-610): per cached layer, end
+        the layer's last GPU reader and unpin its slots, step_decode, wait for the urgent reads if
+        any are pending, the SwitchGLU over the slot ids the scheduler wrote, mark the reader,
+        then queue the next layer's prefetch."""
+        c, L, P = self.cfg, self.L, self.p1
+        main = torch.cuda.current_stream()
+        for l in range(c.n_layers):
+            self._router(l)
+            if l == 0:
+                self._glu(0)
+                if c.prefetch and c.n_layers > 1:
+                    p = self.pred[0, :c.top_m].tolist()
+                    L.moe_p1_start_prefetch(P, self.cidx(1), (ctypes.c_int32 * c.top_m)(*p), c.top_m,
+                                            c.prefetch_cap)
+                continue
+            sel = torch.cat([self.ids[l], self.pred[l, :c.top_m]]).tolist()      # the one sync per layer
+            ids, pred = sel[:c.top_k], sel[c.top_k:]
+            li = self.cidx(l)
+            L.moe_p1_unpin_layer_slots(P, li)           # the layer's last reader ended before that sync
+            n = L.moe_p1_step_decode(P, li, (ctypes.c_uint32 * c.top_k)(*ids), c.top_k, None)
+            _lib.check(n, "p1 step_decode")
+            if n > 0:
+                L.moe_p1_wait_layer_urgent(P, li)
+            rc = L.moe_q2_switch_glu(self.xs[l].data_ptr(), self.pools[l].data_ptr(), self.blob_bytes,
+                                     self.capacities[l], self.slot_inds[l].data_ptr(), self.scores[l].data_ptr(),
+                                     c.top_k, c.hidden, c.inter, c.group, self.xs[l].data_ptr(),
+                                     self.h_ws.data_ptr(), self.hs[l].data_ptr(), 0, main.cuda_stream)
+            _lib.check(rc, "switch_glu")
+            _lib.check(L.moe_p1_mark_read(P, li, ctypes.c_void_p(main.cuda_stream)), "p1 mark_read")
+            if c.prefetch and l + 1 < c.n_layers:
+                L.moe_p1_start_prefetch(P, self.cidx(l + 1), (ctypes.c_int32 * c.top_m)(*pred), c.top_m,
+                                        c.prefetch_cap)
+        _lib.check_error("decode_token_p1")
+        _lib.check(L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
+                                 c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), main.cuda_stream), "rmsnorm")
+
     def _decode_token_sched(self, main):
         """The runner's decode loop (cpp/src/engine.cpp:545-560,700-730): after the resident
         layer 0 a prefetch-only call for layer 1, then per cached layer one
@@ -439,6 +508,8 @@ class DecodeStack:
                 self.graph.replay()
             else:
                 self.decode_token_device()
+        elif self.p1 is not None:
+            self.decode_token_p1()
         else:
             self.decode_token_host()
         return self.xs[self.cfg.n_layers]
@@ -458,8 +529,15 @@ class DecodeStack:
         self.graph = g
 
     def decode_totals(self) -> list[int]:
+        """(hits, prefetch hits, misses, requests, demand bytes, prefetch bytes) over the cached
+        layers; with the P1 scheduler: (lru_hits, prefetch_used, urgent_reads, decode_requests, bytes
+        read, 0)."""
         if self.cfg.resident:
             return [0] * 6
+        if self.p1 is not None:
+            t = (ctypes.c_uint64 * 16)()
+            self.L.moe_p1_get_total_stats(self.p1, self.cidx(self.cfg.n_layers), t)
+            return [t[1], t[6], t[2], t[0], t[9], 0]
         o = (ctypes.c_uint64 * 6)()
         self.L.c_get_decode_totals(self.cidx(self.cfg.n_layers), o)
         return list(o)
@@ -470,9 +548,14 @@ class DecodeStack:
         if self.cfg.resident:
             self.full_pools = None
             return
-        self.L.c_sync_copies()
-        for l in range(1, self.cfg.n_layers):
-            self.L.c_layer_init(self.cidx(l), -1, 16, None, None, None, 0)
+        if self.p1 is not None:
+            self.L.moe_p1_wait_all(self.p1)
+            self.L.moe_p1_destroy(self.p1)
+            self.p1 = None
+        else:
+            self.L.c_sync_copies()
+            for l in range(1, self.cfg.n_layers):
+                self.L.c_layer_init(self.cidx(l), -1, 16, None, None, None, 0)
         self.store.close()
         if self.cfg.store_file is not None:
             self.L.c_io_set_direct(0)

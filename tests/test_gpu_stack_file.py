@@ -5,7 +5,10 @@ whose misses are read from a blob file by the reader threads (host-driven tables
   the experts taken from the file;
 * the id/prediction stream replayed through the oracle LRU in the reference's call order
   (loader.py:920-977) gives the same slots and counters;
-* 1 reader thread with O_DIRECT and 8 threads through the page cache give bit-identical tokens.
+* 1 reader thread with O_DIRECT and 8 threads through the page cache give bit-identical tokens;
+* the same stack on the P1 I/O scheduler (the C++ runner's `--io p1`: its own slot decisions, reads
+  by 6 reader threads straight into HBM slot rows) gives bit-identical tokens too (the slots differ,
+  the experts and their bytes do not), with the scheduler's counters consistent.
 """
 import ctypes
 
@@ -22,11 +25,11 @@ pytestmark = pytest.mark.gpu
 N_LAYERS, N_TOK = 6, 10
 
 
-def _run(path, layer_base, threads, direct):
+def _run(path, layer_base, threads, direct, io="exact"):
     from moe_offload.stack import DecodeStack, StackConfig
-    print(f"file stack: threads={threads} direct={direct}", flush=True)
+    print(f"file stack: io={io} threads={threads} direct={direct}", flush=True)
     cfg = StackConfig(n_layers=N_LAYERS, seed=6, layer_base=layer_base, store_file=str(path), io_threads=threads,
-                      io_direct=direct)
+                      io_direct=direct, io=io)
     st = DecodeStack(cfg, mode="host")
     gen = torch.Generator(device="cuda")
     gen.manual_seed(98)
@@ -100,3 +103,36 @@ def test_file_backed_stack(tmp_path):
         assert stats2 == stats
     finally:
         st2.close()
+
+
+@pytest.mark.parametrize("threads", [0, 6])
+def test_p1_scheduler_stack_gives_the_same_tokens(tmp_path, threads):
+    from moe_offload import q2format
+    from moe_offload.stack import StackConfig, random_blobs
+    c = StackConfig()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    blobs = random_blobs(c.n_exp, c.hidden, c.inter, c.group, gen, "cuda").cpu().numpy()
+    path = tmp_path / "layer.q2blob"
+    q2format.write_blob_file(path, blobs, c.hidden, c.inter)
+    st, rec, _ = _run(path, 50, 8, False)
+    st.close()
+    p1, prec, _ = _run(path, 0, threads, False, io="p1")
+    try:
+        for t in range(N_TOK):
+            assert np.array_equal(prec[t]["xs"], rec[t]["xs"]), t
+            assert np.array_equal(prec[t]["ids"], rec[t]["ids"]), t
+        for l in range(1, N_LAYERS):                 # every routed slot held its expert's bytes
+            pool = p1.pools[l].cpu().numpy()
+            for j, s in enumerate(prec[-1]["slots"][l]):
+                assert np.array_equal(pool[s], blobs[prec[-1]["ids"][l][j]]), (l, j)
+        tot = p1.decode_totals()
+        assert tot[3] == N_TOK * (N_LAYERS - 1) * p1.cfg.top_k
+        for l in range(1, N_LAYERS):
+            s16 = p1.layer_stats(l)
+            assert s16[0] == N_TOK * p1.cfg.top_k
+            assert s16[4] + s16[6] + s16[7] <= s16[3]     # cancelled + used + wasted <= issued
+        from moe_offload import _lib
+        assert _lib.last_error() == ""
+    finally:
+        p1.close()
