@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--sched", action="store_true",
                     help="the C++ runner's scheduler variant of the expert cache (c_layer_decode_step_sched)")
     ap.add_argument("--split", action="store_true", help="with --sched --mode host: hit experts before misses land")
+    ap.add_argument("--native-host", action="store_true",
+                    help="with --mode host: the per-layer loop runs in the library (moe_stack_token_host)")
     ap.add_argument("--nemo-layers", type=int, default=40, help="layers of the codebook (Nemotron-style) workload")
     ap.add_argument("--only", choices=["headline", "resident", "roofline", "prefill", "calib", "floor", "nemotron", "filetier"], default=None,
                     help="run one pass and print its own JSON line (for sweeps and profiling); "
@@ -653,7 +655,7 @@ def main():
     # ---- headline: 20% cache, misses staged from the pinned host store ---------------------
     cfg = StackConfig(n_layers=args.layers, budget_pct=args.budget_pct, prefetch=not args.no_prefetch,
                       stage_ctas=args.stage_ctas, pf_stage_ctas=args.pf_stage_ctas, sched=args.sched,
-                      split=args.split)
+                      split=args.split, native_host=args.native_host)
     if args.only == "roofline":
         # the roofline kernel's timing pass alone (the profile command for the rocprof summary)
         rst = DecodeStack(StackConfig(n_layers=args.layers, prefetch=False, resident=True), mode="device")
@@ -670,6 +672,7 @@ def main():
         return
     t0 = time.perf_counter()
     st = DecodeStack(cfg, mode=args.mode)
+    st.mirror_ids = False                     # the bench reads no per-token ids
     setup_s = time.perf_counter() - t0
     xs = torch.randn((n_tok, cfg.hidden), device="cuda", generator=gen).half()
     elapsed, tot0, tot1 = timed_tokens(st, xs, args.warmup, args.steps, use_graph)
@@ -683,7 +686,8 @@ def main():
     del st
     torch.cuda.empty_cache()
     if args.only == "headline":
-        print(json.dumps({"value": round(tok_s, 2), "driver": args.mode + ("+graph" if use_graph else ""),
+        print(json.dumps({"value": round(tok_s, 2), "driver": args.mode + ("+graph" if use_graph else "") +
+                          ("+native" if args.native_host and args.mode == "host" else ""),
                           "sched": args.sched, "split": args.split, "stage_ctas": args.stage_ctas,
                           "pf_stage_ctas": args.pf_stage_ctas or args.stage_ctas,
                           "effective_hit_rate": round((tot1[0] - tot0[0] + tot1[1] - tot0[1]) / req, 4),

@@ -334,6 +334,38 @@ int moe_calibrate_copy(void* dst, const void* src, uint64_t bytes, void* stream)
 int moe_calibrate_stream(const void* src, uint64_t bytes, int grid, float* out, void* stream);
 int c_abi_version(void);
 
+/* ---- Part 3b: native host-driven decode token ---------------------------------------------- */
+/* No counterpart in the reference's C ABI: the C++ runner's per-layer loop (cpp/src/engine.cpp:
+ * 572-660, loader.py:920-977) over the entry points above, for host-driven layers.  Layer 0's
+ * experts are all resident in pool0 (slot == expert id); layers 1.. are cached layers
+ * layer_base + l set up with c_layer_init / c_layer_set_format.  Per layer the router writes its
+ * ids and next-layer predictions into pinned host memory (ids_host, pred_host: c_host_alloc), the
+ * host steps the table (copies queued to the DMA engines), launches the SwitchGLU and the next
+ * layer's prefetch.  Shapes of the buffers (fp16 unless noted):
+ *   xs [n_layers + 1][hidden] (xs[0] is the token's input, xs[n_layers] its output), hs fp32
+ *   [n_layers][hidden], router_w [n_layers][n_exp][hidden], norm_w [n_layers][hidden], scores
+ *   [n_layers][top_k], ids0 u32 [top_k] (device), ids_host u32 [n_layers][top_k], pred_host i32
+ *   [n_layers][top_m], router_ws n_layers x router_ws_bytes (moe_router_workspace_bytes), h_ws
+ *   [top_k * inter]. */
+typedef struct moe_stack_desc {
+    int n_layers, layer_base, hidden, n_exp, top_k, top_m, inter, group, prefetch, prefetch_cap;
+    float eps;
+    void* xs;
+    float* hs;
+    const void* router_w;
+    const void* norm_w;
+    void* scores;
+    uint32_t* ids0;
+    uint32_t* ids_host;
+    int32_t* pred_host;
+    void* router_ws;
+    uint64_t router_ws_bytes;
+    const void* pool0;
+    uint64_t blob_bytes;
+    void* h_ws;
+} moe_stack_desc;
+int moe_stack_token_host(const moe_stack_desc* d, void* stream);
+
 /* ---- Part 4: P1 I/O scheduler (mlx-qwen38/cpp/src/io_sched.h:46-245) ---------------------- */
 /* The C++ runner's `--io p1` cache: urgent and prefetch read queues served by reader threads,
  * cancel / promote of queued prefetches, slots pinned while a GPU reader uses them, resize and

@@ -20,6 +20,17 @@ _u32p, _i32p, _u64p = (ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_
                        ctypes.POINTER(ctypes.c_uint64))
 
 # name -> (restype, argtypes)
+class StackDesc(ctypes.Structure):
+    """moe_stack_desc (include/moe_offload.h)."""
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layers", "layer_base", "hidden", "n_exp", "top_k", "top_m", "inter",
+                                            "group", "prefetch", "prefetch_cap")] + [
+        ("eps", ctypes.c_float), ("xs", ctypes.c_void_p), ("hs", ctypes.c_void_p), ("router_w", ctypes.c_void_p),
+        ("norm_w", ctypes.c_void_p), ("scores", ctypes.c_void_p), ("ids0", ctypes.c_void_p),
+        ("ids_host", ctypes.c_void_p), ("pred_host", ctypes.c_void_p), ("router_ws", ctypes.c_void_p),
+        ("router_ws_bytes", ctypes.c_uint64), ("pool0", ctypes.c_void_p), ("blob_bytes", ctypes.c_uint64),
+        ("h_ws", ctypes.c_void_p)]
+
+
 SIGNATURES: dict[str, tuple] = {
     # expert_io.c entry points
     "c_io_init": (None, [_c_int]),
@@ -117,6 +128,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_calibrate_copy": (_c_int, [_c_vp, _c_vp, _c_u64, _c_vp]),
     "moe_calibrate_stream": (_c_int, [_c_vp, _c_u64, _c_int, _c_vp, _c_vp]),
     "c_abi_version": (_c_int, []),
+    "moe_stack_token_host": (_c_int, [_c_vp, _c_vp]),
     # P1 I/O scheduler (cpp/src/io_sched.h)
     "moe_p1_create": (_c_vp, []),
     "moe_p1_destroy": (None, [_c_vp]),

@@ -28,6 +28,7 @@ from __future__ import annotations
 import ctypes
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _lib, q2format
@@ -69,6 +70,8 @@ class StackConfig:
     io_direct: bool = False      # file tier: O_DIRECT reads (page cache bypassed)
     io: str = "exact"            # file tier cache: "exact" (expert_io.c's, c_layer_*) or "p1" (the
                                  # C++ runner's P1 I/O scheduler, moe_p1_*: cancel/promote, pins)
+    native_host: bool = False    # host mode: the per-layer loop runs in the library
+                                 # (moe_stack_token_host) instead of Python
 
 
 def effective_fetch_cap(prefetch_cap: int, top_m: int) -> int:
@@ -124,6 +127,7 @@ class DecodeStack:
             return
         self.full_pools = None
         self.p1 = None
+        self.mirror_ids = True
         if c.io not in ("exact", "p1"):
             raise ValueError(f"io={c.io!r}: 'exact' or 'p1'")
         if c.io == "p1" and c.store_file is None:
@@ -196,6 +200,30 @@ class DecodeStack:
         self.ev_copy = [torch.cuda.Event() for _ in range(c.n_layers)]
         self.ev_demand = [torch.cuda.Event() for _ in range(c.n_layers)]
         self.graph = None
+        self._host_sel = []
+        if c.native_host and self.mode == "host" and not c.resident and self.p1 is None and not c.sched:
+            self._init_native()
+
+    def _init_native(self):
+        """Pinned host mirrors for the router's ids / predictions and the runner's descriptor."""
+        c, L = self.cfg, self.L
+        k, m = c.top_k, max(c.top_m, 1)
+        ids_p, pred_p = L.c_host_alloc(c.n_layers * k * 4), L.c_host_alloc(c.n_layers * m * 4)
+        if not ids_p or not pred_p:
+            raise _lib.NativeError(f"pinned id buffers: {_lib.last_error()}")
+        self._host_sel = [ids_p, pred_p]
+        self.ids_host = np.ctypeslib.as_array(ctypes.cast(ids_p, ctypes.POINTER(ctypes.c_int32)), shape=(c.n_layers, k))
+        self.pred_host = np.ctypeslib.as_array(ctypes.cast(pred_p, ctypes.POINTER(ctypes.c_int32)),
+                                               shape=(c.n_layers, m))
+        self._ws_flat = torch.zeros(c.n_layers * self.router_ws[0].numel(), dtype=torch.uint8, device=self.device)
+        self.desc = _lib.StackDesc(
+            n_layers=c.n_layers, layer_base=c.layer_base, hidden=c.hidden, n_exp=c.n_exp, top_k=k, top_m=c.top_m,
+            inter=c.inter, group=c.group, prefetch=int(c.prefetch), prefetch_cap=c.prefetch_cap, eps=c.eps,
+            xs=self.xs.data_ptr(), hs=self.hs.data_ptr(), router_w=self.router_w.data_ptr(),
+            norm_w=self.norm_w.data_ptr(), scores=self.scores.data_ptr(), ids0=self.ids[0].data_ptr(),
+            ids_host=ids_p, pred_host=pred_p, router_ws=self._ws_flat.data_ptr(),
+            router_ws_bytes=self.router_ws[0].numel(), pool0=self.pool0.data_ptr(), blob_bytes=self.blob_bytes,
+            h_ws=self.h_ws.data_ptr())
 
     # C-ABI layer index of stack layer l
     def cidx(self, l: int) -> int:
@@ -510,6 +538,13 @@ class DecodeStack:
                 self.decode_token_device()
         elif self.p1 is not None:
             self.decode_token_p1()
+        elif self._host_sel:
+            stream = torch.cuda.current_stream()
+            _lib.check(self.L.moe_stack_token_host(ctypes.byref(self.desc), ctypes.c_void_p(stream.cuda_stream)),
+                       "moe_stack_token_host")
+            if self.mirror_ids:                      # the device copies the Python drivers keep
+                self.ids[1:].copy_(torch.from_numpy(self.ids_host[1:]), non_blocking=True)
+                self.pred[:, :self.pred_host.shape[1]].copy_(torch.from_numpy(self.pred_host), non_blocking=True)
         else:
             self.decode_token_host()
         return self.xs[self.cfg.n_layers]
@@ -545,6 +580,9 @@ class DecodeStack:
     def close(self):
         torch.cuda.synchronize()
         self.graph = None
+        for ptr in self._host_sel:
+            self.L.c_host_free(ptr)
+        self._host_sel = []
         if self.cfg.resident:
             self.full_pools = None
             return

@@ -7,7 +7,9 @@
   order (prefetch(1) after layer 0, then step(l), prefetch(l+1); loader.py:920-977) gives the
   same slots and counters as the library;
 * the table work fused into the router and the separate table kernels agree; a graph replay
-  equals eager execution.
+  equals eager execution;
+* the host-driven loop run natively (moe_stack_token_host) equals the Python host driver bit for
+  bit (ids, predictions, slots, outputs, counters).
 """
 import numpy as np
 import pytest
@@ -22,9 +24,9 @@ pytestmark = pytest.mark.gpu
 N_LAYERS, N_TOK = 6, 12
 
 
-def run_stack(mode, layer_base, graph=False, fused=True):
+def run_stack(mode, layer_base, graph=False, fused=True, native=False):
     from moe_offload.stack import DecodeStack, StackConfig
-    cfg = StackConfig(n_layers=N_LAYERS, seed=5, layer_base=layer_base, fused_tables=fused)
+    cfg = StackConfig(n_layers=N_LAYERS, seed=5, layer_base=layer_base, fused_tables=fused, native_host=native)
     st = DecodeStack(cfg, mode=mode)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(99)
@@ -148,3 +150,19 @@ def test_router_tables_reject_one_layer_for_step_and_prefetch(runs):
                                   torch.cuda.current_stream().cuda_stream)
     with pytest.raises(_lib.NativeError, match="same layer"):
         _lib.check(rc, "router_tables")
+
+
+def test_native_host_runner_matches_python_host_driver(runs):
+    _, (_, h, hs) = runs
+    st, nat, ns = run_stack("host", 30, native=True)
+    try:
+        assert st._host_sel, "the native runner was not used"
+        for t in range(N_TOK):
+            assert np.array_equal(nat[t]["ids"], h[t]["ids"]), f"token {t}"
+            assert np.array_equal(nat[t]["pred"], h[t]["pred"]), f"token {t}"
+            assert np.array_equal(nat[t]["xs"], h[t]["xs"]), f"token {t}"
+            for l in range(1, N_LAYERS):
+                assert np.array_equal(nat[t]["slots"][l], h[t]["slots"][l]), (t, l)
+        assert ns == hs
+    finally:
+        st.close()
