@@ -30,9 +30,12 @@ for p in (str(ROOT), str(ROOT / "moe-offload_amd")):
 METRIC = "MoE decode tok/s, 48L top-10/512 Q2 @20% cache; achieved HBM GB/s"
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per k_q2_gate_up launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE over the
-# roofline pass, scaled by a known-size copy (profiles/q2_gemv_roofline_loop_rocprof.md); a counter
-# run cannot happen inside bench.
-GATE_UP_TRAFFIC_BYTES = 6_678_528
+# roofline pass of this build (median over 480 dispatches: 3,250.5 KiB fetched x 2 + 20 KiB
+# written, the factors from a known-size copy), profiles/q2_gemv_roofline_loop_rocprof.md; a
+# counter run cannot happen inside bench, so the line names where the figure comes from.
+GATE_UP_TRAFFIC_BYTES = 6_677_504
+GATE_UP_TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over bench.py --only roofline, scaled by "
+                          "moe_calibrate_copy (profiles/q2_gemv_roofline_loop_rocprof.md)")
 
 
 def parse():
@@ -726,6 +729,7 @@ def main():
                    "driver": args.mode + ("+graph" if use_graph else ""), "tokens": args.steps, "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
+                     "traffic_source": GATE_UP_TRAFFIC_SOURCE,
                      "kernel": "k_q2_gate_up",
                      "measured_in": f"resident stack (all experts in HBM): {res['gemv_back_to_back_us']['launches']} "
                                     "launches back to back over the 48 layer pools, fresh top-10 draws, bracketed "
