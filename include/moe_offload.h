@@ -136,6 +136,20 @@ int moe_router(const float* h_in, const void* norm_w, float eps, const void* x_i
                void* workspace, uint32_t* ids_out, void* scores_out, int32_t* pred_out,
                void* stream);
 uint64_t moe_router_workspace_bytes(int n_exp);
+/* The real checkpoint's router / predictor (loader.py:903-908, 237-242, 950-958;
+ * cpp/src/kernels.cpp:997-1019 QLinear::forward with bits 8, group 64): an 8-bit affine quantized
+ * linear layer over a bf16 vector x [hidden] -- codes u32 [n_rows][hidden / 4] (4 bytes per word,
+ * LSB first), scales and biases bf16 [n_rows][hidden / 64] -- with logits rounded to bf16 once
+ * (fp64 accumulation).  Route mode (k > 0, m == 0): ids_out u32 [k] and scores_out bf16 [k] in
+ * ascending gate order (gates = bf16(softmax), scores = bf16(g / s), s the left-to-right bf16 sum).
+ * Predict mode (m > 0, k == 0): pred_out i32 [m], the top m logits by descending value (equal
+ * values by ascending id).  logits_out (bf16 [n_rows], optional; required when k == m == 0).
+ * hidden a multiple of 64 up to 4096, n_rows <= 1024.  workspace: moe_router_q8_workspace_bytes,
+ * zero-filled before its first use (the kernel leaves it reusable). */
+uint64_t moe_router_q8_workspace_bytes(int n_rows);
+int moe_router_q8(const void* x, const uint32_t* codes, const void* scales, const void* biases, int hidden,
+                  int n_rows, int group, int k, int m, void* workspace, uint32_t* ids_out, void* scores_out,
+                  int32_t* pred_out, void* logits_out, void* stream);
 /* No counterpart in the reference.  moe_router for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc): no workspace argument;
  * the logits and the arrival counter live in a static device array of the library (8,448 bytes

@@ -129,6 +129,9 @@ SIGNATURES: dict[str, tuple] = {
     "moe_calibrate_stream": (_c_int, [_c_vp, _c_u64, _c_int, _c_vp, _c_vp]),
     "c_abi_version": (_c_int, []),
     "moe_stack_token_host": (_c_int, [_c_vp, _c_vp]),
+    "moe_router_q8_workspace_bytes": (_c_u64, [_c_int]),
+    "moe_router_q8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp,
+                               _c_vp, _c_vp, _c_vp, _c_vp]),
     # P1 I/O scheduler (cpp/src/io_sched.h)
     "moe_p1_create": (_c_vp, []),
     "moe_p1_destroy": (None, [_c_vp]),
