@@ -218,20 +218,70 @@ class ShardExpertStore:
         self.fds.clear()
 
 
+class HostShardStore:
+    """The reference's shards in pinned, device-mapped host memory: per layer, the 9 tensors of
+    `experts-{l:02d}.safetensors` (as ShardExpertStore lists them: ascending file offset, with
+    their roles) each read whole -- one read per tensor, by the library's reader threads
+    (c_io_read_ranges) -- into its own pinned buffer [n_exp, bytes per expert].  Layers bound to
+    it stage misses from host memory (DMA, or the staging kernel when device-driven)."""
+
+    def __init__(self, shards: "dict[int, str] | str | Path", layers=None, threads: int = 8):
+        files = ShardExpertStore(shards, layers)
+        L = _lib.lib()
+        self.layout, self.ptrs = files.layout, {}
+        self.n_exp, self.hidden, self.inter, self.group = files.n_exp, files.hidden, files.inter, files.group
+        self.blob_bytes = files.blob_bytes
+        L.c_io_init(threads)
+        try:
+            for l, lay in self.layout.items():
+                ptrs = []
+                for rb in lay["row_bytes"]:
+                    ptr = L.c_host_alloc(self.n_exp * rb)
+                    if not ptr:
+                        raise _lib.NativeError(f"pinned shard store: {_lib.last_error()}")
+                    ptrs.append(ptr)
+                self.ptrs[l] = ptrs
+                n = len(ptrs)
+                u64 = ctypes.c_uint64 * n
+                rc = L.c_io_read_ranges(files.fds[l], u64(*lay["offsets"]),
+                                        u64(*[self.n_exp * rb for rb in lay["row_bytes"]]), u64(*ptrs), n)
+                _lib.check(rc, f"reading the layer {l} shard")
+        except Exception:
+            self.close()
+            raise
+        finally:
+            files.close()
+
+    def tensor(self, l: int, t: int) -> np.ndarray:
+        """uint8 [n_exp, bytes per expert] view of layer l's tensor t (file-offset order)."""
+        rb = self.layout[l]["row_bytes"][t]
+        return np.ctypeslib.as_array(ctypes.cast(self.ptrs[l][t], ctypes.POINTER(ctypes.c_uint8)),
+                                     shape=(self.n_exp, rb))
+
+    def close(self):
+        L = _lib.lib()
+        for ptrs in self.ptrs.values():
+            for ptr in ptrs:
+                L.c_host_free(ptr)
+        self.ptrs.clear()
+
+
 class CachedSwitchGLU:
     """Per-layer slot cache over an HBM pool + Q2 SwitchGLU (loader.py:306-749).
 
     `store` is a HostExpertStore (pinned host memory, fd == -1), a FileExpertStore (a blob file,
-    fd >= 0; the pool holds `capacity` blobs) or a ShardExpertStore (the reference's shard read in
+    fd >= 0; the pool holds `capacity` blobs), a ShardExpertStore (the reference's shard read in
     place, fd >= 0; `pools` are the 9 tensors' slot pools, each [capacity, bytes per expert], as
-    loader.py:336-366 allocates them, and hidden/inter/group come from the shard).
+    loader.py:336-366 allocates them, and hidden/inter/group come from the shard) or a
+    HostShardStore (the same 9 tensors from pinned host memory, fd == -1).
     decode: __call__(x [1,1,H] fp16, indices [1,1,k]) -> per-expert outputs [1,1,k,H], exactly
     like SwitchGLU; forward_combined() returns the score-weighted sum directly.
     """
 
-    def __init__(self, store: "HostExpertStore | FileExpertStore | ShardExpertStore", layer_idx: int, capacity: int,
+    def __init__(self, store: "HostExpertStore | FileExpertStore | ShardExpertStore | HostShardStore", layer_idx: int,
+                 capacity: int,
                  hidden: int = 2048, inter: int = 512, group: int = 64, device: str | torch.device = "cuda"):
-        shard = isinstance(store, ShardExpertStore)
+        shard = isinstance(store, (ShardExpertStore, HostShardStore))
         if shard:
             hidden, inter, group = store.hidden, store.inter, store.group
         self.layer_idx, self.capacity = layer_idx, capacity
@@ -248,7 +298,11 @@ class CachedSwitchGLU:
             self.blob_bytes = sum(lay["row_bytes"])
             self.pool = None
             self.pools = [torch.zeros((capacity, rb), dtype=torch.uint8, device=dev) for rb in lay["row_bytes"]]
-            L.c_layer_init(layer_idx, store.fds[layer_idx], capacity, u64(*lay["offsets"]), u64(*lay["row_bytes"]),
+            if isinstance(store, HostShardStore):         # host addresses in place of file offsets
+                fd, src = -1, store.ptrs[layer_idx]
+            else:
+                fd, src = store.fds[layer_idx], lay["offsets"]
+            L.c_layer_init(layer_idx, fd, capacity, u64(*src), u64(*lay["row_bytes"]),
                            u64(*[p.data_ptr() for p in self.pools]), self._slot_inds_buf.data_ptr())
             _lib.check_error("c_layer_init")
             _lib.check(L.c_layer_set_format9(layer_idx, hidden, inter, group, (ctypes.c_int32 * 9)(*lay["roles"]),

@@ -145,3 +145,65 @@ def test_reference_shard_read_in_place(tmp_path, threads, direct):
         L.c_io_set_direct(0)
         L.c_io_init(8)
         store.close()
+
+
+@pytest.mark.parametrize("mode", ["host", "device"])
+def test_reference_shard_in_pinned_host_memory(tmp_path, mode):
+    """HostShardStore: the shard's 9 tensors read whole into pinned memory (one read per tensor by
+    the reader threads); a layer bound to it decodes with host- or device-driven staging."""
+    from moe_offload import _lib
+    from moe_offload.loader import CachedSwitchGLU, HostShardStore
+    Hs, Is, Es, cap = 2560, 640, 40, 12
+    layer = 36 if mode == "host" else 37
+    print(f"host shard store: mode={mode}", flush=True)
+    mlx = experts_bf16(Es, Hs, Is, seed=41)
+    write_reference_shard(tmp_path / f"experts-{layer:02d}.safetensors", layer, mlx)
+    want_rows = role_arrays(mlx)
+    dev = torch.device("cuda:0")
+    L = _lib.lib()
+    store = HostShardStore(tmp_path, layers=[layer], threads=4)
+    mod = None
+    try:
+        lay = store.layout[layer]
+        for t, r in enumerate(lay["roles"]):
+            assert np.array_equal(store.tensor(layer, t), want_rows[r]), t
+        mod = CachedSwitchGLU(store, layer, cap)
+        stream = torch.cuda.current_stream().cuda_stream
+        if mode == "device":
+            _lib.check(L.c_layer_set_device_mode(layer, 1), "device_mode")
+        ora = olru.CLru(layer, cap, expert_bytes=mod.blob_bytes)
+        ora.reset_stats()
+        rng = np.random.default_rng(42)
+        f = lambda e: tuple((p[0][e], p[1][e], p[2][e]) for p in mlx)
+        y = torch.empty(Hs, dtype=torch.float32, device=dev)
+        for t in range(12):
+            ids = [int(v) for v in rng.choice(Es, K, replace=False)]
+            x = rng.standard_normal(Hs).astype(np.float16)
+            sc = rng.dirichlet(np.ones(K)).astype(np.float16)
+            xt, sct = torch.from_numpy(x).to(dev), torch.from_numpy(sc).to(dev)
+            if mode == "host":
+                out = mod.forward_combined(xt, ids, sct)
+            else:
+                it = torch.tensor(ids, dtype=torch.int32, device=dev)
+                _lib.check(L.c_layer_step_decode_dev(layer, it.data_ptr(), K, 0, stream), "step_dev")
+                _lib.check(L.c_layer_stage_dev(layer, 0, 2, stream), "stage_dev")
+                _lib.check(L.c_layer_switch_glu(layer, xt.data_ptr(), sct.data_ptr(), None, mod._h_ws.data_ptr(),
+                                                y.data_ptr(), 0, K, stream), "switch_glu")
+                out = y
+            slots, _ = ora.step(ids)
+            assert mod._slot_inds_buf[:K].cpu().tolist() == slots, t
+            if t in (0, 11):
+                want = q2.moe_combine(x.astype(np.float64), np.array(ids), sc.astype(np.float64), f, bits=2, group=64,
+                                      sdtype="bf16")
+                assert_close_rms(out.cpu().numpy(), want, 1e-2, f"step {t}")
+        torch.cuda.synchronize()
+        for e, sl in zip(*ora.get_state()):
+            for tt, r in enumerate(lay["roles"]):
+                assert np.array_equal(mod.pools[tt][sl].cpu().numpy(), want_rows[r][e]), (e, sl, tt)
+        assert _lib.last_error() == ""
+    finally:
+        if mod is not None:
+            if mode == "device":
+                L.c_layer_set_device_mode(layer, 0)
+            mod.close()
+        store.close()
