@@ -281,6 +281,13 @@ int c_layer_set_format(int layer_idx, int hidden, int inter, int group);
 enum { MOE_Q2T_GATE_W = 0, MOE_Q2T_GATE_S, MOE_Q2T_GATE_B, MOE_Q2T_UP_W, MOE_Q2T_UP_S, MOE_Q2T_UP_B,
        MOE_Q2T_DOWN_W, MOE_Q2T_DOWN_S, MOE_Q2T_DOWN_B };
 int c_layer_set_format9(int layer_idx, int hidden, int inter, int group, const int32_t* roles, int scale_bf16);
+/* The prefill grouped SwitchGLU (as moe_q2_grouped_switch_glu) over the 9 tensors' pools (as
+ * moe_q2t_switch_glu: ptrs / slot_bytes in MOE_Q2T_* role order, scale_bf16); hidden and inter
+ * multiples of 64 up to 2560.  c_layer_grouped_switch_glu takes this path for format9 layers. */
+int moe_q2t_grouped_switch_glu(const void* x, int n_tokens, const int32_t* row_token, const int32_t* row_out,
+                               int n_rows, int n_out_rows, const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
+                               const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots, int hidden,
+                               int inter, int group, void* h_ws, void* y_out, void* stream);
 /* SwitchGLU over the layer's pool with its current slot ids; orders after pending copies. */
 int c_layer_switch_glu(int layer_idx, const void* x, const void* scores, const void* residual,
                        void* h_ws, float* y_out, int per_expert, int k, void* stream);

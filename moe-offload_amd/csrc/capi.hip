@@ -1279,6 +1279,20 @@ int moe_q2_grouped_switch_glu(const void* x, int n_tokens, const int32_t* row_to
                                hidden, inter, group, y_out, stream);
 }
 
+int moe_q2t_grouped_switch_glu(const void* x, int n_tokens, const int32_t* row_token, const int32_t* row_out,
+                               int n_rows, int n_out_rows, const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
+                               const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots, int hidden,
+                               int inter, int group, void* h_ws, void* y_out, void* stream) {
+    Q2Experts E;
+    if (!experts9("q2t_grouped_switch_glu", ptrs, slot_bytes, scale_bf16, hidden, inter, E)) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    if (launch_q2t_grouped_gate_up((const __half*)x, n_tokens, row_token, n_rows, seg_start, seg_slot, n_seg, E, n_slots,
+                                   hidden, inter, group, (__half*)h_ws, s))
+        return -1;
+    return launch_q2t_grouped_down((const __half*)h_ws, n_rows, row_out, n_out_rows, seg_start, seg_slot, n_seg, E,
+                                   n_slots, hidden, inter, group, (__half*)y_out, s);
+}
+
 uint64_t moe_cb_expert_bytes(int hidden, int inter) {
     if (hidden <= 0 || inter <= 0 || hidden % 256 || inter % 256) return 0;
     return cb_layout(hidden, inter).bytes;
@@ -1324,7 +1338,6 @@ int c_layer_grouped_switch_glu(int layer, const void* x, int n_tokens, const int
     }
     LayerState& L = g_layers[layer];
     if (!L.dst[0]) { moe_set_error("layer_grouped_switch_glu: layer %d has no pool", layer); return -1; }
-    if (L.fmt9) { moe_set_error("layer_grouped_switch_glu: layer %d holds 9 tensors (the grouped GEMM takes blob pools)", layer); return -1; }
     if (n_seg > L.capacity) {
         moe_set_error("layer_grouped_switch_glu: %d segments > capacity %d", n_seg, L.capacity);
         return -1;
@@ -1332,10 +1345,17 @@ int c_layer_grouped_switch_glu(int layer, const void* x, int n_tokens, const int
     hipStream_t s = (hipStream_t)stream;
     if (wait_copies_gpu(L, s)) return -1;
     if (ensure_events(L)) return -1;
-    if (moe_q2_grouped_switch_glu(x, n_tokens, row_token, row_out, n_rows, n_out_rows, seg_start, nullptr, n_seg,
-                                  (const void*)L.dst[0], L.row_bytes[0], L.capacity, L.hidden, L.inter, L.group, h_ws,
-                                  y_out, stream))
+    if (L.fmt9) {
+        if (launch_q2t_grouped_gate_up((const __half*)x, n_tokens, row_token, n_rows, seg_start, nullptr, n_seg, L.E9,
+                                       L.capacity, L.hidden, L.inter, L.group, (__half*)h_ws, s) ||
+            launch_q2t_grouped_down((const __half*)h_ws, n_rows, row_out, n_out_rows, seg_start, nullptr, n_seg, L.E9,
+                                    L.capacity, L.hidden, L.inter, L.group, (__half*)y_out, s))
+            return -1;
+    } else if (moe_q2_grouped_switch_glu(x, n_tokens, row_token, row_out, n_rows, n_out_rows, seg_start, nullptr, n_seg,
+                                         (const void*)L.dst[0], L.row_bytes[0], L.capacity, L.hidden, L.inter, L.group,
+                                         h_ws, y_out, stream)) {
         return -1;
+    }
     HIP_TRY(hipEventRecord(L.read_done, s));
     L.read_recorded = true;
     return 0;

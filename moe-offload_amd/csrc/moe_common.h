@@ -234,6 +234,12 @@ int launch_q2_grouped_down(const __half* h, int n_rows, const int32_t* row_out, 
                            const int32_t* seg_start, const int32_t* seg_slot, int n_seg,
                            const uint8_t* pool, size_t stride, int n_slots, int hidden, int inter,
                            int group, __half* y_out, hipStream_t s);
+int launch_q2t_grouped_gate_up(const __half* x, int n_tokens, const int32_t* row_token, int n_rows,
+                               const int32_t* seg_start, const int32_t* seg_slot, int n_seg, const Q2Experts& E,
+                               int n_slots, int hidden, int inter, int group, __half* h_out, hipStream_t s);
+int launch_q2t_grouped_down(const __half* h, int n_rows, const int32_t* row_out, int n_out_rows,
+                            const int32_t* seg_start, const int32_t* seg_slot, int n_seg, const Q2Experts& E,
+                            int n_slots, int hidden, int inter, int group, __half* y_out, hipStream_t s);
 int launch_cb_up(const __half* x, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots, int k,
                  int hidden, int inter, const uint8_t* grid, uint16_t* h_out, hipStream_t s);
 int launch_cb_down(const uint16_t* h, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots,

@@ -26,6 +26,11 @@
 // K order.  Inside an MFMA the K positions are permuted identically for A and B: the even codes
 // of a 32-bit word pair with activations [x0 x2 .. x14] of its 16 inputs and the odd codes with
 // [x1 x3 .. x15]; the activation halves are regrouped in registers with v_perm_b32.
+//
+// Weight sources (SBF): 0 = the blob pool, (scale, bias) interleaved as fp16 words; 1 / 2 = the
+// reference's 9 tensors (loader.py:332-406: codes, scales, biases in pools of their own), scales and
+// biases fp16 / bf16, turned into the same (scale, bias) fp16 words as they are loaded (bf16 ->
+// fp16 is exact for the normal range of fp16).
 #include <hip/hip_fp16.h>
 
 #include "moe_common.h"
@@ -89,17 +94,26 @@ __device__ __forceinline__ void lds_barrier() {
 template <int MODE>
 constexpr int max_mt() { return MODE == 0 ? 4 : 2; }
 
-template <int NCH, int MODE, bool SBL>
+// One (scale, bias) fp16 word from two 16-bit values of the 9-tensor form.
+template <int SBF>
+__device__ __forceinline__ uint32_t sb_word(uint32_t sc, uint32_t bi) {
+    if constexpr (SBF == 2) {
+        sc = __half_as_ushort(__float2half_rn(__uint_as_float(sc << 16)));
+        bi = __half_as_ushort(__float2half_rn(__uint_as_float(bi << 16)));
+    }
+    return (sc & 0xFFFFu) | (bi << 16);
+}
+
+template <int NCH, int MODE, bool SBL, int SBF>
 __global__ __launch_bounds__(256, 2) void k_q2g_proj(
     const __half* __restrict__ src, int n_src_rows, const int32_t* __restrict__ row_map,
     const int32_t* __restrict__ row_out, int n_out_rows,
     const int32_t* __restrict__ seg_start, const int32_t* __restrict__ seg_slot, int n_seg, int n_rows,
-    const uint8_t* __restrict__ pool, size_t stride, int n_slots, BlobLayout L, int tiles_per_seg,
-    __half* __restrict__ out) {
+    Q2Experts E, int n_slots, int hidden, int inter, int tiles_per_seg, __half* __restrict__ out) {
     constexpr int kMaxMT = max_mt<MODE>();
     constexpr bool kPrefetch = MODE == kGateUp;        // a short K (down) gains nothing from it
-    const int K = MODE == kGateUp ? L.hidden : L.inter;          // contraction length
-    const int N = MODE == kGateUp ? L.inter : L.hidden;          // output rows per projection
+    const int K = MODE == kGateUp ? hidden : inter;              // contraction length
+    const int N = MODE == kGateUp ? inter : hidden;              // output rows per projection
     const int kg = K / 64;
     const int work = xcd_order(blockIdx.x, gridDim.x);
     const int seg = work / tiles_per_seg, tile = work % tiles_per_seg;
@@ -112,35 +126,36 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
 
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, kq = lane >> 4;
-    const uint8_t* blob = pool + (size_t)slot * stride;
-    const size_t code_row = (size_t)K / 4, sb_row = (size_t)kg;   // bytes / words per weight row
+    const size_t code_row = (size_t)K / 4, sb_row = (size_t)kg;   // bytes / (scale, bias) pairs per weight row
 
     // Weight row of lane n in subtile s = base_s + n: a wave-uniform base per subtile plus one
     // per-lane offset shared by all subtiles.
     const uint8_t* codes[kSub];
-    const uint32_t* sbp[kSub];
+    const uint32_t* sbp[kSub];                 // SBF 0: (scale, bias) words of the subtile's rows
+    const uint16_t* scp[kSub];                 // SBF 1 / 2: scales and biases
+    const uint16_t* bip[kSub];
     bool rv[kSub];
     int col[kSub];
 #pragma unroll
     for (int s = 0; s < kSub; ++s) {
-        size_t co, so;
-        int base;
+        int base, p;
         if (MODE == kGateUp) {
             base = tile * 128 + wv * 32 + (s >> 1) * 16;
-            co = (s & 1) ? L.up_codes : L.gate_codes;
-            so = (s & 1) ? L.up_sb : L.gate_sb;
+            p = (s & 1) ? 1 : 0;
         } else {
             base = tile * 256 + wv * 64 + s * 16;
-            co = L.down_codes;
-            so = L.down_sb;
+            p = 2;
         }
         col[s] = base + n;
         // N is a multiple of 64, so a subtile is wholly in range or wholly out; one that is out
         // reads the last in-range subtile (unconditional loads) and is never written
         rv[s] = base < N;
         if (base >= N) base = N - 16;
-        codes[s] = blob + co + (size_t)base * code_row;
-        sbp[s] = reinterpret_cast<const uint32_t*>(blob + so) + (size_t)base * sb_row;
+        const Q2Proj& P = E.p[p];
+        codes[s] = P.w + (size_t)slot * P.w_stride + (size_t)base * code_row;
+        sbp[s] = reinterpret_cast<const uint32_t*>(P.s + (size_t)slot * P.s_stride) + (size_t)base * sb_row;
+        scp[s] = reinterpret_cast<const uint16_t*>(P.s + (size_t)slot * P.s_stride) + (size_t)base * sb_row;
+        bip[s] = reinterpret_cast<const uint16_t*>(P.b + (size_t)slot * P.b_stride) + (size_t)base * sb_row;
     }
     const uint32_t lane_code0 = (uint32_t)((size_t)n * code_row + (size_t)kq * 16);
     const uint32_t lane_sb0 = (uint32_t)((size_t)n * sb_row + kq);
@@ -167,7 +182,16 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
     auto fetch_sb = [&](int jj) {
         const int gs = sb_piece(jj, kq);
 #pragma unroll
-        for (int s = 0; s < kSub; ++s) sbn[s] = *reinterpret_cast<const uint4*>(sbp[s] + lane_row_sb + gs);
+        for (int s = 0; s < kSub; ++s) {
+            if constexpr (SBF == 0) {
+                sbn[s] = *reinterpret_cast<const uint4*>(sbp[s] + lane_row_sb + gs);
+            } else {                           // 4 scales and 4 biases (8-byte aligned: kg % 4 == 0)
+                const uint2 sc = *reinterpret_cast<const uint2*>(scp[s] + lane_row_sb + gs);
+                const uint2 bi = *reinterpret_cast<const uint2*>(bip[s] + lane_row_sb + gs);
+                sbn[s] = make_uint4(sb_word<SBF>(sc.x & 0xFFFFu, bi.x & 0xFFFFu), sb_word<SBF>(sc.x >> 16, bi.x >> 16),
+                                    sb_word<SBF>(sc.y & 0xFFFFu, bi.y & 0xFFFFu), sb_word<SBF>(sc.y >> 16, bi.y >> 16));
+            }
+        }
     };
     auto put_sb = [&](int jj) {
 #pragma unroll
@@ -231,7 +255,11 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
 #pragma unroll
             for (int s = 0; s < kSub; ++s) {
                 cw[s] = *reinterpret_cast<const uint4*>(codes[s] + lane_code + (size_t)j * 64 + (ptrdiff_t)gdelta * 16);
-                if constexpr (!kSbLds) sw[s] = sbp[s][lane_sb + 4 * j + gdelta];
+                if constexpr (!kSbLds) {
+                    const uint32_t gi = lane_sb + 4 * j + gdelta;
+                    if constexpr (SBF == 0) sw[s] = sbp[s][gi];
+                    else sw[s] = sb_word<SBF>(scp[s][gi], bip[s][gi]);
+                }
             }
         };
         // After chunk j's multiply: the loads of the next block's words (needed from chunk
@@ -383,27 +411,27 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
     }
 }
 
-template <int NCH, int MODE, bool SBL>
+template <int NCH, int MODE, bool SBL, int SBF>
 int launch_proj(const __half* src, int n_src_rows, const int32_t* row_map, const int32_t* row_out, int n_out_rows,
-                const int32_t* seg_start, const int32_t* seg_slot, int n_seg, int n_rows, const uint8_t* pool,
-                size_t stride, int n_slots, const BlobLayout& L, __half* out, hipStream_t s) {
-    const int N = MODE == kGateUp ? L.inter : L.hidden;
+                const int32_t* seg_start, const int32_t* seg_slot, int n_seg, int n_rows, const Q2Experts& E,
+                int n_slots, int hidden, int inter, __half* out, hipStream_t s) {
+    const int N = MODE == kGateUp ? inter : hidden;
     const int rows_per_block = MODE == kGateUp ? 128 : 256;
     const int tiles = (N + rows_per_block - 1) / rows_per_block;
     const long long nb = (long long)n_seg * tiles;
     if (nb <= 0) return 0;
     if (nb > 0x7FFFFFFFLL) { moe_set_error("grouped q2: grid too large"); return -1; }
-    MOE_LAUNCH(MODE == kGateUp ? TK_PF_GATE_UP : TK_PF_DOWN, (k_q2g_proj<NCH, MODE, SBL>), dim3((unsigned)nb), dim3(256),
-               0, s, src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg, n_rows, pool, stride,
-               n_slots, L, tiles, out);
+    MOE_LAUNCH(MODE == kGateUp ? TK_PF_GATE_UP : TK_PF_DOWN, (k_q2g_proj<NCH, MODE, SBL, SBF>), dim3((unsigned)nb),
+               dim3(256), 0, s, src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg, n_rows, E,
+               n_slots, hidden, inter, tiles, out);
     HIP_TRY(hipGetLastError());
     return 0;
 }
 
-template <int MODE>
-int dispatch_proj(int K, const __half* src, int n_src_rows, const int32_t* row_map, const int32_t* row_out,
-                  int n_out_rows, const int32_t* seg_start, const int32_t* seg_slot, int n_seg, int n_rows,
-                  const uint8_t* pool, size_t stride, int n_slots, const BlobLayout& L, __half* out, hipStream_t s) {
+template <int MODE, int SBF>
+int dispatch_proj_f(int K, const __half* src, int n_src_rows, const int32_t* row_map, const int32_t* row_out,
+                    int n_out_rows, const int32_t* seg_start, const int32_t* seg_slot, int n_seg, int n_rows,
+                    const Q2Experts& E, int n_slots, int hidden, int inter, __half* out, hipStream_t s) {
     // the four-chunk scale/bias blocks pay on gate/up's long K; down (K = inter, often 2 chunks)
     // is faster with the per-chunk loads
     const bool sbl = MODE == kGateUp && K % 256 == 0 && K >= 512;
@@ -411,16 +439,30 @@ int dispatch_proj(int K, const __half* src, int n_src_rows, const int32_t* row_m
 #define PF_CASE(c) \
     case c: \
         if (sbl) \
-            return launch_proj<c, MODE, (c >= 2 && MODE == kGateUp)>(src, n_src_rows, row_map, row_out, n_out_rows, \
-                                                                     seg_start, seg_slot, n_seg, n_rows, pool, stride, \
-                                                                     n_slots, L, out, s); \
-        return launch_proj<c, MODE, false>(src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg, \
-                                           n_rows, pool, stride, n_slots, L, out, s);
+            return launch_proj<c, MODE, (c >= 2 && MODE == kGateUp), SBF>(src, n_src_rows, row_map, row_out, n_out_rows, \
+                                                                          seg_start, seg_slot, n_seg, n_rows, E, n_slots, \
+                                                                          hidden, inter, out, s); \
+        return launch_proj<c, MODE, false, SBF>(src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, \
+                                                n_seg, n_rows, E, n_slots, hidden, inter, out, s);
         PF_CASE(1) PF_CASE(2) PF_CASE(3) PF_CASE(4) PF_CASE(5)
         PF_CASE(6) PF_CASE(7) PF_CASE(8) PF_CASE(9) PF_CASE(10)
 #undef PF_CASE
         default: moe_set_error("grouped q2: contraction length %d unsupported (<= %d)", K, kMaxChunks * 256); return -1;
     }
+}
+
+template <int MODE>
+int dispatch_proj(int K, const __half* src, int n_src_rows, const int32_t* row_map, const int32_t* row_out,
+                  int n_out_rows, const int32_t* seg_start, const int32_t* seg_slot, int n_seg, int n_rows,
+                  const Q2Experts& E, int n_slots, int hidden, int inter, __half* out, hipStream_t s) {
+    if (E.p[0].sb_step == 4)
+        return dispatch_proj_f<MODE, 0>(K, src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg,
+                                        n_rows, E, n_slots, hidden, inter, out, s);
+    if (E.bf16)
+        return dispatch_proj_f<MODE, 2>(K, src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg,
+                                        n_rows, E, n_slots, hidden, inter, out, s);
+    return dispatch_proj_f<MODE, 1>(K, src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg,
+                                    n_rows, E, n_slots, hidden, inter, out, s);
 }
 
 bool check_grouped(const char* who, int hidden, int inter, int group, int n_seg, int n_rows, const void* pool,
@@ -478,9 +520,9 @@ int launch_q2_grouped_gate_up(const __half* x, int n_tokens, const int32_t* row_
         moe_set_error("q2_grouped_gate_up: %d rows but no tokens", n_rows);
         return -1;
     }
-    BlobLayout L = blob_layout(hidden, inter, group);
-    return dispatch_proj<kGateUp>(hidden, x, n_tokens, row_token, nullptr, 0, seg_start, seg_slot, n_seg, n_rows, pool,
-                                  stride, n_slots, L, h_out, s);
+    const Q2Experts E = q2_experts_from_blob(pool, stride, blob_layout(hidden, inter, group));
+    return dispatch_proj<kGateUp>(hidden, x, n_tokens, row_token, nullptr, 0, seg_start, seg_slot, n_seg, n_rows, E,
+                                  n_slots, hidden, inter, h_out, s);
 }
 
 int launch_q2_grouped_down(const __half* h, int n_rows, const int32_t* row_out, int n_out_rows,
@@ -490,9 +532,37 @@ int launch_q2_grouped_down(const __half* h, int n_rows, const int32_t* row_out, 
                        y_out))
         return -1;
     if (n_seg == 0 || n_rows == 0) return 0;
-    BlobLayout L = blob_layout(hidden, inter, group);
+    const Q2Experts E = q2_experts_from_blob(pool, stride, blob_layout(hidden, inter, group));
     return dispatch_proj<kDown>(inter, h, n_rows, nullptr, row_out, row_out ? n_out_rows : n_rows, seg_start, seg_slot,
-                                n_seg, n_rows, pool, stride, n_slots, L, y_out, s);
+                                n_seg, n_rows, E, n_slots, hidden, inter, y_out, s);
+}
+
+// The same over the reference's 9 tensors (E from their pools; see q2t_shape_ok for the shapes the
+// decode kernels take -- the grouped kernels take any multiple of 64 up to 2560).
+int launch_q2t_grouped_gate_up(const __half* x, int n_tokens, const int32_t* row_token, int n_rows,
+                               const int32_t* seg_start, const int32_t* seg_slot, int n_seg, const Q2Experts& E,
+                               int n_slots, int hidden, int inter, int group, __half* h_out, hipStream_t s) {
+    if (!check_grouped("q2t_grouped_gate_up", hidden, inter, group, n_seg, n_rows, E.p[0].w, ~size_t(0), n_slots, x,
+                       seg_start, h_out))
+        return -1;
+    if (n_seg == 0 || n_rows == 0) return 0;
+    if (n_tokens <= 0) {
+        moe_set_error("q2t_grouped_gate_up: %d rows but no tokens", n_rows);
+        return -1;
+    }
+    return dispatch_proj<kGateUp>(hidden, x, n_tokens, row_token, nullptr, 0, seg_start, seg_slot, n_seg, n_rows, E,
+                                  n_slots, hidden, inter, h_out, s);
+}
+
+int launch_q2t_grouped_down(const __half* h, int n_rows, const int32_t* row_out, int n_out_rows,
+                            const int32_t* seg_start, const int32_t* seg_slot, int n_seg, const Q2Experts& E,
+                            int n_slots, int hidden, int inter, int group, __half* y_out, hipStream_t s) {
+    if (!check_grouped("q2t_grouped_down", hidden, inter, group, n_seg, n_rows, E.p[2].w, ~size_t(0), n_slots, h,
+                       seg_start, y_out))
+        return -1;
+    if (n_seg == 0 || n_rows == 0) return 0;
+    return dispatch_proj<kDown>(inter, h, n_rows, nullptr, row_out, row_out ? n_out_rows : n_rows, seg_start, seg_slot,
+                                n_seg, n_rows, E, n_slots, hidden, inter, y_out, s);
 }
 
 int launch_pair_combine(const __half* y, const __half* scores, const __half* residual, int n_tokens, int k,

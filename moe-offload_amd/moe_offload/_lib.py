@@ -108,6 +108,8 @@ SIGNATURES: dict[str, tuple] = {
     "c_host_free": (_c_int, [_c_vp]),
     "c_layer_set_format": (_c_int, [_c_int, _c_int, _c_int, _c_int]),
     "c_layer_set_format9": (_c_int, [_c_int, _c_int, _c_int, _c_int, _i32p, _c_int]),
+    "moe_q2t_grouped_switch_glu": (_c_int, [_c_vp, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_int, _u64p,
+                                            _u64p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp]),
     "c_layer_switch_glu": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
     "c_layer_mark_read": (_c_int, [_c_int, _c_vp]),
     "c_router_tables_dev": (_c_int, [_c_int, _c_int, _c_int, _c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_vp, _c_vp, _c_int,

@@ -385,9 +385,6 @@ class CachedSwitchGLU:
                                                out.data_ptr(), 1, K, torch.cuda.current_stream().cuda_stream)
             _lib.check(rc, "c_layer_switch_glu")
             return out.to(x.dtype).reshape(1, 1, K, self.hidden)
-        if self.pool is None:
-            raise NotImplementedError("prefill over a layer bound to the shard's 9 tensors: the grouped kernels "
-                                      "read the blob layout (FileExpertStore / HostExpertStore)")
         from .prefill import cached_prefill
         return cached_prefill(self, x, indices)
 

@@ -207,3 +207,60 @@ def test_reference_shard_in_pinned_host_memory(tmp_path, mode):
                 L.c_layer_set_device_mode(layer, 0)
             mod.close()
         store.close()
+
+
+def test_reference_shard_prefill(tmp_path):
+    """Prefill through a layer bound to the reference's shard (9 tensors, bf16 scales, 2560 x 640):
+    the grouped kernels read the 9 pools; outputs, LRU state, counters and pool contents follow
+    the oracle's prefill plan after a few decode steps."""
+    from moe_offload import _lib
+    from moe_offload.loader import CachedSwitchGLU, ShardExpertStore
+    Hs, Is, Es, cap, layer = 2560, 640, 40, 16, 38
+    mlx = experts_bf16(Es, Hs, Is, seed=51)
+    write_reference_shard(tmp_path / f"experts-{layer:02d}.safetensors", layer, mlx)
+    want_rows = role_arrays(mlx)
+    dev = torch.device("cuda:0")
+    L = _lib.lib()
+    L.c_io_init(8)
+    store = ShardExpertStore(tmp_path, layers=[layer])
+    mod = None
+    try:
+        mod = CachedSwitchGLU(store, layer, cap)
+        ora = olru.CLru(layer, cap, expert_bytes=mod.blob_bytes)
+        ora.reset_stats()
+        rng = np.random.default_rng(52)
+        for t in range(5):
+            ids = [int(v) for v in rng.choice(Es, K, replace=False)]
+            x = rng.standard_normal(Hs).astype(np.float16)
+            mod.forward_combined(torch.from_numpy(x).to(dev), ids, torch.ones(K, dtype=torch.float16, device=dev))
+            ora.step(ids)
+        n_tok = 12
+        pids = np.stack([rng.choice(Es, K, replace=False) for _ in range(n_tok)]).astype(np.int32)
+        px = rng.standard_normal((n_tok, Hs)).astype(np.float16)
+        e0, s0 = ora.get_state()
+        plan = q2.prefill_plan(pids.reshape(-1), e0, s0, cap)
+        y = mod(torch.from_numpy(px).to(dev)[None], torch.from_numpy(pids).to(dev)[None])
+        torch.cuda.synchronize()
+        yh = y[0].reshape(n_tok * K, Hs).cpu().numpy().astype(np.float64)
+        flat = pids.reshape(-1)
+        f = lambda e: tuple((p[0][e], p[1][e], p[2][e]) for p in mlx)
+        for e in sorted(set(flat.tolist()))[:8]:
+            pairs = np.nonzero(flat == e)[0]
+            want = q2.switch_glu_expert(px[pairs // K].astype(np.float64), *f(e), bits=2, group=64, sdtype="bf16")
+            assert_close_rms(yh[pairs], want, 1e-2, f"prefill expert {e}")
+        for _, _, le, ls in plan["chunks"]:
+            if le:
+                ora.load_sync(le, ls, 1)
+        ora.set_state(*plan["new_lru"], plan["add_req"], plan["add_hits"], plan["add_misses"])
+        assert _state(L, layer) == ora.get_state()
+        mod.sync_stats_from_c()
+        assert [int(v) for v in mod._c_stats_buf] == ora.stats()
+        lay = store.layout[layer]
+        for e, sl in zip(*ora.get_state()):
+            for tt, r in enumerate(lay["roles"]):
+                assert np.array_equal(mod.pools[tt][sl].cpu().numpy(), want_rows[r][e]), (e, sl, tt)
+        assert _lib.last_error() == ""
+    finally:
+        if mod is not None:
+            mod.close()
+        store.close()

@@ -208,3 +208,62 @@ def test_nine_tensor_layer_in_file_offset_order(mode):
         L.c_layer_init(layer, -1, 16, None, None, None, 0)
         for p in host:
             L.c_host_free(p)
+
+
+def _grouped_t(L, x, row_tok, row_out, seg_start, seg_slot, ptrs, nbytes, bf16, n_slots, H, I, n_out):
+    from moe_offload import _lib
+    dev = x.device
+    M, n_seg = row_tok.numel(), seg_start.numel() - 1
+    h_ws = torch.empty((M, I), dtype=torch.float16, device=dev)
+    y = torch.empty((n_out, H), dtype=torch.float16, device=dev)
+    rc = L.moe_q2t_grouped_switch_glu(x.data_ptr(), x.shape[0], row_tok.data_ptr(), row_out.data_ptr(), M, n_out,
+                                      seg_start.data_ptr(), seg_slot.data_ptr(), n_seg, ptrs, nbytes, bf16, n_slots, H,
+                                      I, 64, h_ws.data_ptr(), y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "moe_q2t_grouped_switch_glu")
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def test_grouped_tensor_form_equals_blob_kernels():
+    """fp16 scales: the 9-tensor grouped path loads the same (scale, bias) values as the blob path
+    and gives bit-identical outputs (512 tokens x top-10 of 64 experts, hidden 2048 / inter 512)."""
+    from moe_offload import _lib, ops, prefill, q2format, synth
+    L = _lib.lib()
+    dev = torch.device("cuda")
+    H, I, E, K = 2048, 512, 64, 10
+    gate, up, down = synth.q2_experts(E, H, I, seed=21)
+    pool = torch.from_numpy(q2format.to_blobs(gate, up, down, H, I)).to(dev)
+    ts, ptrs, nbytes = _pools((gate, up, down), dev)
+    ids, _ = synth.prefill_routing(256, K, E)
+    xs = synth.hidden_states(256, H, seed=22)
+    row_tok, row_out, seg_start, seg_slot = prefill.resident_plan(ids, K)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    want = ops.q2_grouped_switch_glu(t(xs), t(row_tok), t(seg_start), pool, H, I, row_out=t(row_out),
+                                     n_out_rows=ids.size, seg_slot=t(seg_slot)).cpu().numpy()
+    got = _grouped_t(L, t(xs), t(row_tok), t(row_out), t(seg_start), t(seg_slot), ptrs, nbytes, 0, E, H, I, ids.size)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+def test_grouped_tensor_form_bf16_real_shape():
+    """bf16 scales at hidden 2560 / inter 640 (the real model's layer): every row of a subset of
+    experts against the fp64 oracle within 1e-2 x RMS."""
+    from moe_offload import _lib, prefill, synth
+    L = _lib.lib()
+    dev = torch.device("cuda")
+    H, I, E, K = 2560, 640, 48, 10
+    mlx = experts_bf16(E, H, I, seed=23)
+    ts, ptrs, nbytes = _pools(mlx, dev)
+    ids, _ = synth.prefill_routing(128, K, E)
+    xs = synth.hidden_states(128, H, seed=24)
+    row_tok, row_out, seg_start, seg_slot = prefill.resident_plan(ids, K)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    y = _grouped_t(L, t(xs), t(row_tok), t(row_out), t(seg_start), t(seg_slot), ptrs, nbytes, 1, E, H, I,
+                   ids.size).astype(np.float64)
+    flat = ids.reshape(-1)
+    f = _fn(mlx, "bf16")
+    counts = np.diff(seg_start)
+    chosen = [int(seg_slot[np.argmax(counts)])] + [int(e) for e in np.random.default_rng(25).choice(seg_slot, 8, replace=False)]
+    for e in chosen:
+        pairs = np.nonzero(flat == e)[0]
+        want = q2.switch_glu_expert(xs[pairs // K].astype(np.float64), *f(e), bits=2, group=64, sdtype="bf16")
+        assert_close_rms(y[pairs], want, 1e-2, f"expert {e}")
