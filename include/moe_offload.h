@@ -261,6 +261,14 @@ int moe_cb_down(const void* h, const void* pool, uint64_t stride, int n_slots, c
 int moe_cb_moe(const void* x, const void* pool, uint64_t stride, int n_slots, const uint32_t* slots,
                const void* scores, int k, int hidden, int inter, const void* grid, const void* residual,
                void* h_ws, float* y_out, int per_expert, void* stream);
+/* One layer of the codebook stack from the previous layer's fp32 output: x = RMSNorm(h_in) * norm_w
+ * (fp64, one fp16 rounding; the arithmetic of moe_rmsnorm), written to x_out [hidden] fp16, then
+ * y_out = x + sum_j scores[j] * D_j relu(U_j x)^2.  The norm runs inside the up-projection (every
+ * block normalises h while its weight loads are in flight), so the layer is two launches, not three.
+ * norm_w may be null (no weight). */
+int moe_cb_moe_norm(const float* h_in, const void* norm_w, float eps, void* x_out, const void* pool,
+                    uint64_t stride, int n_slots, const uint32_t* slots, const void* scores, int k,
+                    int hidden, int inter, const void* grid, void* h_ws, float* y_out, void* stream);
 
 /* ---- Part 3: no counterpart in the reference ----------------------------------------------- */
 

@@ -1320,6 +1320,15 @@ int moe_cb_moe(const void* x, const void* pool, uint64_t stride, int n_slots, co
                        stream);
 }
 
+int moe_cb_moe_norm(const float* h_in, const void* norm_w, float eps, void* x_out, const void* pool, uint64_t stride,
+                    int n_slots, const uint32_t* slots, const void* scores, int k, int hidden, int inter,
+                    const void* grid, void* h_ws, float* y_out, void* stream) {
+    if (launch_cb_up_norm(h_in, (const __half*)norm_w, eps, (__half*)x_out, (const uint8_t*)pool, stride, n_slots,
+                          slots, k, hidden, inter, (const uint8_t*)grid, (uint16_t*)h_ws, (hipStream_t)stream))
+        return -1;
+    return moe_cb_down(h_ws, pool, stride, n_slots, slots, scores, k, hidden, inter, grid, x_out, y_out, 0, stream);
+}
+
 int moe_pair_combine(const void* y, const void* scores, const void* residual, int n_tokens, int k, int hidden,
                      float* out, void* stream) {
     return launch_pair_combine((const __half*)y, (const __half*)scores, (const __half*)residual, n_tokens, k, hidden, out,

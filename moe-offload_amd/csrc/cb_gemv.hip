@@ -27,6 +27,7 @@
 
 #include "lane_reduce.h"
 #include "moe_common.h"
+#include "norm_f64.h"
 
 namespace {
 
@@ -112,15 +113,26 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
-template <int T>
-__global__ __launch_bounds__(256) void k_cb_up(const __half* __restrict__ x, const uint8_t* __restrict__ pool,
-                                               size_t stride, const uint32_t* __restrict__ slots, int n_slots,
-                                               CbLayout L, const uint8_t* __restrict__ grid,
-                                               uint16_t* __restrict__ h_out) {
+// NORM: the input is the previous layer's fp32 output h, normalised here (norm64: every block
+// computes x = RMSNorm(h) into LDS while its weight loads fly; block (0, 0) also writes x to
+// x_out for the down projection's residual), instead of an fp16 x read from memory.
+template <int T, bool NORM>
+__global__ __launch_bounds__(256) void k_cb_up(const __half* __restrict__ x, const float* __restrict__ h_in,
+                                               const __half* __restrict__ norm_w, float eps, __half* __restrict__ x_out,
+                                               const uint8_t* __restrict__ pool, size_t stride,
+                                               const uint32_t* __restrict__ slots, int n_slots, CbLayout L,
+                                               const uint8_t* __restrict__ grid, uint16_t* __restrict__ h_out) {
     __shared__ uint4 gtab[256];
     __shared__ uint4 stab[128];
+    __shared__ __align__(16) uint16_t xs[NORM ? norm64::kMaxHidden : 8];
+    __shared__ double red[4];
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint2 gentry = reinterpret_cast<const uint2*>(grid)[tid];     // blockDim == 256
+    norm64::NormIn nin;
+    if constexpr (NORM) {
+        norm64::load(nin, h_in, norm_w, L.hidden);
+        __builtin_amdgcn_sched_barrier(0);                // the norm's loads ahead of the weights'
+    }
 
     const int j = blockIdx.y;
     const uint32_t slot = slots[j];
@@ -151,23 +163,31 @@ __global__ __launch_bounds__(256) void k_cb_up(const __half* __restrict__ x, con
         }
     }
 
-    // activation slice: sub-blocks li + 32 t, 16 pairs each (zeros past the end)
+    // activation slice: sub-blocks li + 32 t, 16 pairs each (a clamped sub-block past the end
+    // is masked by its scale below); from memory, or from the block's normalised copy in LDS
     uint32_t xa[T][16];
+    auto take_x = [&](const __half* src) {
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const int sb = li + 32 * t;
-        const int sc = sb < nsub ? sb : nsub - 1;
+        for (int t = 0; t < T; ++t) {
+            const int sb = li + 32 * t;
+            const int sc = sb < nsub ? sb : nsub - 1;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const uint4 u = reinterpret_cast<const uint4*>(x + (size_t)sc * 32)[v];
-            xa[t][4 * v] = u.x;
-            xa[t][4 * v + 1] = u.y;
-            xa[t][4 * v + 2] = u.z;
-            xa[t][4 * v + 3] = u.w;
+            for (int v = 0; v < 4; ++v) {
+                const uint4 u = reinterpret_cast<const uint4*>(src + (size_t)sc * 32)[v];
+                xa[t][4 * v] = u.x;
+                xa[t][4 * v + 1] = u.y;
+                xa[t][4 * v + 2] = u.z;
+                xa[t][4 * v + 3] = u.w;
+            }
         }
-    }
+    };
+    if constexpr (!NORM) take_x(x);
     build_tables(gentry, gtab, stab, tid, false);
-    __syncthreads();                                      // tables built
+    if constexpr (NORM)
+        norm64::finish(nin, norm_w != nullptr, eps, L.hidden, xs,
+                       blockIdx.x == 0 && blockIdx.y == 0 ? x_out : nullptr, red);
+    __syncthreads();                                      // tables (and the normalised x) built
+    if constexpr (NORM) take_x(reinterpret_cast<const __half*>(xs));
     // a lane whose sub-block, row or expert is out of range contributes nothing (scale 0)
     float dv[4][T];
 #pragma unroll
@@ -321,10 +341,16 @@ bool check_cb(const char* who, int k, int hidden, int inter, const void* pool, i
 }
 
 template <int T>
-int up_t(const __half* x, const uint8_t* pool, size_t stride, const uint32_t* slots, int n_slots, int k,
-         const CbLayout& L, const uint8_t* grid, uint16_t* h_out, hipStream_t s) {
+int up_t(const __half* x, const float* h_in, const __half* norm_w, float eps, __half* x_out, const uint8_t* pool,
+         size_t stride, const uint32_t* slots, int n_slots, int k, const CbLayout& L, const uint8_t* grid,
+         uint16_t* h_out, hipStream_t s) {
     dim3 g((L.inter + kUpRowsPerBlock - 1) / kUpRowsPerBlock, k);
-    MOE_LAUNCH(TK_CB_UP, (k_cb_up<T>), g, dim3(256), 0, s, x, pool, stride, slots, n_slots, L, grid, h_out);
+    if (h_in)
+        MOE_LAUNCH(TK_CB_UP, (k_cb_up<T, true>), g, dim3(256), 0, s, x, h_in, norm_w, eps, x_out, pool, stride, slots,
+                   n_slots, L, grid, h_out);
+    else
+        MOE_LAUNCH(TK_CB_UP, (k_cb_up<T, false>), g, dim3(256), 0, s, x, h_in, norm_w, eps, x_out, pool, stride, slots,
+                   n_slots, L, grid, h_out);
     HIP_TRY(hipGetLastError());
     return 0;
 }
@@ -342,16 +368,34 @@ int down_t(const uint16_t* h, const uint8_t* pool, size_t stride, const uint32_t
 
 }  // namespace
 
+namespace {
+
+int up_any(const __half* x, const float* h_in, const __half* norm_w, float eps, __half* x_out, const uint8_t* pool,
+           size_t stride, int n_slots, const uint32_t* slots, int k, int hidden, int inter, const uint8_t* grid,
+           uint16_t* h_out, hipStream_t s) {
+    const CbLayout L = cb_layout(hidden, inter);
+    switch ((hidden / 32 + 31) / 32) {
+        case 1: return up_t<1>(x, h_in, norm_w, eps, x_out, pool, stride, slots, n_slots, k, L, grid, h_out, s);
+        case 2: return up_t<2>(x, h_in, norm_w, eps, x_out, pool, stride, slots, n_slots, k, L, grid, h_out, s);
+        case 3: return up_t<3>(x, h_in, norm_w, eps, x_out, pool, stride, slots, n_slots, k, L, grid, h_out, s);
+        default: return up_t<4>(x, h_in, norm_w, eps, x_out, pool, stride, slots, n_slots, k, L, grid, h_out, s);
+    }
+}
+
+}  // namespace
+
 int launch_cb_up(const __half* x, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots, int k,
                  int hidden, int inter, const uint8_t* grid, uint16_t* h_out, hipStream_t s) {
     if (!check_cb("cb_up", k, hidden, inter, pool, n_slots, stride, slots, grid, x, h_out)) return -1;
-    const CbLayout L = cb_layout(hidden, inter);
-    switch ((hidden / 32 + 31) / 32) {
-        case 1: return up_t<1>(x, pool, stride, slots, n_slots, k, L, grid, h_out, s);
-        case 2: return up_t<2>(x, pool, stride, slots, n_slots, k, L, grid, h_out, s);
-        case 3: return up_t<3>(x, pool, stride, slots, n_slots, k, L, grid, h_out, s);
-        default: return up_t<4>(x, pool, stride, slots, n_slots, k, L, grid, h_out, s);
-    }
+    return up_any(x, nullptr, nullptr, 0.f, nullptr, pool, stride, n_slots, slots, k, hidden, inter, grid, h_out, s);
+}
+
+int launch_cb_up_norm(const float* h_in, const __half* norm_w, float eps, __half* x_out, const uint8_t* pool,
+                      size_t stride, int n_slots, const uint32_t* slots, int k, int hidden, int inter,
+                      const uint8_t* grid, uint16_t* h_out, hipStream_t s) {
+    if (!check_cb("cb_up_norm", k, hidden, inter, pool, n_slots, stride, slots, grid, h_in, h_out)) return -1;
+    if (!x_out) { moe_set_error("cb_up_norm: x_out is null"); return -1; }
+    return up_any(nullptr, h_in, norm_w, eps, x_out, pool, stride, n_slots, slots, k, hidden, inter, grid, h_out, s);
 }
 
 int launch_cb_down(const uint16_t* h, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots,

@@ -242,6 +242,9 @@ int launch_q2t_grouped_down(const __half* h, int n_rows, const int32_t* row_out,
                             int n_slots, int hidden, int inter, int group, __half* y_out, hipStream_t s);
 int launch_cb_up(const __half* x, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots, int k,
                  int hidden, int inter, const uint8_t* grid, uint16_t* h_out, hipStream_t s);
+int launch_cb_up_norm(const float* h_in, const __half* norm_w, float eps, __half* x_out, const uint8_t* pool,
+                      size_t stride, int n_slots, const uint32_t* slots, int k, int hidden, int inter,
+                      const uint8_t* grid, uint16_t* h_out, hipStream_t s);
 int launch_cb_down(const uint16_t* h, const uint8_t* pool, size_t stride, int n_slots, const uint32_t* slots,
                    const __half* scores, int k, int hidden, int inter, const uint8_t* grid, const __half* residual,
                    float* y_out, int per_expert, hipStream_t s);

@@ -28,6 +28,7 @@
 
 #include "lane_reduce.h"
 #include "moe_common.h"
+#include "norm_f64.h"
 #include "route_select.h"
 #include "slot_table_dev.h"
 
@@ -46,52 +47,11 @@ constexpr int kMaxHidden = 4096;
 // A zeroed table, read (never written) by the last block in place of a missing one.
 __device__ SlotTable g_no_table;
 
-// fp64 RMSNorm of h (fp32 [hidden]) into fp16 bits in LDS; every block computes it.
-// Thread tid owns elements 4 (c kThreads + tid) + 0..3 for chunk c (hidden is a multiple of 8).
-// The loads are issued by the caller, all of them before the weight loads (loads retire in
-// issue order), so the normalisation overlaps the weights' flight.
-constexpr int kNormChunks = kMaxHidden / (4 * kThreads);
-struct NormIn {
-    float4 hv[kNormChunks];
-    uint2 w2[kNormChunks];
-};
-
-__device__ void norm_finish(const NormIn& in, bool has_w, float eps, int hidden, uint16_t* xs, __half* x_out,
-                            double* red) {
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    double ss = 0.0;
-#pragma unroll
-    for (int c = 0; c < kNormChunks; ++c) {
-        if (4 * (c * kThreads + tid) >= hidden) continue;
-        const double a = in.hv[c].x, b = in.hv[c].y, d = in.hv[c].z, e = in.hv[c].w;
-        ss += a * a;
-        ss += b * b;
-        ss += d * d;
-        ss += e * e;
-    }
-    ss = wave_sum_f64(ss);
-    if (lane == 0) red[wv] = ss;
-    __syncthreads();
-    const double tot = red[0] + red[1] + red[2] + red[3];
-    const double denom = sqrt(tot / hidden + (double)eps);
-#pragma unroll
-    for (int c = 0; c < kNormChunks; ++c) {
-        const int i = 4 * (c * kThreads + tid);
-        if (i >= hidden) continue;
-        const float hh[4] = {in.hv[c].x, in.hv[c].y, in.hv[c].z, in.hv[c].w};
-        const uint32_t ww[2] = {in.w2[c].x, in.w2[c].y};
-        uint16_t b[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            double v = (double)hh[j] / denom;
-            if (has_w) v *= (double)__half2float(__ushort_as_half((uint16_t)(ww[j >> 1] >> (16 * (j & 1)))));
-            b[j] = f64_to_f16_bits(v);
-        }
-        const uint2 packed = make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
-        *reinterpret_cast<uint2*>(&xs[i]) = packed;
-        if (x_out) *reinterpret_cast<uint2*>(x_out + i) = packed;
-    }
-}
+// The RMSNorm prologue (every block computes it) is norm64::finish over chunks this kernel loads
+// itself, ahead of its weight loads.
+using norm64::NormIn;
+constexpr int kNormChunks = norm64::kChunks;
+static_assert(norm64::kThreads == kThreads && norm64::kMaxHidden == kMaxHidden, "norm block shape");
 
 // NC = 16-byte weight units per lane and row: hidden <= 512 * NC.  NORM: the input is h (fp32,
 // normalised here) rather than x (fp16); a compile-time choice, so that no branch lets the
@@ -145,7 +105,7 @@ __global__ __launch_bounds__(kThreads) void k_router(
     __builtin_amdgcn_sched_barrier(0);   // every weight load issued before anything waits
 
     if constexpr (NORM) {
-        norm_finish(nin, norm_w != nullptr, eps, hidden, xs, (x_out && blockIdx.x == 0) ? x_out : nullptr, red);
+        norm64::finish(nin, norm_w != nullptr, eps, hidden, xs, (x_out && blockIdx.x == 0) ? x_out : nullptr, red);
     } else {
 #pragma unroll
         for (int c = 0; c < kNormChunks; ++c) {
@@ -274,15 +234,8 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ 
     __shared__ __align__(16) uint16_t xs[kMaxHidden];
     __shared__ double red[kThreads / 64];
     NormIn nin;
-    const __half* wsrc = norm_w ? norm_w : reinterpret_cast<const __half*>(h_in);
-#pragma unroll
-    for (int c = 0; c < kNormChunks; ++c) {
-        const int i = 4 * (c * kThreads + threadIdx.x);
-        const int ic = i < hidden ? i : hidden - 4;
-        nin.hv[c] = *reinterpret_cast<const float4*>(h_in + ic);
-        nin.w2[c] = *reinterpret_cast<const uint2*>(wsrc + ic);
-    }
-    norm_finish(nin, norm_w != nullptr, eps, hidden, xs, x_out, red);
+    norm64::load(nin, h_in, norm_w, hidden);
+    norm64::finish(nin, norm_w != nullptr, eps, hidden, xs, x_out, red);
 }
 
 __global__ void k_f64_to_f16(const double* __restrict__ in, uint16_t* __restrict__ out, int n) {

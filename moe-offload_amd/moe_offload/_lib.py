@@ -99,6 +99,8 @@ SIGNATURES: dict[str, tuple] = {
                              _c_int, _c_vp]),
     "moe_cb_moe": (_c_int, [_c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_vp,
                             _c_vp, _c_int, _c_vp]),
+    "moe_cb_moe_norm": (_c_int, [_c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_vp, _c_int,
+                                 _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp]),
     "moe_pair_combine": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
     # no reference counterpart
     "c_last_error": (ctypes.c_char_p, []),

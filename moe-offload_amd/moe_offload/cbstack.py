@@ -8,6 +8,9 @@ normalised), and an fp16 RMSNorm after it (builder glue, as in `stack.py`):
     h_l     = x_l + sum_j scores_j * down_j(relu(up_j x_l)^2)      (fp32)
     x_{l+1} = RMSNorm(h_l)                                          (fp16, eps 1e-6)
 
+A layer is two launches: the up-projection of layer l > 0 normalises h_{l-1} itself
+(`moe_cb_moe_norm`), so only the last layer's output needs a standalone RMSNorm.
+
 Every layer keeps `capacity` slots in HBM (the expert-cache budget split evenly over the
 layers), fed from a pinned host store; the slot tables are device-driven (same decisions as the
 reference's expert_io.c LRU) and misses are staged by the staging kernel.  No prefetch: the
@@ -122,12 +125,21 @@ class CodebookStack:
                 _lib.check(L.c_layer_step_decode_dev(self.cidx(l), self.ids[l].data_ptr(), c.top_k, c.stage_ctas,
                                                      stream), "step_dev")
                 pool, n_slots, slots = self.pools[l], self.capacity, self.slot_inds[l]
-            _lib.check(L.moe_cb_moe(self.xs[l].data_ptr(), pool.data_ptr(), self.blob_bytes, n_slots, slots.data_ptr(),
-                                    self.scores[l].data_ptr(), c.top_k, c.hidden, c.inter, self.grid.data_ptr(),
-                                    self.xs[l].data_ptr(), self.h_ws.data_ptr(), self.hs[l].data_ptr(), 0, stream),
-                       "cb_moe")
-            _lib.check(L.moe_rmsnorm(self.hs[l].data_ptr(), self.norm_w[l].data_ptr(), c.eps, c.hidden,
-                                     self.xs[l + 1].data_ptr(), stream), "rmsnorm")
+            if l == 0:
+                _lib.check(L.moe_cb_moe(self.xs[0].data_ptr(), pool.data_ptr(), self.blob_bytes, n_slots,
+                                        slots.data_ptr(), self.scores[0].data_ptr(), c.top_k, c.hidden, c.inter,
+                                        self.grid.data_ptr(), self.xs[0].data_ptr(), self.h_ws.data_ptr(),
+                                        self.hs[0].data_ptr(), 0, stream), "cb_moe")
+            else:
+                # x_l = RMSNorm(h_{l-1}) inside the up-projection (also written to xs[l])
+                _lib.check(L.moe_cb_moe_norm(self.hs[l - 1].data_ptr(), self.norm_w[l - 1].data_ptr(), c.eps,
+                                             self.xs[l].data_ptr(), pool.data_ptr(), self.blob_bytes, n_slots,
+                                             slots.data_ptr(), self.scores[l].data_ptr(), c.top_k, c.hidden, c.inter,
+                                             self.grid.data_ptr(), self.h_ws.data_ptr(), self.hs[l].data_ptr(),
+                                             stream), "cb_moe_norm")
+        n = c.n_layers
+        _lib.check(L.moe_rmsnorm(self.hs[n - 1].data_ptr(), self.norm_w[n - 1].data_ptr(), c.eps, c.hidden,
+                                 self.xs[n].data_ptr(), stream), "rmsnorm")
 
     def capture_graph(self):
         torch.cuda.synchronize()

@@ -100,3 +100,61 @@ def test_codebook_rejects_bad_shapes(grid_dev):
     assert L.moe_cb_up(x.data_ptr(), pool.data_ptr(), pool.shape[1], 2, s.data_ptr(), 2, 3000, 1536,
                        grid_dev.data_ptr(), h.data_ptr(), 0) == -1          # not a multiple of 256
     L.c_clear_error()
+
+
+@pytest.mark.parametrize("hidden,inter,k,with_w", [(3072, 1536, 9, True), (1024, 512, 4, False), (4096, 2048, 16, True)])
+def test_norm_fused_layer_equals_rmsnorm_then_moe(grid_dev, hidden, inter, k, with_w):
+    """moe_cb_moe_norm (RMSNorm inside the up-projection) gives bit for bit the x of moe_rmsnorm
+    (and the oracle's fp64 norm rounded once) and the y of moe_cb_moe on that x."""
+    import ctypes
+
+    from moe_offload import _lib
+    from oracle import q2
+    L = _lib.lib()
+    n_exp = 24
+    pool = torch.from_numpy(random_pool(n_exp, hidden, inter, seed=hidden + k)).cuda()
+    rng = np.random.default_rng(k)
+    ids = torch.from_numpy(rng.choice(n_exp, size=k, replace=False).astype(np.int32)).cuda()
+    scores = torch.from_numpy(rng.random(k).astype(np.float16)).cuda()
+    h = torch.from_numpy((rng.standard_normal(hidden) * 3).astype(np.float32)).cuda()
+    w = torch.from_numpy((1 + 0.1 * rng.standard_normal(hidden)).astype(np.float16)).cuda() if with_w else None
+    wp = w.data_ptr() if with_w else None
+    stride = pool.shape[1]
+    s = torch.cuda.current_stream().cuda_stream
+    eps = 1e-6
+    x_ref = torch.zeros(hidden, dtype=torch.float16, device="cuda")
+    y_ref = torch.zeros(hidden, dtype=torch.float32, device="cuda")
+    ws = torch.zeros(k * inter, dtype=torch.bfloat16, device="cuda")
+    _lib.check(L.moe_rmsnorm(h.data_ptr(), wp, eps, hidden, x_ref.data_ptr(), s), "rmsnorm")
+    _lib.check(L.moe_cb_moe(x_ref.data_ptr(), pool.data_ptr(), stride, n_exp, ids.data_ptr(), scores.data_ptr(), k,
+                            hidden, inter, grid_dev.data_ptr(), x_ref.data_ptr(), ws.data_ptr(), y_ref.data_ptr(), 0,
+                            s), "cb_moe")
+    for rep in range(2):                                  # the second call overwrites the first's outputs
+        x = torch.full((hidden,), float("nan"), dtype=torch.float16, device="cuda")
+        y = torch.full((hidden,), float("nan"), dtype=torch.float32, device="cuda")
+        ws2 = torch.zeros(k * inter, dtype=torch.bfloat16, device="cuda")
+        _lib.check(L.moe_cb_moe_norm(h.data_ptr(), wp, ctypes.c_float(eps), x.data_ptr(), pool.data_ptr(), stride,
+                                     n_exp, ids.data_ptr(), scores.data_ptr(), k, hidden, inter, grid_dev.data_ptr(),
+                                     ws2.data_ptr(), y.data_ptr(), s), "cb_moe_norm")
+        torch.cuda.synchronize()
+        assert torch.equal(x.view(torch.int16), x_ref.view(torch.int16)), rep
+        assert torch.equal(ws2.view(torch.int16), ws.view(torch.int16)), rep
+        assert torch.equal(y.view(torch.int32), y_ref.view(torch.int32)), rep
+    w64 = w.cpu().numpy() if with_w else np.ones(hidden, np.float16)
+    want_x = q2.round_to(q2.rmsnorm(h.cpu().numpy().astype(np.float64), w64, eps), "f16")
+    assert np.array_equal(x.cpu().numpy().astype(np.float64), want_x)
+
+
+def test_norm_fused_layer_rejects_bad_arguments(grid_dev):
+    import ctypes
+
+    from moe_offload import _lib
+    L = _lib.lib()
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    p = buf.data_ptr()
+    s = torch.cuda.current_stream().cuda_stream
+    f = ctypes.c_float(1e-6)
+    assert L.moe_cb_moe_norm(p, None, f, None, p, 4096, 4, p, p, 4, 1024, 512, grid_dev.data_ptr(), p, p, s) == -1
+    assert L.moe_cb_moe_norm(None, None, f, p, p, 4096, 4, p, p, 4, 1024, 512, grid_dev.data_ptr(), p, p, s) == -1
+    assert L.moe_cb_moe_norm(p, None, f, p, p, 4096, 4, p, p, 4, 1000, 512, grid_dev.data_ptr(), p, p, s) == -1
+    L.c_clear_error()
