@@ -19,9 +19,11 @@
 //                 grid (inter / 32, k).  h = relu(u)^2 is written as bf16 [k][inter] (fp32
 //                 range: a square can exceed fp16).
 //   k_cb_down<T>: 16 lanes per row, 8 output rows per block x all k experts (4 waves split the
-//                 experts, the next expert's codes and h slice loaded while the current one is
-//                 multiplied); the block reduces over experts in a fixed order and writes
-//                 y = residual + sum_j s_j y_j (fp32) or the per-expert rows.
+//                 experts: whole experts in rounds of 4, then the remaining experts' 4-row halves
+//                 dealt round robin, so no wave carries a whole expert more than another; the next
+//                 task's codes and h slice loaded while the current one is multiplied); the block
+//                 reduces over its waves in a fixed order and writes y = residual + sum_j s_j y_j
+//                 (fp32) or the per-expert rows.
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
 
@@ -235,6 +237,7 @@ __global__ __launch_bounds__(256) void k_cb_down(const uint16_t* __restrict__ h,
                                                  const __half* __restrict__ scores, int k, CbLayout L,
                                                  const uint8_t* __restrict__ grid, const __half* __restrict__ residual,
                                                  float* __restrict__ y_out, int per_expert) {
+    constexpr int kMaxTasks = (MOE_MAX_K + 3) / 4 + 1;
     __shared__ uint4 gtab[256];
     __shared__ uint4 stab[128];
     __shared__ float red[4][kDownRows];
@@ -244,18 +247,38 @@ __global__ __launch_bounds__(256) void k_cb_down(const uint16_t* __restrict__ h,
     const int row0 = blockIdx.x * kDownRows;
     const uint2 gentry = reinterpret_cast<const uint2*>(grid)[tid];     // blockDim == 256
 
-    // Wave wv takes experts wv, wv + 4, ... (k <= 16: at most 4); the next expert's operands are
-    // loaded while the current one is multiplied.  Loads are unconditional from clamped
-    // addresses (see k_cb_up).
-    auto load = [&](int jj, DownLoad<T>& b) {
-        const uint32_t slot = slots[jj];
+    // The wave's tasks, in order: whole experts wv, wv + 4, ... (every expert when rows per expert
+    // are written; else only the k / 4 full rounds), then the remaining experts' row halves
+    // (4 rows each) dealt round robin, so no wave multiplies more than a half expert beyond the
+    // others.  The next task's operands are loaded while the current one is multiplied.
+    const int nfull = per_expert ? 0 : k / 4;
+    const int nwhole = per_expert ? (k > wv ? (k - wv + 3) / 4 : 0) : nfull;
+    const int nhalf_all = per_expert ? 0 : 2 * (k - 4 * nfull);
+    const int ntask = nwhole + (nhalf_all > wv ? (nhalf_all - wv + 3) / 4 : 0);
+    auto task = [&](int tk, int& e, int& hsel) {           // hsel -1: both row halves
+        if (tk < nwhole) {
+            e = wv + 4 * tk;
+            hsel = -1;
+        } else {
+            const int idx = wv + 4 * (tk - nwhole);
+            e = 4 * nfull + (idx >> 1);
+            hsel = idx & 1;
+        }
+        e = e < k ? e : k - 1;                             // a task past the wave's last reloads it
+    };
+    // Loads are unconditional from clamped addresses (see k_cb_up); a half task loads its rows
+    // into both row slots.
+    auto load = [&](int tk, DownLoad<T>& b) {
+        int e, hsel;
+        task(tk, e, hsel);
+        const uint32_t slot = slots[e];
         b.ok = slot < (uint32_t)n_slots;
         const uint8_t* blob = pool + (size_t)(b.ok ? slot : 0) * stride;
         const uint2* qs = reinterpret_cast<const uint2*>(blob + L.down_qs);
         const uint16_t* dd = reinterpret_cast<const uint16_t*>(blob + L.down_d);
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
-            const int row = row0 + 4 * it + rsel;
+            const int row = row0 + 4 * (hsel < 0 ? it : hsel) + rsel;
             const int rc = row < hidden ? row : hidden - 1;
 #pragma unroll
             for (int t = 0; t < T; ++t) {
@@ -268,7 +291,7 @@ __global__ __launch_bounds__(256) void k_cb_down(const uint16_t* __restrict__ h,
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int sc = li + 16 * t < nsub ? li + 16 * t : nsub - 1;
-            const uint4* hp = reinterpret_cast<const uint4*>(h + (size_t)jj * inter + (size_t)sc * 32);
+            const uint4* hp = reinterpret_cast<const uint4*>(h + (size_t)e * inter + (size_t)sc * 32);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const uint4 u = hp[v];
@@ -279,23 +302,35 @@ __global__ __launch_bounds__(256) void k_cb_down(const uint16_t* __restrict__ h,
             }
         }
     };
+    // every task's score, read unconditionally (any k halves stand in for absent scores)
+    const __half* sp = scores ? scores : reinterpret_cast<const __half*>(grid);
+    float sjv[kMaxTasks];
+#pragma unroll
+    for (int tk = 0; tk < kMaxTasks; ++tk) {
+        int e, hsel;
+        task(tk, e, hsel);
+        const float sv = __half2float(sp[e]);
+        sjv[tk] = scores ? sv : 1.0f;
+    }
 
     DownLoad<T> buf[2];
-    if (wv < k) load(wv, buf[0]);
+    load(0, buf[0]);
     build_tables(gentry, gtab, stab, tid, true);
     __syncthreads();
 
     float acc[2] = {0.f, 0.f};
 #pragma unroll
-    for (int qi = 0; qi < (MOE_MAX_K + 3) / 4; ++qi) {
-        const int jj = wv + 4 * qi;
-        if (jj >= k) break;
-        if (jj + 4 < k) load(jj + 4, buf[(qi + 1) & 1]);
-        const DownLoad<T>& b = buf[qi & 1];
-        const float sj = scores ? __half2float(scores[jj]) : 1.0f;
+    for (int tk = 0; tk < kMaxTasks; ++tk) {
+        if (tk >= ntask) break;                            // wave-uniform
+        if (tk + 1 < kMaxTasks) load(tk + 1, buf[(tk + 1) & 1]);
+        const DownLoad<T>& b = buf[tk & 1];
+        int e, hsel;
+        task(tk, e, hsel);
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
-            const int row = row0 + 4 * it + rsel;
+            if (hsel >= 0 && it == 1) break;               // a half task has one row slot
+            const int rit = hsel < 0 ? it : hsel;
+            const int row = row0 + 4 * rit + rsel;
             float part = 0.f;
 #pragma unroll
             for (int t = 0; t < T; ++t) {
@@ -305,9 +340,11 @@ __global__ __launch_bounds__(256) void k_cb_down(const uint16_t* __restrict__ h,
             }
             part = lanes::group_sum<16>(part);
             if (per_expert) {
-                if (li == 0 && row < hidden) y_out[(size_t)jj * hidden + row] = part;
+                if (li == 0 && row < hidden) y_out[(size_t)e * hidden + row] = part;
             } else {
-                acc[it] += sj * part;
+                const float c = sjv[tk] * part;
+                acc[0] += rit == 0 ? c : 0.f;
+                acc[1] += rit == 1 ? c : 0.f;
             }
         }
     }
