@@ -471,11 +471,12 @@ def launch_floor(byte_counts, grids=(320, 640, 1280, 2560), reps=50):
     return res
 
 
-def gemv_loop_timing(st, tokens=8, warm=2):
+def gemv_loop_timing(st, tokens=8, warm=2, repeats=3):
     """Average duration of k_q2_gate_up and k_q2_down launched back to back at the decode shape:
     for each of `tokens` fresh top-k draws and each of the resident stack's layers (its own 503 MB
     pool, so the bytes come from HBM, not the 256 MB MALL), one launch; the run of launches is
-    bracketed by two HIP events on the launch stream and divided by the count.  Per-launch
+    bracketed by two HIP events on the launch stream and divided by the count; the median of
+    `repeats` such runs is reported (each run's figure beside it).  Per-launch
     begin/end stamps are not used here: a kernel's begin stamp can precede the end of the kernel
     queued before it, so stamped durations of a mixed sequence overlap and sum to more than the
     wall time (the decode pass's stamped figures are reported beside these)."""
@@ -511,13 +512,17 @@ def gemv_loop_timing(st, tokens=8, warm=2):
     for name, fn in (("gate_up", gate_up), ("down", down)):
         for i in range(warm * c.n_layers):
             fn(n - 1 - i)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for i in range(n):
-            fn(i)
-        e1.record(s)
-        e1.synchronize()
-        out[name] = e0.elapsed_time(e1) * 1e3 / n
+        per = []
+        for _ in range(repeats):                        # the median of `repeats` bracketed loops
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for i in range(n):
+                fn(i)
+            e1.record(s)
+            e1.synchronize()
+            per.append(e0.elapsed_time(e1) * 1e3 / n)
+        out[name] = sorted(per)[len(per) // 2]
+        out[name + "_loops"] = [round(v, 3) for v in per]
     out["launches"] = n
     return out
 
@@ -548,7 +553,8 @@ def resident_pass(args, cfg, gen, n_tok, xs=None):
             "routed_frac_of_peak": round(routed * args.steps / r_elapsed / 1e9 / HBM_PEAK_GBS, 4),
             "kernels_us": {k: round(v["avg_us"], 3) for k, v in res_k.items() if v["launches"]},
             "gemv_back_to_back_us": {"gate_up": round(loop["gate_up"], 3), "down": round(loop["down"], 3),
-                                     "launches": loop["launches"]},
+                                     "launches": loop["launches"], "gate_up_loops": loop["gate_up_loops"],
+                                     "down_loops": loop["down_loops"]},
             "_gu_avg": gu_avg, "_dn_avg": dn_avg, "_gu_bytes": gu_bytes, "_dn_bytes": dn_bytes, "_kernels": res_k,
             "_routed": routed, "_elapsed": r_elapsed}
 
@@ -733,7 +739,7 @@ def main():
                      "kernel": "k_q2_gate_up",
                      "measured_in": f"resident stack (all experts in HBM): {res['gemv_back_to_back_us']['launches']} "
                                     "launches back to back over the 48 layer pools, fresh top-10 draws, bracketed "
-                                    "by HIP events on the launch stream",
+                                    "by HIP events on the launch stream; median of 3 such runs",
                      "bytes_per_launch": gu_bytes, "avg_launch_us": round(gu_avg * 1e6, 3),
                      "launch_floor_us": round(floor_us, 3),
                      "frac_of_launch_floor": round(floor_us / (gu_avg * 1e6), 4)},
