@@ -11,6 +11,8 @@
 // stays busy while the GLU and the next router run).  Layer 0's experts are all resident.
 #include <string.h>
 
+#include <chrono>
+
 #include "moe_common.h"
 #include "moe_offload.h"
 
@@ -19,15 +21,24 @@ namespace {
 hipEvent_t g_router_done = nullptr;
 
 // The router event has fired (the ids and predictions are in host memory).  Spins on the event:
-// the wait is a few microseconds and sits on the token's critical path.
+// the wait is a few microseconds and sits on the token's critical path.  A router that has not
+// finished after kRouterWaitSec (a stalled device) is reported as an error instead of spinning on.
+constexpr double kRouterWaitSec = 10.0;
+
 int wait_router(hipStream_t s) {
     if (!g_router_done) HIP_TRY(hipEventCreateWithFlags(&g_router_done, hipEventDisableTiming));
     HIP_TRY(hipEventRecord(g_router_done, s));
-    for (;;) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (uint32_t n = 0;; ++n) {
         const hipError_t e = hipEventQuery(g_router_done);
         if (e == hipSuccess) return 0;
         if (e != hipErrorNotReady) {
             moe_set_error("runner: router event: %s", hipGetErrorString(e));
+            return -1;
+        }
+        if ((n & 1023u) == 1023u &&
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > kRouterWaitSec) {
+            moe_set_error("runner: the router has not finished after %.0f s", kRouterWaitSec);
             return -1;
         }
     }
