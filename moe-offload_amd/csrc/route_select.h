@@ -17,15 +17,18 @@ constexpr int kThreads = 256;                  // the selection runs on a block 
 constexpr int kMaxExperts = 1024;
 constexpr int kPer = kMaxExperts / kThreads;   // logits per thread
 
-// Wave-wide max of a uint32 with DPP inside each 16-lane row, then the four row results.
+// Wave-wide max of a uint32: DPP butterflies inside each 16-lane row, then the row pairs and the
+// wave halves exchanged with v_permlane16_swap / v_permlane32_swap, so every lane ends with the
+// maximum in a vector register (no readlane -> scalar -> vector round trip in a selection round).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
-    uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-    uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-    return max(max(a, b), max(c, d));
+    v = max(v, lanes::partner<1>(v));
+    v = max(v, lanes::partner<2>(v));
+    v = max(v, lanes::partner<4>(v));
+    v = max(v, lanes::partner<8>(v));
+    auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max((uint32_t)p[0], (uint32_t)p[1]);
+    p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max((uint32_t)p[0], (uint32_t)p[1]);
 }
 
 
