@@ -294,3 +294,75 @@ def test_set_format9_validates_roles_and_sizes():
     finally:
         L.c_layer_init(layer, -1, 16, None, None, None, 0)
         L.c_clear_error()
+
+
+# ---- the ctypes table against the header, argument by argument --------------------------------
+
+_FN_PTRS = {"moe_p1_reader_fn", "moe_p1_uniform_fn"}
+_C_KINDS = {"void": None, "float": "f32", "double": "f64", "int": "i32", "unsigned": "i32", "uint32_t": "i32",
+            "int32_t": "i32", "uint64_t": "i64", "int64_t": "i64", "size_t": "i64", "uint16_t": "i16"}
+
+
+def _c_kind(decl):
+    """Kind of one C parameter or return type: 'ptr', 'f32', 'f64', 'i16', 'i32', 'i64' or None (void)."""
+    decl = decl.strip()
+    words = decl.replace("*", " * ").replace("[", " [ ").split()
+    if "*" in words or "[" in words or any(w in _FN_PTRS for w in words):
+        return "ptr"
+    words = [w for w in words if w not in ("const", "struct")]
+    return _C_KINDS[words[0]]
+
+
+def _py_kind(t):
+    if t is None:
+        return None
+    if t in (ctypes.c_void_p, ctypes.c_char_p) or issubclass(t, (ctypes._Pointer, ctypes._CFuncPtr)):
+        return "ptr"
+    if t in (ctypes.c_float, ctypes.c_double):
+        return "f32" if t is ctypes.c_float else "f64"
+    return {2: "i16", 4: "i32", 8: "i64"}[ctypes.sizeof(t)]
+
+
+def header_declarations():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    out = {}
+    for m in re.finditer(r"([A-Za-z_][A-Za-z0-9_ *]*?)\s*\b((?:c|moe)_[a-z0-9_]+)\s*\(([^;{()]*)\)\s*;", text):
+        ret, name, params = m.group(1), m.group(2), m.group(3).strip()
+        plist = [] if params in ("", "void") else [p for p in params.split(",")]
+        out[name] = (_c_kind(ret), [_c_kind(p) for p in plist])
+    return out
+
+
+def test_ctypes_signatures_match_the_header():
+    """Every entry point's ctypes restype and argtypes have the header's count and kinds (pointer,
+    16/32/64-bit integer, float, double): a mismatch would pass wrong values without an error."""
+    decls = header_declarations()
+    assert sorted(decls) == declared_symbols()
+    bad = []
+    for name, (ret, args) in decls.items():
+        pret, pargs = _lib.SIGNATURES[name]
+        got = (_py_kind(pret), [_py_kind(a) for a in pargs])
+        if got != (ret, args):
+            bad.append((name, (ret, args), got))
+    assert not bad, bad
+
+
+def test_stack_descriptor_layout_matches_the_header():
+    """moe_stack_desc: the ctypes structure has the header's fields in order with the same kinds."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = re.search(r"typedef struct moe_stack_desc\s*\{(.*?)\}\s*moe_stack_desc\s*;", text, flags=re.S).group(1)
+    fields = []
+    for line in body.split(";"):
+        line = re.sub(r"//[^\n]*", "", line).strip()
+        if not line:
+            continue
+        # "int a, b, c" declares several fields of one type
+        m = re.match(r"((?:const\s+)?[A-Za-z_0-9]+\s*\**)\s*(.*)", line)
+        typ, rest = m.group(1), m.group(2)
+        for nm in rest.split(","):
+            nm = nm.strip()
+            stars = nm.count("*")
+            fields.append((nm.lstrip("*").strip(), _c_kind(typ + "*" * stars)))
+    got = [(n, _py_kind(t)) for n, t in _lib.StackDesc._fields_]
+    assert got == fields
