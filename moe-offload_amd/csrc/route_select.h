@@ -31,6 +31,18 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return max((uint32_t)p[0], (uint32_t)p[1]);
 }
 
+// Wave-wide min of a uint32, the same butterflies.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, lanes::partner<1>(v));
+    v = min(v, lanes::partner<2>(v));
+    v = min(v, lanes::partner<4>(v));
+    v = min(v, lanes::partner<8>(v));
+    auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = min((uint32_t)p[0], (uint32_t)p[1]);
+    p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return min((uint32_t)p[0], (uint32_t)p[1]);
+}
+
 
 // f64 -> f16 with a single round-to-nearest-even: truncate to f32, set the sticky bit when
 // inexact (round-to-odd with 24 >= 11 + 2 bits), then let the f32 -> f16 conversion round.
@@ -45,8 +57,13 @@ __device__ __forceinline__ float round_f16(double v) {
 }
 
 // The n largest keys of keys[lo, hi) (LDS; distinct, 0 = empty) by one wave: lane r < n gets
-// the r-th largest (0 once the range runs out).  KPL keys per lane cover the range; each round
-// takes the wave maximum and clears it where it sits.
+// the r-th largest (0 once the range runs out).  KPL keys per lane cover the range.  The keys
+// are distinct except for zeros (padding, and a zero gate of expert 0), so round r > 0 picks the
+// largest key below the previous pick b: with d = (b - 1) - key in unsigned arithmetic, every key
+// below b gives d < b and every other key d >= b, so the pick is b - 1 - (wave minimum of d).  A
+// pick of 0 stays 0 (all later ranks are 0 keys).  No key is rewritten, so a round is one
+// subtraction per key, a minimum tree and the wave minimum.  When no key is left below the pick
+// (more ranks than keys), the pick is 0, as once the keys run out.
 template <int KPL>
 __device__ __forceinline__ uint32_t wave_topn_k(const uint32_t* keys, int lo, int hi, int n, int lane) {
     uint32_t key[KPL];
@@ -55,14 +72,18 @@ __device__ __forceinline__ uint32_t wave_topn_k(const uint32_t* keys, int lo, in
         const int idx = lo + lane + 64 * i;
         key[i] = idx < hi ? keys[idx] : 0u;
     }
-    uint32_t mine = 0;
-    for (int r = 0; r < n; ++r) {
-        uint32_t best = key[0];
+    uint32_t best = key[0];
 #pragma unroll
-        for (int i = 1; i < KPL; ++i) best = max(best, key[i]);
-        best = wave_max_u32(best);
+    for (int i = 1; i < KPL; ++i) best = max(best, key[i]);
+    best = wave_max_u32(best);
+    uint32_t mine = lane == 0 ? best : 0u;
+    for (int r = 1; r < n; ++r) {
+        const uint32_t bm1 = best - 1u;
+        uint32_t d = bm1 - key[0];
 #pragma unroll
-        for (int i = 0; i < KPL; ++i) key[i] = key[i] == best ? 0u : key[i];
+        for (int i = 1; i < KPL; ++i) d = min(d, bm1 - key[i]);
+        d = wave_min_u32(d);
+        best = (best == 0u || d >= best) ? 0u : bm1 - d;      // d >= best: no key left below
         if (lane == r) mine = best;
     }
     return mine;
