@@ -68,6 +68,7 @@ __device__ __forceinline__ void gate_up_body(
     __builtin_amdgcn_sched_barrier(0);
 
     uint32_t slot;
+    uint32_t top_key = 0;                              // routed, wave 0: lane r's r-th largest key
     if constexpr (ROUTED) {
         __shared__ uint32_t keys[route::kMaxExperts];
         __shared__ double redm[4], reds[4];
@@ -79,17 +80,11 @@ __device__ __forceinline__ void gate_up_body(
             lraw[i] = logits[e < n_slots ? e : 0];
         }
         route::gate_keys(lraw, n_slots, keys, redm, reds);
+        // the ids first; the scores (only block (0, 0) writes them) wait until the weight loads
+        // are in flight
         if (wv == 0) {
-            uint32_t id;
-            __half sc;
-            const int pos = route::select_topk(keys, ((n_slots + 63) / 64) * 64, k, lane, id, sc);
-            if (pos >= 0) {
-                sel[pos] = id;
-                if (blockIdx.x == 0 && blockIdx.y == 0) {
-                    ids_out[pos] = id;
-                    scores_out[pos] = sc;
-                }
-            }
+            top_key = route::wave_topn(keys, 0, ((n_slots + 63) / 64) * 64, k, lane);
+            if (lane < k) sel[k - 1 - lane] = top_key & 0xFFFFu;
         }
         __syncthreads();
         slot = sel[j];
@@ -114,6 +109,17 @@ __device__ __forceinline__ void gate_up_body(
         sb[it] = sbv[(size_t)row * GPR + g];
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (ROUTED) {
+        if (wv == 0 && blockIdx.x == 0 && blockIdx.y == 0) {
+            uint32_t id;
+            __half sc;
+            const int pos = route::topk_scores(top_key, k, lane, id, sc);
+            if (pos >= 0) {
+                ids_out[pos] = id;
+                scores_out[pos] = sc;
+            }
+        }
+    }
 
     stage_pairs(xlo, xhi, tid < n_units, xp[uc >> 2], xc[uc >> 2], uc & 3, (uc >> 2) & 7);
     __builtin_amdgcn_sched_barrier(0);                  // no weight use ahead of the barrier

@@ -144,14 +144,10 @@ __device__ __forceinline__ void gate_keys(const float (&lraw)[kPer], int n_exp, 
     __syncthreads();
 }
 
-// One wave: the selection from the keys.  Lane r < k returns the id and score that go to output
-// position k - 1 - r (ascending gate order); other lanes return position -1.
-__device__ __forceinline__ int select_topk(const uint32_t* keys, int n_pad, int k, int lane, uint32_t& id,
-                                           __half& score) {
-    // Top-k by rounds of wave maxima, one wave over all keys: a round is a short dependent chain,
-    // and splitting the keys over waves adds a barrier and a second selection over the
-    // candidates, which costs more than it saves.
-    const uint32_t mine = wave_topn(keys, 0, n_pad, k, lane);  // lane j: the j-th largest
+// One wave, from the k largest keys (lane r holds the r-th largest, wave_topn): the id and score
+// that go to output position k - 1 - r (ascending gate order) for lanes r < k; position -1 for the
+// other lanes.
+__device__ __forceinline__ int topk_scores(uint32_t mine, int k, int lane, uint32_t& id, __half& score) {
     const float g = __half2float(__ushort_as_half((uint16_t)(mine >> 16)));
     // left-to-right sum over ascending order, each partial rounded to fp16; the gates are fp16
     // values in ascending order, so every partial sum is exact in fp32 before rounding
@@ -163,6 +159,16 @@ __device__ __forceinline__ int select_topk(const uint32_t* keys, int n_pad, int 
     id = mine & 0xFFFFu;
     score = __float2half_rn(g / s);                    // correctly rounded f32 division, then f16
     return lane < k ? k - 1 - lane : -1;
+}
+
+// One wave: the selection from the keys.  Lane r < k returns the id and score that go to output
+// position k - 1 - r (ascending gate order); other lanes return position -1.
+__device__ __forceinline__ int select_topk(const uint32_t* keys, int n_pad, int k, int lane, uint32_t& id,
+                                           __half& score) {
+    // Top-k by rounds of wave maxima, one wave over all keys: a round is a short dependent chain,
+    // and splitting the keys over waves adds a barrier and a second selection over the
+    // candidates, which costs more than it saves.
+    return topk_scores(wave_topn(keys, 0, n_pad, k, lane), k, lane, id, score);
 }
 
 }  // namespace route
