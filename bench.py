@@ -33,7 +33,7 @@ HBM_PEAK_GBS = 8000.0
 # roofline pass of this build (median over 480 dispatches: 3,250.5 KiB fetched x 2 + 20 KiB
 # written, the factors from a known-size copy), profiles/q2_gemv_roofline_loop_rocprof.md; a
 # counter run cannot happen inside bench, so the line names where the figure comes from.
-GATE_UP_TRAFFIC_BYTES = 6_677_504
+GATE_UP_TRAFFIC_BYTES = 6_676_480
 GATE_UP_TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over bench.py --only roofline, scaled by "
                           "moe_calibrate_copy (profiles/q2_gemv_roofline_loop_rocprof.md)")
 
