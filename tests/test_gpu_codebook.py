@@ -68,13 +68,18 @@ def test_codebook_moe_at_the_nemotron_shape(grid_dev):
     assert_close_rms(y, want, 1e-2, "combine (fp64)")
 
 
-@pytest.mark.parametrize("hidden,inter,k", [(256, 256, 1), (512, 256, 16), (1024, 768, 5), (4096, 2048, 12)])
+# k covers every remainder of k mod 4: the down kernel gives its 4 waves whole experts in rounds of
+# four and deals the remaining experts' row halves round robin (k = 1..3 are remainders only)
+@pytest.mark.parametrize("hidden,inter,k", [(256, 256, 1), (512, 256, 16), (1024, 768, 5), (4096, 2048, 12),
+                                            (256, 256, 2), (256, 256, 3), (512, 512, 6), (512, 512, 7),
+                                            (768, 512, 10), (768, 512, 11), (1024, 256, 14), (1024, 256, 15)])
 def test_codebook_moe_shapes(grid_dev, hidden, inter, k):
     x, ids, scores, res, y, yp, experts, grid, _ = run_case(grid_dev, k + 2, hidden, inter, k, seed=hidden + k)
     want = cbo.moe_combine(x, ids, scores, experts, grid, residual=res, h_bf16=True)
     assert_close_rms(y, want, 1e-3, f"{hidden}x{inter} k={k}")
-    up, down = experts(int(ids[-1]))
-    assert_close_rms(yp[-1], cbo.expert(x, up, down, grid, h_bf16=True), 1e-3, "last expert")
+    for j in (0, k - 1):                                 # per-expert rows: first and last expert
+        up, down = experts(int(ids[j]))
+        assert_close_rms(yp[j], cbo.expert(x, up, down, grid, h_bf16=True), 1e-3, f"expert {j}")
 
 
 def test_codebook_out_of_range_slot_contributes_zero(grid_dev):
