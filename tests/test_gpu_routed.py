@@ -107,3 +107,35 @@ def test_resident_stack_routed_equals_router_path():
         for t in range(6):
             for a, b in zip(rec[t], ref[t]):
                 assert torch.equal(a, b), f"{key} token {t}"
+
+
+
+@pytest.mark.parametrize("n_exp,k,peaks", [(512, 10, {5: 30.0, 200: 25.0}), (16, 16, {3: 30.0}), (100, 12, {99: 40.0})])
+def test_peaked_softmax_selects_zero_gates_by_descending_id(n_exp, k, peaks):
+    """A router whose softmax rounds all but one or two gates to fp16 zero: the other picks are
+    zero-gate experts, whose keys are their ids alone, taken by descending id (down to expert 0,
+    whose key equals the padding's, when k = n_exp).  The router's last block and the routed
+    gate/up both give the oracle's ids, scores and next-layer predictions (ties of equal logits)."""
+    from moe_offload import _lib, ops
+    L = _lib.lib()
+    hidden, inter = 256, 64
+    pool = _pool(n_exp, hidden, inter, seed=n_exp)
+    w = np.zeros((n_exp, hidden), np.float16)
+    for e, v in peaks.items():
+        w[e, 0] = v
+    x = np.zeros(hidden, np.float16)
+    x[0] = 1.0
+    wt, xt = torch.from_numpy(w).cuda(), torch.from_numpy(x).cuda()
+    a, b, logits = _both(L, wt, hidden, inter, n_exp, k, pool, x=xt)
+    want_i, want_s, _ = q2.route(q2.router_logits(x, w, "f16")[None], k, "f16")
+    zero = sorted(e for e in range(n_exp) if e not in peaks)[n_exp - len(peaks) - (k - len(peaks)):]
+    assert sorted(e for e in want_i[0].tolist() if e not in peaks) == zero      # the oracle's own rule
+    if k == n_exp:
+        assert 0 in want_i[0].tolist()
+    assert a[0].cpu().numpy().astype(np.int64).tolist() == want_i[0].astype(np.int64).tolist()
+    assert np.array_equal(a[1].cpu().numpy().astype(np.float64), want_s[0])
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) and torch.equal(a[2].view(-1), b[2])
+    m = min(12, n_exp)
+    _, _, pred = ops.router(wt, k, x=xt, w_next=wt, m=m)
+    want_p = q2.predict_topm(q2.router_logits(x, w, "f16")[None], m)
+    assert pred.cpu().numpy().tolist() == want_p[0].tolist()
