@@ -308,8 +308,7 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
     wall = (time.perf_counter() - t0) / iters
 
     # each step timed alone, `iters` times back to back, bracketed by two HIP events (per-launch
-    # stamps overlap the kernel queued before; gate/up is two launches: one-tile and longer
-    # segments)
+    # stamps overlap the kernel queued before)
     def bracketed(fn):
         s = torch.cuda.current_stream()
         fn()

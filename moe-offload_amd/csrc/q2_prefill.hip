@@ -9,14 +9,14 @@
 // with W = scale * q + bias per group of 64 inputs (2-bit codes, 16 per u32, LSB first).
 //
 // Tiling.  The rows of a segment form M tiles of 16 (v_mfma_f32_16x16x32_f16), taken in
-// batches of up to 4 tiles.  A block of 4 waves works on one segment and one slice of weight
+// batches of up to 2 tiles.  A block of 4 waves works on one segment and one slice of weight
 // rows; each wave owns 4 subtiles of 16 weight rows (gate/up: 2 x 16 rows of each projection =
 // 128 intermediate rows per block; down: 4 x 16 = 256 output rows).  Per 256-wide K chunk j a
 // lane (n = lane & 15, kq = lane >> 4) loads group 4j + kq of weight row n (one 16-byte load of
 // 64 codes plus the (scale, bias) word), dequantises it once and multiplies it into every tile
 // of the batch; the chunk's activations of the batch's rows are staged in LDS (each thread
-// stages 2 units of 16 bytes per tile).  The next chunk's weights are loaded while the current
-// chunk is multiplied.
+// stages 2 units of 16 bytes per tile).  The next chunk's weights and activations are loaded
+// while the current chunk is multiplied.
 //
 // Dequantisation.  A 2-bit code in the low bits of a nibble is the fp4 (e2m1) value q/2, so
 // w & 0x33333333 (even codes) and (w >> 2) & 0x33333333 (odd codes) are 8 fp4 values each;
@@ -87,12 +87,13 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// M tiles multiplied per pass over a segment's weights: 4 for gate/up (K = hidden: the long
-// contraction pays for the extra accumulators), 2 for down (a short K: every pass is two chunks of
-// dependent round trips, so fewer passes help; 4 tiles cost more in resident blocks than they save:
-// 62 us per 512-token chunk at 2, 70 at 1 and at 4).
+// M tiles multiplied per pass over a segment's weights: 2 for both projections.  Gate/up: the
+// registers 4 tiles would hold leave no room for the next chunk's activations in flight (only
+// segments of more than 32 rows take a second pass; 128 us per 512-token chunk against 133 with
+// 4 tiles and the activations loaded after the multiply).  Down: a short K, every pass is two
+// chunks of dependent round trips (62 us at 2 tiles, 70 at 1 and at 4).
 template <int MODE>
-constexpr int max_mt() { return MODE == 0 ? 4 : 2; }
+constexpr int max_mt() { return 2; }
 
 // One (scale, bias) fp16 word from two 16-bit values of the 9-tensor form.
 template <int SBF>
@@ -178,27 +179,31 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
         const int g0 = 16 * jj + 4 * q;
         return g0 + 4 <= kg ? g0 : kg - 4;
     };
-    uint4 sbn[kSub];                                           // a block's pieces on their way to LDS
+    // a block's pieces on their way to LDS, one named register set per subtile (as an array the
+    // compiler keeps them in memory: in LDS, or in scratch with a wait right after the loads)
+    uint4 sbn0, sbn1, sbn2, sbn3;
+    static_assert(kSub == 4, "one named piece per subtile");
+    auto sbn = [&](int s) -> uint4& { return s == 0 ? sbn0 : s == 1 ? sbn1 : s == 2 ? sbn2 : sbn3; };
     auto fetch_sb = [&](int jj) {
         const int gs = sb_piece(jj, kq);
 #pragma unroll
         for (int s = 0; s < kSub; ++s) {
             if constexpr (SBF == 0) {
-                sbn[s] = *reinterpret_cast<const uint4*>(sbp[s] + lane_row_sb + gs);
+                sbn(s) = *reinterpret_cast<const uint4*>(sbp[s] + lane_row_sb + gs);
             } else {                           // 4 scales and 4 biases (8-byte aligned: kg % 4 == 0)
                 const uint2 sc = *reinterpret_cast<const uint2*>(scp[s] + lane_row_sb + gs);
                 const uint2 bi = *reinterpret_cast<const uint2*>(bip[s] + lane_row_sb + gs);
-                sbn[s] = make_uint4(sb_word<SBF>(sc.x & 0xFFFFu, bi.x & 0xFFFFu), sb_word<SBF>(sc.x >> 16, bi.x >> 16),
+                sbn(s) = make_uint4(sb_word<SBF>(sc.x & 0xFFFFu, bi.x & 0xFFFFu), sb_word<SBF>(sc.x >> 16, bi.x >> 16),
                                     sb_word<SBF>(sc.y & 0xFFFFu, bi.y & 0xFFFFu), sb_word<SBF>(sc.y >> 16, bi.y >> 16));
             }
         }
     };
     auto put_sb = [&](int jj) {
 #pragma unroll
-        for (int s = 0; s < kSub; ++s) reinterpret_cast<uint4*>(&sb_lds[jj & 1][wv][s][0])[lane] = sbn[s];
+        for (int s = 0; s < kSub; ++s) reinterpret_cast<uint4*>(&sb_lds[jj & 1][wv][s][0])[lane] = sbn(s);
     };
 
-    // The segment's rows are taken in batches of up to kMaxMT M tiles (64 rows); within a batch
+    // The segment's rows are taken in batches of up to kMaxMT M tiles (32 rows); within a batch
     // every K chunk's weights are loaded and dequantised once and multiplied into every tile, so
     // a long segment costs one pass over its weights per batch, not one per tile.
     //
@@ -262,10 +267,9 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
                 }
             }
         };
-        // After chunk j's multiply: the loads of the next block's words (needed from chunk
-        // 4 jj + 4 on), issued before the next activation loads, so that staging those waits for
-        // these too; staging chunk j writes them to the buffer of block jj - 1, which the wave's
-        // reads have left.
+        // After chunk j's multiply (j = 4 jj): the loads of the next block's words (needed from
+        // chunk 4 jj + 4 on); staging chunk j + 1 writes them to the buffer of block jj - 1, which
+        // the wave's reads have left.
         auto next_sb_block = [&](int j) {
             if constexpr (kSbLds) {
                 if ((j & 3) == 0 && 4 * ((j >> 2) + 1) < NCH) fetch_sb((j >> 2) + 1);
@@ -344,10 +348,11 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
                 }
             }
         };
-        // Software pipeline, one chunk deep: chunk j + 1's weights are in flight while chunk j is
-        // multiplied.  Loads retire in issue order, so the activations of chunk j are issued
-        // before the weights of chunk j + 1: staging j then waits for its activations only.  The
-        // last chunk's look-ahead re-reads the last chunk (an L2 hit), so no load is conditional.
+        // Software pipeline, one chunk deep: chunk j + 1's weights and activations are in flight
+        // while chunk j is multiplied (the activation registers are free once chunk j is staged).
+        // Loads retire in issue order: staging chunk j + 1 waits for its activations, and with
+        // them for chunk j + 1's weights, issued before them and needed next anyway.  The last
+        // chunk's look-ahead re-reads the last chunk (an L2 hit), so no load is conditional.
         if constexpr (kSbLds) fetch_sb(0);
         if constexpr (kPrefetch) {
             load_x(0);
@@ -359,9 +364,9 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
                 stage(j);
                 stage_sb(j);
                 lds_barrier();
+                load_x(j + 1 < NCH ? j + 1 : NCH - 1);
                 compute(j, cwa, swa);
                 next_sb_block(j);
-                load_x(j + 1 < NCH ? j + 1 : NCH - 1);
 #pragma unroll
                 for (int s = 0; s < kSub; ++s) {
                     cwa[s] = cwb[s];
