@@ -38,6 +38,7 @@ typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kUpRowsPerBlock = 32;
 constexpr int kDownRows = 8;
+static_assert((kDownRows & (kDownRows - 1)) == 0, "the epilogue row of a thread is tid & (kDownRows - 1)");
 
 // fp16 / bf16 bit pattern of a grid magnitude (any byte value is exact in both: bf16 keeps 8
 // significant bits).
@@ -313,6 +314,11 @@ __global__ __launch_bounds__(256) void k_cb_down(const uint16_t* __restrict__ h,
         sjv[tk] = scores ? sv : 1.0f;
     }
 
+    // the residual row of the epilogue, loaded now so that no round trip follows the reduction
+    // (without a residual, y_out's first bytes, unused)
+    const int erow = row0 + (tid & (kDownRows - 1)) < hidden ? row0 + (tid & (kDownRows - 1)) : hidden - 1;
+    const __half r_prev = (residual ? residual : reinterpret_cast<const __half*>(y_out))[erow];
+
     DownLoad<T> buf[2];
     load(0, buf[0]);
     build_tables(gentry, gtab, stab, tid, true);
@@ -357,7 +363,7 @@ __global__ __launch_bounds__(256) void k_cb_down(const uint16_t* __restrict__ h,
         const int row = row0 + tid;
         if (row < hidden) {
             float y = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
-            if (residual) y += __half2float(residual[row]);
+            if (residual) y += __half2float(r_prev);
             y_out[row] = y;
         }
     }

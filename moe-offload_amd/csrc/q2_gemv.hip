@@ -170,6 +170,7 @@ __global__ __launch_bounds__(256) void k_q2_gate_up_routed(
 }
 
 constexpr int kDownRows = 8;      // output rows per block (one wave instruction at GPR = 8)
+static_assert((kDownRows & (kDownRows - 1)) == 0, "the epilogue row of a thread is tid & (kDownRows - 1)");
 
 template <int GPR>
 __global__ __launch_bounds__(256) void k_q2_down(
@@ -231,6 +232,12 @@ __global__ __launch_bounds__(256) void k_q2_down(
     }
     const bool weighted = scores != nullptr;
     const float s_lane = __half2float((weighted ? scores : h)[lane < k ? lane : 0]);
+    // The epilogue's operands, loaded here so that no round trip follows the reduction: y_out's
+    // current value (mode 2 adds to it) and the residual row (mode 0).  Both unconditional from a
+    // clamped row; without a residual the load reads y_out's first bytes and is not used.
+    const int erow = row0 + (tid & (kDownRows - 1)) < hidden ? row0 + (tid & (kDownRows - 1)) : hidden - 1;
+    const float y_prev = y_out[erow];
+    const __half r_prev = (residual ? residual : reinterpret_cast<const __half*>(y_out))[erow];
 
 #pragma unroll
     for (int ui = 0; ui < kUnitIters; ++ui) {
@@ -287,9 +294,9 @@ __global__ __launch_bounds__(256) void k_q2_down(
         if (row < hidden) {
             float y = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
             if (per_expert == 2) {
-                y_out[row] += y;
+                y_out[row] = y_prev + y;
             } else {
-                if (residual) y += __half2float(residual[row]);
+                if (residual) y += __half2float(r_prev);
                 y_out[row] = y;
             }
         }

@@ -29,6 +29,7 @@ using namespace q2dot;
 constexpr int kTMaxGroups = 64;         // hidden <= 4096
 constexpr int kTMaxPasses = 8;          // groups per lane of a gate/up row
 constexpr int kTDownRows = 8;           // output rows per down block
+static_assert((kTDownRows & (kTDownRows - 1)) == 0, "the epilogue row of a thread is tid & (kTDownRows - 1)");
 constexpr int kTDownLanes = 16;         // lanes per down row: intermediate <= 1024
 
 template <bool BF16>
@@ -162,6 +163,11 @@ __global__ __launch_bounds__(256) void k_q2t_down(const __half* __restrict__ h, 
     }
     const bool weighted = scores != nullptr;
     const float s_lane = __half2float((weighted ? scores : h)[lane < k ? lane : 0]);
+    // the epilogue's operands, loaded now (as in k_q2_down): y_out's current value for mode 2, the
+    // residual row for mode 0 (without a residual, y_out's first bytes, unused)
+    const int erow = row0 + (tid & (kTDownRows - 1)) < hidden ? row0 + (tid & (kTDownRows - 1)) : hidden - 1;
+    const float y_prev = y_out[erow];
+    const __half r_prev = (residual ? residual : reinterpret_cast<const __half*>(y_out))[erow];
 
 #pragma unroll
     for (int ui = 0; ui < kUnitIters; ++ui) {
@@ -218,9 +224,9 @@ __global__ __launch_bounds__(256) void k_q2t_down(const __half* __restrict__ h, 
         if (row < hidden) {
             float y = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
             if (per_expert == 2) {
-                y_out[row] += y;
+                y_out[row] = y_prev + y;
             } else {
-                if (residual) y += __half2float(residual[row]);
+                if (residual) y += __half2float(r_prev);
                 y_out[row] = y;
             }
         }
