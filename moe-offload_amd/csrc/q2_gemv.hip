@@ -18,7 +18,7 @@
 // Kernels
 //   k_q2_gate_up<GPR>: rows of gate and up for one selected expert; lanes 0-31 gate, 32-63 up,
 //                      GPR = hidden/64 lanes per row.  Writes h = silu(g)*u as fp16 [k][inter].
-//   k_q2_down<GPR>:    8 output rows per block x all k experts (4 waves split the experts);
+//   k_q2_down<GPR>:    8 output rows per block x all k experts (8 waves split the experts);
 //                      h is staged in LDS in dot2 pair order; the block reduces over experts in
 //                      a fixed order and writes y = residual + sum_j s_j y_j (fp32, mode 0), the
 //                      per-expert rows (mode 1), or adds sum_j s_j y_j to y (mode 2: the second
@@ -170,22 +170,27 @@ __global__ __launch_bounds__(256) void k_q2_gate_up_routed(
 }
 
 constexpr int kDownRows = 8;      // output rows per block (one wave instruction at GPR = 8)
+// Waves per down block.  With 8, a wave multiplies 1-2 of the top-10 experts instead of 2-3: its
+// chain of dependent dot products after the loads land is shorter (resident decode 1,294 tok/s
+// against 1,254 with 4 waves; back to back, where one launch's tail hides under the next, both
+// take 5.3-5.5 us).
+constexpr int kDownWaves = 8;
 static_assert((kDownRows & (kDownRows - 1)) == 0, "the epilogue row of a thread is tid & (kDownRows - 1)");
 
 template <int GPR>
-__global__ __launch_bounds__(256) void k_q2_down(
+__global__ __launch_bounds__(64 * kDownWaves) void k_q2_down(
     const __half* __restrict__ h, const uint8_t* __restrict__ pool, size_t stride,
     const uint32_t* __restrict__ slots, int n_slots, const __half* __restrict__ scores, int k, int hidden,
     BlobLayout L, const __half* __restrict__ residual, float* __restrict__ y_out, int per_expert) {
     constexpr int LPR = GPR;                       // lanes per row
     constexpr int RPI = 64 / LPR;                  // rows per wave instruction
     constexpr int ITERS = (kDownRows + RPI - 1) / RPI;
-    constexpr int MAXJ = (MOE_MAX_K + 3) / 4;      // experts per wave
+    constexpr int MAXJ = (MOE_MAX_K + kDownWaves - 1) / kDownWaves;   // experts per wave
     constexpr int kUnits = MOE_MAX_K * GPR * 4;    // 16-value units of h at the largest k
-    constexpr int kUnitIters = (kUnits + 255) / 256;
+    constexpr int kUnitIters = (kUnits + 64 * kDownWaves - 1) / (64 * kDownWaves);
     __shared__ uint4 hp[MOE_MAX_K][GPR][8];        // per (expert, group): 32 dot2 pairs
     __shared__ float hc[MOE_MAX_K][GPR][2];
-    __shared__ float red[4][kDownRows];
+    __shared__ float red[kDownWaves][kDownRows];
 
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane % LPR, rl = lane / LPR;
@@ -199,13 +204,13 @@ __global__ __launch_bounds__(256) void k_q2_down(
     uint4 hv[kUnitIters][2];
 #pragma unroll
     for (int ui = 0; ui < kUnitIters; ++ui) {
-        const int u = tid + 256 * ui;
+        const int u = tid + 64 * kDownWaves * ui;
         const int uc = u < n_units ? u : 0;
         const __half* src = h + (size_t)uc * 16;          // units are contiguous in h
         hv[ui][0] = reinterpret_cast<const uint4*>(src)[0];
         hv[ui][1] = reinterpret_cast<const uint4*>(src)[1];
     }
-    // This wave's weight loads (experts wv, wv+4, ...), all unconditional from clamped
+    // This wave's weight loads (experts wv, wv + kDownWaves, ...), all unconditional from clamped
     // in-range addresses: a value loaded inside a branch and merged with another value at the
     // join is waited for in the branch, which would serialise the round trips.  A position past
     // k re-reads expert k-1's rows, which another wave of the block loads too (an L2 hit); the
@@ -213,7 +218,7 @@ __global__ __launch_bounds__(256) void k_q2_down(
     uint32_t slot_q[MAXJ];
 #pragma unroll
     for (int q = 0; q < MAXJ; ++q) {
-        const int j = wv + 4 * q;
+        const int j = wv + kDownWaves * q;
         slot_q[q] = slots[j < k ? j : k - 1];
     }
     uint4 c[MAXJ][ITERS];
@@ -241,8 +246,8 @@ __global__ __launch_bounds__(256) void k_q2_down(
 
 #pragma unroll
     for (int ui = 0; ui < kUnitIters; ++ui) {
-        const int u = tid + 256 * ui;
-        if (256 * ui >= n_units) break;            // block-uniform: no lane of this pass is valid
+        const int u = tid + 64 * kDownWaves * ui;
+        if (64 * kDownWaves * ui >= n_units) break;   // block-uniform: no lane of this pass is valid
         const int uc = u < n_units ? u : 0;
         const int jj = uc / (GPR * 4), gg = (uc >> 2) % GPR;
         stage_pairs(hv[ui][0], hv[ui][1], u < n_units, hp[jj][gg], hc[jj][gg], uc & 3, gg & 7);
@@ -254,7 +259,7 @@ __global__ __launch_bounds__(256) void k_q2_down(
     for (int it = 0; it < ITERS; ++it) acc[it] = 0.f;
 #pragma unroll
     for (int q = 0; q < MAXJ; ++q) {
-        const int j = wv + 4 * q;
+        const int j = wv + kDownWaves * q;
         if (j >= k) break;
         h2_t P[32];
         const uint4* src = hp[j][g];
@@ -292,7 +297,9 @@ __global__ __launch_bounds__(256) void k_q2_down(
     if (tid < kDownRows) {
         int row = row0 + tid;
         if (row < hidden) {
-            float y = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+            float y = red[0][tid];                      // the waves' sums in a fixed order
+#pragma unroll
+            for (int w = 1; w < kDownWaves; ++w) y += red[w][tid];
             if (per_expert == 2) {
                 y_out[row] = y_prev + y;
             } else {
@@ -329,7 +336,7 @@ int down_t(const __half* h, const uint8_t* pool, size_t stride, const uint32_t* 
            const __half* scores, int k, int hidden, BlobLayout L, const __half* residual,
            float* y_out, int per_expert, hipStream_t s) {
     dim3 grid((hidden + kDownRows - 1) / kDownRows);
-    MOE_LAUNCH(TK_DOWN, (k_q2_down<GPR>), grid, dim3(256), 0, s, h, pool, stride, slots, n_slots, scores, k,
+    MOE_LAUNCH(TK_DOWN, (k_q2_down<GPR>), grid, dim3(64 * kDownWaves), 0, s, h, pool, stride, slots, n_slots, scores, k,
                        hidden, L, residual, y_out, per_expert);
     HIP_TRY(hipGetLastError());
     return 0;
