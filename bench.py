@@ -11,7 +11,8 @@ resident in HBM when the timed region starts; the expert store is host memory by
 Prints one JSON line.  `value` = tokens/s over the timed steps.  `roofline` covers the
 dominant kernel (the Q2 gate/up GEMV), timed with HIP events on its stream in an instrumented
 pass over the same number of tokens right after the timed region; `cpu_baseline` times the
-oracle's CPU restatement of one token-layer on the host cores.
+reference's CPU path for one token-layer on the host cores; `tensor_form` times the decode kernels
+on the reference's own 9-tensor expert format at its production shape (2560 x 640, bf16 scales).
 """
 from __future__ import annotations
 
@@ -56,6 +57,8 @@ def parse():
                     help="staging blocks per prefetched expert (0: --stage-ctas)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill grouped-GEMM pass")
     ap.add_argument("--no-file-tier", action="store_true", help="skip the on-disk tier pass")
+    ap.add_argument("--no-tensor-form", action="store_true",
+                    help="skip the pass over the reference's 9-tensor expert format at 2560 x 640")
     ap.add_argument("--io-threads", type=int, default=8, help="reader threads of the on-disk tier pass")
     ap.add_argument("--sched", action="store_true",
                     help="the C++ runner's scheduler variant of the expert cache (c_layer_decode_step_sched)")
@@ -63,7 +66,8 @@ def parse():
     ap.add_argument("--native-host", action="store_true",
                     help="with --mode host: the per-layer loop runs in the library (moe_stack_token_host)")
     ap.add_argument("--nemo-layers", type=int, default=40, help="layers of the codebook (Nemotron-style) workload")
-    ap.add_argument("--only", choices=["headline", "resident", "roofline", "prefill", "calib", "floor", "nemotron", "filetier"], default=None,
+    ap.add_argument("--only", choices=["headline", "resident", "roofline", "prefill", "calib", "floor", "nemotron", "filetier", "tensorform"],
+                    default=None,
                     help="run one pass and print its own JSON line (for sweeps and profiling); "
                          "calib runs the known-size copy kernel used to scale memory counters")
     return ap.parse_args()
@@ -526,6 +530,82 @@ def gemv_loop_timing(st, tokens=8, warm=2, repeats=3):
     return out
 
 
+def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6, repeats=3):
+    """The reference's own expert format at its production layer shape (loader.py:88-92 and
+    332-406: 9 slot-pool tensors per layer, bf16 scales and biases, 1,536,000 B per expert), every
+    expert in HBM: k_q2t_gate_up and k_q2t_down launched back to back over fresh top-k draws, each
+    launch on the next of `layers` layers' pools (786 MB each, so the bytes come from HBM rather
+    than the 256 MB MALL), bracketed by two HIP events; the median of `repeats` loops, as the blob
+    kernels' roofline loop.  Random codes, N(0, 0.02) scales, biases -1.5 x scale."""
+    import ctypes
+
+    import torch
+
+    from moe_offload import _lib
+    L = _lib.lib()
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(55)
+
+    def layer_pools():
+        ts = []
+        for rows, cols in ((inter, hidden), (inter, hidden), (hidden, inter)):       # gate, up, down
+            w = torch.randint(-2 ** 31, 2 ** 31 - 1, (n_exp, rows, cols // 16), dtype=torch.int32, device=dev,
+                              generator=g)
+            s = (torch.randn((n_exp, rows, cols // 64), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+            ts += [w, s, (-1.5 * s.float()).to(torch.bfloat16)]
+        return ts
+
+    u64_9 = ctypes.c_uint64 * 9
+    sets = [layer_pools() for _ in range(layers)]
+    ptrs = [u64_9(*[t.data_ptr() for t in ts]) for ts in sets]
+    nbytes = u64_9(*[t[0].numel() * t.element_size() for t in sets[0]])
+    expert = sum(nbytes)
+    gc = torch.Generator(device="cpu")
+    gc.manual_seed(56)
+    n = draws * layers
+    ids = torch.stack([torch.randperm(n_exp, generator=gc)[:k] for _ in range(n)]).to(torch.int32).to(dev)
+    sc = torch.full((k,), 1.0 / k, dtype=torch.float16, device=dev)
+    x = torch.randn(hidden, device=dev, generator=g).half()
+    h = torch.zeros(k * inter, dtype=torch.float16, device=dev)
+    y = torch.zeros(hidden, dtype=torch.float32, device=dev)
+    s = torch.cuda.current_stream()
+
+    def gate_up(i):
+        _lib.check(L.moe_q2t_gate_up(x.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, ids[i].data_ptr(), k, hidden,
+                                     inter, 64, h.data_ptr(), s.cuda_stream), "q2t_gate_up")
+
+    def down(i):
+        _lib.check(L.moe_q2t_down(h.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, ids[i].data_ptr(), sc.data_ptr(), k,
+                                  hidden, inter, 64, x.data_ptr(), y.data_ptr(), 0, s.cuda_stream), "q2t_down")
+
+    per_launch = {"gate_up": k * (nbytes[0] + nbytes[1] + nbytes[2] + nbytes[3] + nbytes[4] + nbytes[5]),
+                  "down": k * (nbytes[6] + nbytes[7] + nbytes[8])}
+    out = {"workload": f"one decode layer in the reference's 9-tensor format: hidden {hidden}, inter {inter}, "
+                       f"{n_exp} experts in HBM ({expert:,} B each, bf16 scales), top-{k}; {layers} layers' pools "
+                       f"rotated, {n} fresh draws per loop",
+           "bytes_per_launch": per_launch}
+    for name, fn in (("gate_up", gate_up), ("down", down)):
+        for i in range(layers):
+            fn(n - 1 - i)
+        per = []
+        for _ in range(repeats):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for i in range(n):
+                fn(i)
+            e1.record(s)
+            e1.synchronize()
+            per.append(e0.elapsed_time(e1) * 1e3 / n)
+        med = sorted(per)[len(per) // 2]
+        out[name + "_us"] = round(med, 3)
+        out[name + "_loops"] = [round(v, 3) for v in per]
+        out[name + "_gb_s"] = round(per_launch[name] / (med * 1e-6) / 1e9, 1)
+    del sets
+    torch.cuda.empty_cache()
+    return out
+
+
 def resident_pass(args, cfg, gen, n_tok, xs=None):
     """48 layers with every expert in HBM (no cache, no staging): the GEMV kernels' own roofline."""
     import torch
@@ -637,6 +717,9 @@ def main():
     if args.only == "nemotron":
         print(json.dumps({"nemotron": nemotron_pass(min(args.steps, 64), min(args.warmup, 8), args.nemo_layers)}),
               flush=True)
+        return
+    if args.only == "tensorform":
+        print(json.dumps({"tensor_form": tensor_form_pass()}), flush=True)
         return
     if args.only == "filetier":
         print(json.dumps({"file_tier": file_tier_pass(args.layers, threads=args.io_threads)}), flush=True)
@@ -758,6 +841,8 @@ def main():
                           "routed_bytes_per_token": routed}
     if not args.no_prefill:
         line["prefill"] = prefill_pass()
+    if not args.no_tensor_form:
+        line["tensor_form"] = tensor_form_pass()
     if not args.no_file_tier:
         line["file_tier"] = file_tier_pass(args.layers, threads=args.io_threads)
     if not args.no_cpu_baseline:

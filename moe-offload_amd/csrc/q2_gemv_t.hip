@@ -29,6 +29,7 @@ using namespace q2dot;
 constexpr int kTMaxGroups = 64;         // hidden <= 4096
 constexpr int kTMaxPasses = 8;          // groups per lane of a gate/up row
 constexpr int kTDownRows = 8;           // output rows per down block
+constexpr int kTDownWaves = 8;          // waves per down block (1-2 of the top-10 experts each)
 static_assert((kTDownRows & (kTDownRows - 1)) == 0, "the epilogue row of a thread is tid & (kTDownRows - 1)");
 constexpr int kTDownLanes = 16;         // lanes per down row: intermediate <= 1024
 
@@ -113,18 +114,18 @@ __global__ __launch_bounds__(256) void k_q2t_gate_up(const __half* __restrict__ 
 }
 
 template <bool BF16>
-__global__ __launch_bounds__(256) void k_q2t_down(const __half* __restrict__ h, Q2Experts E,
+__global__ __launch_bounds__(64 * kTDownWaves) void k_q2t_down(const __half* __restrict__ h, Q2Experts E,
                                                   const uint32_t* __restrict__ slots, int n_slots,
                                                   const __half* __restrict__ scores, int k, int hidden, int inter,
                                                   const __half* __restrict__ residual, float* __restrict__ y_out,
                                                   int per_expert) {
     constexpr int RPI = 64 / kTDownLanes;                 // rows per wave instruction
     constexpr int ITERS = kTDownRows / RPI;
-    constexpr int MAXJ = (MOE_MAX_K + 3) / 4;
-    constexpr int kUnitIters = (MOE_MAX_K * 1024 / 16 + 255) / 256;
+    constexpr int MAXJ = (MOE_MAX_K + kTDownWaves - 1) / kTDownWaves;
+    constexpr int kUnitIters = (MOE_MAX_K * 1024 / 16 + 64 * kTDownWaves - 1) / (64 * kTDownWaves);
     __shared__ uint4 hp[MOE_MAX_K][kTDownLanes][8];
     __shared__ float hc[MOE_MAX_K][kTDownLanes][2];
-    __shared__ float red[4][kTDownRows];
+    __shared__ float red[kTDownWaves][kTDownRows];
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int IPR = inter >> 6;
     const int g = lane & (kTDownLanes - 1), rl = lane / kTDownLanes;
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(256) void k_q2t_down(const __half* __restrict__ h, 
     uint4 hv[kUnitIters][2];
 #pragma unroll
     for (int ui = 0; ui < kUnitIters; ++ui) {
-        const int u = tid + 256 * ui;
+        const int u = tid + 64 * kTDownWaves * ui;
         const int uc = u < n_units ? u : 0;
         hv[ui][0] = reinterpret_cast<const uint4*>(h + (size_t)uc * 16)[0];
         hv[ui][1] = reinterpret_cast<const uint4*>(h + (size_t)uc * 16)[1];
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(256) void k_q2t_down(const __half* __restrict__ h, 
     uint16_t sc[MAXJ][ITERS], bi[MAXJ][ITERS];
 #pragma unroll
     for (int q = 0; q < MAXJ; ++q) {
-        const int jq = wv + 4 * q;
+        const int jq = wv + kTDownWaves * q;
         slot_q[q] = slots[jq < k ? jq : k - 1];
         const size_t s = slot_q[q] < (uint32_t)n_slots ? slot_q[q] : 0u;
         const uint8_t* wb = Pd.w + s * Pd.w_stride;
@@ -171,8 +172,8 @@ __global__ __launch_bounds__(256) void k_q2t_down(const __half* __restrict__ h, 
 
 #pragma unroll
     for (int ui = 0; ui < kUnitIters; ++ui) {
-        const int u = tid + 256 * ui;
-        if (256 * ui >= n_units) break;                   // block-uniform
+        const int u = tid + 64 * kTDownWaves * ui;
+        if (64 * kTDownWaves * ui >= n_units) break;      // block-uniform
         const int uc = u < n_units ? u : 0;
         const int jj = uc / (IPR * 4), gg = (uc >> 2) % IPR;
         stage_pairs(hv[ui][0], hv[ui][1], u < n_units, hp[jj][gg], hc[jj][gg], uc & 3, gg & 7);
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(256) void k_q2t_down(const __half* __restrict__ h, 
     for (int it = 0; it < ITERS; ++it) acc[it] = 0.f;
 #pragma unroll
     for (int q = 0; q < MAXJ; ++q) {
-        const int jq = wv + 4 * q;
+        const int jq = wv + kTDownWaves * q;
         if (jq >= k) break;
         h2_t P[32];
         const uint4* src = hp[jq][gc];
@@ -222,7 +223,9 @@ __global__ __launch_bounds__(256) void k_q2t_down(const __half* __restrict__ h, 
     if (tid < kTDownRows) {
         const int row = row0 + tid;
         if (row < hidden) {
-            float y = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+            float y = red[0][tid];                      // the waves' sums in a fixed order
+#pragma unroll
+            for (int w = 1; w < kTDownWaves; ++w) y += red[w][tid];
             if (per_expert == 2) {
                 y_out[row] = y_prev + y;
             } else {
@@ -279,10 +282,10 @@ int launch_q2t_down(const __half* h, const Q2Experts& E, int n_slots, const uint
     if (n_slots <= 0 || !slots || !h || !y_out) { moe_set_error("q2t_down: empty pool or null pointer"); return -1; }
     dim3 grid((hidden + kTDownRows - 1) / kTDownRows);
     if (E.bf16)
-        MOE_LAUNCH(TK_DOWN, (k_q2t_down<true>), grid, dim3(256), 0, s, h, E, slots, n_slots, scores, k, hidden, inter,
+        MOE_LAUNCH(TK_DOWN, (k_q2t_down<true>), grid, dim3(64 * kTDownWaves), 0, s, h, E, slots, n_slots, scores, k, hidden, inter,
                    residual, y_out, per_expert);
     else
-        MOE_LAUNCH(TK_DOWN, (k_q2t_down<false>), grid, dim3(256), 0, s, h, E, slots, n_slots, scores, k, hidden, inter,
+        MOE_LAUNCH(TK_DOWN, (k_q2t_down<false>), grid, dim3(64 * kTDownWaves), 0, s, h, E, slots, n_slots, scores, k, hidden, inter,
                    residual, y_out, per_expert);
     HIP_TRY(hipGetLastError());
     return 0;
