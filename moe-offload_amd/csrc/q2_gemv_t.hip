@@ -15,7 +15,7 @@
 //   k_q2t_gate_up: 8 lanes per row, each lane looping over the row's groups g = l8, l8 + 8, ...;
 //                  gate rows on lanes 0-31, up rows on lanes 32-63 (4 rows per wave).
 //   k_q2t_down:    16 lanes per output row (one group each: intermediate <= 1024), 8 rows per
-//                  block, the block's 4 waves split the experts; fixed-order cross-wave sum.
+//                  block, the block's 8 waves split the experts; fixed-order cross-wave sum.
 #include <hip/hip_fp16.h>
 
 #include "lane_reduce.h"

@@ -144,6 +144,35 @@ def test_switch_glu_per_expert_and_gate_up(dev, layer):
         assert_close_rms(y[j], q2.qmatvec(hh, *d, 2, 64), 1e-2, f"y expert {e}")
 
 
+@pytest.mark.parametrize("k", [1, 7, 8, 9, 16])
+def test_down_every_expert_count(dev, layer, k):
+    """The down kernel deals expert j to wave j mod 8 of its block: with k <= 8 some waves have no
+    expert, with k = 9..16 some have two, at 16 every wave has two.  Each of its three outputs
+    against the fp64 oracle: the weighted sum plus residual, every expert's row, and the weighted
+    sum added to a y that already holds values (the second half of a hit/miss split)."""
+    from moe_offload import ops, synth
+    from helpers import expert_fn
+    mlx, blobs, pool = layer
+    x = synth.hidden_states(1, H, seed=40 + k)[0]
+    rng = np.random.default_rng(41 + k)
+    inds = rng.choice(E, size=k, replace=False).astype(np.int32)
+    sc = rng.dirichlet(np.ones(k)).astype(np.float16)
+    xt, slots, st = torch.from_numpy(x).to(dev), torch.from_numpy(inds).to(dev), torch.from_numpy(sc).to(dev)
+    h = ops.q2_gate_up(xt, pool, slots, H, I)
+    y = ops.q2_down(h, pool, slots, H, I, scores=st, residual=xt).cpu().numpy()
+    assert_close_rms(y, oracle_moe(x, inds, sc, mlx, residual=x), 1e-2, f"k={k} weighted")
+    yk = ops.q2_down(h, pool, slots, H, I, per_expert=True).cpu().numpy()
+    f = expert_fn(mlx)
+    for j, e in enumerate(inds):
+        want = q2.switch_glu_expert(x.astype(np.float64), *f(int(e)), bits=2, group=64)
+        assert_close_rms(yk[j], want, 1e-2, f"k={k} expert {e}")
+    base = np.linspace(-1.0, 1.0, H).astype(np.float32)
+    y2 = torch.from_numpy(base.copy()).to(dev)
+    ops.q2_down(h, pool, slots, H, I, scores=st, per_expert=2, out=y2)
+    got = y2.cpu().numpy().astype(np.float64) - base
+    assert_close_rms(got, oracle_moe(x, inds, sc, mlx), 1e-2, f"k={k} added")
+
+
 def test_switch_glu_golden_fixture_shapes(dev, golden_moe):
     """The reference's own 16-expert fixture (hidden 256, inter 128, top-4): the routed part of
     moe.y_dec / moe.y_pre (golden minus the golden shared-expert output) within the reference's
