@@ -267,3 +267,31 @@ def test_grouped_tensor_form_bf16_real_shape():
         pairs = np.nonzero(flat == e)[0]
         want = q2.switch_glu_expert(xs[pairs // K].astype(np.float64), *f(e), bits=2, group=64, sdtype="bf16")
         assert_close_rms(y[pairs], want, 1e-2, f"expert {e}")
+
+
+@pytest.mark.parametrize("k", [1, 9, 16])
+def test_tensor_form_every_expert_count(k):
+    """The tensor-form down block deals expert j to wave j mod 8: one expert (seven idle waves),
+    nine (one wave with two), sixteen (every wave with two), at hidden 1024 / inter 320 (5 groups
+    per down row) with bf16 scales: the weighted sum with residual and every expert's row against
+    the fp64 oracle."""
+    from moe_offload import _lib
+    L = _lib.lib()
+    dev = torch.device("cuda")
+    H, I, E = 1024, 320, 24
+    mlx = experts_bf16(E, H, I, seed=50 + k)
+    ts, ptrs, nbytes = _pools(mlx, dev)
+    f = _fn(mlx, "bf16")
+    rng = np.random.default_rng(51 + k)
+    x = rng.standard_normal(H).astype(np.float16)
+    ids = rng.choice(E, size=k, replace=False).astype(np.int32)
+    sc = rng.dirichlet(np.ones(k)).astype(np.float16)
+    xt = torch.from_numpy(x).to(dev)
+    y = _run(L, xt, ptrs, nbytes, 1, E, torch.from_numpy(ids).to(dev), torch.from_numpy(sc).to(dev), k, H, I,
+             residual=xt)
+    want = q2.moe_combine(x.astype(np.float64), ids, sc.astype(np.float64), f, bits=2, group=64, sdtype="bf16")
+    assert_close_rms(y, want + x.astype(np.float64), 1e-2, f"k={k} weighted")
+    yk = _run(L, xt, ptrs, nbytes, 1, E, torch.from_numpy(ids).to(dev), None, k, H, I, per_expert=1)
+    for j, e in enumerate(ids):
+        want = q2.switch_glu_expert(x.astype(np.float64), *f(int(e)), bits=2, group=64, sdtype="bf16")
+        assert_close_rms(yk[j], want, 1e-2, f"k={k} expert {e}")
