@@ -536,7 +536,9 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
     expert in HBM: k_q2t_gate_up and k_q2t_down launched back to back over fresh top-k draws, each
     launch on the next of `layers` layers' pools (786 MB each, so the bytes come from HBM rather
     than the 256 MB MALL), bracketed by two HIP events; the median of `repeats` loops, as the blob
-    kernels' roofline loop.  Random codes, N(0, 0.02) scales, biases -1.5 x scale."""
+    kernels' roofline loop.  Random codes, N(0, 0.02) scales, biases -1.5 x scale.  Then the
+    checkpoint's 8-bit router (512 x 2560, top-10 in the reference's order) over 48 layers' routers
+    in turn, timed the same way."""
     import ctypes
 
     import torch
@@ -602,6 +604,40 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
         out[name + "_loops"] = [round(v, 3) for v in per]
         out[name + "_gb_s"] = round(per_launch[name] / (med * 1e-6) / 1e9, 1)
     del sets
+
+    # the real checkpoint's router (8-bit affine, group 64, bf16 x; loader.py:903-908), route mode,
+    # over 48 layers' routers in turn
+    n_r = 48
+    rcodes = torch.randint(-2 ** 31, 2 ** 31 - 1, (n_r, n_exp, hidden // 4), dtype=torch.int32, device=dev, generator=g)
+    rs = (torch.rand((n_r, n_exp, hidden // 64), device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    rb = (-127.5 * rs.float()).to(torch.bfloat16)
+    xb = torch.randn(hidden, device=dev, generator=g).to(torch.bfloat16)
+    ws = torch.zeros(int(L.moe_router_q8_workspace_bytes(n_exp)), dtype=torch.uint8, device=dev)
+    rids = torch.empty(k, dtype=torch.int32, device=dev)
+    rsc = torch.empty(k, dtype=torch.bfloat16, device=dev)
+
+    def router(i):
+        r = i % n_r
+        _lib.check(L.moe_router_q8(xb.data_ptr(), rcodes[r].data_ptr(), rs[r].data_ptr(), rb[r].data_ptr(), hidden,
+                                   n_exp, 64, k, 0, ws.data_ptr(), rids.data_ptr(), rsc.data_ptr(), None, None,
+                                   s.cuda_stream), "router_q8")
+
+    for i in range(n_r):
+        router(i)
+    per = []
+    for _ in range(repeats):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for i in range(2 * n_r):
+            router(i)
+        e1.record(s)
+        e1.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e3 / (2 * n_r))
+    r_bytes = n_exp * (hidden + 2 * (hidden // 64) * 2)
+    out["router_q8_us"] = round(sorted(per)[len(per) // 2], 3)
+    out["router_q8_loops"] = [round(v, 3) for v in per]
+    out["router_q8_bytes_per_launch"] = r_bytes
+    del rcodes, rs, rb
     torch.cuda.empty_cache()
     return out
 
