@@ -538,7 +538,8 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
     than the 256 MB MALL), bracketed by two HIP events; the median of `repeats` loops, as the blob
     kernels' roofline loop.  Random codes, N(0, 0.02) scales, biases -1.5 x scale.  Then the
     checkpoint's 8-bit router (512 x 2560, top-10 in the reference's order) over 48 layers' routers
-    in turn, timed the same way."""
+    in turn, timed the same way, and a whole MoE layer (router, gate/up, down) with the top-k
+    selection in the router's last block or inside the gate/up blocks."""
     import ctypes
 
     import torch
@@ -603,7 +604,6 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
         out[name + "_us"] = round(med, 3)
         out[name + "_loops"] = [round(v, 3) for v in per]
         out[name + "_gb_s"] = round(per_launch[name] / (med * 1e-6) / 1e9, 1)
-    del sets
 
     # the real checkpoint's router (8-bit affine, group 64, bf16 x; loader.py:903-908), route mode,
     # over 48 layers' routers in turn
@@ -637,7 +637,48 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
     out["router_q8_us"] = round(sorted(per)[len(per) // 2], 3)
     out["router_q8_loops"] = [round(v, 3) for v in per]
     out["router_q8_bytes_per_launch"] = r_bytes
-    del rcodes, rs, rb
+
+    # One MoE layer of the real checkpoint, every expert resident, as the dependent sequence a
+    # decode runs: router (route mode) -> gate/up of its ids -> down; and router (logits only) ->
+    # gate/up whose blocks select the ids themselves -> down.  48 layers in turn (each its own
+    # router, the pools of 8 layers rotated), bracketed, per layer.
+    lg = torch.empty(n_exp, dtype=torch.bfloat16, device=dev)
+    ids_b = torch.empty(k, dtype=torch.int32, device=dev)
+    sc_b = torch.empty(k, dtype=torch.bfloat16, device=dev)
+
+    def layer_routed_in_router(i):
+        router(i)
+        _lib.check(L.moe_q2t_gate_up(x.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, rids.data_ptr(), k, hidden,
+                                     inter, 64, h.data_ptr(), s.cuda_stream), "q2t_gate_up")
+        _lib.check(L.moe_q2t_down(h.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, rids.data_ptr(), sc.data_ptr(), k,
+                                  hidden, inter, 64, x.data_ptr(), y.data_ptr(), 0, s.cuda_stream), "q2t_down")
+
+    def layer_routed_in_gate_up(i):
+        r = i % n_r
+        _lib.check(L.moe_router_q8(xb.data_ptr(), rcodes[r].data_ptr(), rs[r].data_ptr(), rb[r].data_ptr(), hidden,
+                                   n_exp, 64, 0, 0, ws.data_ptr(), None, None, None, lg.data_ptr(), s.cuda_stream),
+                   "router_q8 logits")
+        _lib.check(L.moe_q2t_gate_up_routed(x.data_ptr(), lg.data_ptr(), n_exp, k, ptrs[i % layers], nbytes, 1,
+                                            hidden, inter, 64, ids_b.data_ptr(), sc_b.data_ptr(), h.data_ptr(),
+                                            s.cuda_stream), "q2t_gate_up_routed")
+        _lib.check(L.moe_q2t_down(h.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, ids_b.data_ptr(), sc.data_ptr(), k,
+                                  hidden, inter, 64, x.data_ptr(), y.data_ptr(), 0, s.cuda_stream), "q2t_down")
+
+    out["layer_us"] = {}
+    for name, fn in (("selection_in_router", layer_routed_in_router), ("selection_in_gate_up", layer_routed_in_gate_up)):
+        for i in range(n_r):
+            fn(i)
+        per = []
+        for _ in range(repeats):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for i in range(2 * n_r):
+                fn(i)
+            e1.record(s)
+            e1.synchronize()
+            per.append(e0.elapsed_time(e1) * 1e3 / (2 * n_r))
+        out["layer_us"][name] = round(sorted(per)[len(per) // 2], 3)
+    del sets, rcodes, rs, rb
     torch.cuda.empty_cache()
     return out
 

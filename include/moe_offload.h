@@ -208,6 +208,14 @@ int moe_q2_switch_glu(const void* x, const void* pool, uint64_t stride, int n_sl
  * shapes for blob pools. */
 int moe_q2t_gate_up(const void* x, const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots,
                     const uint32_t* slots, int k, int hidden, int inter, int group, void* h_out, void* stream);
+/* No counterpart in the reference: moe_q2t_gate_up for a pool holding every expert (slot = id),
+ * whose blocks select the top k themselves from the bf16 logits of moe_router_q8 (logits-only
+ * mode, k == m == 0) by the router's own rule and code -- ids u32 [k] and bf16 scores [k] out,
+ * bit-identical to moe_router_q8 in route mode -- so a resident layer of the real checkpoint
+ * needs no router selection pass (loader.py:903-908 + 557-564 fused). */
+int moe_q2t_gate_up_routed(const void* x, const void* logits, int n_exp, int k, const uint64_t* ptrs,
+                           const uint64_t* slot_bytes, int scale_bf16, int hidden, int inter, int group,
+                           uint32_t* ids_out, void* scores_out, void* h_out, void* stream);
 int moe_q2t_down(const void* h, const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots,
                  const uint32_t* slots, const void* scores, int k, int hidden, int inter, int group,
                  const void* residual, float* y_out, int per_expert, void* stream);

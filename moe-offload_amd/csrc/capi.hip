@@ -1176,6 +1176,16 @@ int moe_q2t_gate_up(const void* x, const uint64_t* ptrs, const uint64_t* slot_by
     return launch_q2t_gate_up((const __half*)x, E, n_slots, slots, k, hidden, inter, (__half*)h_out, (hipStream_t)stream);
 }
 
+int moe_q2t_gate_up_routed(const void* x, const void* logits, int n_exp, int k, const uint64_t* ptrs,
+                           const uint64_t* slot_bytes, int scale_bf16, int hidden, int inter, int group,
+                           uint32_t* ids_out, void* scores_out, void* h_out, void* stream) {
+    Q2Experts E;
+    if (!q2t_shape_ok("q2t_gate_up_routed", k, hidden, inter, group)) return -1;
+    if (!experts9("q2t_gate_up_routed", ptrs, slot_bytes, scale_bf16, hidden, inter, E)) return -1;
+    return launch_q2t_gate_up_routed((const __half*)x, E, (const uint16_t*)logits, n_exp, k, hidden, inter, ids_out,
+                                     (uint16_t*)scores_out, (__half*)h_out, (hipStream_t)stream);
+}
+
 int moe_q2t_down(const void* h, const uint64_t* ptrs, const uint64_t* slot_bytes, int scale_bf16, int n_slots,
                  const uint32_t* slots, const void* scores, int k, int hidden, int inter, int group,
                  const void* residual, float* y_out, int per_expert, void* stream) {

@@ -211,6 +211,9 @@ bool q2t_shape_ok(const char* who, int k, int hidden, int inter, int group);
 Q2Experts q2_experts_from_blob(const uint8_t* pool, size_t stride, const BlobLayout& L);
 int launch_q2t_gate_up(const __half* x, const Q2Experts& E, int n_slots, const uint32_t* slots, int k, int hidden,
                        int inter, __half* h_out, hipStream_t s);
+int launch_q2t_gate_up_routed(const __half* x, const Q2Experts& E, const uint16_t* logits, int n_exp, int k,
+                              int hidden, int inter, uint32_t* ids_out, uint16_t* scores_out, __half* h_out,
+                              hipStream_t s);
 int launch_q2t_down(const __half* h, const Q2Experts& E, int n_slots, const uint32_t* slots, const __half* scores,
                     int k, int hidden, int inter, const __half* residual, float* y_out, int per_expert, hipStream_t s);
 int launch_slot_step(SlotTable* t, const uint32_t* ids, int k, uint32_t* slot_inds,

@@ -21,6 +21,7 @@
 #include "lane_reduce.h"
 #include "moe_common.h"
 #include "q2_dot.h"
+#include "route_select.h"
 
 namespace {
 
@@ -39,10 +40,16 @@ __device__ __forceinline__ float half_bits(uint16_t v) {
     else return __half2float(__ushort_as_half(v));
 }
 
-template <bool BF16, int LPR>
-__global__ __launch_bounds__(256) void k_q2t_gate_up(const __half* __restrict__ x, Q2Experts E,
-                                                     const uint32_t* __restrict__ slots, int n_slots, int hidden,
-                                                     int inter, __half* __restrict__ h_out) {
+// Rows of gate and up for one selected expert.  ROUTED: the block first selects the top-k experts
+// itself from the logits of the checkpoint's router (bf16, moe_router_q8's rule in bf16, the same
+// code: route_select.h) over a pool holding every expert (slot = id); block (0, 0) also writes the
+// ids and bf16 scores, after its weight loads are issued.
+template <bool BF16, int LPR, bool ROUTED>
+__device__ __forceinline__ void q2t_gate_up_body(const __half* __restrict__ x, const Q2Experts& E,
+                                                 const uint32_t* __restrict__ slots, int n_slots, int hidden,
+                                                 int inter, __half* __restrict__ h_out,
+                                                 const uint16_t* __restrict__ logits, int k,
+                                                 uint32_t* __restrict__ ids_out, uint16_t* __restrict__ scores_out) {
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = blockIdx.y;
     const int GPR = hidden >> 6;
@@ -58,7 +65,29 @@ __global__ __launch_bounds__(256) void k_q2t_gate_up(const __half* __restrict__ 
     const int uc = tid < n_units ? tid : 0;
     const uint4 xlo = reinterpret_cast<const uint4*>(x)[2 * uc];
     const uint4 xhi = reinterpret_cast<const uint4*>(x)[2 * uc + 1];
-    const uint32_t slot = slots[j];
+    uint32_t slot;
+    uint32_t top_key = 0;                                 // routed, wave 0: lane r's r-th largest key
+    if constexpr (ROUTED) {
+        __builtin_amdgcn_sched_barrier(0);
+        __shared__ uint32_t keys[route::kMaxExperts];
+        __shared__ double redm[4], reds[4];
+        __shared__ uint32_t sel[MOE_MAX_K];
+        float lraw[route::kPer];
+#pragma unroll
+        for (int i = 0; i < route::kPer; ++i) {
+            const int e = tid + route::kThreads * i;
+            lraw[i] = route::bf16_to_f32(logits[e < n_slots ? e : 0]);
+        }
+        route::gate_keys<true>(lraw, n_slots, keys, redm, reds);
+        if (wv == 0) {
+            top_key = route::wave_topn(keys, 0, ((n_slots + 63) / 64) * 64, k, lane);
+            if (lane < k) sel[k - 1 - lane] = top_key & 0xFFFFu;
+        }
+        __syncthreads();
+        slot = sel[j];
+    } else {
+        slot = slots[j];
+    }
     const bool ok = slot < (uint32_t)n_slots;             // an invalid slot yields h = 0
     const size_t s = ok ? slot : 0;
     const int rowc = row < inter ? row : inter - 1;
@@ -83,6 +112,17 @@ __global__ __launch_bounds__(256) void k_q2t_gate_up(const __half* __restrict__ 
         bi[t] = *reinterpret_cast<const uint16_t*>(bb + (size_t)g * step);
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (ROUTED) {
+        if (wv == 0 && blockIdx.x == 0 && blockIdx.y == 0) {
+            uint32_t id;
+            uint16_t scb;
+            const int pos = route::topk_score_bits<true>(top_key, k, lane, id, scb);
+            if (pos >= 0) {
+                ids_out[pos] = id;
+                scores_out[pos] = scb;
+            }
+        }
+    }
     stage_pairs(xlo, xhi, tid < n_units, xp[uc >> 2], xc[uc >> 2], uc & 3, (uc >> 2) & 7);
     __syncthreads();
 
@@ -112,6 +152,22 @@ __global__ __launch_bounds__(256) void k_q2t_gate_up(const __half* __restrict__ 
         const float hval = ok ? gt / (1.0f + __expf(-gt)) * up : 0.0f;
         h_out[(size_t)j * inter + row] = __float2half_rn(hval);
     }
+}
+
+template <bool BF16, int LPR>
+__global__ __launch_bounds__(256) void k_q2t_gate_up(const __half* __restrict__ x, Q2Experts E,
+                                                     const uint32_t* __restrict__ slots, int n_slots, int hidden,
+                                                     int inter, __half* __restrict__ h_out) {
+    q2t_gate_up_body<BF16, LPR, false>(x, E, slots, n_slots, hidden, inter, h_out, nullptr, 0, nullptr, nullptr);
+}
+
+template <bool BF16, int LPR>
+__global__ __launch_bounds__(256) void k_q2t_gate_up_routed(const __half* __restrict__ x, Q2Experts E,
+                                                            const uint16_t* __restrict__ logits, int n_exp, int k,
+                                                            int hidden, int inter, uint32_t* __restrict__ ids_out,
+                                                            uint16_t* __restrict__ scores_out,
+                                                            __half* __restrict__ h_out) {
+    q2t_gate_up_body<BF16, LPR, true>(x, E, nullptr, n_exp, hidden, inter, h_out, logits, k, ids_out, scores_out);
 }
 
 template <bool BF16>
@@ -265,16 +321,26 @@ Q2Experts q2_experts_from_blob(const uint8_t* pool, size_t stride, const BlobLay
     return E;
 }
 
+namespace {
+
+// Lanes per gate/up row: the widest of 32, 16 and 8 whose passes over the row's groups keep at
+// least 80% of the lanes busy (one group per lane at hidden 2048: 5.5 us against 7.1 with 8
+// lanes; 16 lanes at 2560, 40 groups: 8.0 us against 8.4 with 8 and 9.3 with 32).
+template <class F>
+void with_lanes_per_row(int hidden, F&& go) {
+    const int gpr = hidden / 64;
+    auto busy = [&](int lpr) { return 5 * gpr >= 4 * lpr * ((gpr + lpr - 1) / lpr); };
+    if (busy(32)) go(std::integral_constant<int, 32>());
+    else if (busy(16)) go(std::integral_constant<int, 16>());
+    else go(std::integral_constant<int, 8>());
+}
+
+}  // namespace
+
 int launch_q2t_gate_up(const __half* x, const Q2Experts& E, int n_slots, const uint32_t* slots, int k, int hidden,
                        int inter, __half* h_out, hipStream_t s) {
     if (!q2t_shape_ok("q2t_gate_up", k, hidden, inter, 64)) return -1;
     if (n_slots <= 0 || !slots || !x || !h_out) { moe_set_error("q2t_gate_up: empty pool or null pointer"); return -1; }
-    // Lanes per row: the widest of 32, 16 and 8 whose passes over the row's groups keep at least
-    // 80% of the lanes busy (one group per lane at hidden 2048: 5.5 us against 7.1 with 8 lanes;
-    // 16 lanes at 2560, 40 groups: 8.0 us against 8.4 with 8 and 9.3 with 32).
-    const int gpr = hidden / 64;
-    auto busy = [&](int lpr) { return 5 * gpr >= 4 * lpr * ((gpr + lpr - 1) / lpr); };
-    const int lpr = busy(32) ? 32 : busy(16) ? 16 : 8;
     auto go = [&](auto lc) {
         constexpr int L = decltype(lc)::value;
         constexpr int rpb = 4 * (32 / L);                 // rows per block and projection
@@ -282,9 +348,32 @@ int launch_q2t_gate_up(const __half* x, const Q2Experts& E, int n_slots, const u
         if (E.bf16) MOE_LAUNCH(TK_GATE_UP, (k_q2t_gate_up<true, L>), grid, dim3(256), 0, s, x, E, slots, n_slots, hidden, inter, h_out);
         else MOE_LAUNCH(TK_GATE_UP, (k_q2t_gate_up<false, L>), grid, dim3(256), 0, s, x, E, slots, n_slots, hidden, inter, h_out);
     };
-    if (lpr == 32) go(std::integral_constant<int, 32>());
-    else if (lpr == 16) go(std::integral_constant<int, 16>());
-    else go(std::integral_constant<int, 8>());
+    with_lanes_per_row(hidden, go);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int launch_q2t_gate_up_routed(const __half* x, const Q2Experts& E, const uint16_t* logits, int n_exp, int k,
+                              int hidden, int inter, uint32_t* ids_out, uint16_t* scores_out, __half* h_out,
+                              hipStream_t s) {
+    if (!q2t_shape_ok("q2t_gate_up_routed", k, hidden, inter, 64)) return -1;
+    if (n_exp <= 0 || n_exp > route::kMaxExperts || k > n_exp) {
+        moe_set_error("q2t_gate_up_routed: n_exp=%d (<= %d, >= k=%d)", n_exp, route::kMaxExperts, k);
+        return -1;
+    }
+    if (!x || !logits || !ids_out || !scores_out || !h_out) { moe_set_error("q2t_gate_up_routed: null pointer"); return -1; }
+    auto go = [&](auto lc) {
+        constexpr int L = decltype(lc)::value;
+        constexpr int rpb = 4 * (32 / L);
+        dim3 grid((inter + rpb - 1) / rpb, k);
+        if (E.bf16)
+            MOE_LAUNCH(TK_GATE_UP, (k_q2t_gate_up_routed<true, L>), grid, dim3(256), 0, s, x, E, logits, n_exp, k, hidden,
+                       inter, ids_out, scores_out, h_out);
+        else
+            MOE_LAUNCH(TK_GATE_UP, (k_q2t_gate_up_routed<false, L>), grid, dim3(256), 0, s, x, E, logits, n_exp, k, hidden,
+                       inter, ids_out, scores_out, h_out);
+    };
+    with_lanes_per_row(hidden, go);
     HIP_TRY(hipGetLastError());
     return 0;
 }

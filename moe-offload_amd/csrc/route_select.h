@@ -56,6 +56,33 @@ __device__ __forceinline__ float round_f16(double v) {
     return __half2float(__ushort_as_half(f64_to_f16_bits(v)));
 }
 
+// f64 -> bf16 bits with one round-to-nearest-even: f32 by round-to-odd (sticky bit when inexact;
+// 24 >= 8 + 2 bits), then the f32 -> bf16 rounding.
+__device__ __forceinline__ uint16_t f64_to_bf16_bits(double d) {
+    float f = __double2float_rz(d);
+    if ((double)f != d) f = __uint_as_float(__float_as_uint(f) | 1u);
+    const uint32_t u = __float_as_uint(f);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// The rule's 16-bit format: fp16 (the workload's fp16 router, loader.py:903-908 at fp16) or bf16
+// (the real checkpoint's router, whose gates, sums and scores are bf16).
+template <bool BF16>
+__device__ __forceinline__ uint16_t rule_from_f64(double d) { return BF16 ? f64_to_bf16_bits(d) : f64_to_f16_bits(d); }
+template <bool BF16>
+__device__ __forceinline__ float rule_to_f32(uint32_t b) {
+    return BF16 ? bf16_to_f32(b) : __half2float(__ushort_as_half((uint16_t)b));
+}
+template <bool BF16>
+__device__ __forceinline__ uint16_t rule_from_f32(float f) {
+    return BF16 ? f32_to_bf16_bits(f) : __half_as_ushort(__float2half_rn(f));
+}
+
 // The n largest keys of keys[lo, hi) (LDS; distinct, 0 = empty) by one wave: lane r < n gets
 // the r-th largest (0 once the range runs out).  KPL keys per lane cover the range.  The keys
 // are distinct except for zeros (padding, and a zero gate of expert 0), so round r > 0 picks the
@@ -108,7 +135,8 @@ __device__ __forceinline__ uint32_t f16_order(uint16_t b) {
 
 // Block-wide: the gate keys of the logits this thread holds (lraw[i] = logit tid + kThreads i,
 // any value where that index is >= n_exp) into keys[0, n_pad) (n_pad = n_exp rounded up to 64;
-// padding keys 0).  Ends with a barrier.
+// padding keys 0).  Gates rounded to fp16, or to bf16 with BF16.  Ends with a barrier.
+template <bool BF16 = false>
 __device__ __forceinline__ void gate_keys(const float (&lraw)[kPer], int n_exp, uint32_t* keys, double* redm,
                                           double* reds) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -139,26 +167,34 @@ __device__ __forceinline__ void gate_keys(const float (&lraw)[kPer], int n_exp, 
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         int e = tid + kThreads * i;
-        if (e < n_pad) keys[e] = (e < n_exp) ? (((uint32_t)f64_to_f16_bits(lv[i] / sum) << 16) | (uint32_t)e) : 0u;
+        if (e < n_pad) keys[e] = (e < n_exp) ? (((uint32_t)rule_from_f64<BF16>(lv[i] / sum) << 16) | (uint32_t)e) : 0u;
     }
     __syncthreads();
 }
 
 // One wave, from the k largest keys (lane r holds the r-th largest, wave_topn): the id and score
-// that go to output position k - 1 - r (ascending gate order) for lanes r < k; position -1 for the
-// other lanes.
-__device__ __forceinline__ int topk_scores(uint32_t mine, int k, int lane, uint32_t& id, __half& score) {
-    const float g = __half2float(__ushort_as_half((uint16_t)(mine >> 16)));
-    // left-to-right sum over ascending order, each partial rounded to fp16; the gates are fp16
-    // values in ascending order, so every partial sum is exact in fp32 before rounding
+// bits that go to output position k - 1 - r (ascending gate order) for lanes r < k; position -1
+// for the other lanes.  The scores are g / s with s the left-to-right sum over ascending order,
+// each partial rounded to the rule's format: fp16 (11 bits) or bf16 (8 bits); an f32 sum or
+// quotient of two such values, rounded again, equals the single rounding (24 >= 2 p + 2).
+template <bool BF16>
+__device__ __forceinline__ int topk_score_bits(uint32_t mine, int k, int lane, uint32_t& id, uint16_t& score) {
+    const float g = rule_to_f32<BF16>(mine >> 16);
     float s = 0.0f;
     for (int j = 0; j < k; ++j) {
         float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), k - 1 - j));
-        s = __half2float(__float2half_rn(s + gj));
+        s = rule_to_f32<BF16>(rule_from_f32<BF16>(s + gj));
     }
     id = mine & 0xFFFFu;
-    score = __float2half_rn(g / s);                    // correctly rounded f32 division, then f16
+    score = rule_from_f32<BF16>(g / s);                // correctly rounded f32 division, then rounded
     return lane < k ? k - 1 - lane : -1;
+}
+
+__device__ __forceinline__ int topk_scores(uint32_t mine, int k, int lane, uint32_t& id, __half& score) {
+    uint16_t b;
+    const int pos = topk_score_bits<false>(mine, k, lane, id, b);
+    score = __ushort_as_half(b);
+    return pos;
 }
 
 // One wave: the selection from the keys.  Lane r < k returns the id and score that go to output

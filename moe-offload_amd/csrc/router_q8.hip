@@ -30,19 +30,9 @@ constexpr int kRows = kThreads / 64;          // one wave per weight row
 constexpr int kMaxHidden = 4096;
 constexpr int kMaxUnits = kMaxHidden / 16;    // 16-code units per row
 
-// f64 -> bf16 bits with one round-to-nearest-even: f32 by round-to-odd (sticky bit when
-// inexact; 24 >= 8 + 2 bits), then the f32 -> bf16 rounding.
-__device__ __forceinline__ uint16_t f64_to_bf16_bits(double d) {
-    float f = __double2float_rz(d);
-    if ((double)f != d) f = __uint_as_float(__float_as_uint(f) | 1u);
-    const uint32_t u = __float_as_uint(f);
-    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-}
-__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-    const uint32_t u = __float_as_uint(f);
-    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-}
+using route::bf16_to_f32;
+using route::f32_to_bf16_bits;
+using route::f64_to_bf16_bits;
 // Order-preserving map of a bf16 value to 16 bits (-0 folded onto +0).
 __device__ __forceinline__ uint32_t bf16_order(uint32_t b) {
     if (b == 0x8000u) b = 0;
@@ -123,46 +113,18 @@ __global__ __launch_bounds__(kThreads) void k_router_q8(
         lraw[i] = __hip_atomic_load(&scratch[e < n_rows ? e : 0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (k > 0) {
-        // gates = bf16(softmax in fp64); keys (gate bits << 16 | id)
-        double lv[kPer], mx = -1e300;
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            lv[i] = tid + kThreads * i < n_rows ? (double)lraw[i] : -1e300;
-            mx = fmax(mx, lv[i]);
-        }
-        mx = lanes::wave_max_f64(mx);
-        if (lane == 0) redm[wv] = mx;
-        __syncthreads();
-        mx = fmax(fmax(redm[0], redm[1]), fmax(redm[2], redm[3]));
-        double sum = 0.0;
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            lv[i] = tid + kThreads * i < n_rows ? exp(lv[i] - mx) : 0.0;
-            sum += lv[i];
-        }
-        sum = lanes::wave_sum_f64(sum);
-        if (lane == 0) reds[wv] = sum;
-        __syncthreads();
-        sum = (reds[0] + reds[1]) + (reds[2] + reds[3]);
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int e = tid + kThreads * i;
-            if (e < n_pad) keys[e] = e < n_rows ? (((uint32_t)f64_to_bf16_bits(lv[i] / sum) << 16) | (uint32_t)e) : 0u;
-        }
-        __syncthreads();
+        // gates = bf16(softmax in fp64), keys (gate bits << 16 | id), the top k, scores = bf16(g / s)
+        // with s the left-to-right bf16-rounded sum in ascending order: the router rule in bf16,
+        // the same code as the routed tensor-form gate/up (k_q2t_gate_up_routed)
+        route::gate_keys<true>(lraw, n_rows, keys, redm, reds);
         if (wv == 0) {
             const uint32_t mine = route::wave_topn(keys, 0, n_pad, k, lane);   // lane j: j-th largest
-            const float g = bf16_to_f32(mine >> 16);
-            // left-to-right sum in ascending order, each partial rounded to bf16 (f32 then bf16:
-            // 24 >= 2 * 8 + 2 bits, so the double rounding of a sum or a quotient is exact)
-            float s = 0.0f;
-            for (int j = 0; j < k; ++j) {
-                const float gj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g), k - 1 - j));
-                s = bf16_to_f32(f32_to_bf16_bits(s + gj));
-            }
-            if (lane < k) {
-                ids_out[k - 1 - lane] = mine & 0xFFFFu;
-                scores_out[k - 1 - lane] = f32_to_bf16_bits(g / s);
+            uint32_t id;
+            uint16_t sc;
+            const int pos = route::topk_score_bits<true>(mine, k, lane, id, sc);
+            if (pos >= 0) {
+                ids_out[pos] = id;
+                scores_out[pos] = sc;
             }
         }
     } else {

@@ -83,6 +83,8 @@ SIGNATURES: dict[str, tuple] = {
                                    _c_vp, _c_vp, _c_vp, _c_int, _c_vp]),
     "moe_q2t_gate_up": (_c_int, [_c_vp, _u64p, _u64p, _c_int, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp,
                                  _c_vp]),
+    "moe_q2t_gate_up_routed": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _u64p, _u64p, _c_int, _c_int, _c_int, _c_int,
+                                        _c_vp, _c_vp, _c_vp, _c_vp]),
     "moe_q2t_down": (_c_int, [_c_vp, _u64p, _u64p, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp,
                               _c_vp, _c_int, _c_vp]),
     "moe_q2t_switch_glu": (_c_int, [_c_vp, _u64p, _u64p, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int,
