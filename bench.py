@@ -391,8 +391,10 @@ def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8):
     file of 512 experts (q2format.write_blob_file, 503 MB, shared by the 47 cached layers) with the
     reader threads, host-driven tables (one device->host read of ids per layer).  Timed through
     the page cache (the file is cached after the warm-up) and with O_DIRECT (every read goes to the
-    device), beside the same host driver over the pinned host store; and the same file through the
-    P1 I/O scheduler (the C++ runner's `--io p1`: its own slot decisions, reads staged per reader)."""
+    device), beside the same host driver over the pinned host store; the same file through the
+    P1 I/O scheduler (the C++ runner's `--io p1`: its own slot decisions, reads staged per reader);
+    and device-driven (`device_*`: the headline's graph-replayed token, the tables publishing their
+    misses to the library's feeder thread, whose reads the staging kernels wait for)."""
     import shutil
     import tempfile
 
@@ -405,7 +407,7 @@ def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8):
     gen.manual_seed(4321)
     d = tempfile.mkdtemp(prefix="moe_file_tier_")
     out = {"workload": f"{n_layers}-layer decode as the headline, misses read by {threads} reader threads from one "
-                       f"512-expert blob file shared by the cached layers, host-driven tables, {steps} tokens",
+                       f"512-expert blob file shared by the cached layers, host-driven tables (device_*: device-driven, graph-replayed), {steps} tokens",
            "threads": threads}
     try:
         path = os.path.join(d, "experts.q2blob")
@@ -413,15 +415,19 @@ def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8):
         q2format.write_blob_file(path, blobs, base.hidden, base.inter)
         del blobs
         xs = torch.randn((warmup + steps, base.hidden), device="cuda", generator=gen).half()
-        for name, kw in (("host_store", {}), ("page_cache", {"store_file": path}),
-                         ("o_direct", {"store_file": path, "io_direct": True}),
-                         ("p1_page_cache", {"store_file": path, "io": "p1"})):
+        for name, kw, mode in (("host_store", {}, "host"), ("page_cache", {"store_file": path}, "host"),
+                               ("o_direct", {"store_file": path, "io_direct": True}, "host"),
+                               ("p1_page_cache", {"store_file": path, "io": "p1"}, "host"),
+                               ("device_page_cache", {"store_file": path}, "device"),
+                               ("device_o_direct", {"store_file": path, "io_direct": True}, "device")):
             cfg = StackConfig(n_layers=n_layers, io_threads=threads, **kw)
-            st = DecodeStack(cfg, mode="host")
+            st = DecodeStack(cfg, mode=mode)
             try:
                 direct = bool(_lib.lib().c_layer_io_direct(st.cidx(1))) if kw and st.p1 is None else None
-                elapsed, tot0, tot1 = timed_tokens(st, xs, warmup, steps, False)
+                elapsed, tot0, tot1 = timed_tokens(st, xs, warmup, steps, mode == "device")
                 _lib.check_error("file tier decode")
+                if st.table_status():
+                    raise RuntimeError(f"file tier {name}: table status {st.table_status()}")
                 read = (tot1[4] - tot0[4]) + (tot1[5] - tot0[5])
                 out[name] = {"tok_s": round(steps / elapsed, 2), "ms_per_token": round(elapsed / steps * 1e3, 3),
                              "read_mb_per_token": round(read / steps / 1e6, 2),

@@ -327,7 +327,10 @@ int c_layer_set_sched(int layer_idx, int on);
 /* Record that work queued on `stream` so far reads the layer's pool (copies into it wait). */
 int c_layer_mark_read(int layer_idx, void* stream);
 /* Move a layer's slot table to device memory (on != 0) or back.  Device-driven layers take
- * their ids from device memory and stage misses with a kernel that reads the pinned store. */
+ * their ids from device memory and stage misses with a kernel that reads the pinned store, or,
+ * for a file-backed layer (fd >= 0), the bounce entries the feeder thread reads the published
+ * misses into (c_layer_publish_dev).  No reference counterpart: the reference's tables live on
+ * the host (expert_io.c:583-708). */
 int c_layer_set_device_mode(int layer_idx, int on);
 /* Device-driven decode step / prefetch (same decisions as c_layer_step_decode_ex /
  * c_layer_start_prefetch), queued on `stream`; stage_ctas == 0 picks a default staging grid,
@@ -348,10 +351,21 @@ int c_router_tables_dev(int step_layer, int pf_layer, int max_fetch, const float
 /* Queue the copies of the layer's last device-side decode step (list 0) or prefetch (list 1)
  * on `stream` (the two lists are kept apart so a step may run while prefetch copies queue). */
 int c_layer_stage_dev(int layer_idx, int list, int stage_ctas, void* stream);
+/* File-backed device-driven layers: publish the copy list of the layer's last device-side decode
+ * step (list 0) or prefetch (list 1) to the feeder thread, queued on `stream` after that table
+ * operation and before c_layer_stage_dev of the same list.  The feeder reads the listed experts
+ * (the reader threads, one read per expert and tensor, O_DIRECT when c_io_set_direct was on at
+ * c_layer_init) into the layer's bounce entries; the staging kernel waits for each entry and
+ * copies it into its slot.  Replaces the reference's step-time reads of the misses
+ * (expert_io.c:187-356, 583-685) for tables that run on the GPU. */
+int c_layer_publish_dev(int layer_idx, int list, void* stream);
+/* Longest a file-backed staging kernel waits for one expert's read (0: 10 s); past it the
+ * layer's table status becomes 17 (a failed read: 16).  Applies to copies queued afterwards. */
+void c_io_set_feed_timeout_us(uint64_t us);
 /* Device address of a device-driven layer's table; 0 otherwise. */
 uint64_t c_layer_device_table(int layer_idx);
-/* Status word of the last device-side operation (0 ok, 1 id out of range, 2 repeated id);
- * blocks.  (The reference accepts repeated ids and leaks a slot; both paths here reject them.) */
+/* Status word of the last device-side operation (0 ok, 1 id out of range, 2 repeated id, 16 a
+ * file-backed layer's read failed, 17 its staging wait timed out); blocks.  (The reference accepts repeated ids and leaks a slot; both paths here reject them.) */
 int c_layer_table_status(int layer_idx);
 /* Block the host until every queued copy has landed. */
 int c_sync_copies(void);

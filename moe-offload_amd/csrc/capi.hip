@@ -39,6 +39,7 @@
 #include <numeric>
 #include <string>
 
+#include "file_feed.h"
 #include "file_io.h"
 #include "moe_common.h"
 #include "moe_offload.h"
@@ -567,6 +568,12 @@ int c_io_read_ranges(int fd, const uint64_t* offs, const uint64_t* lens, const u
 }
 
 void c_io_shutdown(void) {
+    for (int l = 0; l < MOE_MAX_LAYERS; ++l)
+        if (filefeed::attached(l)) {          // device-driven file layers: their staging kernels
+            (void)hipDeviceSynchronize();     // wait on the feeder, so they end first
+            break;
+        }
+    filefeed::shutdown();
     for (int l = 0; l < MOE_MAX_LAYERS; ++l) (void)join_file(g_layers[l]);
     fileio::shutdown();
     if (!g_ready) return;
@@ -623,6 +630,10 @@ void c_layer_init(int layer, int fd, int capacity, const uint64_t* base_offsets,
         return;
     }
     LayerState& L = g_layers[layer];
+    if (filefeed::attached(layer)) {
+        (void)hipDeviceSynchronize();         // its staging kernels wait on the feeder
+        filefeed::detach(layer);
+    }
     (void)join_file(L);
     if (L.inflight) (void)hipEventSynchronize(L.copy_done);
     release_file(L);
@@ -895,18 +906,33 @@ int c_layer_set_device_mode(int layer, int on) {
     if (!valid_layer(layer) || !g_layers[layer].init) { moe_set_error("set_device_mode: bad layer %d", layer); return -1; }
     LayerState& L = g_layers[layer];
     if (on && !L.device_mode) {
-        if (L.fd >= 0) { moe_set_error("device-driven staging needs a pinned host store (fd == -1)"); return -1; }
-        for (int t = 0; t < MOE_NUM_TENSORS; ++t)
+        for (int t = 0; t < MOE_NUM_TENSORS && L.fd < 0; ++t)
             if (L.row_bytes[t] && L.src[t] && L.dst[t] && !L.dev_src[t]) {
                 moe_set_error("device-driven staging: tensor %d store is not pinned host memory", t);
                 return -1;
             }
         if (!L.slot_inds || !L.slot_inds_device) { moe_set_error("device-driven layers need a device slot_inds buffer"); return -1; }
+        if (L.fd >= 0) {                      // file-backed: misses published to the feeder
+            if (drain_copies(L)) return -1;
+            filefeed::LayerIO io;
+            io.fd = L.fd;
+            io.fd_direct = L.fd_direct;
+            for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
+                io.src[t] = L.src[t];
+                io.row_bytes[t] = L.row_bytes[t];
+                io.dst[t] = L.dst[t];
+            }
+            if (filefeed::attach(layer, io)) return -1;
+        }
         if (!L.dtab) HIP_TRY(hipMalloc((void**)&L.dtab, sizeof(SlotTable)));
         L.device_mode = true;
         return push_table(L);
     }
     if (!on && L.device_mode) {
+        if (L.fd >= 0) {
+            HIP_TRY(hipDeviceSynchronize());  // staging kernels still waiting on the feeder end first
+            filefeed::detach(layer);
+        }
         if (pull_table(L)) return -1;
         L.device_mode = false;
     }
@@ -918,7 +944,8 @@ uint64_t c_layer_device_table(int layer) {
     return (uint64_t)g_layers[layer].dtab;
 }
 
-static int stage_device(LayerState& L, int list, hipStream_t s, int ctas) {
+static int stage_device(int layer, LayerState& L, int list, hipStream_t s, int ctas) {
+    if (L.fd >= 0) return filefeed::stage(layer, list, L.dtab, ctas, s);
     for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
         uint64_t rb = L.row_bytes[t];
         if (!rb || !L.dev_src[t] || !L.dst[t]) continue;
@@ -937,7 +964,9 @@ int c_layer_step_decode_dev(int layer, const uint32_t* ids_dev, int k, int stage
     if (k <= 0 || k > MOE_MAX_K || k > L.capacity) { moe_set_error("step_decode_dev: k=%d out of range", k); return -1; }
     hipStream_t s = (hipStream_t)stream;
     if (launch_slot_step(L.dtab, ids_dev, k, L.slot_inds, s)) return -1;
-    return stage_ctas < 0 ? 0 : stage_device(L, 0, s, stage_ctas);
+    if (stage_ctas < 0) return 0;
+    if (L.fd >= 0 && filefeed::publish(layer, 0, L.dtab, s)) return -1;
+    return stage_device(layer, L, 0, s, stage_ctas);
 }
 
 int c_layer_start_prefetch_dev(int layer, const int32_t* preds_dev, int m, int max_fetch, int stage_ctas,
@@ -949,7 +978,9 @@ int c_layer_start_prefetch_dev(int layer, const int32_t* preds_dev, int m, int m
     LayerState& L = g_layers[layer];
     hipStream_t s = (hipStream_t)stream;
     if (launch_slot_prefetch(L.dtab, preds_dev, m, max_fetch, s)) return -1;
-    return stage_ctas < 0 ? 0 : stage_device(L, 1, s, stage_ctas);
+    if (stage_ctas < 0) return 0;
+    if (L.fd >= 0 && filefeed::publish(layer, 1, L.dtab, s)) return -1;
+    return stage_device(layer, L, 1, s, stage_ctas);
 }
 
 // Queue the copies listed by the layer's last device-side decode step (list 0) or prefetch
@@ -960,8 +991,22 @@ int c_layer_stage_dev(int layer, int list, int stage_ctas, void* stream) {
         return -1;
     }
     if (list != 0 && list != 1) { moe_set_error("stage_dev: list %d (0 = decode step, 1 = prefetch)", list); return -1; }
-    return stage_device(g_layers[layer], list, (hipStream_t)stream, stage_ctas < 0 ? 0 : stage_ctas);
+    return stage_device(layer, g_layers[layer], list, (hipStream_t)stream, stage_ctas < 0 ? 0 : stage_ctas);
 }
+
+// File-backed device-driven layers: hand the list of the layer's last device-side decode step
+// (list 0) or prefetch (list 1) to the feeder thread, which reads those experts into the layer's
+// bounce entries while the stream goes on; c_layer_stage_dev then waits for each entry and copies
+// it into its slot.
+int c_layer_publish_dev(int layer, int list, void* stream) {
+    if (!valid_layer(layer) || !g_layers[layer].init || !g_layers[layer].device_mode || g_layers[layer].fd < 0) {
+        moe_set_error("publish_dev: layer %d is not a device-driven file-backed layer", layer);
+        return -1;
+    }
+    return filefeed::publish(layer, list, g_layers[layer].dtab, (hipStream_t)stream);
+}
+
+void c_io_set_feed_timeout_us(uint64_t us) { filefeed::set_timeout_us(us); }
 
 int c_layer_table_status(int layer) {
     if (!valid_layer(layer)) return -1;

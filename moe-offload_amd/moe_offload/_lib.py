@@ -126,6 +126,8 @@ SIGNATURES: dict[str, tuple] = {
     "c_layer_step_decode_dev": (_c_int, [_c_int, _c_vp, _c_int, _c_int, _c_vp]),
     "c_layer_start_prefetch_dev": (_c_int, [_c_int, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
     "c_layer_stage_dev": (_c_int, [_c_int, _c_int, _c_int, _c_vp]),
+    "c_layer_publish_dev": (_c_int, [_c_int, _c_int, _c_vp]),
+    "c_io_set_feed_timeout_us": (None, [_c_u64]),
     "c_layer_device_table": (_c_u64, [_c_int]),
     "c_layer_table_status": (_c_int, [_c_int]),
     "c_sync_copies": (_c_int, []),

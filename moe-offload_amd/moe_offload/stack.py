@@ -64,8 +64,10 @@ class StackConfig:
                                  # c_layer_decode_step_sched call per layer; device mode tables
                                  # take the variant's decisions
     split: bool = False          # host mode with sched: hit experts run before the misses land
-    store_file: str | None = None  # host mode: layers 1.. read their misses from this blob file
-                                 # (q2format.write_blob_file) instead of a pinned host store
+    store_file: str | None = None  # layers 1.. read their misses from this blob file
+                                 # (q2format.write_blob_file) instead of a pinned host store;
+                                 # device mode: the tables publish their misses to the library's
+                                 # feeder thread (c_layer_publish_dev), io="exact", fused tables
     io_threads: int = 8          # reader threads of the file tier
     io_direct: bool = False      # file tier: O_DIRECT reads (page cache bypassed)
     io: str = "exact"            # file tier cache: "exact" (expert_io.c's, c_layer_*) or "p1" (the
@@ -110,6 +112,7 @@ class DecodeStack:
         caps = compute_layer_capacities(budget_gb=c.budget_gb, budget_pct=c.budget_pct, num_layers=c.n_layers,
                                         num_experts=c.n_exp, expert_bytes=self.blob_bytes)
         self.capacities = caps
+        self.file_device = False
         gen = torch.Generator(device=self.device)
         gen.manual_seed(c.seed)
         dev = self.device
@@ -132,10 +135,11 @@ class DecodeStack:
             raise ValueError(f"io={c.io!r}: 'exact' or 'p1'")
         if c.io == "p1" and c.store_file is None:
             raise ValueError("io='p1' reads from a file: set store_file")
+        self.file_device = c.store_file is not None and mode == "device"
         if c.store_file is not None:
             # layers 1..: misses read from a blob file by the reader threads
-            if mode != "host":
-                raise ValueError("a file-backed stack is host-driven (mode='host')")
+            if self.file_device and (c.io != "exact" or not c.fused_tables or c.sched):
+                raise ValueError("a device-driven file-backed stack takes io='exact', fused tables, no sched")
             L.c_io_init(c.io_threads)
             L.c_io_set_direct(int(c.io_direct))
             self.store = FileExpertStore({l: c.store_file for l in range(1, c.n_layers)})
@@ -409,6 +413,11 @@ class DecodeStack:
         c = self.cfg
         self._router(l, tables=True)
         pf = c.prefetch and l + 1 < c.n_layers
+        if self.file_device:                           # the misses go to the feeder's readers now
+            if l >= 1:
+                _lib.check(self.L.c_layer_publish_dev(self.cidx(l), 0, main.cuda_stream), "publish_demand")
+            if pf:
+                _lib.check(self.L.c_layer_publish_dev(self.cidx(l + 1), 1, main.cuda_stream), "publish_prefetch")
         if l >= 1:
             early = c.prefetch and self.demand_overlaps_prefetch(l)
             if c.prefetch and not early:
@@ -548,6 +557,14 @@ class DecodeStack:
         else:
             self.decode_token_host()
         return self.xs[self.cfg.n_layers]
+
+    def table_status(self) -> dict[int, int]:
+        """Nonzero status words of the device-driven tables (blocks): 1 / 2 rejected ids, 16 a
+        file read failed, 17 a file-backed staging wait timed out."""
+        if self.mode != "device" or self.cfg.resident:
+            return {}
+        st = {l: self.L.c_layer_table_status(self.cidx(l)) for l in range(1, self.cfg.n_layers)}
+        return {l: v for l, v in st.items() if v}
 
     def capture_graph(self):
         """Capture one device-driven token into a HIP graph (replayed by decode_token)."""

@@ -6,6 +6,10 @@ whose misses are read from a blob file by the reader threads (host-driven tables
 * the id/prediction stream replayed through the oracle LRU in the reference's call order
   (loader.py:920-977) gives the same slots and counters;
 * 1 reader thread with O_DIRECT and 8 threads through the page cache give bit-identical tokens;
+* device-driven tables (the misses published to the library's feeder thread, staged by a kernel
+  that waits for each read) give bit-identical tokens, slots and counters, eager and replayed
+  from a HIP graph, through the page cache and with O_DIRECT; a truncated file and a staging
+  wait past its (tiny) time limit are reported in the table status instead of hanging;
 * the same stack on the P1 I/O scheduler (the C++ runner's `--io p1`: its own slot decisions, reads
   by 6 reader threads straight into HBM slot rows) gives bit-identical tokens too (the slots differ,
   the experts and their bytes do not), with the scheduler's counters consistent.
@@ -25,19 +29,23 @@ pytestmark = pytest.mark.gpu
 N_LAYERS, N_TOK = 6, 10
 
 
-def _run(path, layer_base, threads, direct, io="exact"):
+def _run(path, layer_base, threads, direct, io="exact", mode="host", graph=False):
     from moe_offload.stack import DecodeStack, StackConfig
-    print(f"file stack: io={io} threads={threads} direct={direct}", flush=True)
+    print(f"file stack: io={io} threads={threads} direct={direct} mode={mode} graph={graph}", flush=True)
     cfg = StackConfig(n_layers=N_LAYERS, seed=6, layer_base=layer_base, store_file=str(path), io_threads=threads,
                       io_direct=direct, io=io)
-    st = DecodeStack(cfg, mode="host")
+    st = DecodeStack(cfg, mode=mode)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(98)
     xs = torch.randn((N_TOK, cfg.hidden), device="cuda", generator=gen).half()
     rec = []
     for t in range(N_TOK):
+        if graph and t == 1:                          # token 0 eager, the rest replayed
+            st.capture_graph()
         st.decode_token(xs[t])
         torch.cuda.synchronize()
+        if mode == "device":
+            assert st.table_status() == {}, t
         rec.append({"ids": st.ids.cpu().numpy().copy(), "scores": st.scores.cpu().numpy().copy(),
                     "pred": st.pred.cpu().numpy().copy(), "xs": st.xs.cpu().numpy().copy(),
                     "hs": st.hs.cpu().numpy().copy(),
@@ -136,3 +144,75 @@ def test_p1_scheduler_stack_gives_the_same_tokens(tmp_path, threads):
         assert _lib.last_error() == ""
     finally:
         p1.close()
+
+
+def _blob_file(tmp_path, name="layer.q2blob"):
+    from moe_offload import q2format
+    from moe_offload.stack import StackConfig, random_blobs
+    c = StackConfig()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    blobs = random_blobs(c.n_exp, c.hidden, c.inter, c.group, gen, "cuda").cpu().numpy()
+    path = tmp_path / name
+    q2format.write_blob_file(path, blobs, c.hidden, c.inter)
+    return path, blobs
+
+
+@pytest.mark.parametrize("graph,threads,direct", [(False, 8, False), (True, 8, False), (True, 1, True)])
+def test_device_driven_file_stack_matches_host_driven(tmp_path, graph, threads, direct):
+    path, blobs = _blob_file(tmp_path)
+    st, rec, stats = _run(path, 50, 8, False)
+    st.close()
+    dv, drec, dstats = _run(path, 44, threads, direct, mode="device", graph=graph)
+    try:
+        for t in range(N_TOK):
+            assert np.array_equal(drec[t]["xs"], rec[t]["xs"]), t
+            assert np.array_equal(drec[t]["ids"], rec[t]["ids"]), t
+            for l in range(1, N_LAYERS):
+                assert np.array_equal(drec[t]["slots"][l], rec[t]["slots"][l]), (t, l)
+        assert dstats == stats
+        for l in range(1, N_LAYERS):                  # every slot holds the expert its table names
+            e, s, n = (ctypes.c_int32 * 512)(), (ctypes.c_int32 * 512)(), ctypes.c_int(0)
+            dv.L.c_layer_get_lru_state(dv.cidx(l), e, s, ctypes.byref(n))
+            pool = dv.pools[l].cpu().numpy()
+            for i in range(n.value):
+                assert np.array_equal(pool[s[i]], blobs[e[i]]), (l, e[i], s[i])
+    finally:
+        dv.close()
+
+
+def test_device_driven_file_stack_reports_failed_reads_and_timeouts(tmp_path):
+    import os
+
+    from moe_offload.stack import DecodeStack, StackConfig
+    path, _ = _blob_file(tmp_path)
+    cfg = StackConfig(n_layers=3, seed=6, layer_base=40, store_file=str(path))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    x = torch.randn(cfg.hidden, device="cuda", generator=gen).half()
+    # every expert past the first 8 lies beyond the end of the file: its read comes up short
+    from moe_offload import q2format
+    hdr = q2format.read_blob_header(str(path))
+    short = tmp_path / "short.q2blob"
+    with open(path, "rb") as f, open(short, "wb") as g:
+        g.write(f.read(hdr["data_offset"] + 8 * hdr["blob_bytes"]))
+    assert os.path.getsize(short) < os.path.getsize(path)
+    print("file stack: truncated file", flush=True)
+    st = DecodeStack(StackConfig(n_layers=3, seed=6, layer_base=40, store_file=str(short)), mode="device")
+    try:
+        st.decode_token(x)
+        torch.cuda.synchronize()
+        assert 16 in st.table_status().values()
+    finally:
+        st.close()
+    # a wait limit far below one read's time: the cold layer's demand entries time out
+    print("file stack: 1 us staging wait", flush=True)
+    st = DecodeStack(cfg, mode="device")
+    try:
+        st.L.c_io_set_feed_timeout_us(1)
+        st.decode_token(x)
+        torch.cuda.synchronize()
+        assert st.table_status().get(1) == 17
+    finally:
+        st.L.c_io_set_feed_timeout_us(0)
+        st.close()
