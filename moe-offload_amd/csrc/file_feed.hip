@@ -70,7 +70,7 @@ struct Feed {
     std::atomic<bool> stop{false};
     bool running = false;
     FeedLayer layers[MOE_MAX_LAYERS];
-    uint64_t timeout_us = 10'000'000;
+    std::atomic<uint64_t> timeout_us{10'000'000};
 };
 
 // Never destroyed: the feeder may still be running when the process exits.
@@ -400,7 +400,7 @@ int stage(int layer, int list, SlotTable* dtab, int ctas, hipStream_t s) {
     HIP_TRY(hipGetDevice(&dev));
     HIP_TRY(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
     if (khz <= 0) khz = 100000;
-    const uint64_t ticks = G().timeout_us * (uint64_t)khz / 1000;
+    const uint64_t ticks = G().timeout_us.load(std::memory_order_relaxed) * (uint64_t)khz / 1000;
     if (ctas <= 0) ctas = 2;
     for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
         const uint64_t rb = F.io.row_bytes[t];
@@ -424,7 +424,7 @@ int stage(int layer, int list, SlotTable* dtab, int ctas, hipStream_t s) {
     return 0;
 }
 
-void set_timeout_us(uint64_t us) { G().timeout_us = us ? us : 10'000'000; }
+void set_timeout_us(uint64_t us) { G().timeout_us.store(us ? us : 10'000'000, std::memory_order_relaxed); }
 
 void shutdown() {
     for (int l = 0; l < MOE_MAX_LAYERS; ++l) detach(l);
