@@ -60,6 +60,9 @@ def parse():
     ap.add_argument("--no-tensor-form", action="store_true",
                     help="skip the pass over the reference's 9-tensor expert format at 2560 x 640")
     ap.add_argument("--io-threads", type=int, default=8, help="reader threads of the on-disk tier pass")
+    ap.add_argument("--file-tier-runs", default=None,
+                    help="comma-separated subset of the on-disk tier runs (host_store, page_cache, o_direct, "
+                         "p1_page_cache, device_page_cache, device_o_direct); default all")
     ap.add_argument("--sched", action="store_true",
                     help="the C++ runner's scheduler variant of the expert cache (c_layer_decode_step_sched)")
     ap.add_argument("--split", action="store_true", help="with --sched --mode host: hit experts before misses land")
@@ -386,7 +389,7 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
     return res
 
 
-def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8):
+def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8, runs=None):
     """The decode stack with the on-disk tier: every cached layer reads its misses from one blob
     file of 512 experts (q2format.write_blob_file, 503 MB, shared by the 47 cached layers) with the
     reader threads, host-driven tables (one device->host read of ids per layer).  Timed through
@@ -420,6 +423,8 @@ def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8):
                                ("p1_page_cache", {"store_file": path, "io": "p1"}, "host"),
                                ("device_page_cache", {"store_file": path}, "device"),
                                ("device_o_direct", {"store_file": path, "io_direct": True}, "device")):
+            if runs and name not in runs:
+                continue
             cfg = StackConfig(n_layers=n_layers, io_threads=threads, **kw)
             st = DecodeStack(cfg, mode=mode)
             try:
@@ -805,7 +810,8 @@ def main():
         print(json.dumps({"tensor_form": tensor_form_pass()}), flush=True)
         return
     if args.only == "filetier":
-        print(json.dumps({"file_tier": file_tier_pass(args.layers, threads=args.io_threads)}), flush=True)
+        runs = set(args.file_tier_runs.split(",")) if args.file_tier_runs else None
+        print(json.dumps({"file_tier": file_tier_pass(args.layers, threads=args.io_threads, runs=runs)}), flush=True)
         return
     if args.only == "floor":
         fl = launch_floor([3_276_800, 6_553_600, 9_830_400, 64 << 20])
