@@ -24,6 +24,9 @@ namespace {
 // read failed.  Epochs stay below 2^31.
 constexpr uint32_t kFeedError = 0x80000000u;
 constexpr uint64_t kAlign = 4096;             // O_DIRECT granularity (and the bounce slack)
+// Reads are cut into pieces of this size, so a short list (a layer's few misses) still keeps
+// every reader thread busy.
+constexpr uint64_t kPiece = 256 * 1024;
 
 // One (layer, list) mailbox, host-coherent: written by k_file_publish, read by the feeder.
 struct Mail {
@@ -170,15 +173,16 @@ __global__ __launch_bounds__(256) void k_stage_file(StageArgs a) {
 
 // ---- feeder ---------------------------------------------------------------------------------
 
-// Reads of a newly published list: entry c <- expert mail.eid[c], one read per tensor (a blob
-// file has one), straight into the entry (O_DIRECT: the 4 KiB-aligned range around the bytes,
-// placed so the bytes land at the entry's data offset; the entry keeps 4 KiB of slack on each
-// side of every tensor for that).  The worker finishing an entry's last read sets its flag.
+// Reads of a newly published list: entry c <- expert mail.eid[c], per tensor (a blob file has
+// one) the expert's bytes in pieces of kPiece, straight into the entry (O_DIRECT: the 4 KiB-aligned
+// range around the bytes, placed so the bytes land at the entry's data offset; the entry keeps
+// 4 KiB of slack on each side of every tensor for that).  The worker finishing an entry's last
+// piece sets its flag.
 void start_reads(FeedLayer& F, int li, uint32_t epoch, int n) {
     FeedList& Q = F.list[li];
     const LayerIO& io = F.io;
     const bool direct = io.fd_direct >= 0;
-    int per = 0;
+    int per = 0;                                        // tensors to read per expert
     for (int t = 0; t < MOE_NUM_TENSORS; ++t)
         if (io.row_bytes[t] && io.dst[t]) ++per;
     auto b = std::make_shared<fileio::Batch>();
@@ -188,21 +192,25 @@ void start_reads(FeedLayer& F, int li, uint32_t epoch, int n) {
             __atomic_store_n(&Q.landed[c], epoch | kFeedError, __ATOMIC_RELEASE);
             continue;
         }
-        Q.left[c].store(per, std::memory_order_relaxed);
         uint8_t* entry = Q.bounce + (uint64_t)c * F.entry_bytes;
+        int pieces = 0;
         for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
             const uint64_t rb = io.row_bytes[t];
             if (!rb || !io.dst[t]) continue;
             const uint64_t off = io.src[t] + (uint64_t)e * rb;
-            fileio::Read r;
-            if (direct) {
-                const uint64_t a = off & ~(kAlign - 1), end = (off + rb + kAlign - 1) & ~(kAlign - 1);
-                r = fileio::Read{io.fd_direct, a, end - a, off - a + rb, entry + F.toff[t] - (off - a), true, c};
-            } else {
-                r = fileio::Read{io.fd, off, rb, rb, entry + F.toff[t], false, c};
+            // [a, end): the bytes read (O_DIRECT: the 4 KiB-aligned range around [off, off + rb)),
+            // landing at dst + (p - a); cut into pieces of kPiece (a multiple of 4 KiB)
+            const uint64_t a = direct ? off & ~(kAlign - 1) : off;
+            const uint64_t end = direct ? (off + rb + kAlign - 1) & ~(kAlign - 1) : off + rb;
+            uint8_t* dst = entry + F.toff[t] - (off - a);
+            for (uint64_t p = a; p < end; p += kPiece) {
+                const uint64_t pe = p + kPiece < end ? p + kPiece : end;
+                const uint64_t need = (pe < off + rb ? pe : off + rb) - p;
+                b->reads.push_back(fileio::Read{direct ? io.fd_direct : io.fd, p, pe - p, need, dst + (p - a), direct, c});
+                ++pieces;
             }
-            b->reads.push_back(r);
         }
+        Q.left[c].store(pieces, std::memory_order_relaxed);
     }
     if (b->reads.empty()) return;
     uint32_t* landed = Q.landed;
