@@ -5,6 +5,7 @@
 #include "file_feed.h"
 
 #include <sched.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <atomic>
@@ -277,6 +278,21 @@ void feeder_main() {
     }
 }
 
+// At process exit (registered after the HIP runtime was loaded, so it runs before the runtime's
+// own teardown frees the mailboxes): end the feeder's polling; reads in flight are left alone.
+void stop_feeder() {
+    Feed& g = G();
+    std::thread t;
+    {
+        std::lock_guard<std::mutex> lk(g.mu);
+        if (!g.running) return;
+        g.stop.store(true, std::memory_order_release);
+        t.swap(g.thread);
+        g.running = false;
+    }
+    t.join();
+}
+
 void free_layer(FeedLayer& F) {
     if (F.epochs_dev) (void)hipFree(F.epochs_dev);
     if (F.host_block) (void)hipHostFree(F.host_block);
@@ -357,6 +373,8 @@ int attach(int layer, const LayerIO& io) {
         g.stop.store(false);
         g.thread = std::thread(feeder_main);
         g.running = true;
+        static std::once_flag at_exit;                // the feeder polls pinned memory: it stops
+        std::call_once(at_exit, [] { std::atexit(stop_feeder); });   // before the runtime's teardown
     }
     return 0;
 }
@@ -436,16 +454,7 @@ void set_timeout_us(uint64_t us) { G().timeout_us.store(us ? us : 10'000'000, st
 
 void shutdown() {
     for (int l = 0; l < MOE_MAX_LAYERS; ++l) detach(l);
-    Feed& g = G();
-    std::thread t;
-    {
-        std::lock_guard<std::mutex> lk(g.mu);
-        if (!g.running) return;
-        g.stop.store(true, std::memory_order_release);
-        t.swap(g.thread);
-        g.running = false;
-    }
-    t.join();
+    stop_feeder();
 }
 
 }  // namespace filefeed

@@ -216,3 +216,27 @@ def test_device_driven_file_stack_reports_failed_reads_and_timeouts(tmp_path):
     finally:
         st.L.c_io_set_feed_timeout_us(0)
         st.close()
+
+
+def test_device_driven_file_stack_exits_cleanly_without_close(tmp_path):
+    """A process that ends with a device-driven file stack still open (the feeder thread polling its
+    pinned mailboxes) exits with status 0: the feeder stops before the runtime's teardown."""
+    import os
+    import subprocess
+    import sys
+    path, _ = _blob_file(tmp_path)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = (
+        "import sys, torch\n"
+        f"sys.path[:0] = [{root!r}, {os.path.join(root, 'moe-offload_amd')!r}]\n"
+        "from moe_offload.stack import DecodeStack, StackConfig\n"
+        f"st = DecodeStack(StackConfig(n_layers=3, seed=6, layer_base=40, store_file={str(path)!r}), mode='device')\n"
+        "st.decode_token(torch.randn(st.cfg.hidden, device='cuda').half())\n"
+        "torch.cuda.synchronize()\n"
+        "assert st.table_status() == {}\n"
+        "print('token done', flush=True)\n"
+    )
+    print("file stack: child process exits without close()", flush=True)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
+    assert "token done" in r.stdout
