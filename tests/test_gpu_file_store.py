@@ -4,7 +4,8 @@ HBM slot pools (the reference reads its shard the same way, `mlx-qwen38/expert_i
 
 Blob file: 40 decode steps (capacity 16 over 64 experts) then an 8-token prefill.  Reference
 shard read in place (9 tensors, bf16 scales, hidden 2560 / inter 640): decode steps with
-prefetches, 1 and 8 reader threads, page cache and O_DIRECT.  Slot decisions and counters match
+prefetches, 1 and 8 reader threads, page cache and O_DIRECT, with host- and device-driven tables
+(the latter through the feeder thread and the waiting staging kernels).  Slot decisions and counters match
 the oracle LRU, every slot holds the expert the table names, outputs match the fp64 oracle within
 1e-2 x RMS.
 """
@@ -141,6 +142,73 @@ def test_reference_shard_read_in_place(tmp_path, threads, direct):
         assert _lib.last_error() == ""
     finally:
         if mod is not None:
+            mod.close()
+        L.c_io_set_direct(0)
+        L.c_io_init(8)
+        store.close()
+
+
+@pytest.mark.parametrize("threads,direct", [(8, 0), (2, 1)])
+def test_reference_shard_read_in_place_device_driven(tmp_path, threads, direct):
+    """The same shard bound in place with device-driven tables: each decode step and prefetch
+    publishes its misses to the feeder thread (c_layer_step_decode_dev / c_layer_start_prefetch_dev
+    with staging), which reads the 9 tensors of each expert into its bounce entry; the staging
+    kernels copy every tensor into its pool.  Slots, counters, pool rows and outputs as host-driven."""
+    from moe_offload import _lib
+    from moe_offload.loader import CachedSwitchGLU, ShardExpertStore
+    Hs, Is, Es, cap, layer = 2560, 640, 40, 12, 38
+    print(f"shard in place, device-driven: threads={threads} direct={direct}", flush=True)
+    mlx = experts_bf16(Es, Hs, Is, seed=51)
+    write_reference_shard(tmp_path / f"experts-{layer:02d}.safetensors", layer, mlx)
+    want_rows = role_arrays(mlx)
+    dev = torch.device("cuda:0")
+    L = _lib.lib()
+    L.c_io_init(threads)
+    L.c_io_set_direct(direct)
+    store = ShardExpertStore(tmp_path, layers=[layer])
+    mod = None
+    try:
+        mod = CachedSwitchGLU(store, layer, cap)
+        _lib.check(L.c_layer_set_device_mode(layer, 1), "device_mode")
+        stream = torch.cuda.current_stream().cuda_stream
+        lay = store.layout[layer]
+        ora = olru.CLru(layer, cap, expert_bytes=mod.blob_bytes)
+        ora.reset_stats()
+        rng = np.random.default_rng(52)
+        f = lambda e: tuple((p[0][e], p[1][e], p[2][e]) for p in mlx)
+        y = torch.empty(Hs, dtype=torch.float32, device=dev)
+        for t in range(16):
+            ids = [int(v) for v in rng.choice(Es, K, replace=False)]
+            x = rng.standard_normal(Hs).astype(np.float16)
+            sc = rng.dirichlet(np.ones(K)).astype(np.float16)
+            xt, sct = torch.from_numpy(x).to(dev), torch.from_numpy(sc).to(dev)
+            it = torch.tensor(ids, dtype=torch.int32, device=dev)
+            _lib.check(L.c_layer_step_decode_dev(layer, it.data_ptr(), K, 0, stream), "step_dev")
+            _lib.check(L.c_layer_switch_glu(layer, xt.data_ptr(), sct.data_ptr(), None, mod._h_ws.data_ptr(),
+                                            y.data_ptr(), 0, K, stream), "switch_glu")
+            slots, _ = ora.step(ids)
+            assert mod._slot_inds_buf[:K].cpu().tolist() == slots, t
+            assert L.c_layer_table_status(layer) == 0, t
+            if t in (0, 9, 15):
+                want = q2.moe_combine(x.astype(np.float64), np.array(ids), sc.astype(np.float64), f, bits=2, group=64,
+                                      sdtype="bf16")
+                assert_close_rms(y.cpu().numpy(), want, 1e-2, f"step {t}")
+            if t % 3 == 1:                       # prefetch 3 of 12 predicted experts for the next step
+                pred = [int(v) for v in rng.choice(Es, 12, replace=False)]
+                pt = torch.tensor(pred, dtype=torch.int32, device=dev)
+                _lib.check(L.c_layer_start_prefetch_dev(layer, pt.data_ptr(), 12, 3, 0, stream), "prefetch_dev")
+                ora.prefetch(pred, 3)
+        torch.cuda.synchronize()
+        assert L.c_layer_table_status(layer) == 0
+        mod.sync_stats_from_c()
+        assert [int(v) for v in mod._c_stats_buf] == ora.stats()
+        for e, sl in zip(*ora.get_state()):
+            for tt, r in enumerate(lay["roles"]):
+                assert np.array_equal(mod.pools[tt][sl].cpu().numpy(), want_rows[r][e]), (e, sl, tt)
+        assert _lib.last_error() == ""
+    finally:
+        if mod is not None:
+            L.c_layer_set_device_mode(layer, 0)
             mod.close()
         L.c_io_set_direct(0)
         L.c_io_init(8)
