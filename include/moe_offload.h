@@ -359,7 +359,8 @@ int c_layer_stage_dev(int layer_idx, int list, int stage_ctas, void* stream);
  * copies it into its slot.  Replaces the reference's step-time reads of the misses
  * (expert_io.c:187-356, 583-685) for tables that run on the GPU. */
 int c_layer_publish_dev(int layer_idx, int list, void* stream);
-/* Longest a file-backed staging kernel waits for one expert's read (0: 10 s); past it the
+/* No counterpart in the reference (its reads block the calling thread, expert_io.c:312-356).
+ * Longest a file-backed staging kernel waits for one expert's read (0: 10 s); past it the
  * layer's table status becomes 17 (a failed read: 16).  Applies to copies queued afterwards. */
 void c_io_set_feed_timeout_us(uint64_t us);
 /* Device address of a device-driven layer's table; 0 otherwise. */
