@@ -437,13 +437,19 @@ class OffloadEngine:
     def __init__(self, model_path=None, budget_gb: float | None = None, budget_pct: float | None = 20.0,
                  alloc_mode: str = "even", prefetch: bool = True, prefetch_top_m: int = PREFETCH_TOP_M,
                  prefetch_cap: int = PREFETCH_MAX_CAP, mode: str = "device", n_layers: int = NUM_LAYERS,
-                 hidden: int = 2048, inter: int = 512, seed: int = 0):
+                 hidden: int = 2048, inter: int = 512, seed: int = 0, store_file: str | None = None,
+                 io_threads: int = 8, io_direct: bool = False):
+        """store_file: the cached layers read their misses from this blob file (the on-disk tier, as
+        the reference's engine reads its expert shards) with `io_threads` reader threads, through
+        the page cache or with O_DIRECT; device mode then publishes each layer's misses to the
+        library's feeder thread.  Without it they come from a pinned host store."""
         from .stack import DecodeStack, StackConfig
         t0 = time.perf_counter()
         self.model_path, self.alloc_mode = model_path, alloc_mode
         self.prefetch, self.prefetch_top_m, self.prefetch_cap = prefetch, prefetch_top_m, prefetch_cap
         cfg = StackConfig(n_layers=n_layers, hidden=hidden, inter=inter, budget_pct=budget_pct, budget_gb=budget_gb,
-                          prefetch=prefetch, top_m=prefetch_top_m, prefetch_cap=prefetch_cap, seed=seed)
+                          prefetch=prefetch, top_m=prefetch_top_m, prefetch_cap=prefetch_cap, seed=seed,
+                          store_file=store_file, io_threads=io_threads, io_direct=io_direct)
         self.model = DecodeStack(cfg, mode=mode)
         self.capacities = self.model.capacities
         self.total_cached_slots = sum(self.capacities.values())
