@@ -361,12 +361,23 @@ int c_layer_stage_dev(int layer_idx, int list, int stage_ctas, void* stream);
 int c_layer_publish_dev(int layer_idx, int list, void* stream);
 /* No counterpart in the reference (its reads block the calling thread, expert_io.c:312-356).
  * Longest a file-backed staging kernel waits for one expert's read (0: 10 s); past it the
- * layer's table status becomes 17 (a failed read: 16).  Applies to copies queued afterwards. */
+ * layer's table status becomes 17 (a failed read: 16).  Applies to copies queued afterwards.
+ * Both faults are sticky: the slot keeps its old bytes, so the table stays faulted (and its
+ * later stagings copy nothing) until c_layer_reset_cache.  Staging a list that a table
+ * operation changed since its last c_layer_publish_dev fails with -1. */
 void c_io_set_feed_timeout_us(uint64_t us);
+/* No counterpart in the reference (its reads report nothing: expert_io.c:118-127).  The
+ * library-wide sticky fault word of the device-driven file tier: 0, or the code (16 / 17) a
+ * staging kernel last stored on a failed read or a timed-out wait.  Host memory, so it is read
+ * without synchronising the GPU (it reflects the kernels that have run); cleared by
+ * c_io_clear_fault. */
+int c_io_fault(void);
+void c_io_clear_fault(void);
 /* Device address of a device-driven layer's table; 0 otherwise. */
 uint64_t c_layer_device_table(int layer_idx);
-/* Status word of the last device-side operation (0 ok, 1 id out of range, 2 repeated id, 16 a
- * file-backed layer's read failed, 17 its staging wait timed out); blocks.  (The reference accepts repeated ids and leaks a slot; both paths here reject them.) */
+/* Status word of a device-driven table: the sticky file-tier fault if any (16 a file-backed
+ * layer's read failed, 17 its staging wait timed out; cleared by c_layer_reset_cache), else that
+ * of the last device-side table operation (0 ok, 1 id out of range, 2 repeated id); blocks.  (The reference accepts repeated ids and leaks a slot; both paths here reject them.) */
 int c_layer_table_status(int layer_idx);
 /* Block the host until every queued copy has landed. */
 int c_sync_copies(void);

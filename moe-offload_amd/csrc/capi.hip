@@ -964,6 +964,7 @@ int c_layer_step_decode_dev(int layer, const uint32_t* ids_dev, int k, int stage
     if (k <= 0 || k > MOE_MAX_K || k > L.capacity) { moe_set_error("step_decode_dev: k=%d out of range", k); return -1; }
     hipStream_t s = (hipStream_t)stream;
     if (launch_slot_step(L.dtab, ids_dev, k, L.slot_inds, s)) return -1;
+    filefeed::mark_table_op(layer, 0);
     if (stage_ctas < 0) return 0;
     if (L.fd >= 0 && filefeed::publish(layer, 0, L.dtab, s)) return -1;
     return stage_device(layer, L, 0, s, stage_ctas);
@@ -978,6 +979,7 @@ int c_layer_start_prefetch_dev(int layer, const int32_t* preds_dev, int m, int m
     LayerState& L = g_layers[layer];
     hipStream_t s = (hipStream_t)stream;
     if (launch_slot_prefetch(L.dtab, preds_dev, m, max_fetch, s)) return -1;
+    filefeed::mark_table_op(layer, 1);
     if (stage_ctas < 0) return 0;
     if (L.fd >= 0 && filefeed::publish(layer, 1, L.dtab, s)) return -1;
     return stage_device(layer, L, 1, s, stage_ctas);
@@ -1012,8 +1014,12 @@ int c_layer_table_status(int layer) {
     if (!valid_layer(layer)) return -1;
     LayerState& L = g_layers[layer];
     if (pull_table(L)) return -1;
-    return L.tab.status;
+    return L.tab.io_fault ? L.tab.io_fault : L.tab.status;   // a sticky file-tier fault first
 }
+
+int c_io_fault(void) { return filefeed::fault_word(); }
+
+void c_io_clear_fault(void) { filefeed::clear_fault_word(); }
 
 // ---- compute entry points ---------------------------------------------------------------------
 
@@ -1088,9 +1094,13 @@ int c_router_tables_dev(int step_layer, int pf_layer, int max_fetch, const float
     }
     float* scratch = (float*)workspace;
     unsigned* counter = (unsigned*)((uint8_t*)workspace + (size_t)(2 * n_exp) * sizeof(float));
-    return launch_router(h_in, (const __half*)norm_w, eps, (const __half*)x_in, (__half*)x_out,
-                         (const __half*)w, (const __half*)w_next, hidden, n_exp, k, m, scratch, counter,
-                         ids_out, (__half*)scores_out, pred_out, st, slots, pt, max_fetch, (hipStream_t)stream);
+    if (launch_router(h_in, (const __half*)norm_w, eps, (const __half*)x_in, (__half*)x_out, (const __half*)w,
+                      (const __half*)w_next, hidden, n_exp, k, m, scratch, counter, ids_out, (__half*)scores_out,
+                      pred_out, st, slots, pt, max_fetch, (hipStream_t)stream))
+        return -1;
+    if (st) filefeed::mark_table_op(step_layer, 0);
+    if (pt) filefeed::mark_table_op(pf_layer, 1);
+    return 0;
 }
 
 int moe_f64_to_f16(const double* in, uint16_t* out, int n, void* stream) {

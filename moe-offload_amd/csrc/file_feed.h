@@ -13,7 +13,13 @@
 //
 // A bounce entry is rewritten only after the next publication of its (layer, list), which the
 // stream orders after the previous staging of that list has finished (the next token's router of
-// the layer runs after its GEMV, which waits for both lists' copies).
+// the layer runs after its GEMV, which waits for both lists' copies), and the feeder starts a
+// publication's reads only once every read of that list's previous publication has ended (after a
+// staging wait that timed out, the late reads would otherwise land in the reused entries).
+//
+// Failures are sticky: a failed read or a wait past its limit leaves the slot alone, sets the
+// table's io_fault word (cleared only by reset_cache) and the library's fault word (host memory,
+// read without a GPU synchronisation: fault_word()); later stagings of that table copy nothing.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -46,6 +52,12 @@ int publish(int layer, int list, SlotTable* dtab, hipStream_t s);
 int stage(int layer, int list, SlotTable* dtab, int ctas, hipStream_t s);
 // Longest a staging block waits for one entry (0: the default, 10 s).
 void set_timeout_us(uint64_t us);
+// The library's sticky fault word (the first io_fault code any table took; 0 none) and its clear.
+int32_t fault_word();
+void clear_fault_word();
+// The layer's list was changed by a table operation (mark_table_op) or handed to the feeder
+// (publish): stage() refuses a list changed since its last publication.
+void mark_table_op(int layer, int list);
 // Detach every layer and stop the feeder.
 void shutdown();
 

@@ -59,6 +59,7 @@ struct Inflight {
 
 struct FeedLayer {
     std::atomic<bool> active{false};
+    bool unpublished[2] = {false, false};     // a table op changed the list since its publication
     LayerIO io;
     uint64_t entry_bytes = 0;
     uint64_t toff[MOE_NUM_TENSORS] = {};      // data of tensor t inside an entry
@@ -76,6 +77,8 @@ struct Feed {
     bool running = false;
     FeedLayer layers[MOE_MAX_LAYERS];
     std::atomic<uint64_t> timeout_us{10'000'000};
+    int32_t* fault = nullptr;                 // host-coherent sticky fault word (host view)
+    int32_t* fault_dev = nullptr;
 };
 
 // Never destroyed: the feeder may still be running when the process exits.
@@ -117,6 +120,7 @@ __global__ __launch_bounds__(64) void k_file_publish(PubArgs a) {
 
 struct StageArgs {
     SlotTable* t;
+    int32_t* fault;                           // the library's fault word (host-coherent)
     int list, cap;
     const uint32_t* epoch;                    // device word, advanced by k_file_publish
     const uint32_t* landed;
@@ -132,7 +136,9 @@ struct StageArgs {
 // blockIdx.x striding over 16-byte units, four in flight per thread (as k_stage).  The bounce
 // entries are host-coherent (fine-grained) memory: the GPU caches none of their lines, so a
 // rewritten entry is read fresh.  A failed read
-// or a wait past spin_ticks leaves the slot alone and sets the table's status word.
+// or a wait past spin_ticks leaves the slot alone and sets the table's sticky io_fault word and the
+// library's fault word; a table that already carries a fault copies nothing more (it stays wrong
+// until reset_cache, and the host reports it).
 __global__ __launch_bounds__(256) void k_stage_file(StageArgs a) {
     const int c = blockIdx.y;
     const int n = a.list ? a.t->pf_n_copy : a.t->n_copy;
@@ -143,15 +149,20 @@ __global__ __launch_bounds__(256) void k_stage_file(StageArgs a) {
     if (threadIdx.x == 0) {
         const uint32_t e = *a.epoch;
         const uint64_t t0 = wall_clock64();
-        int r = 0;
-        for (;;) {
+        int r = __hip_atomic_load(&a.t->io_fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ? -3 : 0;
+        while (r == 0) {
             const uint32_t v = __hip_atomic_load(a.landed + c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
             if (v == e) { r = 1; break; }
             if (v == (e | kFeedError)) { r = -1; break; }
             if (wall_clock64() - t0 > a.spin_ticks) { r = -2; break; }
             __builtin_amdgcn_s_sleep(4);
         }
-        if (r < 0) atomicCAS(&a.t->status, 0, r == -1 ? kStatusReadFailed : kStatusTimedOut);
+        if (r == -1 || r == -2) {
+            const int32_t code = r == -1 ? kStatusReadFailed : kStatusTimedOut;
+            atomicCAS(&a.t->io_fault, 0, code);
+            // a plain store to host memory (no read-modify-write over the link)
+            __hip_atomic_store(a.fault, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
         ok = r;
     }
     __syncthreads();
@@ -257,10 +268,17 @@ void feeder_main() {
             for (int l = 0; l < MOE_MAX_LAYERS; ++l) {
                 FeedLayer& F = g.layers[l];
                 if (!F.active.load(std::memory_order_acquire)) continue;
+                reap(F);
                 for (int li = 0; li < 2; ++li) {
                     FeedList& Q = F.list[li];
                     const uint32_t e = __atomic_load_n(&Q.mail->epoch, __ATOMIC_ACQUIRE);
                     if (e == Q.seen) continue;
+                    // the list's previous reads write into the same entries and counters: a new
+                    // epoch starts once they have all ended (normally they have: its staging waited
+                    // for every entry; after a timed-out wait they may still be landing)
+                    bool reading = false;
+                    for (const Inflight& f : F.inflight) reading |= f.list == li;
+                    if (reading) { busy = true; continue; }
                     Q.seen = e;
                     work = true;
                     int n = Q.mail->n;
@@ -370,7 +388,19 @@ int attach(int layer, const LayerIO& io) {
         Q.bounce_dev = (uint8_t*)bd;
     }
     std::lock_guard<std::mutex> lk(g.mu);
+    if (!g.fault) {                                   // the library's fault word, kept until exit
+        void *h = nullptr, *d = nullptr;
+        if (hipHostMalloc(&h, 256, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess || dev_ptr(h, &d)) {
+            if (h) (void)hipHostFree(h);
+            moe_set_error("file feed: no pinned memory for the fault word");
+            return fail();
+        }
+        memset(h, 0, 256);
+        g.fault = (int32_t*)h;
+        g.fault_dev = (int32_t*)d;
+    }
     F.active.store(true, std::memory_order_release);
+    F.unpublished[0] = F.unpublished[1] = false;
     if (!g.running) {
         g.stop.store(false);
         g.thread = std::thread(feeder_main);
@@ -404,9 +434,23 @@ void detach(int layer) {
     free_layer(F);
 }
 
+void mark_table_op(int layer, int list) {
+    if (attached(layer) && (list == 0 || list == 1)) G().layers[layer].unpublished[list] = true;
+}
+
+int32_t fault_word() {
+    const int32_t* f = G().fault;
+    return f ? __atomic_load_n(f, __ATOMIC_ACQUIRE) : 0;
+}
+
+void clear_fault_word() {
+    if (G().fault) __atomic_store_n(G().fault, 0, __ATOMIC_RELEASE);
+}
+
 int publish(int layer, int list, SlotTable* dtab, hipStream_t s) {
     if (!attached(layer)) { moe_set_error("file feed: layer %d is not a device-driven file layer", layer); return -1; }
     if (list != 0 && list != 1) { moe_set_error("file feed: list %d (0 decode step, 1 prefetch)", list); return -1; }
+    G().layers[layer].unpublished[list] = false;
     FeedList& Q = G().layers[layer].list[list];
     PubArgs a = {};
     a.t[0] = dtab;
@@ -423,6 +467,11 @@ int stage(int layer, int list, SlotTable* dtab, int ctas, hipStream_t s) {
     if (!attached(layer)) { moe_set_error("file feed: layer %d is not a device-driven file layer", layer); return -1; }
     if (list != 0 && list != 1) { moe_set_error("file feed: list %d (0 decode step, 1 prefetch)", list); return -1; }
     FeedLayer& F = G().layers[layer];
+    if (F.unpublished[list]) {
+        moe_set_error("file feed: layer %d list %d changed by a table operation since its last publication "
+                      "(c_layer_publish_dev before c_layer_stage_dev)", layer, list);
+        return -1;
+    }
     FeedList& Q = F.list[list];
     int dev = 0, khz = 0;
     HIP_TRY(hipGetDevice(&dev));
@@ -436,6 +485,7 @@ int stage(int layer, int list, SlotTable* dtab, int ctas, hipStream_t s) {
         if (rb / 16 > 0xFFFFFFFFull) { moe_set_error("file feed: tensor %d rows too large", t); return -1; }
         StageArgs a = {};
         a.t = dtab;
+        a.fault = G().fault_dev;
         a.list = list;
         a.cap = Q.cap;
         a.epoch = Q.epoch_dev;

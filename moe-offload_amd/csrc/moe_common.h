@@ -125,6 +125,9 @@ struct SlotTable {
     int32_t status;                     // 0 ok; nonzero: rejected input (device kernels)
     int32_t sched;                      // device-driven ops follow the scheduler variant
                                         // (cpp/third_party/expert_io.c:1094-1394) when nonzero
+    int32_t io_fault;                   // sticky: 16 a file read failed, 17 a staging wait timed
+                                        // out (the slot kept its old bytes); set by the file
+                                        // tier's staging kernel, cleared only by reset_cache
 };
 
 // Hit/miss split of one scheduler step (c_layer_get_split_inds): slots of the ids that were

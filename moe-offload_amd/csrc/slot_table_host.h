@@ -71,6 +71,8 @@ static inline void reset_cache(SlotTable* t) {
     t->snap_valid = 0;
     t->n_copy = 0;
     t->pf_n_copy = 0;
+    t->status = 0;
+    t->io_fault = 0;
 }
 
 static inline void reset_stats(SlotTable* t) { memset(t->stats, 0, sizeof(t->stats)); }

@@ -130,6 +130,8 @@ SIGNATURES: dict[str, tuple] = {
     "c_io_set_feed_timeout_us": (None, [_c_u64]),
     "c_layer_device_table": (_c_u64, [_c_int]),
     "c_layer_table_status": (_c_int, [_c_int]),
+    "c_io_fault": (_c_int, []),
+    "c_io_clear_fault": (None, []),
     "c_sync_copies": (_c_int, []),
     "c_timing_begin": (_c_int, [_c_int]),
     "c_timing_end": (_c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int)]),

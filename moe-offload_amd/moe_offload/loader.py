@@ -500,6 +500,7 @@ class OffloadEngine:
             ts = time.perf_counter()
             self.model.decode_token(xs[d])
             torch.cuda.synchronize()
+            self.model.check_io()                    # this token's staging, not only earlier ones
             lat.append(round((time.perf_counter() - ts) * 1000.0, 3))
             if d + 1 == mid:
                 s_mid = self._snapshot_decode_totals()

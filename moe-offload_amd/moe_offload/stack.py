@@ -142,6 +142,7 @@ class DecodeStack:
                 raise ValueError("a device-driven file-backed stack takes io='exact', fused tables, no sched")
             L.c_io_init(c.io_threads)
             L.c_io_set_direct(int(c.io_direct))
+            L.c_io_clear_fault()                     # the library-wide fault word starts clean
             self.store = FileExpertStore({l: c.store_file for l in range(1, c.n_layers)})
             if self.store.blob_bytes != self.blob_bytes:
                 raise ValueError(f"{c.store_file}: blobs of {self.store.blob_bytes} bytes, the stack's are {self.blob_bytes}")
@@ -244,6 +245,9 @@ class DecodeStack:
             return
         for l in range(1, self.cfg.n_layers):
             self.L.c_layer_reset_cache(self.cidx(l))
+        if self.file_device:
+            torch.cuda.synchronize()                 # no staging kernel of an earlier token still runs
+            self.L.c_io_clear_fault()
         _lib.check_error("reset_cache")
 
     def reset_stats(self):
@@ -537,7 +541,18 @@ class DecodeStack:
         _lib.check(L.moe_rmsnorm(self.hs[c.n_layers - 1].data_ptr(), self.norm_w[c.n_layers - 1].data_ptr(),
                                  c.eps, c.hidden, self.xs[c.n_layers].data_ptr(), stream), "rmsnorm")
 
+    def check_io(self):
+        """Raise if a device-driven file-backed layer's staging failed (a read error or a wait past
+        its limit): the slot kept its old bytes, so outputs since then are wrong until
+        reset_caches().  Reads the library's host-memory fault word (no GPU synchronisation: it
+        covers the staging kernels that have run)."""
+        if self.file_device and self.L.c_io_fault():
+            torch.cuda.synchronize()
+            raise _lib.NativeError(f"file tier: staging failed (table status by layer {self.table_status()}: 16 a read "
+                                   "failed, 17 a wait timed out); reset_caches() before decoding on")
+
     def decode_token(self, x0: torch.Tensor | None = None) -> torch.Tensor:
+        self.check_io()                              # a fault of an earlier token
         if x0 is not None:
             self.xs[0].copy_(x0)
         if self.mode == "device" or self.cfg.resident:
@@ -614,6 +629,14 @@ class DecodeStack:
         self.store.close()
         if self.cfg.store_file is not None:
             self.L.c_io_set_direct(0)
+
+    def expert_blob(self, l: int, e: int) -> np.ndarray:
+        """Expert e of layer l as a blob in the standard layout (q2format), from its pool (layer 0,
+        resident stacks) or the host store."""
+        c = self.cfg
+        if l == 0 or c.resident:
+            return (self.full_pools[l] if c.resident else self.pool0)[e].cpu().numpy()
+        return self.store.view(l)[e]
 
     # algorithmic bytes of the routed experts touched per token (the roofline numerator)
     def routed_bytes_per_token(self) -> int:

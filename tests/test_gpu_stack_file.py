@@ -185,7 +185,8 @@ def test_device_driven_file_stack_reports_failed_reads_and_timeouts(tmp_path):
     import os
 
     from moe_offload.stack import DecodeStack, StackConfig
-    path, _ = _blob_file(tmp_path)
+    from moe_offload import _lib
+    path, blobs = _blob_file(tmp_path)
     cfg = StackConfig(n_layers=3, seed=6, layer_base=40, store_file=str(path))
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5)
@@ -205,7 +206,10 @@ def test_device_driven_file_stack_reports_failed_reads_and_timeouts(tmp_path):
         assert 16 in st.table_status().values()
     finally:
         st.close()
-    # a wait limit far below one read's time: the cold layer's demand entries time out
+    # a wait limit far below one read's time: the cold layer's demand entries time out.  The fault
+    # is sticky (the next token raises, the status stays 17) until reset_caches; the tokens after
+    # it -- whose reads start only once the timed-out token's late reads have ended, though they
+    # reuse the same bounce entries -- leave every slot holding the expert its table names.
     print("file stack: 1 us staging wait", flush=True)
     st = DecodeStack(cfg, mode="device")
     try:
@@ -213,8 +217,55 @@ def test_device_driven_file_stack_reports_failed_reads_and_timeouts(tmp_path):
         st.decode_token(x)
         torch.cuda.synchronize()
         assert st.table_status().get(1) == 17
+        assert st.L.c_io_fault() == 17
+        st.L.c_io_set_feed_timeout_us(0)
+        with pytest.raises(_lib.NativeError, match="staging failed"):
+            st.decode_token(x)
+        assert st.table_status().get(1) == 17
+        st.reset_caches()
+        assert st.table_status() == {} and st.L.c_io_fault() == 0
+        gen.manual_seed(6)
+        xs = torch.randn((3, cfg.hidden), device="cuda", generator=gen).half()
+        for t in range(3):
+            st.decode_token(xs[t])
+            torch.cuda.synchronize()
+            assert st.table_status() == {}, t
+        for l in range(1, cfg.n_layers):
+            e, s, n = (ctypes.c_int32 * 512)(), (ctypes.c_int32 * 512)(), ctypes.c_int(0)
+            st.L.c_layer_get_lru_state(st.cidx(l), e, s, ctypes.byref(n))
+            assert n.value > 0
+            pool = st.pools[l].cpu().numpy()
+            for i in range(n.value):
+                assert np.array_equal(pool[s[i]], blobs[e[i]]), (l, e[i], s[i])
     finally:
         st.L.c_io_set_feed_timeout_us(0)
+        st.close()
+
+
+def test_device_driven_file_layer_stages_only_published_lists(tmp_path):
+    """Staging a file-backed device layer's list that a table operation changed since its last
+    publication is refused on the host (it would copy the previous list's entries)."""
+    from moe_offload import _lib
+    from moe_offload.stack import DecodeStack, StackConfig
+    path, blobs = _blob_file(tmp_path)
+    st = DecodeStack(StackConfig(n_layers=2, seed=6, layer_base=46, store_file=str(path)), mode="device")
+    try:
+        L, li = st.L, st.cidx(1)
+        s = torch.cuda.current_stream().cuda_stream
+        ids = torch.arange(10, dtype=torch.int32, device="cuda")
+        assert L.c_layer_step_decode_dev(li, ids.data_ptr(), 10, -1, s) == 0
+        L.c_clear_error()
+        assert L.c_layer_stage_dev(li, 0, 2, s) == -1 and "publication" in _lib.last_error()
+        L.c_clear_error()
+        assert L.c_layer_publish_dev(li, 0, s) == 0
+        assert L.c_layer_stage_dev(li, 0, 2, s) == 0
+        torch.cuda.synchronize()
+        assert st.table_status() == {}
+        pool = st.pools[1].cpu().numpy()
+        slots = st.slot_inds[1][:10].cpu().numpy()
+        for j, sl in enumerate(slots):                # a cold table: all ten missed and were read
+            assert np.array_equal(pool[sl], blobs[j]), j
+    finally:
         st.close()
 
 
