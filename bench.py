@@ -30,13 +30,14 @@ for p in (str(ROOT), str(ROOT / "moe-offload_amd")):
 
 METRIC = "MoE decode tok/s, 48L top-10/512 Q2 @20% cache; achieved HBM GB/s"
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per k_q2_gate_up launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE over the
-# roofline pass of this build (median over 480 dispatches: 3,250.5 KiB fetched x 2 + 20 KiB
-# written, the factors from a known-size copy), profiles/q2_gemv_roofline_loop_rocprof.md; a
-# counter run cannot happen inside bench, so the line names where the figure comes from.
-GATE_UP_TRAFFIC_BYTES = 6_676_480
-GATE_UP_TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over bench.py --only roofline, scaled by "
-                          "moe_calibrate_copy (profiles/q2_gemv_roofline_loop_rocprof.md)")
+# kernel -> (HBM bytes per launch, where the figure comes from), for the roofline line's kernel
+# (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over `bench.py --only roofline`, scaled by the same counters
+# on moe_calibrate_copy: FETCH_SIZE x 2 KiB + WRITE_SIZE x 1 KiB; medians over every dispatch); a
+# counter run cannot happen inside the bench, so the line names where the figure comes from.
+_TRAFFIC_SRC = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over bench.py --only roofline, scaled by moe_calibrate_copy "
+                "(profiles/decode48_resident_kernels_rocprof.md)")
+KERNEL_TRAFFIC = {"k_q2_gate_up_routed": (6_788_208, _TRAFFIC_SRC), "k_q2_down": (3_504_128, _TRAFFIC_SRC),
+                  "k_router (logits)": (2_364_416, _TRAFFIC_SRC), "k_q2_gate_up": (6_676_480, _TRAFFIC_SRC)}
 
 
 def parse():
@@ -69,6 +70,9 @@ def parse():
     ap.add_argument("--native-host", action="store_true",
                     help="with --mode host: the per-layer loop runs in the library (moe_stack_token_host)")
     ap.add_argument("--nemo-layers", type=int, default=40, help="layers of the codebook (Nemotron-style) workload")
+    ap.add_argument("--glu", choices=["routed", "router"], default="routed",
+                    help="resident pass: routed = logits + gate/up selecting the experts itself + down; router = "
+                         "router with last-block selection + gate/up + down")
     ap.add_argument("--only", choices=["headline", "resident", "roofline", "prefill", "calib", "floor", "nemotron", "filetier", "tensorform"],
                     default=None,
                     help="run one pass and print its own JSON line (for sweeps and profiling); "
@@ -451,8 +455,8 @@ def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8, runs=None):
 def launch_floor(byte_counts, grids=(320, 640, 1280, 2560), reps=50):
     """Shortest kernel that only streams B bytes from HBM: moe_calibrate_stream launched `reps`
     times back to back (a fresh offset of a 512 MiB region each launch, so the reads miss the
-    caches), the run bracketed by two HIP events and divided by the count -- timed like the GEMV
-    loop, so the two durations compare like with like; best grid."""
+    caches), captured into a HIP graph whose replay is bracketed by two HIP events and divided by the
+    count -- timed like the GEMV loops, so the durations compare like with like; best grid."""
     import torch
 
     from moe_offload import _lib
@@ -460,24 +464,15 @@ def launch_floor(byte_counts, grids=(320, 640, 1280, 2560), reps=50):
     region = 512 << 20
     buf = torch.ones(region // 4, dtype=torch.float32, device="cuda")
     out = torch.zeros(1, dtype=torch.float32, device="cuda")
-    s = torch.cuda.current_stream()
     res = {}
     for nb in byte_counts:
         best = None
         for grid in grids:
-            def run(i, nb=nb, grid=grid):
+            def run(i, s, nb=nb, grid=grid):
                 off = ((i * nb) % (region - nb)) & ~255
-                _lib.check(L.moe_calibrate_stream(buf.data_ptr() + off, nb, grid, out.data_ptr(), s.cuda_stream),
+                _lib.check(L.moe_calibrate_stream(buf.data_ptr() + off, nb, grid, out.data_ptr(), s),
                            "calibrate_stream")
-            for i in range(5):
-                run(i)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(s)
-            for i in range(reps):
-                run(i)
-            e1.record(s)
-            e1.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / reps
+            us = min(graph_loop_us(run, reps, 2))
             best = us if best is None or us < best else best
         res[nb] = best
     del buf
@@ -489,8 +484,9 @@ def gemv_loop_timing(st, tokens=8, warm=2, repeats=3):
     """Average duration of k_q2_gate_up and k_q2_down launched back to back at the decode shape:
     for each of `tokens` fresh top-k draws and each of the resident stack's layers (its own 503 MB
     pool, so the bytes come from HBM, not the 256 MB MALL), one launch; the run of launches is
-    bracketed by two HIP events on the launch stream and divided by the count; the median of
-    `repeats` such runs is reported (each run's figure beside it).  Per-launch
+    captured into one HIP graph (the host's launch rate does not pace it), the replay bracketed by
+    two HIP events and divided by the count; the median of `repeats` replays is reported (each
+    replay's figure beside it).  Per-launch
     begin/end stamps are not used here: a kernel's begin stamp can precede the end of the kernel
     queued before it, so stamped durations of a mixed sequence overlap and sum to more than the
     wall time (the decode pass's stamped figures are reported beside these)."""
@@ -508,36 +504,108 @@ def gemv_loop_timing(st, tokens=8, warm=2, repeats=3):
     x = st.xs[0]
     h = torch.zeros(c.top_k * c.inter, dtype=torch.float16, device=dev)
     y = torch.zeros(c.hidden, dtype=torch.float32, device=dev)
-    s = torch.cuda.current_stream()
     pools = st.full_pools
 
-    def gate_up(i):
+    def gate_up(i, s):
         _lib.check(L.moe_q2_gate_up(x.data_ptr(), pools[i % c.n_layers].data_ptr(), st.blob_bytes, c.n_exp,
-                                    ids[i].data_ptr(), c.top_k, c.hidden, c.inter, c.group, h.data_ptr(),
-                                    s.cuda_stream), "gate_up")
+                                    ids[i].data_ptr(), c.top_k, c.hidden, c.inter, c.group, h.data_ptr(), s),
+                   "gate_up")
 
-    def down(i):
+    def down(i, s):
         _lib.check(L.moe_q2_down(h.data_ptr(), pools[i % c.n_layers].data_ptr(), st.blob_bytes, c.n_exp,
                                  ids[i].data_ptr(), sc.data_ptr(), c.top_k, c.hidden, c.inter, c.group, x.data_ptr(),
-                                 y.data_ptr(), 0, s.cuda_stream), "down")
+                                 y.data_ptr(), 0, s), "down")
 
     out = {}
     n = tokens * c.n_layers
     for name, fn in (("gate_up", gate_up), ("down", down)):
-        for i in range(warm * c.n_layers):
-            fn(n - 1 - i)
-        per = []
-        for _ in range(repeats):                        # the median of `repeats` bracketed loops
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(s)
-            for i in range(n):
-                fn(i)
-            e1.record(s)
-            e1.synchronize()
-            per.append(e0.elapsed_time(e1) * 1e3 / n)
+        per = graph_loop_us(fn, n, repeats)
         out[name] = sorted(per)[len(per) // 2]
         out[name + "_loops"] = [round(v, 3) for v in per]
     out["launches"] = n
+    return out
+
+
+def graph_loop_us(launch, n, repeats=3):
+    """Per-launch device time of launch(i, stream) for i in range(n): the n launches are captured
+    into one HIP graph (so the host's launch rate does not pace them), the graph is replayed
+    `repeats` times, each replay bracketed by two HIP events on the replay stream; returns the
+    per-launch microseconds of each replay."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for i in range(min(n, 16)):                 # warm-up outside the capture
+            launch(i, s.cuda_stream)
+        s.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n):
+                launch(i, s.cuda_stream)
+    torch.cuda.current_stream().wait_stream(s)
+    g.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    per = []
+    for _ in range(repeats):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        g.replay()
+        e1.record(cur)
+        e1.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e3 / n)
+    del g
+    return per
+
+
+def decode_kernel_loops(st, rounds=4, repeats=3):
+    """Per-launch duration of each kernel the resident decode launches, with the decode's own
+    arguments: after a decoded token the stack holds every layer's inputs (hs[l-1] or xs[0], the
+    logits, xs[l]); each kernel is then launched for layers 0..L-1, `rounds` times, back to back in
+    one captured HIP graph (every layer's weights are its own pool, so the bytes come from HBM),
+    the replay bracketed by two HIP events; the median of `repeats` replays is reported, each
+    beside it.  The kernels rewrite the same values the token wrote (same inputs)."""
+    from moe_offload import _lib, q2format
+    c = st.cfg
+    L = _lib.lib()
+    o = q2format.blob_offsets(c.hidden, c.inter, c.group)
+    gu_b = c.top_k * 2 * ((o["down_codes"] - o["up_codes"]) + (o["up_sb"] - o["gate_sb"]))
+    dn_b = c.top_k * ((o["gate_sb"] - o["down_codes"]) + (o["bytes"] - o["down_sb"]))
+    rt_b = c.n_exp * c.hidden * 2
+
+    def router(i, s):
+        l = i % c.n_layers
+        x_in = st.xs[0] if l == 0 else None
+        h_in = None if l == 0 else st.hs[l - 1]
+        _lib.check(L.moe_router_logits(h_in.data_ptr() if h_in is not None else None,
+                                       st.norm_w[l - 1].data_ptr() if l > 0 else None, c.eps,
+                                       x_in.data_ptr() if x_in is not None else None,
+                                       st.xs[l].data_ptr() if l > 0 else None, st.router_w[l].data_ptr(), c.hidden,
+                                       c.n_exp, st.logits[l].data_ptr(), s), "router_logits")
+
+    def gate_up(i, s):
+        l = i % c.n_layers
+        _lib.check(L.moe_q2_gate_up_routed(st.xs[l].data_ptr(), st.logits[l].data_ptr(), c.n_exp, c.top_k,
+                                           st.full_pools[l].data_ptr(), st.blob_bytes, c.hidden, c.inter, c.group,
+                                           st.ids[l].data_ptr(), st.scores[l].data_ptr(), st.h_ws.data_ptr(), s),
+                   "gate_up_routed")
+
+    def down(i, s):
+        l = i % c.n_layers
+        _lib.check(L.moe_q2_down(st.h_ws.data_ptr(), st.full_pools[l].data_ptr(), st.blob_bytes, c.n_exp,
+                                 st.ids[l].data_ptr(), st.scores[l].data_ptr(), c.top_k, c.hidden, c.inter, c.group,
+                                 st.xs[l].data_ptr(), st.hs[l].data_ptr(), 0, s), "down")
+
+    kernels = [("k_router (logits)", router, rt_b), ("k_q2_gate_up_routed", gate_up, gu_b),
+               ("k_q2_down", down, dn_b)]
+    out = {}
+    n = rounds * c.n_layers
+    for name, fn, nbytes in kernels:
+        per = graph_loop_us(fn, n, repeats)
+        us = sorted(per)[len(per) // 2]
+        out[name] = {"us": round(us, 3), "loops": [round(v, 3) for v in per], "bytes_per_launch": nbytes,
+                     "gb_s": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                     "launches": n, "traffic": KERNEL_TRAFFIC.get(name, (None,))[0]}
     return out
 
 
@@ -546,8 +614,8 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
     332-406: 9 slot-pool tensors per layer, bf16 scales and biases, 1,536,000 B per expert), every
     expert in HBM: k_q2t_gate_up and k_q2t_down launched back to back over fresh top-k draws, each
     launch on the next of `layers` layers' pools (786 MB each, so the bytes come from HBM rather
-    than the 256 MB MALL), bracketed by two HIP events; the median of `repeats` loops, as the blob
-    kernels' roofline loop.  Random codes, N(0, 0.02) scales, biases -1.5 x scale.  Then the
+    than the 256 MB MALL), captured into one HIP graph whose replay is bracketed by two HIP events;
+    the median of `repeats` replays, as the blob kernels' roofline loop.  Random codes, N(0, 0.02) scales, biases -1.5 x scale.  Then the
     checkpoint's 8-bit router (512 x 2560, top-10 in the reference's order) over 48 layers' routers
     in turn, timed the same way, and a whole MoE layer (router, gate/up, down) with the top-k
     selection in the router's last block or inside the gate/up blocks."""
@@ -583,15 +651,14 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
     x = torch.randn(hidden, device=dev, generator=g).half()
     h = torch.zeros(k * inter, dtype=torch.float16, device=dev)
     y = torch.zeros(hidden, dtype=torch.float32, device=dev)
-    s = torch.cuda.current_stream()
 
-    def gate_up(i):
+    def gate_up(i, s):
         _lib.check(L.moe_q2t_gate_up(x.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, ids[i].data_ptr(), k, hidden,
-                                     inter, 64, h.data_ptr(), s.cuda_stream), "q2t_gate_up")
+                                     inter, 64, h.data_ptr(), s), "q2t_gate_up")
 
-    def down(i):
+    def down(i, s):
         _lib.check(L.moe_q2t_down(h.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, ids[i].data_ptr(), sc.data_ptr(), k,
-                                  hidden, inter, 64, x.data_ptr(), y.data_ptr(), 0, s.cuda_stream), "q2t_down")
+                                  hidden, inter, 64, x.data_ptr(), y.data_ptr(), 0, s), "q2t_down")
 
     per_launch = {"gate_up": k * (nbytes[0] + nbytes[1] + nbytes[2] + nbytes[3] + nbytes[4] + nbytes[5]),
                   "down": k * (nbytes[6] + nbytes[7] + nbytes[8])}
@@ -600,17 +667,7 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
                        f"rotated, {n} fresh draws per loop",
            "bytes_per_launch": per_launch}
     for name, fn in (("gate_up", gate_up), ("down", down)):
-        for i in range(layers):
-            fn(n - 1 - i)
-        per = []
-        for _ in range(repeats):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(s)
-            for i in range(n):
-                fn(i)
-            e1.record(s)
-            e1.synchronize()
-            per.append(e0.elapsed_time(e1) * 1e3 / n)
+        per = graph_loop_us(fn, n, repeats)
         med = sorted(per)[len(per) // 2]
         out[name + "_us"] = round(med, 3)
         out[name + "_loops"] = [round(v, 3) for v in per]
@@ -627,23 +684,13 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
     rids = torch.empty(k, dtype=torch.int32, device=dev)
     rsc = torch.empty(k, dtype=torch.bfloat16, device=dev)
 
-    def router(i):
+    def router(i, s):
         r = i % n_r
         _lib.check(L.moe_router_q8(xb.data_ptr(), rcodes[r].data_ptr(), rs[r].data_ptr(), rb[r].data_ptr(), hidden,
-                                   n_exp, 64, k, 0, ws.data_ptr(), rids.data_ptr(), rsc.data_ptr(), None, None,
-                                   s.cuda_stream), "router_q8")
+                                   n_exp, 64, k, 0, ws.data_ptr(), rids.data_ptr(), rsc.data_ptr(), None, None, s),
+                   "router_q8")
 
-    for i in range(n_r):
-        router(i)
-    per = []
-    for _ in range(repeats):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        for i in range(2 * n_r):
-            router(i)
-        e1.record(s)
-        e1.synchronize()
-        per.append(e0.elapsed_time(e1) * 1e3 / (2 * n_r))
+    per = graph_loop_us(router, 2 * n_r, repeats)
     r_bytes = n_exp * (hidden + 2 * (hidden // 64) * 2)
     out["router_q8_us"] = round(sorted(per)[len(per) // 2], 3)
     out["router_q8_loops"] = [round(v, 3) for v in per]
@@ -657,37 +704,27 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
     ids_b = torch.empty(k, dtype=torch.int32, device=dev)
     sc_b = torch.empty(k, dtype=torch.bfloat16, device=dev)
 
-    def layer_routed_in_router(i):
-        router(i)
+    def layer_routed_in_router(i, s):
+        router(i, s)
         _lib.check(L.moe_q2t_gate_up(x.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, rids.data_ptr(), k, hidden,
-                                     inter, 64, h.data_ptr(), s.cuda_stream), "q2t_gate_up")
+                                     inter, 64, h.data_ptr(), s), "q2t_gate_up")
         _lib.check(L.moe_q2t_down(h.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, rids.data_ptr(), sc.data_ptr(), k,
-                                  hidden, inter, 64, x.data_ptr(), y.data_ptr(), 0, s.cuda_stream), "q2t_down")
+                                  hidden, inter, 64, x.data_ptr(), y.data_ptr(), 0, s), "q2t_down")
 
-    def layer_routed_in_gate_up(i):
+    def layer_routed_in_gate_up(i, s):
         r = i % n_r
         _lib.check(L.moe_router_q8(xb.data_ptr(), rcodes[r].data_ptr(), rs[r].data_ptr(), rb[r].data_ptr(), hidden,
-                                   n_exp, 64, 0, 0, ws.data_ptr(), None, None, None, lg.data_ptr(), s.cuda_stream),
+                                   n_exp, 64, 0, 0, ws.data_ptr(), None, None, None, lg.data_ptr(), s),
                    "router_q8 logits")
         _lib.check(L.moe_q2t_gate_up_routed(x.data_ptr(), lg.data_ptr(), n_exp, k, ptrs[i % layers], nbytes, 1,
-                                            hidden, inter, 64, ids_b.data_ptr(), sc_b.data_ptr(), h.data_ptr(),
-                                            s.cuda_stream), "q2t_gate_up_routed")
+                                            hidden, inter, 64, ids_b.data_ptr(), sc_b.data_ptr(), h.data_ptr(), s),
+                   "q2t_gate_up_routed")
         _lib.check(L.moe_q2t_down(h.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, ids_b.data_ptr(), sc.data_ptr(), k,
-                                  hidden, inter, 64, x.data_ptr(), y.data_ptr(), 0, s.cuda_stream), "q2t_down")
+                                  hidden, inter, 64, x.data_ptr(), y.data_ptr(), 0, s), "q2t_down")
 
     out["layer_us"] = {}
     for name, fn in (("selection_in_router", layer_routed_in_router), ("selection_in_gate_up", layer_routed_in_gate_up)):
-        for i in range(n_r):
-            fn(i)
-        per = []
-        for _ in range(repeats):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(s)
-            for i in range(2 * n_r):
-                fn(i)
-            e1.record(s)
-            e1.synchronize()
-            per.append(e0.elapsed_time(e1) * 1e3 / (2 * n_r))
+        per = graph_loop_us(fn, 2 * n_r, repeats)
         out["layer_us"][name] = round(sorted(per)[len(per) // 2], 3)
     del sets, rcodes, rs, rb
     torch.cuda.empty_cache()
@@ -702,10 +739,12 @@ def resident_pass(args, cfg, gen, n_tok, xs=None):
     from moe_offload.stack import DecodeStack, StackConfig
     if xs is None:
         xs = torch.randn((n_tok, cfg.hidden), device="cuda", generator=gen).half()
-    rcfg = StackConfig(n_layers=args.layers, prefetch=False, resident=True)
+    rcfg = StackConfig(n_layers=args.layers, prefetch=False, resident=True, routed_glu=args.glu == "routed")
     rst = DecodeStack(rcfg, mode="device")
     r_elapsed, _, _ = timed_tokens(rst, xs, args.warmup, args.steps, not args.no_graph)
     res_k = kernel_timing(rst, xs, args.warmup, args.steps)
+    rst.decode_token(xs[0])
+    dec_loops = decode_kernel_loops(rst) if args.glu != "router" else {}
     loop = gemv_loop_timing(rst)
     gu_avg, dn_avg = loop["gate_up"] / 1e6, loop["down"] / 1e6
     o = q2format.blob_offsets(cfg.hidden, cfg.inter, cfg.group)
@@ -715,7 +754,11 @@ def resident_pass(args, cfg, gen, n_tok, xs=None):
     rst.close()
     del rst
     torch.cuda.empty_cache()
-    return {"tok_s": round(args.steps / r_elapsed, 1), "ms_per_token": round(r_elapsed / args.steps * 1e3, 4),
+    glu = {"routed": "router logits, gate/up selecting the experts, down",
+           "router": "router with last-block selection, gate/up, down"}[args.glu]
+    return {"glu": glu, "tok_s": round(args.steps / r_elapsed, 1), "ms_per_token": round(r_elapsed / args.steps * 1e3, 4),
+            "us_per_layer": round(r_elapsed / args.steps / rcfg.n_layers * 1e6, 2),
+            "decode_kernels_back_to_back": dec_loops,
             "routed_gb_per_s": round(routed * args.steps / r_elapsed / 1e9, 1),
             "routed_frac_of_peak": round(routed * args.steps / r_elapsed / 1e9 / HBM_PEAK_GBS, 4),
             "kernels_us": {k: round(v["avg_us"], 3) for k, v in res_k.items() if v["launches"]},
@@ -837,13 +880,17 @@ def main():
                       stage_ctas=args.stage_ctas, pf_stage_ctas=args.pf_stage_ctas, sched=args.sched,
                       split=args.split, native_host=args.native_host)
     if args.only == "roofline":
-        # the roofline kernel's timing pass alone (the profile command for the rocprof summary)
-        rst = DecodeStack(StackConfig(n_layers=args.layers, prefetch=False, resident=True), mode="device")
+        # the roofline timing passes alone (the profile command for the rocprof summaries): the
+        # resident decode's kernels with the decode's own arguments, then the isolated gate/up loop
+        rst = DecodeStack(StackConfig(n_layers=args.layers, prefetch=False, resident=True,
+                                      routed_glu=args.glu == "routed"), mode="device")
+        rst.decode_token(torch.randn(cfg.hidden, device="cuda", generator=gen).half())
+        dec = decode_kernel_loops(rst) if args.glu != "router" else {}
         loop = gemv_loop_timing(rst)
         o = q2format.blob_offsets(cfg.hidden, cfg.inter, cfg.group)
         gu_bytes = cfg.top_k * 2 * ((o["down_codes"] - o["up_codes"]) + (o["up_sb"] - o["gate_sb"]))
-        print(json.dumps({"roofline_loop_us": loop, "gate_up_gb_s": round(gu_bytes / loop["gate_up"] / 1e3, 1)}),
-              flush=True)
+        print(json.dumps({"decode_kernels_back_to_back": dec, "isolated_loop_us": loop,
+                          "isolated_gate_up_gb_s": round(gu_bytes / loop["gate_up"] / 1e3, 1)}), flush=True)
         rst.close()
         return
     if args.only == "resident":
@@ -880,10 +927,23 @@ def main():
     res = resident_pass(args, cfg, gen, n_tok, xs)
     gu_avg, dn_avg, gu_bytes, dn_bytes, res_k = res.pop("_gu_avg"), res.pop("_dn_avg"), res.pop("_gu_bytes"), \
         res.pop("_dn_bytes"), res.pop("_kernels")
-    gu_gbs = gu_bytes / gu_avg / 1e9
-    floor_us = launch_floor([gu_bytes])[gu_bytes]
     routed = res.pop("_routed")
     r_elapsed = res.pop("_elapsed")
+    dec = res["decode_kernels_back_to_back"]
+    if dec:
+        # the dominant kernel of the resident decode, timed with the decode's own arguments
+        rk = max(dec, key=lambda n: dec[n]["us"])
+        r_bytes, r_us = dec[rk]["bytes_per_launch"], dec[rk]["us"]
+        measured_in = (f"resident decode (all experts in HBM): {dec[rk]['launches']} launches back to back over the "
+                       f"{cfg.n_layers} layers with the decode's own per-layer inputs, bracketed by HIP events on the "
+                       "launch stream; median of 3 such runs (every kernel of the decode: resident."
+                       "decode_kernels_back_to_back)")
+    else:
+        rk, r_bytes, r_us = "k_q2_gate_up", gu_bytes, gu_avg * 1e6
+        measured_in = "isolated k_q2_gate_up loop (resident.gemv_back_to_back_us)"
+    r_gbs = r_bytes / r_us / 1e3
+    floor_us = launch_floor([r_bytes])[r_bytes]
+    traffic = KERNEL_TRAFFIC.get(rk)
 
     line = {
         "metric": METRIC,
@@ -904,16 +964,14 @@ def main():
                                f"prefetch {'top-%d cap %d' % (cfg.top_m, cfg.prefetch_cap) if cfg.prefetch else 'off'}, "
                                f"batch 1, {args.steps} tokens",
                    "driver": args.mode + ("+graph" if use_graph else ""), "tokens": args.steps, "batch": 1},
-        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
-                     "traffic_source": GATE_UP_TRAFFIC_SOURCE,
-                     "kernel": "k_q2_gate_up",
-                     "measured_in": f"resident stack (all experts in HBM): {res['gemv_back_to_back_us']['launches']} "
-                                    "launches back to back over the 48 layer pools, fresh top-10 draws, bracketed "
-                                    "by HIP events on the launch stream; median of 3 such runs",
-                     "bytes_per_launch": gu_bytes, "avg_launch_us": round(gu_avg * 1e6, 3),
+        "roofline": {"bound": "hbm", "achieved": round(r_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(r_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic[0] if traffic else None,
+                     "traffic_source": traffic[1] if traffic else None,
+                     "kernel": rk, "measured_in": measured_in,
+                     "bytes_per_launch": r_bytes, "avg_launch_us": round(r_us, 3),
                      "launch_floor_us": round(floor_us, 3),
-                     "frac_of_launch_floor": round(floor_us / (gu_avg * 1e6), 4)},
+                     "frac_of_launch_floor": round(floor_us / r_us, 4)},
         "cache": {"effective_hit_rate": round((tot1[0] - tot0[0] + tot1[1] - tot0[1]) / req, 4),
                   "pure_lru_hit_rate": round((tot1[0] - tot0[0]) / req, 4),
                   "staged_mb_per_token": round(staged / args.steps / 1e6, 2),
