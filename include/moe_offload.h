@@ -177,6 +177,11 @@ int moe_f64_to_f16(const double* in, uint16_t* out, int n, void* stream);
  * the same arithmetic as moe_router's prologue. */
 int moe_rmsnorm(const float* h_in, const void* norm_w, float eps, int hidden, void* x_out,
                 void* stream);
+/* The same glue for the reference's bf16 checkpoint (no reference counterpart): norm_w bf16 (or
+ * null), x_bf16_out = bf16(RMSNorm(h_in) * norm_w) rounded once from fp64 -- moe_router_q8's input
+ * -- and x_f16_out = that bf16 value as fp16, the tensor-form expert kernels' input. */
+int moe_rmsnorm_bf16(const float* h_in, const void* norm_w, float eps, int hidden, void* x_bf16_out,
+                     void* x_f16_out, void* stream);
 /* Bytes of one Q2 expert blob (layout in csrc/moe_common.h). */
 uint64_t moe_q2_expert_bytes(int hidden, int inter, int group);
 /* gather_qmm gate+up + SwiGLU (loader.py:564, kernels.cpp:1027-1040,1090-1094):
@@ -202,7 +207,9 @@ int moe_q2_switch_glu(const void* x, const void* pool, uint64_t stride, int n_sl
  * projection a code pool [slots][out][in/16] u32 and scale and bias pools [slots][out][in/64]),
  * each tensor at its own base address with its own bytes per slot.  ptrs / slot_bytes: 9 entries
  * in role order -- gate weight, scales, biases, up weight, scales, biases, down weight, scales,
- * biases; scale_bf16 != 0: scales and biases are bf16 (the reference's checkpoints), else fp16.
+ * biases; scale_bf16 bit 0: scales and biases are bf16 (the reference's checkpoints), else fp16;
+ * bit 1: the down product's scores are bf16 (as moe_router_q8 and moe_q2t_gate_up_routed write
+ * them), else fp16.
  * Any hidden <= 4096 and inter <= 1024 that are multiples of 64 (the real model: 2560 / 640);
  * other arguments as moe_q2_gate_up / moe_q2_down / moe_q2_switch_glu, which also take these
  * shapes for blob pools. */

@@ -1111,6 +1111,12 @@ int moe_rmsnorm(const float* h_in, const void* norm_w, float eps, int hidden, vo
     return launch_rmsnorm(h_in, (const __half*)norm_w, eps, hidden, (__half*)x_out, (hipStream_t)stream);
 }
 
+int moe_rmsnorm_bf16(const float* h_in, const void* norm_w, float eps, int hidden, void* x_bf16_out, void* x_f16_out,
+                     void* stream) {
+    return launch_rmsnorm_bf16(h_in, (const uint16_t*)norm_w, eps, hidden, (uint16_t*)x_bf16_out, (__half*)x_f16_out,
+                               (hipStream_t)stream);
+}
+
 uint64_t moe_q2_expert_bytes(int hidden, int inter, int group) {
     return (uint64_t)blob_layout(hidden, inter, group).bytes;
 }
@@ -1188,7 +1194,8 @@ int c_layer_set_format9(int layer, int hidden, int inter, int group, const int32
         E.p[p].b_stride = L.row_bytes[tensor_of[3 * p + 2]];
         E.p[p].sb_step = 2;
     }
-    E.bf16 = scale_bf16 ? 1 : 0;
+    E.bf16 = scale_bf16 & 1;
+    E.scores_bf16 = (scale_bf16 >> 1) & 1;
     L.hidden = hidden;
     L.inter = inter;
     L.group = group;
@@ -1219,7 +1226,8 @@ static bool experts9(const char* who, const uint64_t* ptrs, const uint64_t* slot
         E.p[p].b_stride = slot_bytes[3 * p + 2];
         E.p[p].sb_step = 2;
     }
-    E.bf16 = scale_bf16 ? 1 : 0;
+    E.bf16 = scale_bf16 & 1;
+    E.scores_bf16 = (scale_bf16 >> 1) & 1;
     return true;
 }
 

@@ -63,6 +63,7 @@ struct Q2Proj {
 struct Q2Experts {
     Q2Proj p[3];
     int bf16;
+    int scores_bf16;      // the down kernel's expert scores are bf16 (the 8-bit router's), else fp16
 };
 
 // Roles of the 9 tensors of a reference layer (c_layer_set_format9).
@@ -202,6 +203,8 @@ int launch_q2_gate_up_routed(const __half* x, const float* logits, int n_exp, in
 int launch_f64_to_f16(const double* in, uint16_t* out, int n, hipStream_t s);
 int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidden, __half* x_out,
                    hipStream_t s);
+int launch_rmsnorm_bf16(const float* h_in, const uint16_t* norm_w, float eps, int hidden, uint16_t* x_bf16,
+                        __half* x_f16, hipStream_t s);
 int launch_q2_gate_up(const __half* x, const uint8_t* pool, size_t expert_stride, int n_slots,
                       const uint32_t* slots, int k, int hidden, int inter, int group,
                       __half* h_out, hipStream_t s);

@@ -78,4 +78,47 @@ __device__ inline void finish(const NormIn& in, bool has_w, float eps, int hidde
     }
 }
 
+// The checkpoint form (bf16 model): the same sum of squares and normalisation with bf16 norm
+// weights, x rounded once from fp64 to bf16 (x_bf16, the 8-bit router's input) and that bf16 value
+// converted to fp16 (x_f16, the expert kernels' input: exact in fp16's normal range).  Every
+// thread writes its own elements; one __syncthreads.
+__device__ inline void finish_bf16(const NormIn& in, bool has_w, float eps, int hidden, uint16_t* __restrict__ x_bf16,
+                                   __half* __restrict__ x_f16, double* red) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        if (4 * (c * kThreads + tid) >= hidden) continue;
+        const double a = in.hv[c].x, b = in.hv[c].y, d = in.hv[c].z, e = in.hv[c].w;
+        ss += a * a;
+        ss += b * b;
+        ss += d * d;
+        ss += e * e;
+    }
+    ss = lanes::wave_sum_f64(ss);
+    if (lane == 0) red[wv] = ss;
+    __syncthreads();
+    const double tot = red[0] + red[1] + red[2] + red[3];
+    const double denom = sqrt(tot / hidden + (double)eps);
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        const int i = 4 * (c * kThreads + tid);
+        if (i >= hidden) continue;
+        const float hh[4] = {in.hv[c].x, in.hv[c].y, in.hv[c].z, in.hv[c].w};
+        const uint32_t ww[2] = {in.w2[c].x, in.w2[c].y};
+        uint16_t b[4], f[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            double v = (double)hh[j] / denom;
+            if (has_w) v *= (double)route::bf16_to_f32((ww[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+            b[j] = route::f64_to_bf16_bits(v);
+            f[j] = __half_as_ushort(__float2half_rn(route::bf16_to_f32(b[j])));
+        }
+        *reinterpret_cast<uint2*>(x_bf16 + i) =
+            make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
+        *reinterpret_cast<uint2*>(x_f16 + i) =
+            make_uint2((uint32_t)f[0] | ((uint32_t)f[1] << 16), (uint32_t)f[2] | ((uint32_t)f[3] << 16));
+    }
+}
+
 }  // namespace norm64

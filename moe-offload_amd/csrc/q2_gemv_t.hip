@@ -220,7 +220,8 @@ __global__ __launch_bounds__(64 * kTDownWaves) void k_q2t_down(const __half* __r
         }
     }
     const bool weighted = scores != nullptr;
-    const float s_lane = __half2float((weighted ? scores : h)[lane < k ? lane : 0]);
+    const uint16_t s_bits = __half_as_ushort((weighted ? scores : h)[lane < k ? lane : 0]);
+    const float s_lane = E.scores_bf16 ? __uint_as_float((uint32_t)s_bits << 16) : __half2float(__ushort_as_half(s_bits));
     // the epilogue's operands, loaded now (as in k_q2_down): y_out's current value for mode 2, the
     // residual row for mode 0 (without a residual, y_out's first bytes, unused)
     const int erow = row0 + (tid & (kTDownRows - 1)) < hidden ? row0 + (tid & (kTDownRows - 1)) : hidden - 1;
@@ -318,6 +319,7 @@ Q2Experts q2_experts_from_blob(const uint8_t* pool, size_t stride, const BlobLay
         E.p[p].sb_step = 4;
     }
     E.bf16 = 0;
+    E.scores_bf16 = 0;
     return E;
 }
 

@@ -238,6 +238,15 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(const float* __restrict__ 
     norm64::finish(nin, norm_w != nullptr, eps, hidden, xs, x_out, red);
 }
 
+__global__ __launch_bounds__(kThreads) void k_rmsnorm_bf16(const float* __restrict__ h_in, const uint16_t* __restrict__ norm_w,
+                                                            float eps, int hidden, uint16_t* __restrict__ x_bf16,
+                                                            __half* __restrict__ x_f16) {
+    __shared__ double red[kThreads / 64];
+    NormIn nin;
+    norm64::load(nin, h_in, reinterpret_cast<const __half*>(norm_w), hidden);
+    norm64::finish_bf16(nin, norm_w != nullptr, eps, hidden, x_bf16, x_f16, red);
+}
+
 __global__ void k_f64_to_f16(const double* __restrict__ in, uint16_t* __restrict__ out, int n) {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = f64_to_f16_bits(in[i]);
@@ -317,6 +326,17 @@ int launch_rmsnorm(const float* h_in, const __half* norm_w, float eps, int hidde
         return -1;
     }
     hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kThreads), 0, s, h_in, norm_w, eps, hidden, x_out);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int launch_rmsnorm_bf16(const float* h_in, const uint16_t* norm_w, float eps, int hidden, uint16_t* x_bf16,
+                        __half* x_f16, hipStream_t s) {
+    if (!h_in || !x_bf16 || !x_f16 || hidden <= 0 || hidden > kMaxHidden || hidden % 8) {
+        moe_set_error("rmsnorm_bf16: hidden=%d (multiple of 8, <= %d) or null pointer", hidden, kMaxHidden);
+        return -1;
+    }
+    hipLaunchKernelGGL(k_rmsnorm_bf16, dim3(1), dim3(kThreads), 0, s, h_in, norm_w, eps, hidden, x_bf16, x_f16);
     HIP_TRY(hipGetLastError());
     return 0;
 }

@@ -73,6 +73,7 @@ SIGNATURES: dict[str, tuple] = {
     "moe_q2_gate_up_routed": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_u64, _c_int, _c_int, _c_int, _c_vp,
                                        _c_vp, _c_vp, _c_vp]),
     "moe_rmsnorm": (_c_int, [_c_vp, _c_vp, _c_f, _c_int, _c_vp, _c_vp]),
+    "moe_rmsnorm_bf16": (_c_int, [_c_vp, _c_vp, _c_f, _c_int, _c_vp, _c_vp, _c_vp]),
     "moe_f64_to_f16": (_c_int, [_c_vp, _c_vp, _c_int, _c_vp]),
     "moe_q2_expert_bytes": (_c_u64, [_c_int, _c_int, _c_int]),
     "moe_q2_gate_up": (_c_int, [_c_vp, _c_vp, _c_u64, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp,

@@ -269,7 +269,9 @@ class HostShardStore:
 class CachedSwitchGLU:
     """Per-layer slot cache over an HBM pool + Q2 SwitchGLU (loader.py:306-749).
 
-    `store` is a HostExpertStore (pinned host memory, fd == -1), a FileExpertStore (a blob file,
+    `store` is the path of the layer's `experts-XX.safetensors` shard, as the reference passes it
+    (loader.py:311, 1045-1046: read in place by the reader threads, a ShardExpertStore the module
+    owns and closes), or a HostExpertStore (pinned host memory, fd == -1), a FileExpertStore (a blob file,
     fd >= 0; the pool holds `capacity` blobs), a ShardExpertStore (the reference's shard read in
     place, fd >= 0; `pools` are the 9 tensors' slot pools, each [capacity, bytes per expert], as
     loader.py:336-366 allocates them, and hidden/inter/group come from the shard) or a
@@ -278,9 +280,12 @@ class CachedSwitchGLU:
     like SwitchGLU; forward_combined() returns the score-weighted sum directly.
     """
 
-    def __init__(self, store: "HostExpertStore | FileExpertStore | ShardExpertStore | HostShardStore", layer_idx: int,
-                 capacity: int,
+    def __init__(self, store: "str | Path | HostExpertStore | FileExpertStore | ShardExpertStore | HostShardStore",
+                 layer_idx: int, capacity: int,
                  hidden: int = 2048, inter: int = 512, group: int = 64, device: str | torch.device = "cuda"):
+        self._own_store = isinstance(store, (str, Path))
+        if self._own_store:                           # the reference's call: a shard path
+            store = ShardExpertStore({layer_idx: str(store)})
         shard = isinstance(store, (ShardExpertStore, HostShardStore))
         if shard:
             hidden, inter, group = store.hidden, store.inter, store.group
@@ -424,37 +429,56 @@ class CachedSwitchGLU:
         torch.cuda.synchronize()
         _lib.lib().c_sync_copies()
         _lib.lib().c_layer_init(self.layer_idx, -1, 16, None, None, None, 0)
+        if self._own_store:
+            self.store.close()
 
 
 class OffloadEngine:
-    """Routed-expert offload engine (loader.py:1004-1343) over the synthetic decode stack.
+    """Routed-expert offload engine (loader.py:1004-1343).
 
-    There is no checkpoint, tokenizer or attention here (out of scope): a "token" is a hidden
-    state fed to the 48-layer routed-expert stack; `generate_greedy` runs that stack and reports
-    the reference's timing and hit-rate keys.
+    model_path: a model directory in the reference's layout (experts-XX.safetensors shards, the
+    8-bit routers in base-*.safetensors): the routed-expert stack over it (ckpt.CheckpointStack:
+    layer 0 pinned, layers 1.. cached).  A path that is not such a directory raises.  Without a
+    model_path, the synthetic 48-layer stack of the benchmark workload (stack.DecodeStack).
+    There is no tokenizer or attention here (out of scope): a "token" is a hidden state fed to the
+    routed-expert stack; `generate_greedy` runs it and reports the reference's timing and hit-rate
+    keys.
     """
 
     def __init__(self, model_path=None, budget_gb: float | None = None, budget_pct: float | None = 20.0,
                  alloc_mode: str = "even", prefetch: bool = True, prefetch_top_m: int = PREFETCH_TOP_M,
                  prefetch_cap: int = PREFETCH_MAX_CAP, mode: str = "device", n_layers: int = NUM_LAYERS,
                  hidden: int = 2048, inter: int = 512, seed: int = 0, store_file: str | None = None,
-                 io_threads: int = 8, io_direct: bool = False):
-        """store_file: the cached layers read their misses from this blob file (the on-disk tier, as
-        the reference's engine reads its expert shards) with `io_threads` reader threads, through
-        the page cache or with O_DIRECT; device mode then publishes each layer's misses to the
-        library's feeder thread.  Without it they come from a pinned host store."""
-        from .stack import DecodeStack, StackConfig
+                 io_threads: int = 8, io_direct: bool = False, shard_store: str = "host"):
+        """Synthetic stack (no model_path) -- store_file: the cached layers read their misses from
+        this blob file (the on-disk tier) with `io_threads` reader threads, through the page cache or
+        with O_DIRECT; device mode then publishes each layer's misses to the library's feeder
+        thread.  Without it they come from a pinned host store.  n_layers / hidden / inter / seed
+        shape the synthetic model.
+        Model directory -- shard_store: "host" reads the cached layers' shards once into pinned host
+        memory (misses are then PCIe copies), "file" reads each miss from the shard in place with
+        the reader threads (mode="host"); the shapes come from the files."""
         t0 = time.perf_counter()
         self.model_path, self.alloc_mode = model_path, alloc_mode
         self.prefetch, self.prefetch_top_m, self.prefetch_cap = prefetch, prefetch_top_m, prefetch_cap
-        cfg = StackConfig(n_layers=n_layers, hidden=hidden, inter=inter, budget_pct=budget_pct, budget_gb=budget_gb,
-                          prefetch=prefetch, top_m=prefetch_top_m, prefetch_cap=prefetch_cap, seed=seed,
-                          store_file=store_file, io_threads=io_threads, io_direct=io_direct)
-        self.model = DecodeStack(cfg, mode=mode)
+        if model_path is not None:
+            from .ckpt import CheckpointStack, CkptConfig
+            if store_file is not None:
+                raise ValueError("store_file names a synthetic stack's blob file; a model directory has its shards")
+            ccfg = CkptConfig(budget_pct=budget_pct, budget_gb=budget_gb, prefetch=prefetch, top_m=prefetch_top_m,
+                              prefetch_cap=prefetch_cap, store=shard_store, io_threads=io_threads)
+            self.model = CheckpointStack(model_path, ccfg, mode=mode)
+        else:
+            from .stack import DecodeStack, StackConfig
+            cfg = StackConfig(n_layers=n_layers, hidden=hidden, inter=inter, budget_pct=budget_pct,
+                              budget_gb=budget_gb, prefetch=prefetch, top_m=prefetch_top_m, prefetch_cap=prefetch_cap,
+                              seed=seed, store_file=store_file, io_threads=io_threads, io_direct=io_direct)
+            self.model = DecodeStack(cfg, mode=mode)
+        n_layers = self.model.cfg.n_layers
         self.capacities = self.model.capacities
         self.total_cached_slots = sum(self.capacities.values())
         self.cache_budget_bytes = self.total_cached_slots * self.model.blob_bytes
-        self.layer0_pinned_bytes = cfg.n_exp * self.model.blob_bytes
+        self.layer0_pinned_bytes = self.model.cfg.n_exp * self.model.blob_bytes
         self.cached_modules = {l: l for l in range(1, n_layers)}
         self.tokenizer = None
         self.load_seconds = time.perf_counter() - t0

@@ -63,6 +63,21 @@ def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
     raise ValueError(dtype)
 
 
+def round_bf16_once(x: np.ndarray) -> np.ndarray:
+    """float64 -> bf16 bit patterns with ONE round-to-nearest-even from float64 (no float32 step):
+    the 53-bit significand is cut to bf16's 8 bits on the integer bit pattern (ties to even), then
+    the exactly representable result is read off its float32 form.  Normal-range values (the
+    RMSNorm glue's outputs); the checkpoint glue's kernel rounds this way."""
+    b = np.ascontiguousarray(np.asarray(x, np.float64)).view(np.uint64).copy()
+    cut = np.uint64(45)                               # 52 - 7 fraction bits dropped
+    rem = b & np.uint64((1 << 45) - 1)
+    half = np.uint64(1 << 44)
+    keep = b >> cut
+    up = (rem > half) | ((rem == half) & ((keep & np.uint64(1)) == np.uint64(1)))
+    r = ((keep + up.astype(np.uint64)) << cut).view(np.float64)
+    return f32_to_bf16_bits(r.astype(np.float32))
+
+
 def to_f64(a: np.ndarray, dtype: str | None = None) -> np.ndarray:
     """Interpret an array (float16/float32, or uint16 bf16 bits when dtype='bf16') as float64."""
     if dtype == "bf16" or (dtype is None and np.asarray(a).dtype == np.uint16):

@@ -83,3 +83,41 @@ def write_reference_shard(path, layer, mlx, scale_dtype="bf16"):
             tensors[f"{pre}.{proj}.{suffix}"] = torch.from_numpy(a.view(np.int16)).view(half)
     save_file(tensors, str(path))
     return path
+
+
+def router_q8(n_exp, hidden, rng, equal_rows=False):
+    """An 8-bit affine group-64 router as the checkpoint stores it: codes uint32 [E, H/4], bf16 bits
+    uint16 scales / biases [E, H/64] (scales ~2e-4, biases ~ -128 x scale: logits of order one)."""
+    rows = 1 if equal_rows else n_exp
+    codes = rng.integers(0, 2**32, size=(rows, hidden // 4), dtype=np.uint32)
+    scales = q2.f32_to_bf16_bits((rng.standard_normal((rows, hidden // 64)) * 2e-4).astype(np.float32))
+    biases = q2.f32_to_bf16_bits((-128 * q2.to_f64(scales, "bf16")
+                                  + rng.standard_normal((rows, hidden // 64)) * 1e-4).astype(np.float32))
+    if equal_rows:
+        codes, scales, biases = (np.repeat(a, n_exp, axis=0) for a in (codes, scales, biases))
+    return codes, scales, biases
+
+
+def write_model_dir(root, n_layers, n_exp, hidden, inter, seed=1):
+    """A model directory in the reference's layout: experts-{l:02d}.safetensors per layer (the 9
+    switch_mlp tensors, bf16 scales) and base-00.safetensors with every layer's 8-bit router
+    `language_model.model.layers.{l}.mlp.gate.{weight,scales,biases}`.  Returns
+    ({layer: MLX-layout experts}, {layer: (codes, scales, biases)})."""
+    import torch
+    from safetensors.torch import save_file
+    from pathlib import Path
+    root = Path(root)
+    root.mkdir(parents=True, exist_ok=True)
+    rng = np.random.default_rng(seed)
+    experts, routers, base = {}, {}, {}
+    for l in range(n_layers):
+        experts[l] = experts_bf16(n_exp, hidden, inter, seed=seed * 100 + l)
+        write_reference_shard(root / f"experts-{l:02d}.safetensors", l, experts[l])
+        routers[l] = router_q8(n_exp, hidden, rng)
+        c, s, b = routers[l]
+        pre = f"language_model.model.layers.{l}.mlp.gate"
+        base[f"{pre}.weight"] = torch.from_numpy(c.view(np.int32)).view(torch.uint32)
+        base[f"{pre}.scales"] = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16)
+        base[f"{pre}.biases"] = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16)
+    save_file(base, str(root / "base-00.safetensors"))
+    return experts, routers

@@ -144,3 +144,48 @@ def test_capacities_proportional_path(tmp_path):
     # a missing summary falls back to the even split
     caps = compute_layer_capacities(analysis_summary=tmp_path / "absent.json", **kw)
     assert caps == {1: 32, 2: 32, 3: 32, 4: 32}
+
+
+def test_offload_engine_model_path_is_never_ignored(tmp_path):
+    """OffloadEngine(model_path=...) binds that directory or raises: it never falls back to the
+    synthetic model (no GPU needed: the directory is checked before any device work)."""
+    import pytest
+    from moe_offload.loader import OffloadEngine
+    with pytest.raises(FileNotFoundError):
+        OffloadEngine(model_path=tmp_path / "missing")
+    (tmp_path / "empty").mkdir()
+    with pytest.raises(FileNotFoundError):
+        OffloadEngine(model_path=tmp_path / "empty")
+
+
+def test_model_directory_routers_are_read_and_checked(tmp_path):
+    """ckpt.load_routers reads each layer's 8-bit router from base-*.safetensors with the shapes
+    the reference's loader checks (loader.cpp:398-404, 450) and rejects a wrong shape."""
+    import numpy as np
+    import pytest
+    import torch
+    from safetensors.torch import save_file
+
+    from helpers import router_q8
+    from moe_offload import ckpt
+    rng = np.random.default_rng(1)
+    E, Hd = 16, 256
+    base = {}
+    want = {}
+    for l in range(3):
+        c, s, b = router_q8(E, Hd, rng)
+        want[l] = (c, s, b)
+        pre = f"language_model.model.layers.{l}.mlp.gate"
+        base[f"{pre}.weight"] = torch.from_numpy(c.view(np.int32)).view(torch.uint32)
+        base[f"{pre}.scales"] = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16)
+        base[f"{pre}.biases"] = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16)
+    save_file(base, str(tmp_path / "base-00.safetensors"))
+    got = ckpt.load_routers(tmp_path, 3, E, Hd)
+    for l in range(3):
+        assert np.array_equal(got[l][0].view(np.uint32), want[l][0])
+        assert np.array_equal(got[l][1].view(np.uint16), want[l][1])
+        assert np.array_equal(got[l][2].view(np.uint16), want[l][2])
+    with pytest.raises(ValueError):
+        ckpt.load_routers(tmp_path, 3, E, 2 * Hd)     # experts of another hidden size
+    with pytest.raises(KeyError):
+        ckpt.load_routers(tmp_path, 4, E, Hd)         # a layer without a router

@@ -212,3 +212,45 @@ def test_prefill_plan_slot_contents_brute_force():
         assert len(set(new_e)) == len(new_e)
         uniq = set(int(e) for e in ids)
         assert plan["add_misses"] == len(uniq - set(prior_e)) and plan["add_req"] == m
+
+
+def test_round_bf16_once_against_exact_rationals():
+    """q2.round_bf16_once rounds float64 to bf16 once (nearest, ties to even), checked against
+    exact rational arithmetic: random values over many binades and constructed ties / near-ties,
+    where a float32 step first (q2.round_to(.., 'bf16'), MLX's double rounding) differs."""
+    from fractions import Fraction
+    rng = np.random.default_rng(7)
+    vals = list(rng.standard_normal(4000) * np.exp2(rng.integers(-20, 20, 4000)))
+    for _ in range(600):                              # exact ties and one-ulp-of-f64 neighbours
+        m = int(rng.integers(128, 256))               # 8 significand bits
+        e = int(rng.integers(-30, 30))
+        tie = (m + 0.5) * 2.0 ** e                    # halfway between two bf16 values
+        vals += [tie, np.nextafter(tie, np.inf), np.nextafter(tie, -np.inf), -tie]
+    # the double-rounding trap: just above a bf16 tie by less than half a float32 ulp
+    for m in (129, 130, 200, 255):
+        t = (m + 0.5) * 2.0 ** -3
+        vals.append(t + 2.0 ** -3 * 2.0 ** -20)
+    x = np.array(vals, np.float64)
+    got = q2.bf16_bits_to_f32(q2.round_bf16_once(x)).astype(np.float64)
+
+    def exact(v):
+        f = Fraction(v)
+        if f == 0:
+            return 0.0
+        sgn = -1 if f < 0 else 1
+        a = abs(f)
+        e = a.numerator.bit_length() - a.denominator.bit_length()
+        while Fraction(2) ** e > a:
+            e -= 1
+        while Fraction(2) ** (e + 1) <= a:
+            e += 1
+        ulp = Fraction(2) ** (e - 7)                  # 8 significand bits
+        lo = (a // ulp) * ulp
+        d = a - lo
+        if d > ulp / 2 or (d == ulp / 2 and (lo / ulp) % 2 == 1):
+            lo += ulp
+        return sgn * float(lo)
+    want = np.array([exact(float(v)) for v in x])
+    assert np.array_equal(got, want)
+    dbl = q2.round_to(x, "bf16")
+    assert not np.array_equal(dbl, want)              # the float32 step rounds some of them twice
