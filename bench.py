@@ -73,7 +73,8 @@ def parse():
     ap.add_argument("--glu", choices=["routed", "router"], default="routed",
                     help="resident pass: routed = logits + gate/up selecting the experts itself + down; router = "
                          "router with last-block selection + gate/up + down")
-    ap.add_argument("--only", choices=["headline", "resident", "roofline", "prefill", "calib", "floor", "nemotron", "filetier", "tensorform"],
+    ap.add_argument("--only", choices=["headline", "resident", "roofline", "prefill", "calib", "floor", "nemotron", "filetier",
+                                       "tensorform", "ckptstack"],
                     default=None,
                     help="run one pass and print its own JSON line (for sweeps and profiling); "
                          "calib runs the known-size copy kernel used to scale memory counters")
@@ -731,6 +732,60 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
     return out
 
 
+def ckpt_stack_pass(layers=48, warmup=4, steps=16, stage_ctas=8, only_cached=False):
+    """The decode stack in the reference checkpoint's own format at its production shape: 48 layers
+    of 512 experts, hidden 2560, inter 640, bf16 scales and biases (1,536,000 B per expert), the
+    8-bit group-64 routers, top-10, bf16 glue (ckpt.CheckpointStack over a SyntheticCheckpoint: the
+    shapes with seeded random content, since the files would be 37.7 GB).  (a) every layer's
+    experts in HBM: router logits -> gate/up selecting the experts -> down; (b) a 20% cache
+    (102 slots per layer 1..47), layer 0 pinned, misses staged from pinned host memory, prefetch
+    top-12 cap 3, device-driven tables, graph replay."""
+    import torch
+
+    from moe_offload.ckpt import CheckpointStack, CkptConfig, SyntheticCheckpoint
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4242)
+    out = {"workload": f"{layers}-layer decode in the checkpoint format: 512 experts, hidden 2560, inter 640, top-10, "
+                       "Q2 g64 with bf16 scales (1,536,000 B per expert), 8-bit g64 routers, bf16 RMSNorm glue, "
+                       f"batch 1, {steps} tokens"}
+    for resident in ((False,) if only_cached else (True, False)):
+        t0 = time.perf_counter()
+        st = CheckpointStack(cfg=CkptConfig(stage_ctas=stage_ctas), synthetic=SyntheticCheckpoint(layers, seed=7),
+                             resident=resident)
+        setup = time.perf_counter() - t0
+        xs = torch.randn((warmup + steps, st.cfg.hidden), device="cuda", generator=gen)
+        st.capture_graph()
+        for i in range(warmup):
+            st.decode_token(xs[i])
+        torch.cuda.synchronize()
+        tot0 = st.decode_totals()
+        t0 = time.perf_counter()
+        for i in range(warmup, warmup + steps):
+            st.decode_token(xs[i])
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        tot1 = st.decode_totals()
+        routed = st.routed_bytes_per_token()
+        rec = {"tok_s": round(steps / el, 2), "ms_per_token": round(el / steps * 1e3, 4),
+               "us_per_layer": round(el / steps / layers * 1e6, 2), "setup_s": round(setup, 1)}
+        if resident:
+            rec.update({"routed_gb_per_s": round(routed * steps / el / 1e9, 1),
+                        "routed_frac_of_peak": round(routed * steps / el / 1e9 / HBM_PEAK_GBS, 4)})
+        else:
+            req = max(1, tot1[3] - tot0[3])
+            staged = (tot1[4] - tot0[4]) + (tot1[5] - tot0[5])
+            rec.update({"slots_per_layer": st.capacities[1],
+                        "effective_hit_rate": round((tot1[0] - tot0[0] + tot1[1] - tot0[1]) / req, 4),
+                        "pure_lru_hit_rate": round((tot1[0] - tot0[0]) / req, 4),
+                        "staged_mb_per_token": round(staged / steps / 1e6, 1),
+                        "staged_gb_per_s": round(staged / el / 1e9, 2), "table_status": st.table_status()})
+        out["resident" if resident else "cache_20pct"] = rec
+        st.close()
+        del st
+        torch.cuda.empty_cache()
+    return out
+
+
 def resident_pass(args, cfg, gen, n_tok, xs=None):
     """48 layers with every expert in HBM (no cache, no staging): the GEMV kernels' own roofline."""
     import torch
@@ -851,6 +906,9 @@ def main():
         return
     if args.only == "tensorform":
         print(json.dumps({"tensor_form": tensor_form_pass()}), flush=True)
+        return
+    if args.only == "ckptstack":
+        print(json.dumps({"ckpt_stack": ckpt_stack_pass(args.layers)}), flush=True)
         return
     if args.only == "filetier":
         runs = set(args.file_tier_runs.split(",")) if args.file_tier_runs else None
@@ -990,6 +1048,7 @@ def main():
         line["prefill"] = prefill_pass()
     if not args.no_tensor_form:
         line["tensor_form"] = tensor_form_pass()
+        line["tensor_form"]["stack"] = ckpt_stack_pass(args.layers)
     if not args.no_file_tier:
         line["file_tier"] = file_tier_pass(args.layers, threads=args.io_threads)
     if not args.no_cpu_baseline:

@@ -946,6 +946,23 @@ uint64_t c_layer_device_table(int layer) {
 
 static int stage_device(int layer, LayerState& L, int list, hipStream_t s, int ctas) {
     if (L.fd >= 0) return filefeed::stage(layer, list, L.dtab, ctas, s);
+    StageSet S = {};
+    uint64_t units = 0;
+    for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
+        const uint64_t rb = L.row_bytes[t];
+        if (!rb || !L.dev_src[t] || !L.dst[t]) continue;
+        if (rb % 16) { S.n = 0; break; }              // (the per-tensor kernel reports it)
+        S.src[S.n] = (const uint8_t*)L.dev_src[t];
+        S.dst[S.n] = (uint8_t*)L.dst[t];
+        S.src_stride[S.n] = S.dst_stride[S.n] = rb;
+        S.first[S.n] = (uint32_t)units;
+        units += rb / 16;
+        ++S.n;
+    }
+    if (S.n > 1 && units <= 0xFFFFFFFFull) {          // several tensors: one launch for all of them
+        S.total = (uint32_t)units;
+        return launch_stage_set(L.dtab, list, S, ctas, s);
+    }
     for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
         uint64_t rb = L.row_bytes[t];
         if (!rb || !L.dev_src[t] || !L.dst[t]) continue;

@@ -228,6 +228,18 @@ int launch_slot_prefetch(SlotTable* t, const int32_t* preds, int m, int max_fetc
                          hipStream_t s);
 int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t store_stride,
                  uint8_t* pool, size_t pool_stride, size_t bytes, int ctas, hipStream_t s);
+// The listed experts' n tensors in one launch: tensor i of expert e is src_stride[i] bytes at
+// src[i] + e * src_stride[i] (units[i] = its bytes / 16 copied), slot row s at dst[i] +
+// s * dst_stride[i]; first[i] = the units of tensors 0..i-1, total = all units.
+struct StageSet {
+    const uint8_t* src[MOE_NUM_TENSORS];
+    uint8_t* dst[MOE_NUM_TENSORS];
+    uint64_t src_stride[MOE_NUM_TENSORS], dst_stride[MOE_NUM_TENSORS];
+    uint32_t first[MOE_NUM_TENSORS];
+    uint32_t total;
+    int n;
+};
+int launch_stage_set(const SlotTable* t, int list, const StageSet& S, int ctas, hipStream_t s);
 int launch_store_u32(uint32_t* dst, const uint32_t* vals, int n, hipStream_t s);
 // slots_out[0..n_hit) / [16..16+n_miss): hit / miss slots; scores_out likewise, gathered from
 // the step's scores (router order) through inv.

@@ -63,6 +63,50 @@ __global__ __launch_bounds__(256) void k_stage(const SlotTable* __restrict__ t, 
     }
 }
 
+// k_stage for a layer whose experts are several tensors (the reference's 9 per layer): one launch
+// per list, each listed expert's tensors copied as one run of 16-byte units (unit u of the
+// concatenation lies in the tensor whose first unit is the last one <= u), so an expert gets the
+// same `ctas` blocks and the link the same requests as a one-blob expert, instead of one launch per
+// tensor.
+__device__ __forceinline__ void stage_unit(const StageSet& S, unsigned u, int eid, int slot, const uint4*& src,
+                                           uint4*& dst) {
+    int i = 0;
+#pragma unroll
+    for (int j = 1; j < MOE_NUM_TENSORS; ++j)
+        if (j < S.n && S.first[j] <= u) i = j;
+    const unsigned v = u - S.first[i];
+    src = reinterpret_cast<const uint4*>(S.src[i] + (size_t)eid * S.src_stride[i]) + v;
+    dst = reinterpret_cast<uint4*>(S.dst[i] + (size_t)slot * S.dst_stride[i]) + v;
+}
+
+__global__ __launch_bounds__(256) void k_stage_set(const SlotTable* __restrict__ t, int list, StageSet S) {
+    const int c = blockIdx.y;
+    const int n = list ? t->pf_n_copy : t->n_copy;
+    if (c >= min(n, MOE_MAX_PREFETCH)) return;
+    const int eid = list ? t->pf_copy_eid[c] : t->copy_eid[c];
+    const int slot = list ? t->pf_copy_slot[c] : t->copy_slot[c];
+    if (eid < 0 || eid >= MOE_NUM_EXPERTS || slot < 0 || slot >= t->capacity) return;
+    const unsigned units = S.total;
+    const unsigned step = gridDim.x * blockDim.x;
+    for (unsigned u = blockIdx.x * blockDim.x + threadIdx.x; u < units; u += 4 * step) {
+        const bool m1 = u + step < units, m2 = u + 2 * step < units, m3 = u + 3 * step < units;
+        const uint4 *s0, *s1 = nullptr, *s2 = nullptr, *s3 = nullptr;
+        uint4 *d0, *d1 = nullptr, *d2 = nullptr, *d3 = nullptr;
+        stage_unit(S, u, eid, slot, s0, d0);
+        if (m1) stage_unit(S, u + step, eid, slot, s1, d1);
+        if (m2) stage_unit(S, u + 2 * step, eid, slot, s2, d2);
+        if (m3) stage_unit(S, u + 3 * step, eid, slot, s3, d3);
+        uint4 a = *s0, b = {}, cc = {}, d = {};
+        if (m1) b = *s1;
+        if (m2) cc = *s2;
+        if (m3) d = *s3;
+        *d0 = a;
+        if (m1) *d1 = b;
+        if (m2) *d2 = cc;
+        if (m3) *d3 = d;
+    }
+}
+
 // Plain device copy of a known byte count: the reference reading for scaling memory counters
 // (FETCH_SIZE / WRITE_SIZE per dispatch) to bytes.
 __global__ __launch_bounds__(256) void k_copy_calib(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16) {
@@ -131,6 +175,14 @@ int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t stor
     if (ctas <= 0) ctas = 2;
     MOE_LAUNCH(TK_STAGE, k_stage, dim3(ctas, MOE_MAX_PREFETCH), dim3(256), 0, s, t, list, store, store_stride,
                pool, pool_stride, bytes);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int launch_stage_set(const SlotTable* t, int list, const StageSet& S, int ctas, hipStream_t s) {
+    if (S.n <= 0 || S.n > MOE_NUM_TENSORS) { moe_set_error("stage_set: %d tensors", S.n); return -1; }
+    if (ctas <= 0) ctas = 2;
+    MOE_LAUNCH(TK_STAGE, k_stage_set, dim3(ctas, MOE_MAX_PREFETCH), dim3(256), 0, s, t, list, S);
     HIP_TRY(hipGetLastError());
     return 0;
 }

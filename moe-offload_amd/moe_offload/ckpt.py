@@ -54,7 +54,8 @@ class CkptConfig:
                                  # "file": read in place by the reader threads at each miss (host mode)
     io_threads: int = 8
     layer_base: int = 0          # first C-ABI layer index used
-    stage_ctas: int = 2
+    stage_ctas: int = 8          # staging blocks per copied expert (its 9 tensors in one launch; at 48 layers,
+                                 # 20% cache: 2 -> 41, 4 -> 69, 8 -> 81, 16 -> 77 tok/s on one box)
     # set from the directory
     n_layers: int = 0
     hidden: int = 0
@@ -121,53 +122,158 @@ def load_routers(model_dir: Path, n_layers: int, n_exp: int, hidden: int, group:
     return out
 
 
-class CheckpointStack:
-    """The 48-layer routed-expert decode over a model directory (module docstring)."""
+class SyntheticCheckpoint:
+    """The real checkpoint's shapes with seeded random content, made on the GPU (no files): per layer
+    the 9 expert tensors in role order (2-bit codes uniform over all patterns, bf16 scales
+    N(0, scale_std), biases -1.5 x scale, as the synthetic blob stacks draw them) and an 8-bit
+    group-64 router (scales ~2e-4, biases ~ -128 x scale: logits of order one).  For measuring the
+    production shape at 48 layers, whose files would be 37.7 GB."""
 
-    def __init__(self, model_path, cfg: CkptConfig | None = None, mode: str = "device", device="cuda"):
+    def __init__(self, n_layers: int = 48, n_exp: int = 512, hidden: int = 2560, inter: int = 640, seed: int = 0,
+                 scale_std: float = 0.02, device="cuda"):
+        self.n_layers, self.n_exp, self.hidden, self.inter, self.group = n_layers, n_exp, hidden, inter, 64
+        self.scale_std = scale_std
+        self.device = torch.device(device)
+        self.gen = torch.Generator(device=self.device)
+        self.gen.manual_seed(seed)
+        self.row_bytes = []
+        for out_f, in_f in ((inter, hidden), (inter, hidden), (hidden, inter)):
+            self.row_bytes += [out_f * in_f // 4, out_f * (in_f // 64) * 2, out_f * (in_f // 64) * 2]
+
+    def layer(self, l: int) -> list[torch.Tensor]:
+        """Layer l's 9 tensors, uint8 [n_exp, bytes per expert] on the GPU, role order."""
+        g, dev, E = self.gen, self.device, self.n_exp
+        out = []
+        for out_f, in_f in ((self.inter, self.hidden), (self.inter, self.hidden), (self.hidden, self.inter)):
+            w = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, out_f, in_f // 16), dtype=torch.int32, device=dev, generator=g)
+            sc = (torch.randn((E, out_f, in_f // 64), device=dev, generator=g) * self.scale_std).to(torch.bfloat16)
+            bi = (-1.5 * sc.float()).to(torch.bfloat16)
+            out += [t.contiguous().view(torch.uint8).reshape(E, -1) for t in (w, sc, bi)]
+        return out
+
+    def routers(self) -> list[tuple]:
+        g, dev, E, H = self.gen, self.device, self.n_exp, self.hidden
+        res = []
+        for _ in range(self.n_layers):
+            codes = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, H // 4), dtype=torch.int32, device=dev, generator=g)
+            sc = (torch.randn((E, H // 64), device=dev, generator=g) * 2e-4).to(torch.bfloat16)
+            bi = (-128 * sc.float() + torch.randn((E, H // 64), device=dev, generator=g) * 1e-4).to(torch.bfloat16)
+            res.append((codes, sc.view(torch.int16), bi.view(torch.int16)))
+        return res
+
+
+class _PinnedLayers:
+    """Layers 1.. of a SyntheticCheckpoint copied into pinned, device-mapped host memory, with the
+    attributes the stack reads from a HostShardStore (layout, ptrs, close)."""
+
+    def __init__(self, src: SyntheticCheckpoint, layers):
+        L = _lib.lib()
+        self.layout, self.ptrs = {}, {}
+        try:
+            for l in layers:
+                ts = src.layer(l)
+                ptrs = []
+                for t in ts:
+                    ptr = L.c_host_alloc(t.numel())
+                    if not ptr:
+                        raise _lib.NativeError(f"pinned synthetic store: {_lib.last_error()}")
+                    ptrs.append(ptr)
+                    host = torch.from_numpy(np.ctypeslib.as_array(ctypes.cast(ptr, ctypes.POINTER(ctypes.c_uint8)),
+                                                                  shape=tuple(t.shape)))
+                    host.copy_(t)
+                self.ptrs[l] = ptrs
+                self.layout[l] = {"offsets": [0] * 9, "row_bytes": list(src.row_bytes), "roles": list(range(9)),
+                                  "scale_bf16": True, "n_exp": src.n_exp, "hidden": src.hidden, "inter": src.inter,
+                                  "group": src.group}
+                del ts
+        except Exception:
+            self.close()
+            raise
+
+    def close(self):
+        L = _lib.lib()
+        for ptrs in self.ptrs.values():
+            for p in ptrs:
+                L.c_host_free(p)
+        self.ptrs.clear()
+
+
+class CheckpointStack:
+    """The 48-layer routed-expert decode over a model directory (module docstring).
+
+    synthetic: a SyntheticCheckpoint in place of a directory (the production shape at any depth).
+    resident=True: every layer's experts in HBM (no cache, no tables): per layer the 8-bit router's
+    logits, then moe_q2t_gate_up_routed (its blocks select the experts), then the down product."""
+
+    def __init__(self, model_path=None, cfg: CkptConfig | None = None, mode: str = "device", device="cuda",
+                 synthetic: SyntheticCheckpoint | None = None, resident: bool = False):
         if mode not in ("device", "host"):
             raise ValueError(f"mode {mode!r}: 'device' or 'host'")
         self.cfg = c = cfg or CkptConfig()
         self.mode = mode
+        self.resident = resident
         self.device = dev = torch.device(device)
-        root = Path(model_path)
-        if not root.is_dir():
-            raise FileNotFoundError(f"{root}: not a model directory")
-        n_layers = expert_layers(root)
-        if n_layers < 2:
-            raise FileNotFoundError(f"{root}: needs experts-00.safetensors and experts-01.safetensors at least")
         if c.store not in ("host", "file"):
             raise ValueError(f"store {c.store!r}: 'host' or 'file'")
         if c.store == "file" and mode == "device":
             raise ValueError("store='file' runs host-driven tables (mode='host')")
+        if resident and mode != "device":
+            raise ValueError("resident=True is device-driven")
+        if synthetic is None:
+            root = Path(model_path)
+            if not root.is_dir():
+                raise FileNotFoundError(f"{root}: not a model directory")
+            n_layers = expert_layers(root)
+            if n_layers < 2:
+                raise FileNotFoundError(f"{root}: needs experts-00.safetensors and experts-01.safetensors at least")
+        else:
+            n_layers = synthetic.n_layers
         self.L = L = _lib.lib()
-        shards = {l: str(root / f"experts-{l:02d}.safetensors") for l in range(n_layers)}
-        lay0 = ShardExpertStore({0: shards[0]})
-        c.n_layers, c.n_exp, c.hidden, c.inter, c.group = n_layers, lay0.n_exp, lay0.hidden, lay0.inter, lay0.group
-        if c.group != 64:
-            lay0.close()
-            raise ValueError(f"{root}: experts of group {c.group} (the kernels take 64)")
-        self.scale_bf16 = int(lay0.layout[0]["scale_bf16"])
-        self.blob_bytes = lay0.blob_bytes                      # bytes per expert over its 9 tensors
+        if synthetic is None:
+            shards = {l: str(root / f"experts-{l:02d}.safetensors") for l in range(n_layers)}
+            lay0 = ShardExpertStore({0: shards[0]})
+            c.n_layers, c.n_exp, c.hidden, c.inter, c.group = n_layers, lay0.n_exp, lay0.hidden, lay0.inter, lay0.group
+            if c.group != 64:
+                lay0.close()
+                raise ValueError(f"{root}: experts of group {c.group} (the kernels take 64)")
+            self.scale_bf16 = int(lay0.layout[0]["scale_bf16"])
+            self.blob_bytes = lay0.blob_bytes                      # bytes per expert over its 9 tensors
+            # layer 0: all 9 tensors in HBM, in role order (MOE_Q2T_*: gate w/s/b, up w/s/b, down w/s/b)
+            try:
+                self.pool0, self.ptrs0, self.nbytes0 = self._pack(self._read_resident(lay0, 0))
+            finally:
+                lay0.close()
+            r = load_routers(root, n_layers, c.n_exp, c.hidden, c.group)
+            self.routers = [tuple(torch.from_numpy(a).to(dev) for a in t) for t in r]
+        else:
+            c.n_layers, c.n_exp, c.hidden, c.inter, c.group = (n_layers, synthetic.n_exp, synthetic.hidden,
+                                                               synthetic.inter, synthetic.group)
+            self.scale_bf16 = 1
+            self.blob_bytes = sum(synthetic.row_bytes)
+            self.routers = synthetic.routers()
+            self.pool0, self.ptrs0, self.nbytes0 = self._pack(synthetic.layer(0))
         self.capacities = compute_layer_capacities(budget_gb=c.budget_gb, budget_pct=c.budget_pct,
                                                    num_layers=n_layers, num_experts=c.n_exp,
                                                    expert_bytes=self.blob_bytes)
-        # layer 0: all 9 tensors in HBM, in role order (MOE_Q2T_* : gate w/s/b, up w/s/b, down w/s/b)
-        try:
-            self.pool0, self.ptrs0, self.nbytes0 = self._load_resident(lay0, 0)
-        finally:
-            lay0.close()
-        r = load_routers(root, n_layers, c.n_exp, c.hidden, c.group)
-        self.routers = [tuple(torch.from_numpy(a).to(dev) for a in t) for t in r]
+        self.pools, self.slot_inds = {}, {}
+        self.full = None
+        if resident:                                      # every layer in HBM, slot = expert id
+            self.store = None
+            self.full = [(self.pool0, self.ptrs0, self.nbytes0)]
+            for l in range(1, n_layers):
+                self.full.append(self._pack(synthetic.layer(l) if synthetic is not None else
+                                            self._read_file_layer(shards[l], l)))
+            self._init_buffers()
+            return
         # layers 1..: cached pools fed from pinned host memory or the files
-        cached = {l: shards[l] for l in range(1, n_layers)}
         L.c_set_compute_stream(ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
-        if c.store == "host":
-            self.store = HostShardStore(cached, threads=c.io_threads)
+        if synthetic is not None:
+            self.store = _PinnedLayers(synthetic, range(1, n_layers))
+        elif c.store == "host":
+            self.store = HostShardStore({l: shards[l] for l in range(1, n_layers)}, threads=c.io_threads)
         else:
             L.c_io_init(c.io_threads)
-            self.store = ShardExpertStore(cached)
-        self.pools, self.slot_inds = {}, {}
+            self.store = ShardExpertStore({l: shards[l] for l in range(1, n_layers)})
         u64 = ctypes.c_uint64 * 9
         for l in range(1, n_layers):
             lay = self.store.layout[l]
@@ -187,6 +293,10 @@ class CheckpointStack:
                                              int(lay["scale_bf16"]) | 2), "c_layer_set_format9")
             if mode == "device":
                 _lib.check(L.c_layer_set_device_mode(li, 1), "set_device_mode")
+        self._init_buffers()
+
+    def _init_buffers(self):
+        c, L, dev, n_layers = self.cfg, self.L, self.device, self.cfg.n_layers
         k, m = c.top_k, max(c.top_m, 1)
         self.xb = torch.zeros((n_layers + 1, c.hidden), dtype=torch.int16, device=dev)   # bf16 bits
         self.xf = torch.zeros((n_layers + 1, c.hidden), dtype=torch.float16, device=dev)
@@ -194,6 +304,7 @@ class CheckpointStack:
         self.ids = torch.zeros((n_layers, k), dtype=torch.int32, device=dev)
         self.scores = torch.zeros((n_layers, k), dtype=torch.int16, device=dev)          # bf16 bits
         self.pred = torch.zeros((n_layers, m), dtype=torch.int32, device=dev)
+        self.logits = torch.zeros((n_layers, c.n_exp), dtype=torch.int16, device=dev)    # bf16 bits
         wsb = int(L.moe_router_q8_workspace_bytes(c.n_exp))
         self.ws_route = [torch.zeros(wsb, dtype=torch.uint8, device=dev) for _ in range(n_layers)]
         self.ws_pred = [torch.zeros(wsb, dtype=torch.uint8, device=dev) for _ in range(n_layers)]
@@ -207,12 +318,27 @@ class CheckpointStack:
         self.file_device = False
         torch.cuda.synchronize()
 
-    def _load_resident(self, files: ShardExpertStore, l: int):
+    def _read_resident(self, files: ShardExpertStore, l: int) -> list[torch.Tensor]:
+        """Layer l's 9 tensors from its shard into HBM, role order."""
         lay = files.layout[l]
         by_role = [None] * 9
         for off, rb, role in zip(lay["offsets"], lay["row_bytes"], lay["roles"]):
             raw = _read(files.fds[l], off, lay["n_exp"] * rb)
             by_role[role] = torch.from_numpy(raw.reshape(lay["n_exp"], rb)).to(self.device)
+        return by_role
+
+    def _read_file_layer(self, path: str, l: int) -> list[torch.Tensor]:
+        files = ShardExpertStore({l: path})
+        try:
+            lay = files.layout[l]
+            if (lay["n_exp"], lay["hidden"], lay["inter"]) != (self.cfg.n_exp, self.cfg.hidden, self.cfg.inter):
+                raise ValueError(f"{path}: shape differs from experts-00")
+            return self._read_resident(files, l)
+        finally:
+            files.close()
+
+    @staticmethod
+    def _pack(by_role: list[torch.Tensor]):
         u64 = ctypes.c_uint64 * 9
         return by_role, u64(*[t.data_ptr() for t in by_role]), u64(*[t.shape[1] for t in by_role])
 
@@ -247,6 +373,22 @@ class CheckpointStack:
         _lib.check(self.L.moe_rmsnorm_bf16(self.hs[l - 1].data_ptr(), None, self.cfg.eps, self.cfg.hidden,
                                            self.xb[l].data_ptr(), self.xf[l].data_ptr(), s), "rmsnorm_bf16")
 
+    def _layer_resident(self, l: int, s: int):
+        """Resident layer: the router's bf16 logits, then gate/up whose blocks select the top k
+        themselves (the router's rule, bit for bit), then the down product with the bf16 scores."""
+        c, L = self.cfg, self.L
+        codes, scales, biases = self.routers[l]
+        _lib.check(L.moe_router_q8(self.xb[l].data_ptr(), codes.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+                                   c.hidden, c.n_exp, c.group, 0, 0, self.ws_route[l].data_ptr(), None, None, None,
+                                   self.logits[l].data_ptr(), s), "router_q8 logits")
+        _, ptrs, nbytes = self.full[l]
+        _lib.check(L.moe_q2t_gate_up_routed(self.xf[l].data_ptr(), self.logits[l].data_ptr(), c.n_exp, c.top_k, ptrs,
+                                            nbytes, self.scale_bf16, c.hidden, c.inter, c.group, self.ids[l].data_ptr(),
+                                            self.scores[l].data_ptr(), self.h_ws.data_ptr(), s), "q2t_gate_up_routed")
+        _lib.check(L.moe_q2t_down(self.h_ws.data_ptr(), ptrs, nbytes, self.scale_bf16 | 2, c.n_exp,
+                                  self.ids[l].data_ptr(), self.scores[l].data_ptr(), c.top_k, c.hidden, c.inter,
+                                  c.group, self.xf[l].data_ptr(), self.hs[l].data_ptr(), 0, s), "q2t_down")
+
     def decode_token_device(self):
         """Device-driven token (DecodeStack's device path with the checkpoint's kernels): main stream
         norm -> router (+ predictor) -> [join prefetch table(l)] -> step(l) -> [join prefetch
@@ -258,6 +400,9 @@ class CheckpointStack:
         for l in range(c.n_layers):
             if l > 0:
                 self._norm(l, ms)
+            if self.resident:
+                self._layer_resident(l, ms)
+                continue
             self._router(l, ms)
             if l >= 1:
                 if c.prefetch:
@@ -344,17 +489,21 @@ class CheckpointStack:
         return None
 
     def table_status(self) -> dict[int, int]:
-        if self.mode != "device":
+        if self.mode != "device" or self.resident:
             return {}
         st = {l: self.L.c_layer_table_status(self.cidx(l)) for l in range(1, self.cfg.n_layers)}
         return {l: v for l, v in st.items() if v}
 
     def reset_caches(self):
+        if self.resident:
+            return
         for l in range(1, self.cfg.n_layers):
             self.L.c_layer_reset_cache(self.cidx(l))
         _lib.check_error("reset_cache")
 
     def reset_stats(self):
+        if self.resident:
+            return
         for l in range(1, self.cfg.n_layers):
             self.L.c_layer_reset_stats(self.cidx(l))
 
@@ -364,6 +513,8 @@ class CheckpointStack:
         return list(o)
 
     def decode_totals(self) -> list[int]:
+        if self.resident:
+            return [0] * 6
         o = (ctypes.c_uint64 * 6)()
         self.L.c_get_decode_totals(self.cidx(self.cfg.n_layers), o)
         return list(o)
@@ -374,6 +525,9 @@ class CheckpointStack:
     def close(self):
         torch.cuda.synchronize()
         self.graph = None
+        if self.resident:
+            self.full = None
+            return
         self.L.c_sync_copies()
         for l in range(1, self.cfg.n_layers):
             self.L.c_layer_init(self.cidx(l), -1, 16, None, None, None, 0)

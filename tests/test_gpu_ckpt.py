@@ -178,3 +178,77 @@ def test_offload_engine_over_model_directory(model_dir, tmp_path):
         eng.close()
     with pytest.raises(FileNotFoundError):
         OffloadEngine(model_path=tmp_path / "no-model")
+
+
+def test_resident_checkpoint_stack_equals_cached(model_dir):
+    """Every layer in HBM (the 8-bit router's logits, gate/up selecting the experts itself, down)
+    gives the cached device-driven stack's tokens bit for bit, eager and graph-replayed: the same
+    selection code, the same weights, the same kernels' arithmetic."""
+    from moe_offload.ckpt import CheckpointStack, CkptConfig
+    root, _, _ = model_dir
+    st, rec, _ = _run(root, "device")
+    st.close()
+    for graph in (False, True):
+        rs = CheckpointStack(root, CkptConfig(), mode="device", resident=True)
+        try:
+            gen = torch.Generator(device="cuda")
+            gen.manual_seed(21)
+            xs = torch.randn((N_TOK, H), device="cuda", generator=gen)
+            for t in range(N_TOK):
+                if graph and t == 1:
+                    rs.capture_graph()
+                rs.decode_token(xs[t])
+                torch.cuda.synchronize()
+                assert np.array_equal(rs.ids.cpu().numpy(), rec[t]["ids"]), (graph, t)
+                assert np.array_equal(rs.scores.cpu().numpy().view(np.uint16), rec[t]["scores"]), (graph, t)
+                assert np.array_equal(rs.xb.cpu().numpy().view(np.uint16), rec[t]["xb"]), (graph, t)
+        finally:
+            rs.close()
+
+
+def test_synthetic_checkpoint_resident_and_cached_agree():
+    """The synthetic source (the checkpoint's shapes generated on the GPU, for 48-layer measurements):
+    cached (16-slot pools fed from pinned host memory) and resident stacks built from the same seed
+    give bit-identical tokens, and a sampled layer matches the oracle given its own input."""
+    from moe_offload.ckpt import CheckpointStack, CkptConfig, SyntheticCheckpoint
+    n_layers, E, Hs, Is = 4, 64, 1024, 320
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    xs = torch.randn((4, Hs), device="cuda", generator=gen)
+    out = {}
+    for resident in (False, True):
+        st = CheckpointStack(cfg=CkptConfig(), synthetic=SyntheticCheckpoint(n_layers, E, Hs, Is, seed=9),
+                             resident=resident)
+        try:
+            rec = []
+            for t in range(4):
+                st.decode_token(xs[t])
+                torch.cuda.synchronize()
+                rec.append((st.ids.cpu().numpy().copy(), st.xb.cpu().numpy().copy(), st.hs.cpu().numpy().copy(),
+                            st.scores.cpu().numpy().view(np.uint16).copy()))
+            if resident:                              # oracle at layer 2 of the last token
+                l = 2
+                ids, xb, hs, sc = rec[-1]
+                codes, scales, biases = (a.cpu().numpy() for a in st.routers[l])
+                W = q2.dequantize(codes.view(np.uint32), scales.view(np.uint16), biases.view(np.uint16), 8, 64, "bf16")
+                x = q2.to_f64(xb[l].view(np.uint16), "bf16")
+                want_i, want_s, _ = q2.route(q2.round_to(x @ W.T, "bf16")[None], 10, "bf16")
+                assert ids[l].tolist() == want_i[0].astype(np.int64).tolist()
+                assert np.array_equal(q2.to_f64(sc[l], "bf16"), want_s[0])
+                t9 = [t.cpu().numpy() for t in st.full[l][0]]
+                shapes = [(Is, Hs), (Is, Hs), (Hs, Is)]
+                mlx = []
+                for p, (o, i_) in enumerate(shapes):
+                    w = t9[3 * p].view(np.uint32).reshape(E, o, i_ // 16)
+                    s_ = t9[3 * p + 1].view(np.uint16).reshape(E, o, i_ // 64)
+                    b_ = t9[3 * p + 2].view(np.uint16).reshape(E, o, i_ // 64)
+                    mlx.append((w, s_, b_))
+                xf = x.astype(np.float16).astype(np.float64)
+                want = q2.moe_combine(xf, want_i[0], want_s[0], _experts_fn(mlx), bits=2, group=64, sdtype="bf16")
+                assert_close_rms(hs[l].astype(np.float64) - xf, want, 1e-2, "synthetic layer 2")
+            out[resident] = rec
+        finally:
+            st.close()
+    for t in range(4):
+        for a, b in zip(out[False][t], out[True][t]):
+            assert np.array_equal(a, b), t
