@@ -254,3 +254,51 @@ def test_round_bf16_once_against_exact_rationals():
     assert np.array_equal(got, want)
     dbl = q2.round_to(x, "bf16")
     assert not np.array_equal(dbl, want)              # the float32 step rounds some of them twice
+
+
+def _rebuild_by_prior_recency(plan, lru_eids, capacity):
+    """A plausible mistake in the LRU rebuild after prefill: untouched residents kept in their prior
+    recency order (then the last chunk), instead of slot-index order as loader.py:671-680 does."""
+    new_e, new_s = plan["new_lru"]
+    last_len = plan["chunks"][-1][1] - plan["chunks"][-1][0]
+    pos = {e: i for i, e in enumerate(lru_eids)}
+    tail = [(e, s) for e, s in zip(new_e, new_s) if s < last_len]
+    rest = [(e, s) for e, s in zip(new_e, new_s) if s >= last_len]
+    rest.sort(key=lambda t: pos.get(t[0], -1))
+    both = rest + tail
+    return [e for e, _ in both], [s for _, s in both]
+
+
+def test_prefill_plan_known_answers():
+    """q2.prefill_plan on two cases worked by hand from loader.py:566-699 (chunk placement: chunk
+    expert of rank r goes to slot r, loaded when the slot held another expert; LRU rebuilt from the
+    final slot bijection with slots [last chunk length, capacity) oldest in slot order, then the
+    last chunk's slots in slot order; the prefill counters).  The planted prior-recency rebuild
+    fails case B."""
+    # A: capacity 4, prior LRU->MRU (eid, slot) = (7, 2), (3, 0), (9, 3); slot 1 free.  Tokens
+    # (5, 3), (8, 5), (1, 2): unique experts 1 2 3 5 8 -> chunks [1 2 3 5], [8].
+    # chunk 0: slot0 held 3 -> load 1; slot1 free -> load 2; slot2 held 7 -> load 3 (3 left slot 0);
+    #          slot3 held 9 -> load 5.   chunk 1: slot0 held 1 -> load 8.
+    # final slots {0: 8, 1: 2, 2: 3, 3: 5}, last chunk length 1: LRU = slots 1 2 3, then 0.
+    # counters: 6 requests; 3 was cached (1 hit); 5 missed once then hit; 1 2 8 missed: 4 misses, 2 hits.
+    p = q2.prefill_plan(np.array([5, 3, 8, 5, 1, 2]), [7, 3, 9], [2, 0, 3], 4)
+    assert [(u0, u1, le, ls) for u0, u1, le, ls in p["chunks"]] == [(0, 4, [1, 2, 3, 5], [0, 1, 2, 3]),
+                                                                     (4, 5, [8], [0])]
+    assert p["new_lru"] == ([2, 3, 5, 8], [1, 2, 3, 0])
+    assert (p["add_req"], p["add_hits"], p["add_misses"]) == (6, 2, 4)
+    # B: capacity 6, prior LRU->MRU (40, 5), (41, 2), (42, 4), (43, 3); slots 0 1 free.  Tokens
+    # (11, 10), (10, 11): one chunk [10 11] into slots 0 1 (both loaded).  Slots 2..5 keep their
+    # experts untouched and go first in slot order: 41 43 42 40, then 10 11.  4 requests, 2 misses.
+    lru_e, lru_s = [40, 41, 42, 43], [5, 2, 4, 3]
+    p = q2.prefill_plan(np.array([11, 10, 10, 11]), lru_e, lru_s, 6)
+    assert [(u0, u1, le, ls) for u0, u1, le, ls in p["chunks"]] == [(0, 2, [10, 11], [0, 1])]
+    known = ([41, 43, 42, 40, 10, 11], [2, 3, 4, 5, 0, 1])
+    assert p["new_lru"] == known
+    assert (p["add_req"], p["add_hits"], p["add_misses"]) == (4, 2, 2)
+    assert _rebuild_by_prior_recency(p, lru_e, 6) != known          # the planted mistake is caught
+    # C: a chunk expert already in its rank slot is not loaded again: capacity 4, prior (20, 0),
+    # (21, 1); tokens (20, 22): chunk [20 22] -> slot 0 keeps 20, slot 1 (held 21) loads 22.
+    p = q2.prefill_plan(np.array([20, 22]), [20, 21], [0, 1], 4)
+    assert p["chunks"] == [(0, 2, [22], [1])]
+    assert p["new_lru"] == ([20, 22], [0, 1])
+    assert (p["add_req"], p["add_hits"], p["add_misses"]) == (2, 1, 1)
