@@ -9,10 +9,13 @@ A step is one decode token through all 48 layers.  Inputs are synthetic (seeded)
 resident in HBM when the timed region starts; the expert store is host memory by design.
 
 Prints one JSON line.  `value` = tokens/s over the timed steps.  `roofline` covers the
-dominant kernel (the Q2 gate/up GEMV), timed with HIP events on its stream in an instrumented
-pass over the same number of tokens right after the timed region; `cpu_baseline` times the
-reference's CPU path for one token-layer on the host cores; `tensor_form` times the decode kernels
-on the reference's own 9-tensor expert format at its production shape (2560 x 640, bf16 scales).
+dominant kernel of the resident decode (every expert in HBM): the kernels the decode launches
+are timed with the decode's own per-layer inputs, back to back in a captured HIP graph bracketed
+by HIP events, and the slowest is reported; `cpu_baseline` times the reference's CPU path for one
+token-layer on the host cores; `tensor_form` times the decode kernels on the reference's own
+9-tensor expert format at its production shape (2560 x 640, bf16 scales) and, under `stack`, the
+48-layer decode in that format (resident and 20% cache); `nemotron` the codebook workload; `prefill`
+the 512-token chunk; `file_tier` the on-disk tier.
 """
 from __future__ import annotations
 
@@ -58,6 +61,8 @@ def parse():
                     help="staging blocks per prefetched expert (0: --stage-ctas)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill grouped-GEMM pass")
     ap.add_argument("--no-file-tier", action="store_true", help="skip the on-disk tier pass")
+    ap.add_argument("--no-nemotron", action="store_true",
+                    help="skip the codebook (Nemotron-style) workload: 40 layers, 240 experts, top-9, hidden 3072")
     ap.add_argument("--no-tensor-form", action="store_true",
                     help="skip the pass over the reference's 9-tensor expert format at 2560 x 640")
     ap.add_argument("--io-threads", type=int, default=8, help="reader threads of the on-disk tier pass")
@@ -394,6 +399,43 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
     return res
 
 
+def raw_read_gbs(path, threads, direct, piece=8 << 20, repeats=2):
+    """The box's own read rate, no GPU involved: the whole file read by the library's reader threads
+    (c_io_read_ranges, the same threads the file tier uses) into page-aligned host memory in pieces
+    of `piece` bytes, with O_DIRECT or through the page cache; best of `repeats`.  None when the file
+    system refuses O_DIRECT."""
+    import ctypes
+    import mmap
+
+    from moe_offload import _lib
+    L = _lib.lib()
+    L.c_io_init(threads)
+    try:
+        fd = os.open(path, os.O_RDONLY | (os.O_DIRECT if direct else 0))
+    except OSError:
+        return None
+    try:
+        size = os.fstat(fd).st_size // 4096 * 4096
+        buf = mmap.mmap(-1, size)
+        base = ctypes.addressof(ctypes.c_char.from_buffer(buf))
+        offs = list(range(0, size, piece))
+        lens = [min(piece, size - o) for o in offs]
+        u64 = ctypes.c_uint64 * len(offs)
+        best = None
+        for _ in range(repeats):
+            t0 = time.perf_counter()
+            rc = L.c_io_read_ranges(fd, u64(*offs), u64(*lens), u64(*[base + o for o in offs]), len(offs))
+            el = time.perf_counter() - t0
+            if rc != 0:
+                L.c_clear_error()
+                return None
+            best = el if best is None or el < best else best
+        del buf
+        return round(size / best / 1e9, 2)
+    finally:
+        os.close(fd)
+
+
 def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8, runs=None):
     """The decode stack with the on-disk tier: every cached layer reads its misses from one blob
     file of 512 experts (q2format.write_blob_file, 503 MB, shared by the 47 cached layers) with the
@@ -415,13 +457,20 @@ def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8, runs=None):
     gen.manual_seed(4321)
     d = tempfile.mkdtemp(prefix="moe_file_tier_")
     out = {"workload": f"{n_layers}-layer decode as the headline, misses read by {threads} reader threads from one "
-                       f"512-expert blob file shared by the cached layers, host-driven tables (device_*: device-driven, graph-replayed), {steps} tokens",
+                       f"512-expert blob file (503 MB) shared by the 47 cached layers, host-driven tables (device_*: "
+                       f"device-driven, graph-replayed), {steps} tokens; the file is fully in the page cache after the "
+                       "warm-up, so the *page_cache runs read host memory, not the disk (the 47 distinct shards of the "
+                       "real model are 23.6 GB); the *o_direct runs read the device; raw_read: the same threads reading "
+                       "the file alone, without the GPU",
            "threads": threads}
     try:
         path = os.path.join(d, "experts.q2blob")
         blobs = random_blobs(base.n_exp, base.hidden, base.inter, base.group, gen, "cuda").cpu().numpy()
         q2format.write_blob_file(path, blobs, base.hidden, base.inter)
         del blobs
+        out["raw_read"] = {"o_direct_gb_s": raw_read_gbs(path, threads, True),
+                           "page_cache_gb_s": raw_read_gbs(path, threads, False), "piece_bytes": 8 << 20,
+                           "file_bytes": os.path.getsize(path)}
         xs = torch.randn((warmup + steps, base.hidden), device="cuda", generator=gen).half()
         for name, kw, mode in (("host_store", {}, "host"), ("page_cache", {"store_file": path}, "host"),
                                ("o_direct", {"store_file": path, "io_direct": True}, "host"),
@@ -444,6 +493,9 @@ def file_tier_pass(n_layers=48, warmup=4, steps=24, threads=8, runs=None):
                              "read_gb_s": round(read / elapsed / 1e9, 2)}
                 if direct is not None:
                     out[name]["o_direct_in_use"] = direct
+                raw = out["raw_read"]["o_direct_gb_s" if kw.get("io_direct") else "page_cache_gb_s"] if kw else None
+                if raw:
+                    out[name]["frac_of_raw_read"] = round(read / elapsed / 1e9 / raw, 3)
             finally:
                 st.close()
                 del st
@@ -1049,6 +1101,8 @@ def main():
     if not args.no_tensor_form:
         line["tensor_form"] = tensor_form_pass()
         line["tensor_form"]["stack"] = ckpt_stack_pass(args.layers)
+    if not args.no_nemotron:
+        line["nemotron"] = nemotron_pass(min(args.steps, 64), min(args.warmup, 8), args.nemo_layers)
     if not args.no_file_tier:
         line["file_tier"] = file_tier_pass(args.layers, threads=args.io_threads)
     if not args.no_cpu_baseline:
