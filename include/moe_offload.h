@@ -106,17 +106,22 @@ enum { MOE_SCHED_SYNC_DEMAND = 1, MOE_SCHED_NO_PREFETCH = 2, MOE_SCHED_SPLIT = 4
 int c_layer_decode_step_sched(int layer_idx, const int32_t* eids, int k, const int32_t* pred,
                               int n_pred, int next_layer, int prefetch_cap, int flags);
 /* cpp/third_party/expert_io.c:1062-1092.  The last recorded split of the layer: hit slots,
- * miss slots (id order) and each id's position in hits ++ misses (kept until the next split). */
+ * miss slots (id order) and each id's position in hits ++ misses (kept until the next split).
+ * A device-driven layer's split is the one its table kernels recorded (c_layer_set_sched bit 1);
+ * reading it waits for the compute stream. */
 void c_layer_get_split_inds(int layer_idx, uint32_t* out_hit_slots, uint32_t* out_miss_slots,
                             int32_t* out_inv_order);
 /* cpp/third_party/expert_io.c:1048-1060.  Joins the layer's copies on the GPU side (the
  * compute stream waits; the host does not block). */
 void c_layer_wait_demand(int layer_idx);
-/* cpp/third_party/expert_io.c:1002-1038.  Per-token accounting over host-driven calls: out10 =
- * lru hits, demand misses, prefetch loads, prefetch hits, wasted prefetches, demand re-reads
- * within 16 / 64 tokens, prefetch re-reads within 16 / 64 tokens, bytes staged.  Tokens are
- * numbered by the library (token_idx is ignored, as in the reference); layer 1's reset
- * restarts the numbering. */
+/* cpp/third_party/expert_io.c:1002-1038.  Per-token accounting: out10 = lru hits, demand
+ * misses, prefetch loads, prefetch hits, wasted prefetches, demand re-reads within 16 / 64
+ * tokens, prefetch re-reads within 16 / 64 tokens, bytes staged.  Tokens are numbered by the
+ * library (token_idx is ignored, as in the reference); layer 1's reset restarts the numbering.
+ * Host tables count in the library; device-driven tables count in their table kernels: for
+ * them the three calls queue small control kernels on the compute stream (so they order with
+ * the token's kernels and a captured token's table work counts at replay), and
+ * c_end_decode_token adds the device tables' counters, waiting for the compute stream. */
 void c_set_io_accounting(int enabled);
 void c_begin_decode_token(int token_idx);
 void c_end_decode_token(uint64_t* out10);
@@ -328,8 +333,9 @@ int c_layer_grouped_switch_glu(int layer_idx, const void* x, int n_tokens, const
  * sum.  scores in router order; both parts on one stream, part 0 first. */
 int c_layer_switch_glu_split(int layer_idx, int part, const void* x, const void* scores,
                              const void* residual, void* h_ws, float* y_out, void* stream);
-/* Device-driven tables follow the scheduler variant's decisions (on != 0) or the published
- * ones (the default). */
+/* Device-driven tables follow the scheduler variant's decisions (bit 0 of on) or the published
+ * ones (the default); with bit 1 also set, their steps record the split lists as
+ * MOE_SCHED_SPLIT does (read with c_layer_get_split_inds). */
 int c_layer_set_sched(int layer_idx, int on);
 /* Record that work queued on `stream` so far reads the layer's pool (copies into it wait). */
 int c_layer_mark_read(int layer_idx, void* stream);

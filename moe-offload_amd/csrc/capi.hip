@@ -84,7 +84,6 @@ struct LayerState {
     hipEvent_t pf_done = nullptr;
     bool pf_pending = false;
     uint8_t* split_dev = nullptr;             // device copy of the split lists (split GLU)
-    int32_t evicted_at[MOE_NUM_EXPERTS];      // per-token accounting: token of last eviction
 };
 
 LayerState g_layers[MOE_MAX_LAYERS];
@@ -101,13 +100,21 @@ uint64_t g_tok[10] = {0};
 slot_host::Acct* acct_for(LayerState& L, slot_host::Acct& a) {
     if (!g_acct_on) return nullptr;
     a.cur_token = g_cur_token;
-    a.evicted_at = L.evicted_at;
+    a.evicted_at = L.tab.evicted_at;
     a.tok = g_tok;
     return &a;
 }
 
 void reset_evictions(LayerState& L) {
-    for (int e = 0; e < MOE_NUM_EXPERTS; ++e) L.evicted_at[e] = -1;
+    for (int e = 0; e < MOE_NUM_EXPERTS; ++e) L.tab.evicted_at[e] = -1;
+}
+
+// The device-driven tables (for the accounting control and gather kernels).
+TableSet device_tables() {
+    TableSet ts = {};
+    for (int l = 0; l < MOE_MAX_LAYERS; ++l)
+        if (g_layers[l].init && g_layers[l].device_mode && g_layers[l].dtab) ts.t[ts.n++] = g_layers[l].dtab;
+    return ts;
 }
 hipStream_t g_compute = nullptr;             // caller's stream (null stream by default)
 hipStream_t g_copy = nullptr;
@@ -610,8 +617,14 @@ void c_layer_reset_cache(int layer) {
     if (layer == 1) {                         // layer 1's reset restarts the token numbering
         g_token_seq = 0;
         g_cur_token = -1;
+        L.tab.acct_token = -1;
+        L.tab.acct_seq = 0;
     }
-    push_table(L);
+    if (push_table(L)) return;
+    if (layer == 1) {                         // ... of the device-driven tables too
+        const TableSet ts = device_tables();
+        if (ts.n && launch_acct_ctl(ts, 3, g_compute) == 0) (void)hipStreamSynchronize(g_compute);
+    }
 }
 
 void c_layer_reset_stats(int layer) {
@@ -767,7 +780,7 @@ void c_layer_set_lru_state(int layer, const int32_t* eids, const int32_t* slots,
         }
     if (pull_table(L)) return;
     slot_host::set_state(&L.tab, eids, slots, n, add_req, add_hits, add_miss);
-    for (int i = 0; i < n; ++i) L.evicted_at[eids[i]] = -1;
+    for (int i = 0; i < n; ++i) L.tab.evicted_at[eids[i]] = -1;
     push_table(L);
 }
 
@@ -864,24 +877,50 @@ int c_layer_decode_step_sched(int layer, const int32_t* eids, int k, const int32
 
 void c_layer_get_split_inds(int layer, uint32_t* out_hit_slots, uint32_t* out_miss_slots, int32_t* out_inv_order) {
     if (!valid_layer(layer)) return;
-    const SplitLists& S = g_split[layer];
+    LayerState& L = g_layers[layer];
+    if (L.device_mode && pull_table(L)) return;
+    const SplitLists& S = L.device_mode ? L.tab.split : g_split[layer];
     if (S.n_hit > 0 && out_hit_slots) memcpy(out_hit_slots, S.hit, (size_t)S.n_hit * sizeof(uint32_t));
     if (S.n_miss > 0 && out_miss_slots) memcpy(out_miss_slots, S.miss, (size_t)S.n_miss * sizeof(uint32_t));
     if (S.k > 0 && out_inv_order) memcpy(out_inv_order, S.inv, (size_t)S.k * sizeof(int32_t));
 }
 
+// Device-driven tables count on the device: these queue small control kernels on the compute
+// stream (so a captured token replays them), and c_end_decode_token adds the tables' counters.
 void c_set_io_accounting(int enabled) {
     g_acct_on = enabled != 0;
     if (!g_acct_on) g_cur_token = -1;
+    const TableSet ts = device_tables();
+    if (ts.n) (void)launch_acct_ctl(ts, g_acct_on ? 1 : 0, g_compute);
 }
 
 void c_begin_decode_token(int token_idx) {
     (void)token_idx;                          // tokens are numbered by the library, as in the reference
     g_cur_token = g_token_seq++;
     memset(g_tok, 0, sizeof(g_tok));
+    const TableSet ts = device_tables();
+    if (ts.n) (void)launch_acct_ctl(ts, 2, g_compute);
 }
 
-void c_end_decode_token(uint64_t* out10) { memcpy(out10, g_tok, sizeof(g_tok)); }
+void c_end_decode_token(uint64_t* out10) {
+    memcpy(out10, g_tok, sizeof(g_tok));
+    const TableSet ts = device_tables();
+    if (!ts.n) return;
+    static uint64_t* sums = nullptr;          // 10 device counters, kept until the process ends
+    if (!sums && hipMalloc((void**)&sums, 10 * sizeof(uint64_t)) != hipSuccess) {
+        moe_set_error("end_decode_token: no device memory for the sums");
+        sums = nullptr;
+        return;
+    }
+    uint64_t dev[10];
+    if (launch_acct_sum(ts, sums, g_compute) ||
+        hipMemcpyAsync(dev, sums, sizeof(dev), hipMemcpyDeviceToHost, g_compute) != hipSuccess ||
+        hipStreamSynchronize(g_compute) != hipSuccess) {
+        moe_set_error("end_decode_token: reading the device tables' counters failed");
+        return;
+    }
+    for (int i = 0; i < 10; ++i) out10[i] += dev[i];
+}
 
 uint64_t c_get_native_buffer_bytes(void) {
     uint64_t b = sizeof(g_layers) + sizeof(g_split);
@@ -896,7 +935,7 @@ int c_layer_set_sched(int layer, int on) {
     if (!valid_layer(layer) || !g_layers[layer].init) { moe_set_error("set_sched: bad layer %d", layer); return -1; }
     LayerState& L = g_layers[layer];
     if (pull_table(L)) return -1;
-    L.tab.sched = on ? 1 : 0;
+    L.tab.sched = on & 3;                     // bit 0 the variant, bit 1 device split lists
     return push_table(L);
 }
 
@@ -925,6 +964,14 @@ int c_layer_set_device_mode(int layer, int on) {
             if (filefeed::attach(layer, io)) return -1;
         }
         if (!L.dtab) HIP_TRY(hipMalloc((void**)&L.dtab, sizeof(SlotTable)));
+        // per-token accounting now runs on the device: the open token, the switch, and the bytes
+        // a copied expert moves (none for an accounting-only layer)
+        L.tab.acct_on = g_acct_on ? 1 : 0;
+        L.tab.acct_token = g_cur_token;
+        L.tab.acct_seq = g_token_seq;
+        L.tab.stage_bytes = 0;
+        for (int t = 0; t < MOE_NUM_TENSORS; ++t)
+            if (L.row_bytes[t] && L.src[t] && L.dst[t]) L.tab.stage_bytes += L.row_bytes[t];
         L.device_mode = true;
         return push_table(L);
     }

@@ -92,6 +92,14 @@ static inline __host__ __device__ CbLayout cb_layout(int hidden, int inter) {
     return L;
 }
 
+// Hit/miss split of one scheduler step (c_layer_get_split_inds): slots of the ids that were
+// resident, slots of the missed ids (both in id order), and each id's position in hits ++ misses.
+struct SplitLists {
+    uint32_t hit[MOE_MAX_K], miss[MOE_MAX_K];
+    int32_t inv[MOE_MAX_K];
+    int32_t n_hit, n_miss, k;
+};
+
 // Per-layer slot table.  The reference keeps a doubly linked list over slots
 // (mlx-qwen38/expert_io.c:43-91); this keeps the same order as recency stamps: a resident
 // slot carries stamp > 0, the LRU end is the smallest stamp, moving a slot to the MRU end
@@ -124,20 +132,41 @@ struct SlotTable {
     int32_t pf_copy_eid[MOE_MAX_PREFETCH];
     int32_t pf_copy_slot[MOE_MAX_PREFETCH];
     int32_t status;                     // 0 ok; nonzero: rejected input (device kernels)
-    int32_t sched;                      // device-driven ops follow the scheduler variant
-                                        // (cpp/third_party/expert_io.c:1094-1394) when nonzero
+    int32_t sched;                      // bit 0: device-driven ops follow the scheduler variant
+                                        // (cpp/third_party/expert_io.c:1094-1394); bit 1: they
+                                        // record the step's split lists (split below)
     int32_t io_fault;                   // sticky: 16 a file read failed, 17 a staging wait timed
                                         // out (the slot kept its old bytes); set by the file
                                         // tier's staging kernel, cleared only by reset_cache
+    // Per-token accounting (cpp/third_party/expert_io.c:98-111,1002-1038).  Host tables keep the
+    // open token and the counters in the library; device-driven tables keep them here, so the
+    // table kernels can count without the host: acct_on / acct_token / acct_seq set by control
+    // kernels on the compute stream (c_set_io_accounting, c_begin_decode_token, layer 1's
+    // reset), acct[10] the table's share
+    // of the open token's counters, stage_bytes the bytes one copied expert moves (0 for an
+    // accounting-only layer).  evicted_at (both kinds): per expert, the token of its last
+    // eviction, -1 none.
+    int32_t acct_on;
+    int32_t acct_token;                 // -1: no token open
+    int32_t acct_seq;                   // the next token's number
+    int32_t acct_pad;
+    uint64_t stage_bytes;
+    uint64_t acct[10];
+    int32_t evicted_at[MOE_NUM_EXPERTS];
+    // Device-driven tables in scheduler mode with sched bit 1: the split of the last step that
+    // had 0 < misses < k (cpp/third_party/expert_io.c:1062-1092 keeps the last one the same way).
+    SplitLists split;
 };
 
-// Hit/miss split of one scheduler step (c_layer_get_split_inds): slots of the ids that were
-// resident, slots of the missed ids (both in id order), and each id's position in hits ++ misses.
-struct SplitLists {
-    uint32_t hit[MOE_MAX_K], miss[MOE_MAX_K];
-    int32_t inv[MOE_MAX_K];
-    int32_t n_hit, n_miss, k;
+// A set of device tables for the accounting control and gather kernels.
+struct TableSet {
+    SlotTable* t[MOE_MAX_LAYERS];
+    int n;
 };
+int launch_acct_ctl(const TableSet& ts, int mode, hipStream_t s);        // 0 off, 1 on, 2 begin a token,
+                                                                          // 3 restart the token numbering
+int launch_acct_sum(const TableSet& ts, uint64_t* out10, hipStream_t s);  // out10 = sum of the tables' acct
+
 
 // Stats word indices (same order as c_layer_get_stats, expert_io.c:791-812).
 enum {

@@ -145,7 +145,48 @@ __global__ void k_split_lists(SplitLists a, const __half* __restrict__ scores, u
     scores_out[dst] = scores[i];
 }
 
+// Accounting control of the device-driven tables, one thread per table: 0 off (no token open),
+// 1 on, 2 open the next token (its counters start at zero), 3 restart the token numbering.  The
+// host keeps the same state for its own tables (capi.hip), so both number tokens alike.
+__global__ void k_acct_ctl(TableSet ts, int mode) {
+    const int i = threadIdx.x;
+    if (i >= ts.n) return;
+    SlotTable* t = ts.t[i];
+    if (mode == 0) { t->acct_on = 0; t->acct_token = -1; }
+    else if (mode == 1) t->acct_on = 1;
+    else if (mode == 2) {
+        t->acct_token = t->acct_seq++;
+        for (int c = 0; c < 10; ++c) t->acct[c] = 0;
+    } else { t->acct_seq = 0; t->acct_token = -1; }
+}
+
+// The open token's counters summed over the tables (lane c: counter c).
+__global__ void k_acct_sum(TableSet ts, uint64_t* __restrict__ out10) {
+    const int c = threadIdx.x;
+    if (c >= 10) return;
+    uint64_t v = 0;
+    for (int i = 0; i < ts.n; ++i) v += ts.t[i]->acct[c];
+    out10[c] = v;
+}
+
 }  // namespace
+
+int launch_acct_ctl(const TableSet& ts, int mode, hipStream_t s) {
+    if (ts.n <= 0 || ts.n > MOE_MAX_LAYERS || mode < 0 || mode > 3) {
+        moe_set_error("acct_ctl: %d tables, mode %d", ts.n, mode);
+        return -1;
+    }
+    hipLaunchKernelGGL(k_acct_ctl, dim3(1), dim3(64), 0, s, ts, mode);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int launch_acct_sum(const TableSet& ts, uint64_t* out10, hipStream_t s) {
+    if (ts.n <= 0 || ts.n > MOE_MAX_LAYERS || !out10) { moe_set_error("acct_sum: %d tables", ts.n); return -1; }
+    hipLaunchKernelGGL(k_acct_sum, dim3(1), dim3(64), 0, s, ts, out10);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
 
 int launch_slot_step(SlotTable* t, const uint32_t* ids, int k, uint32_t* slot_inds, hipStream_t s) {
     if (k <= 0 || k > MOE_MAX_K) { moe_set_error("slot_step: k=%d out of range", k); return -1; }

@@ -8,10 +8,15 @@
 // slot gives it the next clock value.  Each operation takes the table as fetch_table read it
 // (one round trip for all of it), decides on a copy in LDS (~4.5 KB), and writes it back.
 //
-// With t->sched set, the scheduler variant of mlx-qwen38/cpp/third_party/expert_io.c:1094-1394
-// applies: the step's victim choice also protects the experts the last prefetch fetched
-// (1141-1146), the prefetch skips repeated predictions (1311-1322) and does nothing at all when
-// max_fetch <= 0 (1288-1290).
+// With bit 0 of t->sched set, the scheduler variant of mlx-qwen38/cpp/third_party/expert_io.c:
+// 1094-1394 applies: the step's victim choice also protects the experts the last prefetch
+// fetched (1141-1146), the prefetch skips repeated predictions (1311-1322) and does nothing at
+// all when max_fetch <= 0 (1288-1290).  With bit 1 set, a step with 0 < misses < k records its
+// hit/miss split lists in t->split (1062-1092).
+//
+// With t->acct_on set, the operations count the open token's accounting (expert_io.c:98-111,
+// the same counters as the host table's Acct): hits, misses, prefetch loads / hits / waste,
+// reloads within 16 and 64 tokens of the expert's eviction, and the bytes staged, into t->acct.
 //
 // All synchronisation is wave-level: a wave's LDS accesses complete in program order, so a
 // compiler fence at wavefront scope is all that separates one step from the next.  That lets
@@ -42,6 +47,10 @@ struct LdsTable {
     int32_t n_list;
 };
 
+// Index of each counter in SlotTable::acct (the order of c_end_decode_token's 10 words).
+enum { AC_DEV_LRU_HIT = 0, AC_DEV_MISS, AC_DEV_PF_LOADS, AC_DEV_PF_HITS, AC_DEV_PF_WASTED, AC_DEV_DEM_RE16,
+       AC_DEV_DEM_RE64, AC_DEV_PF_RE16, AC_DEV_PF_RE64, AC_DEV_BYTES };
+
 __device__ __forceinline__ bool bit(const uint32_t* bm, int e) { return (bm[e >> 5] >> (e & 31)) & 1u; }
 
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
@@ -63,7 +72,8 @@ struct TabRegs {
     uint4 so, eo, s0, s1;
     int4 hdr;                  // capacity, n_free, clock, snap_valid
     int32_t sched;
-    uint64_t ebytes;
+    int32_t acct_on, acct_token;
+    uint64_t ebytes, stage_bytes;
     uint64_t stat;             // stats[lane] for lane < 18
     uint32_t sr, sp, sf;       // snapshot bitmap words [lane & 15]
 };
@@ -80,7 +90,10 @@ __device__ __forceinline__ TabRegs fetch_table(const SlotTable* t, int lane) {
     r.s0 = reinterpret_cast<const uint4*>(t->stamp)[2 * lane];
     r.s1 = reinterpret_cast<const uint4*>(t->stamp)[2 * lane + 1];
     r.sched = t->sched;
+    r.acct_on = t->acct_on;
+    r.acct_token = t->acct_token;
     r.ebytes = t->expert_bytes;
+    r.stage_bytes = t->stage_bytes;
     r.stat = t->stats[lane < 18 ? lane : 0];
     r.sr = reinterpret_cast<const uint32_t*>(t->snap_resident)[lane & 15];
     r.sp = reinterpret_cast<const uint32_t*>(t->snap_pred)[lane & 15];
@@ -160,9 +173,10 @@ __device__ inline void renorm(int cap, LdsTable& L, int lane, uint32_t& clock) {
 
 // One victim for a slot allocation (uniform across the wave). Returns the slot.  When every
 // resident expert is protected, the oldest one not in `spare` (may be null) goes before the
-// oldest outright (the host table's rule, slot_table_host.h).
+// oldest outright (the host table's rule, slot_table_host.h).  evlog (null when not counting)
+// gets the open token's number at the evicted expert.
 __device__ inline int take_slot(const SlotTable* t, int cap, LdsTable& L, int lane, int& n_free,
-                                const uint32_t* protect, const uint32_t* spare = nullptr) {
+                                const uint32_t* protect, const uint32_t* spare, int32_t* evlog, int token) {
     if (n_free > 0) {
         --n_free;
         return t->free_stack[n_free];
@@ -185,7 +199,10 @@ __device__ inline int take_slot(const SlotTable* t, int cap, LdsTable& L, int la
     wave_sync();
     if (lane == 0 && pick != ~0ull) {
         int e = L.eid_of[s];
-        if (e >= 0) L.slot_of[e] = -1;
+        if (e >= 0) {
+            L.slot_of[e] = -1;
+            if (evlog) evlog[e] = token;
+        }
         L.eid_of[s] = -1;
         L.stamp[s] = 0;
     }
@@ -223,6 +240,22 @@ __device__ inline void count_runs(LdsTable& L, const int32_t* e, int n) {
     for (int i = 1; i < n; ++i) runs += (v[i] != v[i - 1] + 1);
     L.stats[ST_UNCOAL] += (uint64_t)n * MOE_NUM_TENSORS;
     L.stats[ST_COAL] += (uint64_t)runs * MOE_NUM_TENSORS;
+}
+
+// Reload counting of expert_io.c:98-111 for the experts that lanes with `mine` set are about to
+// load: one whose last eviction was at most 16 / 64 tokens ago counts as a reload; its mark is
+// cleared.  Called only with a token open.  Returns the two counts (uniform).
+__device__ inline int2 note_reloads(int32_t* __restrict__ evicted_at, bool mine, int e, int token) {
+    bool r16 = false, r64 = false;
+    if (mine) {
+        const int32_t ev = evicted_at[e];
+        if (ev >= 0 && token >= ev) {
+            r16 = token - ev <= 16;
+            r64 = token - ev <= 64;
+        }
+        evicted_at[e] = -1;
+    }
+    return make_int2(__popcll(__ballot(r16)), __popcll(__ballot(r64)));
 }
 
 // Decode step of expert_io.c:583-685 for k ids (one wave).  r holds the table as fetch_table
@@ -298,13 +331,40 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
         L.list_e[rank] = e;
     }
     wave_sync();
-    if (r.sched && snap && lane < 16)        // in-flight prefetched experts are protected too
+    if ((r.sched & 1) && snap && lane < 16)  // in-flight prefetched experts are protected too
         L.protect[lane] |= r.sf;
     wave_sync();
 
+    // accounting: the misses' reloads are counted before the victims are marked (the two sets
+    // are disjoint: a victim is resident, a miss is not)
+    const bool counting = r.acct_on != 0;
+    const int token = r.acct_token;
+    int32_t* evlog = (counting && token >= 0) ? t->evicted_at : nullptr;
+    if (counting) {
+        const int2 re = evlog ? note_reloads(t->evicted_at, miss, e, token) : make_int2(0, 0);
+        uint32_t fetched = 0;
+        if (snap) {
+            fetched = lane < 16 ? __popc(r.sf) : 0u;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) fetched += __shfl_xor(fetched, o, 64);
+        }
+        if (lane == 0) {
+            uint64_t* a = t->acct;
+            a[AC_DEV_LRU_HIT] += (uint64_t)n_lru;
+            a[AC_DEV_MISS] += (uint64_t)n_miss;
+            if (snap) {
+                a[AC_DEV_PF_HITS] += (uint64_t)n_pref;
+                if (fetched >= (uint32_t)n_pref) a[AC_DEV_PF_WASTED] += fetched - (uint32_t)n_pref;
+            }
+            a[AC_DEV_DEM_RE16] += (uint64_t)re.x;
+            a[AC_DEV_DEM_RE64] += (uint64_t)re.y;
+            a[AC_DEV_BYTES] += (uint64_t)n_miss * r.stage_bytes;
+        }
+    }
+
     for (int r = 0; r < n_miss; ++r) {
         int me = L.list_e[r];
-        int s = take_slot(t, cap, L, lane, n_free, L.protect, L.spare);
+        int s = take_slot(t, cap, L, lane, n_free, L.protect, L.spare, evlog, token);
         bind(L, lane, me, s, clock);
         if (lane == 0) L.list_s[r] = s;
     }
@@ -316,13 +376,31 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
     wave_sync();
 
     // refresh every id in order; for a repeated id only its last occurrence counts
+    int my_slot = -1;
     if (e >= 0) {                          // ids are distinct: refresh in id order
-        int my_slot = L.slot_of[e];
+        my_slot = L.slot_of[e];
         if (my_slot >= 0) L.stamp[my_slot] = clock + 1 + lane;
         slot_inds[lane] = (uint32_t)my_slot;
     }
     clock += (uint32_t)k;
     wave_sync();
+
+    if ((r.sched & 2) && n_miss > 0 && n_miss < k) {   // the split lists, ids in order
+        const uint64_t below = (1ull << lane) - 1;
+        const uint64_t hit_mask = __ballot(resident);
+        const int n_hit = k - n_miss;
+        SplitLists& S = t->split;
+        if (resident) {
+            const int h = __popcll(hit_mask & below);
+            S.hit[h] = (uint32_t)my_slot;
+            S.inv[lane] = h;
+        } else if (miss) {
+            const int m = __popcll(miss_mask & below);
+            S.miss[m] = (uint32_t)my_slot;
+            S.inv[lane] = n_hit + m;
+        }
+        if (lane == 0) { S.n_hit = n_hit; S.n_miss = n_miss; S.k = k; }
+    }
 
     store_table(t, L, lane);
     if (lane == 0) {
@@ -341,7 +419,7 @@ __device__ inline void dev_slot_step(SlotTable* __restrict__ t, LdsTable& L, con
 // fetch_table read it; preds is in LDS.
 __device__ inline void dev_slot_prefetch(SlotTable* __restrict__ t, LdsTable& L, const TabRegs& r, const int32_t* preds,
                                          int m, int max_fetch, int lane) {
-    const bool sched = r.sched != 0;
+    const bool sched = (r.sched & 1) != 0;
     if (sched && max_fetch <= 0) {            // the scheduler variant prefetches nothing
         if (lane == 0) { t->pf_n_copy = 0; t->status = 0; }
         return;
@@ -380,9 +458,23 @@ __device__ inline void dev_slot_prefetch(SlotTable* __restrict__ t, LdsTable& L,
     }
     int32_t order_e[MOE_MAX_PREFETCH];
     for (int i = 0; i < np; ++i) order_e[i] = L.list_e[np - 1 - i];   // reverse rank order
+    const bool counting = r.acct_on != 0;
+    const int token = r.acct_token;
+    int32_t* evlog = (counting && token >= 0) ? t->evicted_at : nullptr;
+    if (counting) {                           // reloads first: the picks are not resident
+        const int2 re = evlog ? note_reloads(t->evicted_at, lane < np, lane < np ? L.list_e[lane] : 0, token)
+                              : make_int2(0, 0);
+        if (lane == 0) {
+            uint64_t* a = t->acct;
+            a[AC_DEV_PF_LOADS] += (uint64_t)np;
+            a[AC_DEV_PF_RE16] += (uint64_t)re.x;
+            a[AC_DEV_PF_RE64] += (uint64_t)re.y;
+            a[AC_DEV_BYTES] += (uint64_t)np * r.stage_bytes;
+        }
+    }
     wave_sync();
     for (int i = 0; i < np; ++i) {
-        int s = take_slot(t, cap, L, lane, n_free, L.protect);
+        int s = take_slot(t, cap, L, lane, n_free, L.protect, nullptr, evlog, token);
         bind(L, lane, order_e[i], s, clock);
         if (lane == 0) { L.list_e[i] = order_e[i]; L.list_s[i] = s; }
     }

@@ -73,6 +73,7 @@ static inline void reset_cache(SlotTable* t) {
     t->pf_n_copy = 0;
     t->status = 0;
     t->io_fault = 0;
+    for (int i = 0; i < MOE_NUM_EXPERTS; ++i) t->evicted_at[i] = -1;
 }
 
 static inline void reset_stats(SlotTable* t) { memset(t->stats, 0, sizeof(t->stats)); }
@@ -81,6 +82,7 @@ static inline void init(SlotTable* t, int capacity, uint64_t expert_bytes) {
     memset(t, 0, sizeof(*t));
     t->capacity = capacity;
     t->expert_bytes = expert_bytes;
+    t->acct_token = -1;
     reset_cache(t);
 }
 

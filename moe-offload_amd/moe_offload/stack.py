@@ -206,6 +206,8 @@ class DecodeStack:
         self.ev_demand = [torch.cuda.Event() for _ in range(c.n_layers)]
         self.graph = None
         self._host_sel = []
+        self.token_io = False
+        self.last_token_io: list[int] | None = None
         if c.native_host and self.mode == "host" and not c.resident and self.p1 is None and not c.sched:
             self._init_native()
 
@@ -249,6 +251,21 @@ class DecodeStack:
             torch.cuda.synchronize()                 # no staging kernel of an earlier token still runs
             self.L.c_io_clear_fault()
         _lib.check_error("reset_cache")
+
+    def set_token_accounting(self, on: bool):
+        """Per-token I/O accounting (cpp/third_party/expert_io.c:98-111,1002-1038): with it on,
+        decode_token opens a token (c_begin_decode_token) before its work and reads the token's 10
+        counters (c_end_decode_token: LRU hits, misses, prefetch loads / hits / wasted, demand and
+        prefetch reloads within 16 / 64 tokens of the eviction, bytes copied) into last_token_io
+        after it, at the cost of one host synchronisation per token.  Device-driven tables count
+        on the GPU, host tables in the library, with the same rules.  The library's accounting
+        switch and token numbering are process-wide, as the reference's are."""
+        if self.cfg.resident or self.p1 is not None:
+            raise ValueError("per-token accounting needs the expert_io.c slot tables (not resident, io='exact')")
+        self.L.c_set_io_accounting(1 if on else 0)
+        _lib.check_error("set_io_accounting")
+        self.token_io = bool(on)
+        self.last_token_io = None
 
     def reset_stats(self):
         if self.cfg.resident:
@@ -555,6 +572,8 @@ class DecodeStack:
         self.check_io()                              # a fault of an earlier token
         if x0 is not None:
             self.xs[0].copy_(x0)
+        if self.token_io:
+            self.L.c_begin_decode_token(0)
         if self.mode == "device" or self.cfg.resident:
             if self.graph is not None:
                 self.graph.replay()
@@ -571,6 +590,11 @@ class DecodeStack:
                 self.pred[:, :self.pred_host.shape[1]].copy_(torch.from_numpy(self.pred_host), non_blocking=True)
         else:
             self.decode_token_host()
+        if self.token_io:
+            out = (ctypes.c_uint64 * 10)()
+            self.L.c_end_decode_token(out)           # waits for the token's table work
+            _lib.check_error("end_decode_token")
+            self.last_token_io = list(out)
         return self.xs[self.cfg.n_layers]
 
     def table_status(self) -> dict[int, int]:

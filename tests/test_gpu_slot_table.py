@@ -82,40 +82,60 @@ def test_device_table_replays_reference_traces(L, lru_traces):
 class DeviceSched:
     """Device-driven tables in scheduler mode, driven with the golden scheduler traces: the
     step and the next layer's prefetch of a c_layer_decode_step_sched call run as the device
-    table kernels (published ops of the mixed scenario with scheduler mode switched off).
-    Miss counts are read as the change of the layer's demand-miss counter."""
+    table kernels (published ops of the mixed scenario with scheduler mode switched off).  A
+    step whose call carries the SPLIT flag runs with table mode bit 1, so the kernel records the
+    split lists; accounting and token bracketing go through the same c_set_io_accounting /
+    c_begin_decode_token / c_end_decode_token calls as host tables, whose counters the device
+    tables keep themselves.  Miss counts are read as the change of the layer's demand-miss
+    counter.  Layers keep the trace's numbers: layer 1's cache reset restarts the token
+    numbering, as the trace expects."""
 
-    def __init__(self, lib, base):
-        self.L, self.base = lib, base
-        self.slots, self.misses = {}, {}
+    def __init__(self, lib):
+        from sched_replay import TokenMixin
+        self._tokens = TokenMixin()
+        self.L = lib
+        self.slots, self.misses, self.mode = {}, {}, {}
         self.stream = torch.cuda.current_stream().cuda_stream
 
     def begin_if_needed(self):
-        pass
+        if not self._tokens._open:
+            self.L.c_begin_decode_token(0)
+            self._tokens._open = True
 
     def token_done(self):
-        pass
+        self._tokens._open = False
+
+    def end(self):
+        o = (ctypes.c_uint64 * 10)()
+        self.L.c_end_decode_token(o)
+        _check(self.L)
+        return list(o)
 
     def init(self, l, cap):
         self.slots[l] = torch.zeros(16, dtype=torch.int32, device="cuda")
-        _init_layer(self.L, self.base + l, cap, slot_ptr=self.slots[l].data_ptr())
-        assert self.L.c_layer_set_device_mode(self.base + l, 1) == 0
-        assert self.L.c_layer_set_sched(self.base + l, 1) == 0
+        _init_layer(self.L, l, cap, slot_ptr=self.slots[l].data_ptr())
+        assert self.L.c_layer_set_device_mode(l, 1) == 0
+        self._set_mode(l, 1)
         self.misses[l] = 0
 
+    def _set_mode(self, l, mode):
+        if self.mode.get(l) != mode:
+            assert self.L.c_layer_set_sched(l, mode) == 0
+            self.mode[l] = mode
+
     def reset_stats(self, l):
-        self.L.c_layer_reset_stats(self.base + l)
+        self.L.c_layer_reset_stats(l)
         self.misses[l] = 0
 
     def reset_cache(self, l):
-        self.L.c_layer_reset_cache(self.base + l)
+        self.L.c_layer_reset_cache(l)
 
     def accounting(self, on):
-        pass
+        self.L.c_set_io_accounting(1 if on else 0)
 
     def _step(self, l, ids):
         t = torch.tensor(ids, dtype=torch.int32, device="cuda")
-        assert self.L.c_layer_step_decode_dev(self.base + l, t.data_ptr(), len(ids), 0, self.stream) == 0
+        assert self.L.c_layer_step_decode_dev(l, t.data_ptr(), len(ids), 0, self.stream) == 0
         _check(self.L)
         m = self.stats(l)[3]
         n, self.misses[l] = m - self.misses[l], m
@@ -123,20 +143,24 @@ class DeviceSched:
 
     def _prefetch(self, l, preds, cap):
         p = torch.tensor(preds, dtype=torch.int32, device="cuda")
-        assert self.L.c_layer_start_prefetch_dev(self.base + l, p.data_ptr(), len(preds), cap, 0, self.stream) == 0
+        assert self.L.c_layer_start_prefetch_dev(l, p.data_ptr(), len(preds), cap, 0, self.stream) == 0
         _check(self.L)
 
     def sched(self, l, ids, preds, nxt, cap, flags):
-        n, slots = (self._step(l, ids) if (l > 0 and ids) else (0, []))
+        from sched_replay import SPLIT
+        if l > 0 and ids:
+            self._set_mode(l, 1 | (2 if flags & SPLIT else 0))
+            n, slots = self._step(l, ids)
+        else:
+            n, slots = 0, []
         if not (flags & 2) and nxt > 0 and preds:
+            self._set_mode(nxt, self.mode.get(nxt, 1) | 1)
             self._prefetch(nxt, preds, cap)
         return n, slots
 
     def _published(self, l, fn):
-        assert self.L.c_layer_set_sched(self.base + l, 0) == 0
-        out = fn()
-        assert self.L.c_layer_set_sched(self.base + l, 1) == 0
-        return out
+        self._set_mode(l, 0)
+        return fn()
 
     def step(self, l, ids):
         return self._published(l, lambda: self._step(l, ids))
@@ -145,17 +169,22 @@ class DeviceSched:
         self._published(l, lambda: self._prefetch(l, preds, cap))
 
     def stats(self, l):
-        return _stats(self.L, self.base + l)
+        return _stats(self.L, l)
 
     def state(self, l):
-        return _state(self.L, self.base + l)
+        return _state(self.L, l)
 
     def set_state(self, l, e, s, add):
-        self.L.c_layer_set_lru_state(self.base + l, (ctypes.c_int32 * max(1, len(e)))(*e),
+        self.L.c_layer_set_lru_state(l, (ctypes.c_int32 * max(1, len(e)))(*e),
                                      (ctypes.c_int32 * max(1, len(s)))(*s), len(e), *add)
 
     def split(self, l):
-        raise AssertionError("split lists are not compared for device tables")
+        h = (ctypes.c_uint32 * 16)(*([0xFFFFFFFF] * 16))
+        m = (ctypes.c_uint32 * 16)(*([0xFFFFFFFF] * 16))
+        inv = (ctypes.c_int32 * 16)(*([-7] * 16))
+        self.L.c_layer_get_split_inds(l, h, m, inv)
+        _check(self.L)
+        return [[v for v in h if v != 0xFFFFFFFF], [v for v in m if v != 0xFFFFFFFF], [v for v in inv if v != -7]]
 
     def totals(self, n_layers):
         t = [0] * 6
@@ -167,11 +196,17 @@ class DeviceSched:
 
 
 def test_device_tables_replay_reference_scheduler_traces(L):
-    """Scheduler-mode device tables (decisions only: split lists and per-token accounting are
-    host-path features) against the reference's cpp/third_party/expert_io.c traces."""
+    """Scheduler-mode device tables against the reference's cpp/third_party/expert_io.c traces:
+    decisions, counters, split lists and per-token accounting."""
     from sched_replay import load, replay
-    for i, sc in enumerate(load()["scenarios"]):
-        assert replay(sc, DeviceSched(L, 10 * i), check_split=False, check_tokens=False) > 50, sc["name"]
+    try:
+        for sc in load()["scenarios"]:
+            assert replay(sc, DeviceSched(L)) > 50, sc["name"]
+    finally:
+        L.c_set_io_accounting(0)
+        for l in range(1, 8):                 # back to host tables for the tests that follow
+            L.c_layer_init(l, -1, 16, None, None, None, 0)
+        torch.cuda.synchronize()
 
 
 def test_device_table_rejects_bad_ids(L):

@@ -24,7 +24,7 @@ pytestmark = pytest.mark.gpu
 N_LAYERS, N_TOK = 6, 12
 
 
-def run_stack(mode, layer_base, graph=False, fused=True, native=False):
+def run_stack(mode, layer_base, graph=False, fused=True, native=False, token_io=False):
     from moe_offload.stack import DecodeStack, StackConfig
     cfg = StackConfig(n_layers=N_LAYERS, seed=5, layer_base=layer_base, fused_tables=fused, native_host=native)
     st = DecodeStack(cfg, mode=mode)
@@ -34,13 +34,19 @@ def run_stack(mode, layer_base, graph=False, fused=True, native=False):
     rec = []
     if graph:
         st.capture_graph()
-    for t in range(N_TOK):
-        st.decode_token(xs[t])
-        torch.cuda.synchronize()
-        rec.append({"ids": st.ids.cpu().numpy().copy(), "scores": st.scores.cpu().numpy().copy(),
-                    "pred": st.pred.cpu().numpy().copy(), "xs": st.xs.cpu().numpy().copy(),
-                    "hs": st.hs.cpu().numpy().copy(),
-                    "slots": {l: st.slot_inds[l][:cfg.top_k].cpu().numpy().copy() for l in range(1, N_LAYERS)}})
+    if token_io:
+        st.set_token_accounting(True)
+    try:
+        for t in range(N_TOK):
+            st.decode_token(xs[t])
+            torch.cuda.synchronize()
+            rec.append({"ids": st.ids.cpu().numpy().copy(), "scores": st.scores.cpu().numpy().copy(),
+                        "pred": st.pred.cpu().numpy().copy(), "xs": st.xs.cpu().numpy().copy(),
+                        "hs": st.hs.cpu().numpy().copy(), "io": st.last_token_io,
+                        "slots": {l: st.slot_inds[l][:cfg.top_k].cpu().numpy().copy() for l in range(1, N_LAYERS)}})
+    finally:
+        if token_io:
+            st.set_token_accounting(False)
     stats = {l: st.layer_stats(l) for l in range(1, N_LAYERS)}
     return st, rec, stats
 
@@ -166,3 +172,29 @@ def test_native_host_runner_matches_python_host_driver(runs):
         assert ns == hs
     finally:
         st.close()
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_token_accounting_on_device_tables_matches_host_tables(runs, graph):
+    """Per-token I/O accounting (cpp/third_party/expert_io.c:98-111,1002-1038) counted by the
+    device-driven tables' kernels equals the host tables' counts for the same token stream
+    (eager, and with the token replayed from a HIP graph): every token's 10 counters.  Their sums
+    tie to the layers' own counters: LRU hits, prefetch hits and misses are the layers' three
+    classes of requests, and the bytes = (misses + prefetch loads) x blob bytes."""
+    (_, d, ds), _ = runs
+    dst, drec, dstats = run_stack("device", 50, graph=graph, token_io=True)
+    hst, hrec, hstats = run_stack("host", 57, token_io=True)
+    try:
+        assert dstats == ds == hstats                 # the same decisions as without accounting
+        for t in range(N_TOK):
+            assert np.array_equal(drec[t]["xs"], d[t]["xs"]), f"token {t}"
+            assert drec[t]["io"] == hrec[t]["io"], f"token {t}: {drec[t]['io']} vs {hrec[t]['io']}"
+        tot = np.array([r["io"] for r in drec], dtype=np.int64).sum(axis=0)
+        col = lambda i: sum(v[i] for v in dstats.values())   # noqa: E731
+        assert (tot[0], tot[3], tot[1]) == (col(1), col(2), col(3))
+        assert tot[0] + tot[3] + tot[1] == col(0)
+        assert tot[9] == (tot[1] + tot[2]) * dst.blob_bytes
+        assert tot[1] > 0 and tot[2] > 0              # the stream does miss and prefetch
+    finally:
+        dst.close()
+        hst.close()
