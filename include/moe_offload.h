@@ -155,6 +155,15 @@ uint64_t moe_router_q8_workspace_bytes(int n_rows);
 int moe_router_q8(const void* x, const uint32_t* codes, const void* scales, const void* biases, int hidden,
                   int n_rows, int group, int k, int m, void* workspace, uint32_t* ids_out, void* scores_out,
                   int32_t* pred_out, void* logits_out, void* stream);
+/* moe_rmsnorm_bf16 + moe_router_q8 in one launch (no reference counterpart: the glue is the
+ * builder's): every block normalises h_in (fp32 [hidden], norm_w bf16 or null) with
+ * moe_rmsnorm_bf16's arithmetic while its weight loads fly and multiplies the bf16 result; block 0
+ * also writes x_bf16_out / x_f16_out (either may be null), bit-identical to moe_rmsnorm_bf16's.
+ * Other arguments, modes and outputs as moe_router_q8; hidden a multiple of 64 up to 4096. */
+int moe_router_q8_norm(const float* h_in, const void* norm_w, float eps, void* x_bf16_out, void* x_f16_out,
+                       const uint32_t* codes, const void* scales, const void* biases, int hidden, int n_rows,
+                       int group, int k, int m, void* workspace, uint32_t* ids_out, void* scores_out,
+                       int32_t* pred_out, void* logits_out, void* stream);
 /* No counterpart in the reference.  moe_router for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc): no workspace argument;
  * the logits and the arrival counter live in a static device array of the library (8,448 bytes

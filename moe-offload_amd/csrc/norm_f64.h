@@ -81,9 +81,11 @@ __device__ inline void finish(const NormIn& in, bool has_w, float eps, int hidde
 // The checkpoint form (bf16 model): the same sum of squares and normalisation with bf16 norm
 // weights, x rounded once from fp64 to bf16 (x_bf16, the 8-bit router's input) and that bf16 value
 // converted to fp16 (x_f16, the expert kernels' input: exact in fp16's normal range).  Every
-// thread writes its own elements; one __syncthreads.
+// thread writes its own elements to whichever outputs are given: x_bf16 / x_f16 in global memory,
+// xf (LDS, [hidden]) the bf16 value as fp32 for a router that multiplies in this block.  One
+// __syncthreads (the block reduction); xf is complete only after the caller's next barrier.
 __device__ inline void finish_bf16(const NormIn& in, bool has_w, float eps, int hidden, uint16_t* __restrict__ x_bf16,
-                                   __half* __restrict__ x_f16, double* red) {
+                                   __half* __restrict__ x_f16, double* red, float* __restrict__ xf = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     double ss = 0.0;
 #pragma unroll
@@ -114,10 +116,15 @@ __device__ inline void finish_bf16(const NormIn& in, bool has_w, float eps, int 
             b[j] = route::f64_to_bf16_bits(v);
             f[j] = __half_as_ushort(__float2half_rn(route::bf16_to_f32(b[j])));
         }
-        *reinterpret_cast<uint2*>(x_bf16 + i) =
-            make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
-        *reinterpret_cast<uint2*>(x_f16 + i) =
-            make_uint2((uint32_t)f[0] | ((uint32_t)f[1] << 16), (uint32_t)f[2] | ((uint32_t)f[3] << 16));
+        if (x_bf16)
+            *reinterpret_cast<uint2*>(x_bf16 + i) =
+                make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
+        if (x_f16)
+            *reinterpret_cast<uint2*>(x_f16 + i) =
+                make_uint2((uint32_t)f[0] | ((uint32_t)f[1] << 16), (uint32_t)f[2] | ((uint32_t)f[3] << 16));
+        if (xf)
+            *reinterpret_cast<float4*>(xf + i) = make_float4(route::bf16_to_f32(b[0]), route::bf16_to_f32(b[1]),
+                                                             route::bf16_to_f32(b[2]), route::bf16_to_f32(b[3]));
     }
 }
 

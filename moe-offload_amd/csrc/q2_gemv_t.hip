@@ -34,6 +34,14 @@ constexpr int kTDownWaves = 8;          // waves per down block (1-2 of the top-
 static_assert((kTDownRows & (kTDownRows - 1)) == 0, "the epilogue row of a thread is tid & (kTDownRows - 1)");
 constexpr int kTDownLanes = 16;         // lanes per down row: intermediate <= 1024
 
+// Block index -> row block, keeping consecutive row blocks on one XCD (blocks are dealt to the 8
+// XCDs round robin): a down row's scales and biases (2 bytes per group) share 128-byte lines with
+// the neighbouring rows, which another XCD's L2 would fetch again.
+__device__ __forceinline__ int xcd_rank(int b, int nb) {
+    const int per = nb / 8, rem = nb % 8, x = b % 8, i = b / 8;
+    return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
 template <bool BF16>
 __device__ __forceinline__ float half_bits(uint16_t v) {
     if constexpr (BF16) return __uint_as_float((uint32_t)v << 16);
@@ -187,7 +195,7 @@ __global__ __launch_bounds__(64 * kTDownWaves) void k_q2t_down(const __half* __r
     const int IPR = inter >> 6;
     const int g = lane & (kTDownLanes - 1), rl = lane / kTDownLanes;
     const int gc = g < IPR ? g : IPR - 1;
-    const int row0 = blockIdx.x * kTDownRows;
+    const int row0 = xcd_rank(blockIdx.x, gridDim.x) * kTDownRows;
 
     const int n_units = k * IPR * 4;
     uint4 hv[kUnitIters][2];
@@ -294,6 +302,138 @@ __global__ __launch_bounds__(64 * kTDownWaves) void k_q2t_down(const __half* __r
     }
 }
 
+// The down product's sums (modes 0 and 2) with every lane on one (row, group) pair: a wave covers
+// R = 64 / IPR rows at once (IPR = inter / 64 groups per row; 6 rows and 4 idle lanes at inter
+// 640, where k_q2t_down's 16-lane rows leave 6 of 16 lanes idle), a block kRDIters such row sets
+// (2R rows) for all k experts.  The block's (expert, row set) items are dealt to its waves in turn
+// (k = 10: 3 or 2 per wave).  A lane accumulates s_j * (its group's part of row r of expert j)
+// over its items in registers; the block then sums over waves and over the row's groups once, in a
+// fixed order (run-to-run identical).  With hidden 2560 that is 214 blocks, one per CU, so no CU
+// multiplies twice the rows of another.
+constexpr int kRDWaves = 8;
+constexpr int kRDIters = 2;                                  // row sets per block
+constexpr int kRDMaxItems = (MOE_MAX_K * kRDIters + kRDWaves - 1) / kRDWaves;
+
+template <bool BF16>
+__global__ __launch_bounds__(64 * kRDWaves) void k_q2t_down_rows(const __half* __restrict__ h, Q2Experts E,
+                                                               const uint32_t* __restrict__ slots, int n_slots,
+                                                               const __half* __restrict__ scores, int k, int hidden,
+                                                               int inter, const __half* __restrict__ residual,
+                                                               float* __restrict__ y_out, bool add) {
+    constexpr int kUnitIters = (MOE_MAX_K * 1024 / 16 + 64 * kRDWaves - 1) / (64 * kRDWaves);
+    __shared__ uint4 hp[MOE_MAX_K][kTDownLanes][8];
+    __shared__ float hc[MOE_MAX_K][kTDownLanes][2];
+    __shared__ float red[kRDWaves][kRDIters][64];
+    __shared__ float red2[kRDIters][64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int IPR = inter >> 6;
+    const int R = 64 / IPR;                                  // rows per row set
+    const int rl = lane / IPR, g = lane - rl * IPR;
+    const bool lane_ok = rl < R;
+    const int rlc = lane_ok ? rl : R - 1;
+    const int RB = R * kRDIters;
+    const int row0 = xcd_rank(blockIdx.x, gridDim.x) * RB;
+    const int n_items = k * kRDIters;
+
+    // h (as in k_q2t_down), then every item's weights, unconditional from clamped addresses
+    const int n_units = k * IPR * 4;
+    uint4 hv[kUnitIters][2];
+#pragma unroll
+    for (int ui = 0; ui < kUnitIters; ++ui) {
+        const int u = tid + 64 * kRDWaves * ui;
+        const int uc = u < n_units ? u : 0;
+        hv[ui][0] = reinterpret_cast<const uint4*>(h + (size_t)uc * 16)[0];
+        hv[ui][1] = reinterpret_cast<const uint4*>(h + (size_t)uc * 16)[1];
+    }
+    const Q2Proj& Pd = E.p[2];
+    uint32_t slot_q[kRDMaxItems];
+    uint4 c[kRDMaxItems];
+    uint16_t sc[kRDMaxItems], bi[kRDMaxItems];
+#pragma unroll
+    for (int q = 0; q < kRDMaxItems; ++q) {
+        const int i = wv + kRDWaves * q;
+        const int ic = i < n_items ? i : n_items - 1;
+        const int j = ic / kRDIters, it = ic - j * kRDIters;
+        slot_q[q] = slots[j];
+        const size_t s = slot_q[q] < (uint32_t)n_slots ? slot_q[q] : 0u;
+        int row = row0 + it * R + rlc;
+        row = row < hidden ? row : hidden - 1;
+        c[q] = *reinterpret_cast<const uint4*>(Pd.w + s * Pd.w_stride + (size_t)row * (inter >> 2) + (size_t)g * 16);
+        sc[q] = *reinterpret_cast<const uint16_t*>(Pd.s + s * Pd.s_stride + ((size_t)row * IPR + g) * Pd.sb_step);
+        bi[q] = *reinterpret_cast<const uint16_t*>(Pd.b + s * Pd.b_stride + ((size_t)row * IPR + g) * Pd.sb_step);
+    }
+    const bool weighted = scores != nullptr;
+    const uint16_t s_bits = __half_as_ushort((weighted ? scores : h)[lane < k ? lane : 0]);
+    const float s_lane = E.scores_bf16 ? __uint_as_float((uint32_t)s_bits << 16) : __half2float(__ushort_as_half(s_bits));
+    // the epilogue's operands (thread t < RB: row row0 + t): y's current value for mode 2, the
+    // residual for mode 0 (without a residual, y's first bytes, unused)
+    const int erow = row0 + tid < hidden ? row0 + tid : hidden - 1;
+    const float y_prev = y_out[erow];
+    const __half r_prev = (residual ? residual : reinterpret_cast<const __half*>(y_out))[erow];
+
+#pragma unroll
+    for (int ui = 0; ui < kUnitIters; ++ui) {
+        const int u = tid + 64 * kRDWaves * ui;
+        if (64 * kRDWaves * ui >= n_units) break;      // block-uniform
+        const int uc = u < n_units ? u : 0;
+        const int jj = uc / (IPR * 4), gg = (uc >> 2) % IPR;
+        stage_pairs(hv[ui][0], hv[ui][1], u < n_units, hp[jj][gg], hc[jj][gg], uc & 3, gg & 7);
+    }
+    __syncthreads();
+
+    float acc0 = 0.f, acc1 = 0.f;
+    static_assert(kRDIters == 2, "one accumulator per row set");
+#pragma unroll
+    for (int q = 0; q < kRDMaxItems; ++q) {
+        const int i = wv + kRDWaves * q;
+        if (i >= n_items) break;                          // wave-uniform
+        const int j = i / kRDIters, it = i - j * kRDIters;
+        h2_t P[32];
+        const uint4* src = hp[j][g];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint4 v = src[e ^ (g & 7)];
+            P[4 * e] = as_h2(v.x);
+            P[4 * e + 1] = as_h2(v.y);
+            P[4 * e + 2] = as_h2(v.z);
+            P[4 * e + 3] = as_h2(v.w);
+        }
+        const float cst = hc[j][g][0], sum = hc[j][g][1];
+        const bool ok = slot_q[q] < (uint32_t)n_slots && lane_ok;
+        const float sj = weighted ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s_lane), j)) : 1.0f;
+        const float part = ok ? half_bits<BF16>(sc[q]) * (q2_group_dot(c[q], P) - cst) + half_bits<BF16>(bi[q]) * sum
+                              : 0.0f;
+        if (it == 0) acc0 += sj * part;
+        else acc1 += sj * part;
+    }
+    red[wv][0][lane] = acc0;
+    red[wv][1][lane] = acc1;
+    __syncthreads();
+    if (tid < kRDIters * 64) {                           // over the waves, in order
+        const int it = tid >> 6, ln = tid & 63;
+        float v = red[0][it][ln];
+#pragma unroll
+        for (int w = 1; w < kRDWaves; ++w) v += red[w][it][ln];
+        red2[it][ln] = v;
+    }
+    __syncthreads();
+    if (tid < RB) {                                      // over the row's groups, in order
+        const int it = tid / R, rr = tid - it * R;
+        const int row = row0 + tid;
+        if (row < hidden) {
+            const float* rg = &red2[it][rr * IPR];
+            float y = rg[0];
+            for (int gi = 1; gi < IPR; ++gi) y += rg[gi];
+            if (add) {
+                y_out[row] = y_prev + y;
+            } else {
+                if (residual) y += __half2float(r_prev);
+                y_out[row] = y;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 bool q2t_shape_ok(const char* who, int k, int hidden, int inter, int group) {
@@ -385,13 +525,25 @@ int launch_q2t_down(const __half* h, const Q2Experts& E, int n_slots, const uint
     if (!q2t_shape_ok("q2t_down", k, hidden, inter, 64)) return -1;
     if (per_expert < 0 || per_expert > 2) { moe_set_error("q2t_down: mode %d (0 sum, 1 per expert, 2 add)", per_expert); return -1; }
     if (n_slots <= 0 || !slots || !h || !y_out) { moe_set_error("q2t_down: empty pool or null pointer"); return -1; }
-    dim3 grid((hidden + kTDownRows - 1) / kTDownRows);
-    if (E.bf16)
-        MOE_LAUNCH(TK_DOWN, (k_q2t_down<true>), grid, dim3(64 * kTDownWaves), 0, s, h, E, slots, n_slots, scores, k, hidden, inter,
-                   residual, y_out, per_expert);
-    else
-        MOE_LAUNCH(TK_DOWN, (k_q2t_down<false>), grid, dim3(64 * kTDownWaves), 0, s, h, E, slots, n_slots, scores, k, hidden, inter,
-                   residual, y_out, per_expert);
+    hipStream_t st = s;
+    if (per_expert != 1) {                 // the sums: every lane of a wave on a (row, group)
+        const int ipr = inter >> 6, rb = (64 / ipr) * kRDIters;
+        const dim3 grid((hidden + rb - 1) / rb);
+        if (E.bf16)
+            MOE_LAUNCH(TK_DOWN, (k_q2t_down_rows<true>), grid, dim3(64 * kRDWaves), 0, st, h, E, slots, n_slots, scores,
+                       k, hidden, inter, residual, y_out, per_expert == 2);
+        else
+            MOE_LAUNCH(TK_DOWN, (k_q2t_down_rows<false>), grid, dim3(64 * kRDWaves), 0, st, h, E, slots, n_slots, scores,
+                       k, hidden, inter, residual, y_out, per_expert == 2);
+    } else {
+        const dim3 grid((hidden + kTDownRows - 1) / kTDownRows);
+        if (E.bf16)
+            MOE_LAUNCH(TK_DOWN, (k_q2t_down<true>), grid, dim3(64 * kTDownWaves), 0, st, h, E, slots, n_slots, scores, k,
+                       hidden, inter, residual, y_out, per_expert);
+        else
+            MOE_LAUNCH(TK_DOWN, (k_q2t_down<false>), grid, dim3(64 * kTDownWaves), 0, st, h, E, slots, n_slots, scores, k,
+                       hidden, inter, residual, y_out, per_expert);
+    }
     HIP_TRY(hipGetLastError());
     return 0;
 }

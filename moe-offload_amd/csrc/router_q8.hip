@@ -21,6 +21,7 @@
 #include "lane_reduce.h"
 #include "moe_common.h"
 #include "moe_offload.h"
+#include "norm_f64.h"
 #include "route_select.h"
 
 namespace {
@@ -39,19 +40,30 @@ __device__ __forceinline__ uint32_t bf16_order(uint32_t b) {
     return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
 }
 
-template <int NU>
+// NORM: the input is the previous layer's output h (fp32), normalised by every block (the bf16
+// RMSNorm of norm_f64.h, bit-identical to moe_rmsnorm_bf16) while its weight loads fly; block 0
+// also writes x as bf16 and as fp16 (the expert kernels' input and residual).  A compile-time
+// choice, so that no branch lets the compiler sink the input loads behind the weight loads.
+template <int NU, bool NORM>
 __global__ __launch_bounds__(kThreads) void k_router_q8(
-    const uint16_t* __restrict__ x, const uint32_t* __restrict__ codes, const uint16_t* __restrict__ scales,
+    const uint16_t* __restrict__ x, const float* __restrict__ h_in, const uint16_t* __restrict__ norm_w, float eps,
+    uint16_t* __restrict__ xb_out, __half* __restrict__ xh_out,
+    const uint32_t* __restrict__ codes, const uint16_t* __restrict__ scales,
     const uint16_t* __restrict__ biases, int hidden, int n_rows, int k, int m, float* __restrict__ scratch,
     unsigned* __restrict__ counter, uint32_t* __restrict__ ids_out, uint16_t* __restrict__ scores_out,
     int32_t* __restrict__ pred_out, uint16_t* __restrict__ logits_out) {
-    __shared__ float xf[kMaxHidden];
+    __shared__ __align__(16) float xf[kMaxHidden];
     __shared__ double sx[kMaxUnits];
+    __shared__ double redn[kThreads / 64];
     __shared__ int is_last;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int units = hidden / 16, groups = hidden / 64;
     const int row = blockIdx.x * kRows + wv;
     const int rc = row < n_rows ? row : n_rows - 1;             // a row past the end reads the last
+
+    norm64::NormIn nin;
+    if constexpr (NORM) norm64::load(nin, h_in, reinterpret_cast<const __half*>(norm_w), hidden);
+    __builtin_amdgcn_sched_barrier(0);                            // the input loads ahead of the weights
 
     // weight loads first (unconditional, clamped): unit u = lane + 64 c of row rc
     uint4 q[NU];
@@ -63,8 +75,15 @@ __global__ __launch_bounds__(kThreads) void k_router_q8(
         const size_t gi = (size_t)rc * groups + uc / 4;
         sb[c] = (uint32_t)scales[gi] | ((uint32_t)biases[gi] << 16);
     }
+    __builtin_amdgcn_sched_barrier(0);                            // every weight load issued before anything waits
     // the input, as fp32 (exact), and each unit's input sum
-    for (int i = tid; i < hidden; i += kThreads) xf[i] = bf16_to_f32(x[i]);
+    if constexpr (NORM) {
+        const bool first = blockIdx.x == 0;
+        norm64::finish_bf16(nin, norm_w != nullptr, eps, hidden, first ? xb_out : nullptr, first ? xh_out : nullptr,
+                            redn, xf);
+    } else {
+        for (int i = tid; i < hidden; i += kThreads) xf[i] = bf16_to_f32(x[i]);
+    }
     __syncthreads();
     for (int u = tid; u < units; u += kThreads) {
         double s = 0.0;
@@ -159,29 +178,33 @@ extern "C" uint64_t moe_router_q8_workspace_bytes(int n_rows) {
     return (uint64_t)(n_rows > 0 ? n_rows : 0) * sizeof(float) + 256;
 }
 
-extern "C" int moe_router_q8(const void* x, const uint32_t* codes, const void* scales, const void* biases, int hidden,
-                             int n_rows, int group, int k, int m, void* workspace, uint32_t* ids_out, void* scores_out,
-                             int32_t* pred_out, void* logits_out, void* stream) {
+namespace {
+
+int launch_router_q8(const void* x, const float* h_in, const void* norm_w, float eps, void* xb_out, void* xh_out,
+                     const uint32_t* codes, const void* scales, const void* biases, int hidden, int n_rows, int group,
+                     int k, int m, void* workspace, uint32_t* ids_out, void* scores_out, int32_t* pred_out,
+                     void* logits_out, void* stream) {
+    const char* who = h_in ? "router_q8_norm" : "router_q8";
     if (group != 64 || hidden <= 0 || hidden % 64 || hidden > kMaxHidden) {
-        moe_set_error("router_q8: hidden=%d group=%d (group 64, hidden a multiple of 64 up to %d)", hidden, group,
+        moe_set_error("%s: hidden=%d group=%d (group 64, hidden a multiple of 64 up to %d)", who, hidden, group,
                       kMaxHidden);
         return -1;
     }
     if (n_rows <= 0 || n_rows > route::kMaxExperts) {
-        moe_set_error("router_q8: %d rows (1..%d)", n_rows, route::kMaxExperts);
+        moe_set_error("%s: %d rows (1..%d)", who, n_rows, route::kMaxExperts);
         return -1;
     }
     if ((k > 0) == (m > 0) && (k > 0 || m > 0)) {
-        moe_set_error("router_q8: route (k > 0) or predict (m > 0), not both");
+        moe_set_error("%s: route (k > 0) or predict (m > 0), not both", who);
         return -1;
     }
     if (k > MOE_MAX_K || k > n_rows || m > 64 || m > n_rows) {
-        moe_set_error("router_q8: k=%d m=%d for %d rows (k <= %d, m <= 64)", k, m, n_rows, MOE_MAX_K);
+        moe_set_error("%s: k=%d m=%d for %d rows (k <= %d, m <= 64)", who, k, m, n_rows, MOE_MAX_K);
         return -1;
     }
-    if (!x || !codes || !scales || !biases || !workspace || (k > 0 && (!ids_out || !scores_out)) ||
+    if ((!x && !h_in) || !codes || !scales || !biases || !workspace || (k > 0 && (!ids_out || !scores_out)) ||
         (m > 0 && !pred_out) || (k <= 0 && m <= 0 && !logits_out)) {
-        moe_set_error("router_q8: null pointer");
+        moe_set_error("%s: null pointer", who);
         return -1;
     }
     float* scratch = (float*)workspace;
@@ -189,17 +212,44 @@ extern "C" int moe_router_q8(const void* x, const uint32_t* codes, const void* s
     const int units = hidden / 16, nu = (units + 63) / 64;
     const dim3 grid((n_rows + kRows - 1) / kRows);
     hipStream_t s = (hipStream_t)stream;
-#define RQ8(NU)                                                                                                       \
-    MOE_LAUNCH(TK_ROUTER, k_router_q8<NU>, grid, dim3(kThreads), 0, s, (const uint16_t*)x, codes,                     \
-               (const uint16_t*)scales, (const uint16_t*)biases, hidden, n_rows, k, m, scratch, counter, ids_out,     \
-               (uint16_t*)scores_out, pred_out, (uint16_t*)logits_out)
-    switch (nu) {
-        case 1: RQ8(1); break;
-        case 2: RQ8(2); break;
-        case 3: RQ8(3); break;
-        default: RQ8(4); break;
-    }
-#undef RQ8
+    auto go = [&](auto nuc, auto normc) {
+        constexpr int NU = decltype(nuc)::value;
+        constexpr bool NORM = decltype(normc)::value;
+        MOE_LAUNCH(TK_ROUTER, (k_router_q8<NU, NORM>), grid, dim3(kThreads), 0, s, (const uint16_t*)x, h_in,
+                   (const uint16_t*)norm_w, eps, (uint16_t*)xb_out, (__half*)xh_out, codes, (const uint16_t*)scales,
+                   (const uint16_t*)biases, hidden, n_rows, k, m, scratch, counter, ids_out, (uint16_t*)scores_out,
+                   pred_out, (uint16_t*)logits_out);
+    };
+    auto with_nu = [&](auto normc) {
+        switch (nu) {
+            case 1: go(std::integral_constant<int, 1>(), normc); break;
+            case 2: go(std::integral_constant<int, 2>(), normc); break;
+            case 3: go(std::integral_constant<int, 3>(), normc); break;
+            default: go(std::integral_constant<int, 4>(), normc); break;
+        }
+    };
+    if (h_in) with_nu(std::true_type());
+    else with_nu(std::false_type());
     HIP_TRY(hipGetLastError());
     return 0;
+}
+
+}  // namespace
+
+extern "C" int moe_router_q8(const void* x, const uint32_t* codes, const void* scales, const void* biases, int hidden,
+                             int n_rows, int group, int k, int m, void* workspace, uint32_t* ids_out, void* scores_out,
+                             int32_t* pred_out, void* logits_out, void* stream) {
+    if (!x) { moe_set_error("router_q8: null pointer"); return -1; }
+    return launch_router_q8(x, nullptr, nullptr, 0.f, nullptr, nullptr, codes, scales, biases, hidden, n_rows, group, k,
+                            m, workspace, ids_out, scores_out, pred_out, logits_out, stream);
+}
+
+extern "C" int moe_router_q8_norm(const float* h_in, const void* norm_w, float eps, void* x_bf16_out, void* x_f16_out,
+                                  const uint32_t* codes, const void* scales, const void* biases, int hidden, int n_rows,
+                                  int group, int k, int m, void* workspace, uint32_t* ids_out, void* scores_out,
+                                  int32_t* pred_out, void* logits_out, void* stream) {
+    if (!h_in) { moe_set_error("router_q8_norm: null pointer"); return -1; }
+    if (hidden % 8) { moe_set_error("router_q8_norm: hidden=%d (a multiple of 8)", hidden); return -1; }
+    return launch_router_q8(nullptr, h_in, norm_w, eps, x_bf16_out, x_f16_out, codes, scales, biases, hidden, n_rows,
+                            group, k, m, workspace, ids_out, scores_out, pred_out, logits_out, stream);
 }

@@ -143,6 +143,8 @@ SIGNATURES: dict[str, tuple] = {
     "moe_router_q8_workspace_bytes": (_c_u64, [_c_int]),
     "moe_router_q8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp,
                                _c_vp, _c_vp, _c_vp, _c_vp]),
+    "moe_router_q8_norm": (_c_int, [_c_vp, _c_vp, _c_f, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int,
+                                    _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
     # P1 I/O scheduler (cpp/src/io_sched.h)
     "moe_p1_create": (_c_vp, []),
     "moe_p1_destroy": (None, [_c_vp]),

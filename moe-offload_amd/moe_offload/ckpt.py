@@ -56,6 +56,8 @@ class CkptConfig:
     layer_base: int = 0          # first C-ABI layer index used
     stage_ctas: int = 8          # staging blocks per copied expert (its 9 tensors in one launch; at 48 layers,
                                  # 20% cache: 2 -> 41, 4 -> 69, 8 -> 81, 16 -> 77 tok/s on one box)
+    fused_norm: bool = True      # device path: the RMSNorm runs inside the router launch (moe_router_q8_norm)
+                                 # instead of a launch of its own; the host path keeps the two launches
     # set from the directory
     n_layers: int = 0
     hidden: int = 0
@@ -346,12 +348,25 @@ class CheckpointStack:
         return self.cfg.layer_base + l
 
     # ---- one token ---------------------------------------------------------------------------
-    def _router(self, l: int, s: int):
+    def _router_call(self, l: int, s: int, norm: bool, k: int, ids, scores, logits):
+        """Layer l's router (route mode k > 0, or logits only); norm: with the RMSNorm of the
+        previous layer's output fused in (writes xb[l] and xf[l] as the separate norm does)."""
         c, L = self.cfg, self.L
         codes, scales, biases = self.routers[l]
-        _lib.check(L.moe_router_q8(self.xb[l].data_ptr(), codes.data_ptr(), scales.data_ptr(), biases.data_ptr(),
-                                   c.hidden, c.n_exp, c.group, c.top_k, 0, self.ws_route[l].data_ptr(),
-                                   self.ids[l].data_ptr(), self.scores[l].data_ptr(), None, None, s), "router_q8")
+        if norm:
+            rc = L.moe_router_q8_norm(self.hs[l - 1].data_ptr(), None, c.eps, self.xb[l].data_ptr(),
+                                      self.xf[l].data_ptr(), codes.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+                                      c.hidden, c.n_exp, c.group, k, 0, self.ws_route[l].data_ptr(), ids, scores, None,
+                                      logits, s)
+        else:
+            rc = L.moe_router_q8(self.xb[l].data_ptr(), codes.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+                                 c.hidden, c.n_exp, c.group, k, 0, self.ws_route[l].data_ptr(), ids, scores, None,
+                                 logits, s)
+        _lib.check(rc, "router_q8_norm" if norm else "router_q8")
+
+    def _router(self, l: int, s: int, norm: bool = False):
+        c, L = self.cfg, self.L
+        self._router_call(l, s, norm, c.top_k, self.ids[l].data_ptr(), self.scores[l].data_ptr(), None)
         if c.prefetch and l + 1 < c.n_layers:
             codes, scales, biases = self.routers[l + 1]
             _lib.check(L.moe_router_q8(self.xb[l].data_ptr(), codes.data_ptr(), scales.data_ptr(), biases.data_ptr(),
@@ -373,14 +388,11 @@ class CheckpointStack:
         _lib.check(self.L.moe_rmsnorm_bf16(self.hs[l - 1].data_ptr(), None, self.cfg.eps, self.cfg.hidden,
                                            self.xb[l].data_ptr(), self.xf[l].data_ptr(), s), "rmsnorm_bf16")
 
-    def _layer_resident(self, l: int, s: int):
+    def _layer_resident(self, l: int, s: int, norm: bool = False):
         """Resident layer: the router's bf16 logits, then gate/up whose blocks select the top k
         themselves (the router's rule, bit for bit), then the down product with the bf16 scores."""
         c, L = self.cfg, self.L
-        codes, scales, biases = self.routers[l]
-        _lib.check(L.moe_router_q8(self.xb[l].data_ptr(), codes.data_ptr(), scales.data_ptr(), biases.data_ptr(),
-                                   c.hidden, c.n_exp, c.group, 0, 0, self.ws_route[l].data_ptr(), None, None, None,
-                                   self.logits[l].data_ptr(), s), "router_q8 logits")
+        self._router_call(l, s, norm, 0, None, None, self.logits[l].data_ptr())
         _, ptrs, nbytes = self.full[l]
         _lib.check(L.moe_q2t_gate_up_routed(self.xf[l].data_ptr(), self.logits[l].data_ptr(), c.n_exp, c.top_k, ptrs,
                                             nbytes, self.scale_bf16, c.hidden, c.inter, c.group, self.ids[l].data_ptr(),
@@ -391,19 +403,20 @@ class CheckpointStack:
 
     def decode_token_device(self):
         """Device-driven token (DecodeStack's device path with the checkpoint's kernels): main stream
-        norm -> router (+ predictor) -> [join prefetch table(l)] -> step(l) -> [join prefetch
+        (norm in) router (+ predictor) -> [join prefetch table(l)] -> step(l) -> [join prefetch
         copies(l)] -> demand copies(l) -> SwitchGLU; side stream: prefetch table(l+1), then its copies
         once layer l's demand copies are queued."""
         c, L = self.cfg, self.L
         main = torch.cuda.current_stream()
         ms = main.cuda_stream
+        fuse = c.fused_norm
         for l in range(c.n_layers):
-            if l > 0:
+            if l > 0 and not fuse:
                 self._norm(l, ms)
             if self.resident:
-                self._layer_resident(l, ms)
+                self._layer_resident(l, ms, norm=fuse and l > 0)
                 continue
-            self._router(l, ms)
+            self._router(l, ms, norm=fuse and l > 0)
             if l >= 1:
                 if c.prefetch:
                     main.wait_event(self.ev_pref[l])

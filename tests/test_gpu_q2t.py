@@ -295,3 +295,36 @@ def test_tensor_form_every_expert_count(k):
     for j, e in enumerate(ids):
         want = q2.switch_glu_expert(x.astype(np.float64), *f(int(e)), bits=2, group=64, sdtype="bf16")
         assert_close_rms(yk[j], want, 1e-2, f"k={k} expert {e}")
+
+
+@pytest.mark.parametrize("H,I", [(2560, 640), (256, 64), (512, 1024), (1024, 192), (320, 448)])
+def test_down_modes_agree_across_shapes(H, I):
+    """The down product's three modes at shapes that leave the row layout's last block partial
+    and its lanes partly idle (inter / 64 = 1..16 groups per row): the sum (mode 0, against the
+    fp64 oracle), the score-weighted sum of the per-expert rows (mode 1) equal to it within fp32
+    rounding, and mode 2 adding exactly that sum to y's previous value."""
+    from moe_offload import _lib
+    L = _lib.lib()
+    dev = torch.device("cuda")
+    E, K = 12, 10
+    mlx = experts_bf16(E, H, I, seed=H + I)
+    ts, ptrs, nbytes = _pools(mlx, dev)
+    f = _fn(mlx, "bf16")
+    rng = np.random.default_rng(H * 7 + I)
+    x = rng.standard_normal(H).astype(np.float16)
+    ids = rng.choice(E, size=K, replace=False).astype(np.int32)
+    sc = rng.dirichlet(np.ones(K)).astype(np.float16)
+    xt, it, st = torch.from_numpy(x).to(dev), torch.from_numpy(ids).to(dev), torch.from_numpy(sc).to(dev)
+    y0 = _run(L, xt, ptrs, nbytes, 1, E, it, st, K, H, I)
+    want = q2.moe_combine(x.astype(np.float64), ids, sc.astype(np.float64), f, bits=2, group=64, sdtype="bf16")
+    assert_close_rms(y0, want, 1e-2, "mode 0")
+    yk = _run(L, xt, ptrs, nbytes, 1, E, it, None, K, H, I, per_expert=1)
+    comb = (sc.astype(np.float64)[:, None] * yk.astype(np.float64)).sum(axis=0)
+    assert np.abs(comb - y0).max() <= 1e-5 * np.abs(y0).max() + 1e-7
+    base = torch.from_numpy(rng.standard_normal(H).astype(np.float32)).to(dev)
+    y2 = base.clone()
+    h_ws = torch.empty(K * I, dtype=torch.float16, device=dev)
+    rc = L.moe_q2t_switch_glu(xt.data_ptr(), ptrs, nbytes, 1, E, it.data_ptr(), st.data_ptr(), K, H, I, 64, None,
+                              h_ws.data_ptr(), y2.data_ptr(), 2, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "moe_q2t_switch_glu mode 2")
+    assert np.array_equal(y2.cpu().numpy(), (base.cpu().numpy() + y0).astype(np.float32))

@@ -135,3 +135,46 @@ def test_rejects_bad_arguments():
     assert L.moe_router_q8(p, p, p, p, 256, 16, 64, 4, 4, p, p, p, p, p, s) == -1        # both modes
     assert L.moe_router_q8(p, p, p, p, 256, 16, 64, 20, 0, p, p, p, p, p, s) == -1       # k > n_rows
     L.c_clear_error()
+
+
+@pytest.mark.parametrize("with_w", [False, True])
+def test_norm_fused_router_equals_norm_then_router(with_w):
+    """moe_router_q8_norm (the bf16 RMSNorm inside the router launch) against moe_rmsnorm_bf16
+    followed by moe_router_q8, at the real shape: x as bf16 and fp16, logits, ids, scores and
+    predictions bit for bit, in all three modes, over h of varied magnitude."""
+    from moe_offload import _lib
+    rng = np.random.default_rng(13)
+    E, H, eps = 512, 2560, 1e-6
+    codes = rng.integers(0, 2**32, size=(E, H // 4), dtype=np.uint32)
+    scales = _bf16_bits(rng.standard_normal((E, H // 64)) * 2e-4)
+    biases = _bf16_bits(-128 * q2.to_f64(scales, "bf16") + rng.standard_normal((E, H // 64)) * 1e-4)
+    r = Q8(codes, scales, biases)
+    L, s = r.L, torch.cuda.current_stream().cuda_stream
+    nw = _dev(_bf16_bits(1.0 + 0.1 * rng.standard_normal(H)), np.int16) if with_w else None
+    nwp = nw.data_ptr() if with_w else None
+    for t in range(6):
+        h = torch.from_numpy((rng.standard_normal(H) * 10.0 ** (t - 2)).astype(np.float32)).cuda()
+        xb = torch.zeros(H, dtype=torch.int16, device="cuda")
+        xh = torch.zeros(H, dtype=torch.float16, device="cuda")
+        _lib.check(L.moe_rmsnorm_bf16(h.data_ptr(), nwp, eps, H, xb.data_ptr(), xh.data_ptr(), s), "rmsnorm_bf16")
+        torch.cuda.synchronize()
+        xbits = xb.cpu().numpy().view(np.uint16)
+        for k, m in ((10, 0), (0, 12), (0, 0)):
+            ref = r.run(xbits, k=k, m=m)
+            ids = torch.zeros(max(k, 1), dtype=torch.int32, device="cuda")
+            sc = torch.zeros(max(k, 1), dtype=torch.int16, device="cuda")
+            pred = torch.zeros(max(m, 1), dtype=torch.int32, device="cuda")
+            lg = torch.zeros(E, dtype=torch.int16, device="cuda")
+            xb2 = torch.full((H,), -1, dtype=torch.int16, device="cuda")
+            xh2 = torch.full((H,), -1.0, dtype=torch.float16, device="cuda")
+            rc = L.moe_router_q8_norm(h.data_ptr(), nwp, eps, xb2.data_ptr(), xh2.data_ptr(), r.c.data_ptr(),
+                                      r.s.data_ptr(), r.b.data_ptr(), H, E, 64, k, m, r.ws.data_ptr(), ids.data_ptr(),
+                                      sc.data_ptr(), pred.data_ptr(), lg.data_ptr(), s)
+            _lib.check(rc, "moe_router_q8_norm")
+            torch.cuda.synchronize()
+            where = (t, k, m)
+            assert torch.equal(xb2, xb) and torch.equal(xh2.view(torch.int16), xh.view(torch.int16)), where
+            assert np.array_equal(lg.cpu().numpy().view(np.uint16), ref[3]), where
+            assert np.array_equal(ids.cpu().numpy()[:k].astype(np.uint32), ref[0]), where
+            assert np.array_equal(sc.cpu().numpy()[:k].view(np.uint16), ref[1]), where
+            assert np.array_equal(pred.cpu().numpy()[:m], ref[2]), where
