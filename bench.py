@@ -670,8 +670,10 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
     than the 256 MB MALL), captured into one HIP graph whose replay is bracketed by two HIP events;
     the median of `repeats` replays, as the blob kernels' roofline loop.  Random codes, N(0, 0.02) scales, biases -1.5 x scale.  Then the
     checkpoint's 8-bit router (512 x 2560, top-10 in the reference's order) over 48 layers' routers
-    in turn, timed the same way, and a whole MoE layer (router, gate/up, down) with the top-k
-    selection in the router's last block or inside the gate/up blocks."""
+    in turn, timed the same way (and in logits mode with the previous layer's RMSNorm inside it),
+    and a whole MoE layer (router, gate/up, down) with the top-k selection in the router's last
+    block or inside the gate/up blocks, and as the resident checkpoint stack runs it (the norm in
+    the router, the selection in gate/up, each layer's output the next one's input)."""
     import ctypes
 
     import torch
@@ -775,8 +777,32 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
         _lib.check(L.moe_q2t_down(h.data_ptr(), ptrs[i % layers], nbytes, 1, n_exp, ids_b.data_ptr(), sc.data_ptr(), k,
                                   hidden, inter, 64, x.data_ptr(), y.data_ptr(), 0, s), "q2t_down")
 
+    # the resident checkpoint stack's own sequence: the previous layer's RMSNorm inside the router
+    # launch (logits only), then gate/up selecting the ids, then down; its output feeds the next
+    # layer's router
+    xb2 = torch.empty(hidden, dtype=torch.int16, device=dev)
+    xh2 = torch.empty(hidden, dtype=torch.float16, device=dev)
+    y2 = torch.randn(hidden, device=dev, generator=g)
+
+    def router_norm(i, s):
+        r = i % n_r
+        _lib.check(L.moe_router_q8_norm(y2.data_ptr(), None, 1e-6, xb2.data_ptr(), xh2.data_ptr(), rcodes[r].data_ptr(),
+                                        rs[r].data_ptr(), rb[r].data_ptr(), hidden, n_exp, 64, 0, 0, ws.data_ptr(),
+                                        None, None, None, lg.data_ptr(), s), "router_q8_norm")
+
+    def layer_norm_in_router(i, s):
+        router_norm(i, s)
+        _lib.check(L.moe_q2t_gate_up_routed(xh2.data_ptr(), lg.data_ptr(), n_exp, k, ptrs[i % layers], nbytes, 1,
+                                            hidden, inter, 64, ids_b.data_ptr(), sc_b.data_ptr(), h.data_ptr(), s),
+                   "q2t_gate_up_routed")
+        _lib.check(L.moe_q2t_down(h.data_ptr(), ptrs[i % layers], nbytes, 3, n_exp, ids_b.data_ptr(), sc_b.data_ptr(),
+                                  k, hidden, inter, 64, xh2.data_ptr(), y2.data_ptr(), 0, s), "q2t_down")
+
+    per = graph_loop_us(router_norm, 2 * n_r, repeats)
+    out["router_q8_norm_logits_us"] = round(sorted(per)[len(per) // 2], 3)
     out["layer_us"] = {}
-    for name, fn in (("selection_in_router", layer_routed_in_router), ("selection_in_gate_up", layer_routed_in_gate_up)):
+    for name, fn in (("selection_in_router", layer_routed_in_router), ("selection_in_gate_up", layer_routed_in_gate_up),
+                     ("norm_in_router_selection_in_gate_up", layer_norm_in_router)):
         per = graph_loop_us(fn, 2 * n_r, repeats)
         out["layer_us"][name] = round(sorted(per)[len(per) // 2], 3)
     del sets, rcodes, rs, rb
