@@ -68,52 +68,78 @@ __device__ __forceinline__ void gate_up_body(
     __builtin_amdgcn_sched_barrier(0);
 
     uint32_t slot;
-    uint32_t top_key = 0;                              // routed, wave 0: lane r's r-th largest key
+    uint32_t top_key = 0;                              // routed, wave 0: lane r's r-th pick
+    float lraw[route::kPer];
+    __shared__ uint32_t keys[ROUTED ? route::kMaxExperts : 1];
+    __shared__ double reds[4];
+    __shared__ uint32_t sel[MOE_MAX_K];
+    __shared__ uint32_t top1;
+    __shared__ int clash;
+    const int n_pad = ((n_slots + 63) / 64) * 64;
     if constexpr (ROUTED) {
-        __shared__ uint32_t keys[route::kMaxExperts];
-        __shared__ double redm[4], reds[4];
-        __shared__ uint32_t sel[MOE_MAX_K];
-        float lraw[route::kPer];
+        // rank by logit (k + 1 picks) so that the weight loads go out before the softmax
+        // (route_select.h: spec_keys / spec_check)
 #pragma unroll
         for (int i = 0; i < route::kPer; ++i) {
             const int e = tid + route::kThreads * i;
             lraw[i] = logits[e < n_slots ? e : 0];
         }
-        route::gate_keys(lraw, n_slots, keys, redm, reds);
-        // the ids first; the scores (only block (0, 0) writes them) wait until the weight loads
-        // are in flight
+        route::spec_keys<false>(lraw, n_slots, keys);
         if (wv == 0) {
-            top_key = route::wave_topn(keys, 0, ((n_slots + 63) / 64) * 64, k, lane);
+            top_key = route::wave_topn(keys, 0, n_pad, k + 1, lane);
             if (lane < k) sel[k - 1 - lane] = top_key & 0xFFFFu;
+            if (lane == 0) top1 = top_key;
         }
         __syncthreads();
         slot = sel[j];
     } else {
         slot = slots[j];
     }
-    const bool ok = slot < (uint32_t)n_slots;         // an invalid slot yields h = 0
-    const uint8_t* blob = pool + (size_t)(ok ? slot : 0) * stride;
-    const uint8_t* codes = blob + (proj ? L.up_codes : L.gate_codes);
-    const uint32_t* sbv = reinterpret_cast<const uint32_t*>(blob + (proj ? L.up_sb : L.gate_sb));
     const size_t row_bytes = (size_t)GPR * 16;
 
     // Every load is unconditional from a clamped in-range row; nothing is selected on arrival
     // (a load whose value is masked right away is sunk into a branch and waited for there).
+    bool ok;
     uint4 c[kGuRowsPerIter];
     uint32_t sb[kGuRowsPerIter];
+    auto load_w = [&](uint32_t sl) {
+        ok = sl < (uint32_t)n_slots;                   // an invalid slot yields h = 0
+        const uint8_t* blob = pool + (size_t)(ok ? sl : 0) * stride;
+        const uint8_t* codes = blob + (proj ? L.up_codes : L.gate_codes);
+        const uint32_t* sbv = reinterpret_cast<const uint32_t*>(blob + (proj ? L.up_sb : L.gate_sb));
 #pragma unroll
-    for (int it = 0; it < kGuRowsPerIter; ++it) {
-        int row = row_base + it * RPI + rl;
-        row = row < inter ? row : inter - 1;
-        c[it] = *reinterpret_cast<const uint4*>(codes + (size_t)row * row_bytes + g * 16);
-        sb[it] = sbv[(size_t)row * GPR + g];
-    }
+        for (int it = 0; it < kGuRowsPerIter; ++it) {
+            int row = row_base + it * RPI + rl;
+            row = row < inter ? row : inter - 1;
+            c[it] = *reinterpret_cast<const uint4*>(codes + (size_t)row * row_bytes + g * 16);
+            sb[it] = sbv[(size_t)row * GPR + g];
+        }
+    };
+    load_w(slot);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (ROUTED) {
+        // the rule's gates for the k + 1 picks while the weights fly; on a clash the full rule
+        // (fallback_keys) and, if this block's expert changed, its weights again
+        double lv[route::kPer], sum;
+        uint32_t exact = 0;
+        const double mx = (double)route::logit_from_order<false>(top1 >> 16);
+        if (route::spec_check<false>(lraw, n_slots, k, top_key, mx, reds, &clash, lv, sum, exact)) {
+            route::fallback_keys<false>(lv, sum, n_slots, keys);
+            if (wv == 0) {
+                exact = route::wave_topn(keys, 0, n_pad, k, lane);
+                if (lane < k) sel[k - 1 - lane] = exact & 0xFFFFu;
+            }
+            __syncthreads();
+            const uint32_t s2 = sel[j];
+            if (s2 != slot) {                          // block-uniform
+                slot = s2;
+                load_w(slot);
+            }
+        }
         if (wv == 0 && blockIdx.x == 0 && blockIdx.y == 0) {
             uint32_t id;
             __half sc;
-            const int pos = route::topk_scores(top_key, k, lane, id, sc);
+            const int pos = route::topk_scores(exact, k, lane, id, sc);
             if (pos >= 0) {
                 ids_out[pos] = id;
                 scores_out[pos] = sc;

@@ -172,6 +172,105 @@ __device__ __forceinline__ void gate_keys(const float (&lraw)[kPer], int n_exp, 
     __syncthreads();
 }
 
+// ---- the resident gate/up's selection, the weight loads first ----------------------------------
+// Gates are a monotone function of the logits (exp, one division by the same sum, one rounding), so
+// ordering by (logit, id) gives the rule's order -- (gate, id) -- unless two different logits round
+// to one gate among the first k + 1.  The fp16 resident gate/up (k_q2_gate_up_routed) therefore
+// ranks by logit first (no softmax: spec_keys + wave_topn of k + 1 rounds), issues its weight loads
+// for that ranking, and only then computes the k + 1 gates (spec_check); when they decide the same
+// ranking the exact keys follow from them, otherwise the block runs the full rule (fallback_keys +
+// wave_topn) and reloads if its expert changed.  Ids, order and scores are the rule's in both cases.
+// The bf16 rule (the checkpoint's router) keeps the softmax first: its coarser gates tie at the k
+// boundary for 13-20% of tokens, and those fallbacks cost more than the head start saves.
+
+// Order-preserving 16-bit key of a logit held as a float that is exactly a value of the rule's
+// format (-0 folded onto +0), and its inverse.
+template <bool BF16>
+__device__ __forceinline__ uint32_t logit_order(float v) {
+    uint32_t b = rule_from_f32<BF16>(v);
+    if (b == 0x8000u) b = 0;
+    return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+}
+template <bool BF16>
+__device__ __forceinline__ float logit_from_order(uint32_t o) {
+    const uint32_t b = (o & 0x8000u) ? (o & 0x7FFFu) : (~o & 0xFFFFu);
+    return rule_to_f32<BF16>(b);
+}
+
+// Block-wide: keys[0, n_pad) = (logit order << 16 | id) of the logits this thread holds (as
+// gate_keys; padding 0).  Ends with a barrier.
+template <bool BF16>
+__device__ __forceinline__ void spec_keys(const float (&lraw)[kPer], int n_exp, uint32_t* keys) {
+    const int tid = threadIdx.x;
+    const int n_pad = ((n_exp + 63) / 64) * 64;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = tid + kThreads * i;
+        if (e < n_pad) keys[e] = (e < n_exp) ? ((logit_order<BF16>(lraw[i]) << 16) | (uint32_t)e) : 0u;
+    }
+    __syncthreads();
+}
+
+// Block-wide, after spec_keys and the k + 1 rounds: the softmax sum of gate_keys (the same
+// arithmetic and order; mx = the largest logit, wave 0's first pick) and, in wave 0, the gates of
+// the first k + 1 picks (lane r holds pick `top`).  Returns true, block-uniform, when two of them
+// that decide the ranking clash: pick r's gate below pick r + 1's for some r < k, or equal to it
+// from a different logit with pick r's id the lower (r < k - 1), or equal at all (r = k - 1).  lane
+// r < k of wave 0 gets the rule's key in `exact`.  lv / sum are kept for fallback_keys.
+// Contains one barrier, plus one more to broadcast the answer (flag: an int of LDS).
+template <bool BF16>
+__device__ __forceinline__ bool spec_check(const float (&lraw)[kPer], int n_exp, int k, uint32_t top, double mx,
+                                           double* reds, int* flag, double (&lv)[kPer], double& sum,
+                                           uint32_t& exact) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    sum = 0.0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = tid + kThreads * i;
+        lv[i] = (e < n_exp) ? exp((double)lraw[i] - mx) : 0.0;
+        sum += lv[i];
+    }
+    sum = lanes::wave_sum_f64(sum);
+    if (lane == 0) reds[wv] = sum;
+    __syncthreads();
+    sum = (reds[0] + reds[1]) + (reds[2] + reds[3]);
+    if (wv == 0) {
+        const bool valid = lane <= k && top != 0u;
+        const uint32_t g = valid ? (uint32_t)rule_from_f64<BF16>(exp((double)logit_from_order<BF16>(top >> 16) - mx) / sum)
+                                 : 0u;
+        const uint32_t g_next = (uint32_t)__shfl_down((int)g, 1, 64);
+        const uint32_t top_next = (uint32_t)__shfl_down((int)top, 1, 64);
+        const bool next_valid = __shfl_down((int)valid, 1, 64) != 0;
+        // inside the first k, equal gates keep the logit ranking when the logits are equal (both
+        // rankings then order by id) or when the higher logit also has the higher id; at the
+        // boundary any equal gate is a clash, since experts ranked below pick k (lower logits,
+        // possibly higher ids) may share that gate
+        const bool same_logit = (top >> 16) == (top_next >> 16);
+        const bool id_down = (top & 0xFFFFu) > (top_next & 0xFFFFu);
+        const bool clash = lane < k && next_valid &&
+                           (g < g_next || (g == g_next && (lane == k - 1 || (!same_logit && !id_down))));
+        exact = (g << 16) | (top & 0xFFFFu);
+        const bool any_clash = __any(clash);              // the whole wave votes, then lane 0 writes
+        if (lane == 0) *flag = any_clash ? 1 : 0;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
+// Block-wide fallback after spec_check found equal gates: gate_keys' keys from the kept lv / sum.
+// Ends with a barrier.
+template <bool BF16>
+__device__ __forceinline__ void fallback_keys(const double (&lv)[kPer], double sum, int n_exp, uint32_t* keys) {
+    const int tid = threadIdx.x;
+    const int n_pad = ((n_exp + 63) / 64) * 64;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = tid + kThreads * i;
+        if (e < n_pad) keys[e] = (e < n_exp) ? (((uint32_t)rule_from_f64<BF16>(lv[i] / sum) << 16) | (uint32_t)e) : 0u;
+    }
+    __syncthreads();
+}
+
 // One wave, from the k largest keys (lane r holds the r-th largest, wave_topn): the id and score
 // bits that go to output position k - 1 - r (ascending gate order) for lanes r < k; position -1
 // for the other lanes.  The scores are g / s with s the left-to-right sum over ascending order,

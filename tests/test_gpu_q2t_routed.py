@@ -119,3 +119,39 @@ def test_routed_tensor_form_rejects_bad_arguments():
     L.c_clear_error()
     assert call(E, 4) == 0
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4])
+def test_routed_tensor_form_gate_ties_from_distinct_logits(seed):
+    """bf16 logits packed into a band of adjacent values, so that distinct logits round to equal
+    bf16 gates around the k boundary: the blocks' logit ranking gives way to the rule's own
+    selection where the two can differ.  Ids, order and bf16 scores are the oracle's, h is
+    moe_q2t_gate_up's for those ids."""
+    from moe_offload import _lib
+    L = _lib.lib()
+    E, H, I, k = 512, 2560, 640, 10
+    rng = np.random.default_rng(100 + seed)
+    mlx = experts_bf16(E, H, I, seed=21)
+    ts, ptrs, nbytes = _pools(mlx)
+    base = 0x3E80 + 16 * seed                                   # bf16 0.25 and above
+    lg = np.full(E, _bf16(-6.0), dtype=np.uint16)
+    band = rng.choice(E, size=40, replace=False)
+    lg[band] = (base + rng.integers(0, 10, size=40)).astype(np.uint16)
+    logits = _dev(lg, np.int16)
+    x16 = torch.from_numpy(q2.to_f64(_bf16(rng.standard_normal(H)), "bf16").astype(np.float16)).cuda()
+    s = torch.cuda.current_stream().cuda_stream
+    ids = torch.full((k,), -1, dtype=torch.int32, device="cuda")
+    sc = torch.zeros(k, dtype=torch.int16, device="cuda")
+    h = torch.zeros(k * I, dtype=torch.float16, device="cuda")
+    _lib.check(L.moe_q2t_gate_up_routed(x16.data_ptr(), logits.data_ptr(), E, k, ptrs, nbytes, 1, H, I, 64,
+                                        ids.data_ptr(), sc.data_ptr(), h.data_ptr(), s), "q2t_gate_up_routed")
+    torch.cuda.synchronize()
+    want_i, want_s, _ = q2.route(q2.to_f64(lg, "bf16")[None], k, "bf16")
+    assert ids.cpu().numpy().astype(np.int64).tolist() == want_i[0].astype(np.int64).tolist()
+    assert np.array_equal(q2.to_f64(sc.cpu().numpy().view(np.uint16), "bf16"), want_s[0])
+    ids_o = torch.from_numpy(want_i[0].astype(np.int32)).cuda()
+    h_ref = torch.zeros(k * I, dtype=torch.float16, device="cuda")
+    _lib.check(L.moe_q2t_gate_up(x16.data_ptr(), ptrs, nbytes, 1, E, ids_o.data_ptr(), k, H, I, 64, h_ref.data_ptr(), s),
+               "q2t_gate_up")
+    torch.cuda.synchronize()
+    assert torch.equal(h_ref, h)

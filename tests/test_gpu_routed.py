@@ -139,3 +139,36 @@ def test_peaked_softmax_selects_zero_gates_by_descending_id(n_exp, k, peaks):
     _, _, pred = ops.router(wt, k, x=xt, w_next=wt, m=m)
     want_p = q2.predict_topm(q2.router_logits(x, w, "f16")[None], m)
     assert pred.cpu().numpy().tolist() == want_p[0].tolist()
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4])
+def test_routed_selection_gate_ties_from_distinct_logits(seed):
+    """Logits packed into a narrow band of adjacent fp16 values, so that distinct logits round to
+    equal fp16 gates around the k boundary and inside the top k: the gate/up blocks first rank by
+    logit, and where that ranking and the rule's (gate, then id) can differ they take the rule's
+    own selection.  Ids, order and scores are the oracle's, h is moe_q2_gate_up's for those ids."""
+    from moe_offload import _lib, ops
+    L = _lib.lib()
+    n_exp, hidden, inter, k = 512, 2048, 512, 10
+    pool = _pool(n_exp, hidden, inter, seed=11)
+    rng = np.random.default_rng(seed)
+    base = np.float16(0.25 + 0.05 * seed)
+    lg = np.full(n_exp, np.float16(-6.0), dtype=np.float16)
+    band = rng.choice(n_exp, size=40, replace=False)
+    steps = rng.integers(0, 12, size=40)                       # adjacent fp16 values, some repeated
+    lg[band] = (base.view(np.uint16) + steps.astype(np.uint16)).view(np.float16)
+    logits = torch.from_numpy(lg.astype(np.float32)).cuda()
+    x = torch.from_numpy(rng.standard_normal(hidden).astype(np.float16)).cuda()
+    ids = torch.empty(k, dtype=torch.int32, device="cuda")
+    sc = torch.empty(k, dtype=torch.float16, device="cuda")
+    h = torch.empty(k * inter, dtype=torch.float16, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    _lib.check(L.moe_q2_gate_up_routed(x.data_ptr(), logits.data_ptr(), n_exp, k, pool.data_ptr(), pool.shape[1],
+                                       hidden, inter, 64, ids.data_ptr(), sc.data_ptr(), h.data_ptr(), s),
+               "gate_up_routed")
+    torch.cuda.synchronize()
+    want_i, want_s, _ = q2.route(lg.astype(np.float64)[None], k, "f16")
+    assert ids.cpu().numpy().astype(np.int64).tolist() == want_i[0].astype(np.int64).tolist()
+    assert np.array_equal(sc.cpu().numpy().astype(np.float64), want_s[0])
+    h_ref = ops.q2_gate_up(x, pool, torch.from_numpy(want_i[0].astype(np.int32)).cuda(), hidden, inter)
+    assert torch.equal(h_ref.view(-1), h)
