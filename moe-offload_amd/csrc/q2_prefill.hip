@@ -16,7 +16,9 @@
 // 64 codes plus the (scale, bias) word), dequantises it once and multiplies it into every tile
 // of the batch; the chunk's activations of the batch's rows are staged in LDS (each thread
 // stages 2 units of 16 bytes per tile).  The next chunk's weights and activations are loaded
-// while the current chunk is multiplied.
+// while the current chunk is multiplied.  The gate/up grid holds every (segment, slice) item
+// twice: segments of more than one batch run in the first half, so their blocks, the longest,
+// are dispatched before the rest.
 //
 // Dequantisation.  A 2-bit code in the low bits of a nibble is the fp4 (e2m1) value q/2, so
 // w & 0x33333333 (even codes) and (w >> 2) & 0x33333333 (odd codes) are 8 fp4 values each;
@@ -116,7 +118,17 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
     const int K = MODE == kGateUp ? hidden : inter;              // contraction length
     const int N = MODE == kGateUp ? inter : hidden;              // output rows per projection
     const int kg = K / 64;
-    const int work = xcd_order(blockIdx.x, gridDim.x);
+    // Gate/up runs two passes over the (segment, slice) items: the first takes the segments that
+    // need more than one batch of M tiles, whose blocks run longest, so that they are dispatched
+    // first; the second takes the rest (each block of a pass that is not its own exits at once).
+    int work, pass = 0;
+    if constexpr (MODE == kGateUp) {
+        const int items = n_seg * tiles_per_seg;
+        pass = (int)blockIdx.x >= items ? 1 : 0;
+        work = xcd_order((int)blockIdx.x - pass * items, items);
+    } else {
+        work = xcd_order(blockIdx.x, gridDim.x);
+    }
     const int seg = work / tiles_per_seg, tile = work % tiles_per_seg;
     if (seg >= n_seg) return;
     int r0 = seg_start[seg], r1 = seg_start[seg + 1];
@@ -124,6 +136,9 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
     r1 = r1 < r0 ? r0 : (r1 > n_rows ? n_rows : r1);
     const int slot = seg_slot ? seg_slot[seg] : seg;
     if (r1 == r0 || slot < 0 || slot >= n_slots) return;
+    if constexpr (MODE == kGateUp) {
+        if ((pass == 0) != (r1 - r0 > kMT * kMaxMT)) return;
+    }
 
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15, kq = lane >> 4;
@@ -423,7 +438,7 @@ int launch_proj(const __half* src, int n_src_rows, const int32_t* row_map, const
     const int N = MODE == kGateUp ? inter : hidden;
     const int rows_per_block = MODE == kGateUp ? 128 : 256;
     const int tiles = (N + rows_per_block - 1) / rows_per_block;
-    const long long nb = (long long)n_seg * tiles;
+    const long long nb = (MODE == kGateUp ? 2LL : 1LL) * n_seg * tiles;   // gate/up: two passes
     if (nb <= 0) return 0;
     if (nb > 0x7FFFFFFFLL) { moe_set_error("grouped q2: grid too large"); return -1; }
     MOE_LAUNCH(MODE == kGateUp ? TK_PF_GATE_UP : TK_PF_DOWN, (k_q2g_proj<NCH, MODE, SBL, SBF>), dim3((unsigned)nb),
