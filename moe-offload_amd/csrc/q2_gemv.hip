@@ -34,7 +34,13 @@ namespace {
 
 using namespace q2dot;
 
-constexpr int kGuRowsPerIter = 2;   // rows per wave (each iteration covers 32/GPR rows)
+// Row iterations per wave (each covers 32/GPR rows of each projection).  The routed kernel takes 2:
+// every block runs the selection, so fewer, larger blocks pay it less often (resident decode 1,301
+// tok/s against 1,226 with 1).  The plain kernel takes 1: at top-10 its 5,120 waves give every
+// SIMD of the 256 CUs the same count, where 2,560 leave some with 3 and others with 2 (4.35 ->
+// 3.98 us back to back with the decode's inputs).
+template <bool ROUTED>
+constexpr int gu_rows_per_iter() { return ROUTED ? 2 : 1; }
 
 // Rows of gate and up for one selected expert.  ROUTED: the block first selects the top-k
 // experts from the router's logits itself (the router's rule, bit for bit) over a pool holding
@@ -47,6 +53,7 @@ __device__ __forceinline__ void gate_up_body(
     const uint32_t* __restrict__ slots, int n_slots, int inter, const BlobLayout& L, __half* __restrict__ h_out,
     const float* __restrict__ logits, int k, uint32_t* __restrict__ ids_out, __half* __restrict__ scores_out) {
     constexpr int RPI = 32 / GPR;                       // rows per wave instruction
+    constexpr int kGuRowsPerIter = gu_rows_per_iter<ROUTED>();
     constexpr int ROWS_PER_WAVE = RPI * kGuRowsPerIter;
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = blockIdx.y;
@@ -339,7 +346,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void k_q2_down(
 template <int GPR>
 int gate_up_t(const __half* x, const uint8_t* pool, size_t stride, const uint32_t* slots, int n_slots, int k,
               int inter, BlobLayout L, __half* h_out, hipStream_t s) {
-    constexpr int rows_per_block = 4 * (32 / GPR) * kGuRowsPerIter;
+    constexpr int rows_per_block = 4 * (32 / GPR) * gu_rows_per_iter<false>();
     dim3 grid((inter + rows_per_block - 1) / rows_per_block, k);
     MOE_LAUNCH(TK_GATE_UP, (k_q2_gate_up<GPR>), grid, dim3(256), 0, s, x, pool, stride, slots, n_slots, inter, L, h_out);
     HIP_TRY(hipGetLastError());
@@ -349,7 +356,7 @@ int gate_up_t(const __half* x, const uint8_t* pool, size_t stride, const uint32_
 template <int GPR>
 int gate_up_routed_t(const __half* x, const float* logits, int n_exp, int k, const uint8_t* pool, size_t stride,
                      int inter, BlobLayout L, uint32_t* ids_out, __half* scores_out, __half* h_out, hipStream_t s) {
-    constexpr int rows_per_block = 4 * (32 / GPR) * kGuRowsPerIter;
+    constexpr int rows_per_block = 4 * (32 / GPR) * gu_rows_per_iter<true>();
     dim3 grid((inter + rows_per_block - 1) / rows_per_block, k);
     MOE_LAUNCH(TK_GATE_UP, (k_q2_gate_up_routed<GPR>), grid, dim3(256), 0, s, x, logits, n_exp, k, pool, stride, inter, L,
                ids_out, scores_out, h_out);
