@@ -39,8 +39,8 @@ HBM_PEAK_GBS = 8000.0
 # counter run cannot happen inside the bench, so the line names where the figure comes from.
 _TRAFFIC_SRC = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over bench.py --only roofline, scaled by moe_calibrate_copy "
                 "(profiles/decode48_resident_kernels_rocprof.md)")
-KERNEL_TRAFFIC = {"k_q2_gate_up_routed": (6_791_280, _TRAFFIC_SRC), "k_q2_down": (3_511_296, _TRAFFIC_SRC),
-                  "k_router (logits)": (2_370_560, _TRAFFIC_SRC), "k_q2_gate_up": (6_676_480, _TRAFFIC_SRC)}
+KERNEL_TRAFFIC = {"k_q2_gate_up_routed": (6_807_654, _TRAFFIC_SRC), "k_q2_down": (3_511_296, _TRAFFIC_SRC),
+                  "k_router (logits)": (2_370_560, _TRAFFIC_SRC), "k_q2_gate_up": (6_680_576, _TRAFFIC_SRC)}
 
 
 def parse():
