@@ -18,7 +18,9 @@
 // stages 2 units of 16 bytes per tile).  The next chunk's weights and activations are loaded
 // while the current chunk is multiplied.  The gate/up grid holds every (segment, slice) item
 // twice: segments of more than one batch run in the first half, so their blocks, the longest,
-// are dispatched before the rest.
+// are dispatched before the rest.  At K = 2048 gate/up runs in the whole-K form instead
+// (k_q2g_gu_wk: per M tile, each wave's weight subtiles requested over the whole K at once, the
+// tile's activations staged once; the same two-pass grid, long segments first).
 //
 // Dequantisation.  A 2-bit code in the low bits of a nibble is the fp4 (e2m1) value q/2, so
 // w & 0x33333333 (even codes) and (w >> 2) & 0x33333333 (odd codes) are 8 fp4 values each;
@@ -105,6 +107,194 @@ __device__ __forceinline__ uint32_t sb_word(uint32_t sc, uint32_t bi) {
         bi = __half_as_ushort(__float2half_rn(__uint_as_float(bi << 16)));
     }
     return (sc & 0xFFFFu) | (bi << 16);
+}
+
+// Gate/up of one M tile (at most 16 rows r0 .. r0 + rows - 1 of a segment) and one 128-row slice,
+// the weight rows streamed whole: each wave owns two (gate, up) pairs of 16-row subtiles and
+// requests a pair's whole K at once (lane (n, kq) loads groups GPL*kq .. GPL*kq + GPL - 1 of row
+// n: 16 rows x 64 * GPL contiguous bytes per subtile), the second pair's loads issued before the
+// first pair is multiplied.  The tile's activation rows are staged in LDS once for the whole K,
+// already split into the MFMA's even / odd input fragments: one barrier per tile, after which the
+// waves run independently.  A K position of an MFMA pairs lane group kq's group GPL*kq + i with
+// the same inputs on the A side; the even/odd code split inside a word is the one of k_q2g_proj.
+// Bit for bit this is not k_q2g_proj's sum order (another K order inside the MFMAs).
+template <int GPL, int SBF>
+__device__ __forceinline__ void gu_whole_k(const __half* __restrict__ src, int n_src_rows,
+                                           const int32_t* __restrict__ row_map, int r0, int rows, int slot,
+                                           int tile, const Q2Experts& E, int inter, __half* __restrict__ out,
+                                           uint4* __restrict__ a_lds) {
+    constexpr int K = 256 * GPL;
+    constexpr int kg = 4 * GPL;                       // groups per weight row
+    constexpr int UPR = K / 8;                        // 16-byte units per activation row
+    constexpr int kPairsPerThread = UPR / 32;         // unit pairs a thread stages
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));                       // per call: no address is kept across calls
+    const int lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int n = lane & 15, kq = lane >> 4;
+
+    // thread t stages unit pairs (2 pv, 2 pv + 1), pv = (t & 15) + 16 c, of row t >> 4; rows past
+    // the segment and out-of-range source rows are staged as zeros (a_lds: unit v of row m at
+    // m * UPR + (v ^ m), so the 16 lanes reading one unit column hit distinct banks)
+    const int sm = t >> 4, sv0 = t & 15;
+    int srow = -1;
+    if (sm < rows) {
+        srow = row_map ? row_map[r0 + sm] : r0 + sm;
+        if (srow < 0 || srow >= n_src_rows) srow = -1;
+    }
+    uint4 xv[2 * kPairsPerThread];
+    {
+        const uint4* xr = reinterpret_cast<const uint4*>(src + (size_t)(srow < 0 ? 0 : srow) * K);
+#pragma unroll
+        for (int c = 0; c < kPairsPerThread; ++c) {
+            xv[2 * c] = xr[2 * (sv0 + 16 * c)];
+            xv[2 * c + 1] = xr[2 * (sv0 + 16 * c) + 1];
+        }
+    }
+
+    // pair pp: gate and up rows base .. base + 15 (inter is a multiple of 64: a subtile is wholly
+    // in range or wholly out; one that is out re-reads the last subtile and is not written)
+    const Q2Proj& Pg = E.p[0];
+    const Q2Proj& Pu = E.p[1];
+    const size_t code_row = (size_t)K / 4;
+    auto pair_base = [&](int pp) { return tile * 128 + (wv * 2 + pp) * 16; };
+    auto load_pair = [&](int pp, uint4 (&c)[2][GPL], uint32_t (&wd)[2][GPL]) {
+        int base = pair_base(pp);
+        base = base < inter ? base : inter - 16;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const Q2Proj& P = h ? Pu : Pg;
+            const uint8_t* cr = P.w + (size_t)slot * P.w_stride + (size_t)(base + n) * code_row + (size_t)(GPL * kq) * 16;
+#pragma unroll
+            for (int i = 0; i < GPL; ++i) c[h][i] = *reinterpret_cast<const uint4*>(cr + (size_t)i * 16);
+            if constexpr (SBF == 0) {
+                static_assert(GPL % 4 == 0, "whole 16-byte scale/bias pieces");
+                const uint32_t* sr = reinterpret_cast<const uint32_t*>(P.s + (size_t)slot * P.s_stride) +
+                                     (size_t)(base + n) * kg + GPL * kq;
+#pragma unroll
+                for (int i = 0; i < GPL / 4; ++i) {
+                    const uint4 v = reinterpret_cast<const uint4*>(sr)[i];
+                    wd[h][4 * i] = v.x;
+                    wd[h][4 * i + 1] = v.y;
+                    wd[h][4 * i + 2] = v.z;
+                    wd[h][4 * i + 3] = v.w;
+                }
+            } else {
+                static_assert(GPL % 8 == 0, "whole 16-byte scale / bias pieces");
+                const uint16_t* scr = reinterpret_cast<const uint16_t*>(P.s + (size_t)slot * P.s_stride) +
+                                      (size_t)(base + n) * kg + GPL * kq;
+                const uint16_t* bir = reinterpret_cast<const uint16_t*>(P.b + (size_t)slot * P.b_stride) +
+                                      (size_t)(base + n) * kg + GPL * kq;
+#pragma unroll
+                for (int i = 0; i < GPL / 8; ++i) {
+                    const uint4 sc = reinterpret_cast<const uint4*>(scr)[i];
+                    const uint4 bi = reinterpret_cast<const uint4*>(bir)[i];
+                    const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w}, biw[4] = {bi.x, bi.y, bi.z, bi.w};
+#pragma unroll
+                    for (int k2 = 0; k2 < 4; ++k2) {
+                        wd[h][8 * i + 2 * k2] = sb_word<SBF>(scw[k2] & 0xFFFFu, biw[k2] & 0xFFFFu);
+                        wd[h][8 * i + 2 * k2 + 1] = sb_word<SBF>(scw[k2] >> 16, biw[k2] >> 16);
+                    }
+                }
+            }
+        }
+    };
+    auto multiply = [&](int pp, const uint4 (&c)[2][GPL], const uint32_t (&wd)[2][GPL]) {
+        f32x4 accg = (f32x4){0.f, 0.f, 0.f, 0.f}, accu = (f32x4){0.f, 0.f, 0.f, 0.f};
+        const uint4* arow = a_lds + n * UPR;
+#pragma unroll
+        for (int i = 0; i < GPL; ++i) {
+            f16x2 s2[2], b2[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const f16x2 sb = __builtin_bit_cast(f16x2, wd[h][i]);
+                const _Float16 two_s = sb.x * (_Float16)2.0f;
+                s2[h] = (f16x2){two_s, two_s};
+                b2[h] = (f16x2){sb.y, sb.y};
+            }
+            const int u0 = 8 * (GPL * kq + i);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int v = u0 + 2 * q;
+                const f16x8 a_ev = __builtin_bit_cast(f16x8, arow[v ^ n]);
+                const f16x8 a_od = __builtin_bit_cast(f16x8, arow[(v + 1) ^ n]);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint4 cv = c[h][i];
+                    const uint32_t wq = q == 0 ? cv.x : q == 1 ? cv.y : q == 2 ? cv.z : cv.w;
+                    const f16x8 b_ev = dequant8(wq & 0x33333333u, s2[h], b2[h]);
+                    const f16x8 b_od = dequant8((wq >> 2) & 0x33333333u, s2[h], b2[h]);
+                    f32x4& acc = h ? accu : accg;
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_ev, b_ev, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_od, b_od, acc, 0, 0, 0);
+                }
+            }
+        }
+        // lane holds rows 4 kq + i of column n
+        const int base = pair_base(pp);
+        if (base < inter) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 4 * kq + i;
+                if (m < rows) {
+                    const float g = accg[i], u = accu[i];
+                    out[(size_t)(r0 + m) * inter + base + n] = __float2half_rn(g / (1.0f + __expf(-g)) * u);
+                }
+            }
+        }
+    };
+
+    uint4 cw0[2][GPL], cw1[2][GPL];
+    uint32_t sw0[2][GPL], sw1[2][GPL];
+    load_pair(0, cw0, sw0);                           // after the activations: those retire first
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < kPairsPerThread; ++c) {
+        const int v = 2 * (sv0 + 16 * c);
+        f16x8 ev, od;
+        split_even_odd(xv[2 * c], xv[2 * c + 1], ev, od);
+        const uint4 e4 = __builtin_bit_cast(uint4, ev), o4 = __builtin_bit_cast(uint4, od);
+        a_lds[sm * UPR + (v ^ sm)] = srow >= 0 ? e4 : make_uint4(0, 0, 0, 0);
+        a_lds[sm * UPR + ((v + 1) ^ sm)] = srow >= 0 ? o4 : make_uint4(0, 0, 0, 0);
+    }
+    lds_barrier();
+    load_pair(1, cw1, sw1);
+    __builtin_amdgcn_sched_barrier(0);                // pair 1's loads go out before pair 0's multiply
+    multiply(0, cw0, sw0);
+    // both pairs read the same activation fragments; without this fence the compiler keeps pair
+    // 0's 256 fragment registers for pair 1 and spills
+    asm volatile("" ::: "memory");
+    multiply(1, cw1, sw1);
+}
+
+template <int GPL, int SBF>
+__global__ __launch_bounds__(256, 2) void k_q2g_gu_wk(
+    const __half* __restrict__ src, int n_src_rows, const int32_t* __restrict__ row_map,
+    const int32_t* __restrict__ seg_start, const int32_t* __restrict__ seg_slot, int n_seg, int n_rows,
+    Q2Experts E, int n_slots, int inter, int tiles_per_seg, __half* __restrict__ out) {
+    __shared__ uint4 a_lds[16 * 32 * GPL];
+    // two passes over the (segment, slice) items: segments of more than one M tile first (their
+    // blocks run longest); a block takes its segment's tiles one after the other, each tile's
+    // weights loaded again (from L2 while they are still there), since both pairs' weights held
+    // across tiles would not fit beside a tile's staging
+    const int items = n_seg * tiles_per_seg;
+    const int pass = (int)blockIdx.x >= items ? 1 : 0;
+    const int work = xcd_order((int)blockIdx.x - pass * items, items);
+    const int seg = work / tiles_per_seg, tile = work % tiles_per_seg;
+    if (seg >= n_seg) return;
+    int r0 = seg_start[seg], r1 = seg_start[seg + 1];
+    r0 = r0 < 0 ? 0 : (r0 > n_rows ? n_rows : r0);
+    r1 = r1 < r0 ? r0 : (r1 > n_rows ? n_rows : r1);
+    const int slot = seg_slot ? seg_slot[seg] : seg;
+    if (r1 == r0 || slot < 0 || slot >= n_slots) return;
+    if ((pass == 0) != (r1 - r0 > kMT)) return;
+#pragma unroll 1
+    for (int m0 = r0; m0 < r1; m0 += kMT) {          // block-uniform
+        if (m0 > r0) __syncthreads();                // every wave is done with the previous tile
+        int slot_i = slot;                           // opaque: the weights are loaded again per tile
+        asm volatile("" : "+s"(slot_i) : : "memory");
+        gu_whole_k<GPL, SBF>(src, n_src_rows, row_map, m0, (r1 - m0) < kMT ? (r1 - m0) : kMT, slot_i, tile, E, inter,
+                             out, a_lds);
+    }
 }
 
 template <int NCH, int MODE, bool SBL, int SBF>
@@ -441,9 +631,15 @@ int launch_proj(const __half* src, int n_src_rows, const int32_t* row_map, const
     const long long nb = (MODE == kGateUp ? 2LL : 1LL) * n_seg * tiles;   // gate/up: two passes
     if (nb <= 0) return 0;
     if (nb > 0x7FFFFFFFLL) { moe_set_error("grouped q2: grid too large"); return -1; }
-    MOE_LAUNCH(MODE == kGateUp ? TK_PF_GATE_UP : TK_PF_DOWN, (k_q2g_proj<NCH, MODE, SBL, SBF>), dim3((unsigned)nb),
-               dim3(256), 0, s, src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg, n_rows, E,
-               n_slots, hidden, inter, tiles, out);
+    if constexpr (MODE == kGateUp && SBL && NCH == 8) {
+        // K = 2048: the whole-K form (128 rows per block, as here)
+        MOE_LAUNCH(TK_PF_GATE_UP, (k_q2g_gu_wk<NCH, SBF>), dim3((unsigned)nb), dim3(256), 0, s, src, n_src_rows, row_map,
+                   seg_start, seg_slot, n_seg, n_rows, E, n_slots, inter, tiles, out);
+    } else {
+        MOE_LAUNCH(MODE == kGateUp ? TK_PF_GATE_UP : TK_PF_DOWN, (k_q2g_proj<NCH, MODE, SBL, SBF>), dim3((unsigned)nb),
+                   dim3(256), 0, s, src, n_src_rows, row_map, row_out, n_out_rows, seg_start, seg_slot, n_seg, n_rows,
+                   E, n_slots, hidden, inter, tiles, out);
+    }
     HIP_TRY(hipGetLastError());
     return 0;
 }
