@@ -20,7 +20,9 @@
 // twice: segments of more than one batch run in the first half, so their blocks, the longest,
 // are dispatched before the rest.  At K = 2048 gate/up runs in the whole-K form instead
 // (k_q2g_gu_wk: per M tile, each wave's weight subtiles requested over the whole K at once, the
-// tile's activations staged once; the same two-pass grid, long segments first).
+// tile's activations staged once; the same two-pass grid, long segments first).  At K = 512 down
+// runs in the whole-K form as well (k_q2g_dn_wk: each wave's 4 subtiles loaded once over the whole
+// K and kept in registers while the segment's M tiles pass through LDS; two-pass grid).
 //
 // Dequantisation.  A 2-bit code in the low bits of a nibble is the fp4 (e2m1) value q/2, so
 // w & 0x33333333 (even codes) and (w >> 2) & 0x33333333 (odd codes) are 8 fp4 values each;
@@ -621,6 +623,148 @@ __global__ __launch_bounds__(256, 2) void k_q2g_proj(
     }
 }
 
+
+// Down in the whole-K form (K = inter = 256 * GPL): a block takes one segment and 256 output rows,
+// each wave 4 subtiles of 16 rows whose whole K it requests at once and keeps in registers while
+// the segment's 16-row tiles of h pass through LDS (staged for the whole K, split into the MFMA's
+// even / odd fragments; one barrier per tile).  Output row r goes to row_out[r] (or r).
+template <int GPL, int SBF>
+__global__ __launch_bounds__(256, 2) void k_q2g_dn_wk(
+    const __half* __restrict__ src, int n_src_rows, const int32_t* __restrict__ row_out, int n_out_rows,
+    const int32_t* __restrict__ seg_start, const int32_t* __restrict__ seg_slot, int n_seg, int n_rows,
+    Q2Experts E, int n_slots, int hidden, int tiles_per_seg, __half* __restrict__ out) {
+    constexpr int K = 256 * GPL;
+    constexpr int kg = 4 * GPL;
+    constexpr int UPR = K / 8;                        // 16-byte units per h row
+    constexpr int kPairsPerThread = UPR / 32;         // unit pairs a thread stages per tile
+    static_assert(kPairsPerThread >= 1, "K >= 256");
+    __shared__ uint4 a_lds[16 * UPR];
+    const int items = n_seg * tiles_per_seg;
+    const int pass = (int)blockIdx.x >= items ? 1 : 0;
+    const int work = xcd_order((int)blockIdx.x - pass * items, items);
+    const int seg = work / tiles_per_seg, tile = work % tiles_per_seg;
+    if (seg >= n_seg) return;
+    int r0 = seg_start[seg], r1 = seg_start[seg + 1];
+    r0 = r0 < 0 ? 0 : (r0 > n_rows ? n_rows : r0);
+    r1 = r1 < r0 ? r0 : (r1 > n_rows ? n_rows : r1);
+    const int slot = seg_slot ? seg_slot[seg] : seg;
+    if (r1 == r0 || slot < 0 || slot >= n_slots) return;
+    if ((pass == 0) != (r1 - r0 > kMT)) return;       // segments of several tiles first
+
+    const int t0 = threadIdx.x, lane0 = t0 & 63, wv = __builtin_amdgcn_readfirstlane(t0 >> 6);
+    const int n0 = lane0 & 15, kq0 = lane0 >> 4;
+    const Q2Proj& P = E.p[2];
+    const size_t code_row = (size_t)K / 4;
+    // the wave's 4 subtiles: output rows base_s .. base_s + 15 (hidden is a multiple of 64)
+    uint4 cw[4][GPL];
+    uint32_t sw[4][GPL];
+    bool rv[4];
+    int col[4];
+#pragma unroll
+    for (int sIdx = 0; sIdx < 4; ++sIdx) {
+        int base = tile * 256 + wv * 64 + sIdx * 16;
+        rv[sIdx] = base < hidden;
+        col[sIdx] = base + n0;
+        if (base >= hidden) base = hidden - 16;
+        const uint8_t* cr = P.w + (size_t)slot * P.w_stride + (size_t)(base + n0) * code_row + (size_t)(GPL * kq0) * 16;
+#pragma unroll
+        for (int i = 0; i < GPL; ++i) cw[sIdx][i] = *reinterpret_cast<const uint4*>(cr + (size_t)i * 16);
+        if constexpr (SBF == 0) {
+            const uint32_t* sr = reinterpret_cast<const uint32_t*>(P.s + (size_t)slot * P.s_stride) +
+                                 (size_t)(base + n0) * kg + GPL * kq0;
+#pragma unroll
+            for (int i = 0; i < GPL; ++i) sw[sIdx][i] = sr[i];
+        } else {
+            const uint16_t* scr = reinterpret_cast<const uint16_t*>(P.s + (size_t)slot * P.s_stride) +
+                                  (size_t)(base + n0) * kg + GPL * kq0;
+            const uint16_t* bir = reinterpret_cast<const uint16_t*>(P.b + (size_t)slot * P.b_stride) +
+                                  (size_t)(base + n0) * kg + GPL * kq0;
+#pragma unroll
+            for (int i = 0; i < GPL; ++i) sw[sIdx][i] = sb_word<SBF>(scr[i], bir[i]);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int sm = t0 >> 4, sv0 = t0 & 15;
+#pragma unroll 1
+    for (int m0 = r0; m0 < r1; m0 += kMT) {          // block-uniform
+        const int rows_t = (r1 - m0) < kMT ? (r1 - m0) : kMT;
+        int srow = -1;
+        if (sm < rows_t) {
+            srow = m0 + sm;
+            if (srow >= n_src_rows) srow = -1;
+        }
+        uint4 xv[2 * kPairsPerThread];
+        const uint4* xr = reinterpret_cast<const uint4*>(src + (size_t)(srow < 0 ? 0 : srow) * K);
+#pragma unroll
+        for (int c = 0; c < kPairsPerThread; ++c) {
+            xv[2 * c] = xr[2 * (sv0 + 16 * c)];
+            xv[2 * c + 1] = xr[2 * (sv0 + 16 * c) + 1];
+        }
+        if (m0 > r0) lds_barrier();                   // every wave is done with the last tile
+#pragma unroll
+        for (int c = 0; c < kPairsPerThread; ++c) {
+            const int v = 2 * (sv0 + 16 * c);
+            f16x8 ev, od;
+            split_even_odd(xv[2 * c], xv[2 * c + 1], ev, od);
+            const uint4 e4 = __builtin_bit_cast(uint4, ev), o4 = __builtin_bit_cast(uint4, od);
+            a_lds[sm * UPR + (v ^ sm)] = srow >= 0 ? e4 : make_uint4(0, 0, 0, 0);
+            a_lds[sm * UPR + ((v + 1) ^ sm)] = srow >= 0 ? o4 : make_uint4(0, 0, 0, 0);
+        }
+        lds_barrier();
+        // opaque per tile: the converted weights and the fragment addresses are not kept across
+        // tiles
+        uint32_t z;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+        int tq = (int)threadIdx.x;
+        asm volatile("" : "+v"(tq));
+        const int n = tq & 15, kq = (tq & 63) >> 4;
+        f32x4 acc[4];
+#pragma unroll
+        for (int sIdx = 0; sIdx < 4; ++sIdx) acc[sIdx] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        const uint4* arow = a_lds + n * UPR;
+#pragma unroll
+        for (int i = 0; i < GPL; ++i) {
+            f16x2 s2[4], b2[4];
+#pragma unroll
+            for (int sIdx = 0; sIdx < 4; ++sIdx) {
+                const f16x2 sb = __builtin_bit_cast(f16x2, sw[sIdx][i] ^ z);
+                const _Float16 two_s = sb.x * (_Float16)2.0f;
+                s2[sIdx] = (f16x2){two_s, two_s};
+                b2[sIdx] = (f16x2){sb.y, sb.y};
+            }
+            const int u0 = 8 * (GPL * kq + i);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int v = u0 + 2 * q;
+                const f16x8 a_ev = __builtin_bit_cast(f16x8, arow[v ^ n]);
+                const f16x8 a_od = __builtin_bit_cast(f16x8, arow[(v + 1) ^ n]);
+#pragma unroll
+                for (int sIdx = 0; sIdx < 4; ++sIdx) {
+                    const uint4 cv = cw[sIdx][i];
+                    const uint32_t wq = (q == 0 ? cv.x : q == 1 ? cv.y : q == 2 ? cv.z : cv.w) ^ z;
+                    const f16x8 b_ev = dequant8(wq & 0x33333333u, s2[sIdx], b2[sIdx]);
+                    const f16x8 b_od = dequant8((wq >> 2) & 0x33333333u, s2[sIdx], b2[sIdx]);
+                    acc[sIdx] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_ev, b_ev, acc[sIdx], 0, 0, 0);
+                    acc[sIdx] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_od, b_od, acc[sIdx], 0, 0, 0);
+                }
+            }
+        }
+        // lane holds rows 4 kq + i of column n of each subtile
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * kq + i;
+            if (m >= rows_t) continue;
+            const int r = m0 + m;
+            const int orow = row_out ? row_out[r] : r;
+            if (orow < 0 || orow >= n_out_rows) continue;
+#pragma unroll
+            for (int sIdx = 0; sIdx < 4; ++sIdx)
+                if (rv[sIdx]) out[(size_t)orow * hidden + col[sIdx]] = __float2half_rn(acc[sIdx][i]);
+        }
+    }
+}
+
 template <int NCH, int MODE, bool SBL, int SBF>
 int launch_proj(const __half* src, int n_src_rows, const int32_t* row_map, const int32_t* row_out, int n_out_rows,
                 const int32_t* seg_start, const int32_t* seg_slot, int n_seg, int n_rows, const Q2Experts& E,
@@ -628,10 +772,16 @@ int launch_proj(const __half* src, int n_src_rows, const int32_t* row_map, const
     const int N = MODE == kGateUp ? inter : hidden;
     const int rows_per_block = MODE == kGateUp ? 128 : 256;
     const int tiles = (N + rows_per_block - 1) / rows_per_block;
-    const long long nb = (MODE == kGateUp ? 2LL : 1LL) * n_seg * tiles;   // gate/up: two passes
+    // K = 512 exactly (whole 256-wide chunks): down in the whole-K form
+    const bool dn_wk = MODE == kDown && NCH == 2 && !SBL && inter == 256 * NCH;
+    const long long nb = (MODE == kGateUp || dn_wk ? 2LL : 1LL) * n_seg * tiles;   // two passes
     if (nb <= 0) return 0;
     if (nb > 0x7FFFFFFFLL) { moe_set_error("grouped q2: grid too large"); return -1; }
-    if constexpr (MODE == kGateUp && SBL && NCH == 8) {
+    if (dn_wk) {
+        if constexpr (MODE == kDown && NCH == 2 && !SBL)
+            MOE_LAUNCH(TK_PF_DOWN, (k_q2g_dn_wk<NCH, SBF>), dim3((unsigned)nb), dim3(256), 0, s, src, n_src_rows, row_out,
+                       n_out_rows, seg_start, seg_slot, n_seg, n_rows, E, n_slots, hidden, tiles, out);
+    } else if constexpr (MODE == kGateUp && SBL && NCH == 8) {
         // K = 2048: the whole-K form (128 rows per block, as here)
         MOE_LAUNCH(TK_PF_GATE_UP, (k_q2g_gu_wk<NCH, SBF>), dim3((unsigned)nb), dim3(256), 0, s, src, n_src_rows, row_map,
                    seg_start, seg_slot, n_seg, n_rows, E, n_slots, inter, tiles, out);
