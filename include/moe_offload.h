@@ -79,7 +79,9 @@ void c_layer_start_prefetch12(int layer_idx, int max_fetch, int32_t e0, int32_t 
 /* expert_io.c:522-525.  Joins every in-flight copy on the GPU side: the compute stream waits;
  * the host does not block (c_sync_copies blocks). */
 void c_layer_wait_prefetch(int layer_idx);
-/* expert_io.c:710-724.  Blocking copy of (eid -> slot) pairs; counts prefill bytes. */
+/* expert_io.c:710-724.  Blocking copy of (eid -> slot) pairs; counts prefill bytes.  From a
+ * pinned store the copies run as a CU copy kernel (reads of the mapped store) on the copy
+ * stream; from a file-backed store through the reader threads. */
 void c_layer_load_sync(int layer_idx, const int32_t* eids, const int32_t* slots, int count,
                        int is_prefill);
 /* expert_io.c:726-747.  LRU -> MRU order. */

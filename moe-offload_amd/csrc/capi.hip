@@ -365,8 +365,31 @@ int issue_file_batch(LayerState& L, const int32_t* eids, const int32_t* slots, i
 // is ordered after nothing on g_copy, so when this batch writes a slot that an earlier batch's
 // copy may still be writing (a demand victim that a prefetch is filling, or a prefill chunk's
 // load after an in-flight prefetch), the g_copy_more streams first wait for that batch.
+// The layer's tensors as one StageSet over the device-visible store, when every tensor that is
+// copied has one (a pinned store) and whole 16-byte units.
+bool cu_stage_set(const LayerState& L, StageSet& S) {
+    S = {};
+    uint64_t units = 0;
+    for (int t = 0; t < MOE_NUM_TENSORS; ++t) {
+        const uint64_t rb = L.row_bytes[t];
+        if (!rb || !L.src[t] || !L.dst[t]) continue;
+        if (!L.dev_src[t] || rb % 16) return false;
+        S.src[S.n] = (const uint8_t*)L.dev_src[t];
+        S.dst[S.n] = (uint8_t*)L.dst[t];
+        S.src_stride[S.n] = S.dst_stride[S.n] = rb;
+        S.first[S.n] = (uint32_t)units;
+        units += rb / 16;
+        ++S.n;
+    }
+    if (S.n == 0 || units > 0xFFFFFFFFull) return false;
+    S.total = (uint32_t)units;
+    return true;
+}
+
+// cu_copy: a pinned store's copies run as one CU copy kernel on g_copy (k_stage_pairs) instead of
+// DMA requests, for the synchronous loads of a prefill chunk (tens of experts, each a ~1 MB run).
 int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* slots, int n,
-                 bool prefetch = false) {
+                 bool prefetch = false, bool cu_copy = false) {
     if (n <= 0) return 0;
     bool any = false;
     for (int t = 0; t < MOE_NUM_TENSORS; ++t) any |= (L.row_bytes[t] && L.src[t] && L.dst[t]);
@@ -384,8 +407,13 @@ int issue_copies(int layer, LayerState& L, const int32_t* eids, const int32_t* s
     if (L.inflight)
         for (int i = 0; i < n && !overlap; ++i) overlap = (L.inflight_slots[slots[i] >> 6] >> (slots[i] & 63)) & 1u;
     if (L.read_recorded) HIP_TRY(hipStreamWaitEvent(g_copy, L.read_done, 0));
+    StageSet S;
     if (L.fd >= 0) {
         if (issue_file_batch(L, eids, slots, n, prefetch)) return -1;
+    } else if (cu_copy && cu_stage_set(L, S)) {
+        // g_copy runs in queue order after the layer's earlier batches (their g_copy_more copies
+        // were joined into g_copy) and after read_done
+        if (launch_stage_pairs(eids, slots, n, S, g_copy)) return -1;
     } else {
         for (int i = 0; i < kCopyStreams - 1; ++i) {
             if (L.read_recorded) HIP_TRY(hipStreamWaitEvent(g_copy_more[i], L.read_done, 0));
@@ -757,7 +785,7 @@ void c_layer_load_sync(int layer, const int32_t* eids, const int32_t* slots, int
     if (is_prefill) L.tab.stats[ST_PRE_BYTES] += (uint64_t)n * L.tab.expert_bytes;
     slot_host::count_runs(&L.tab, eids, n);
     if (push_table(L)) return;
-    if (issue_copies(layer, L, eids, slots, n)) return;
+    if (issue_copies(layer, L, eids, slots, n, false, true)) return;
     if (drain_copies(L)) return;
     wait_copies_gpu(L, g_compute);
 }

@@ -269,6 +269,9 @@ struct StageSet {
     int n;
 };
 int launch_stage_set(const SlotTable* t, int list, const StageSet& S, int ctas, hipStream_t s);
+// Copies store[eids[i]] -> pool[slots[i]] for i < n over the tensors of S with CU loads from the
+// mapped pinned store (the pairs travel in the kernel arguments, kStagePairsMax per launch).
+int launch_stage_pairs(const int32_t* eids, const int32_t* slots, int n, const StageSet& S, hipStream_t s);
 int launch_store_u32(uint32_t* dst, const uint32_t* vals, int n, hipStream_t s);
 // slots_out[0..n_hit) / [16..16+n_miss): hit / miss slots; scores_out likewise, gathered from
 // the step's scores (router order) through inv.

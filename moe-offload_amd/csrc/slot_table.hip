@@ -107,6 +107,41 @@ __global__ __launch_bounds__(256) void k_stage_set(const SlotTable* __restrict__
     }
 }
 
+// Host-listed copies (a synchronous load of a prefill chunk's experts): copy c of the launch
+// moves expert P.eid[c] to slot P.slot[c] over every tensor of S, blockIdx.x striding over the
+// expert's 16-byte units as in k_stage_set.
+constexpr int kStagePairsMax = 128;
+struct StagePairs {
+    int32_t eid[kStagePairsMax];
+    int32_t slot[kStagePairsMax];
+    int n;
+};
+
+__global__ __launch_bounds__(256) void k_stage_pairs(StagePairs P, StageSet S) {
+    const int c = blockIdx.y;
+    if (c >= P.n) return;
+    const int eid = P.eid[c], slot = P.slot[c];
+    const unsigned units = S.total;
+    const unsigned step = gridDim.x * blockDim.x;
+    for (unsigned u = blockIdx.x * blockDim.x + threadIdx.x; u < units; u += 4 * step) {
+        const bool m1 = u + step < units, m2 = u + 2 * step < units, m3 = u + 3 * step < units;
+        const uint4 *s0, *s1 = nullptr, *s2 = nullptr, *s3 = nullptr;
+        uint4 *d0, *d1 = nullptr, *d2 = nullptr, *d3 = nullptr;
+        stage_unit(S, u, eid, slot, s0, d0);
+        if (m1) stage_unit(S, u + step, eid, slot, s1, d1);
+        if (m2) stage_unit(S, u + 2 * step, eid, slot, s2, d2);
+        if (m3) stage_unit(S, u + 3 * step, eid, slot, s3, d3);
+        uint4 a = *s0, b = {}, cc = {}, d = {};
+        if (m1) b = *s1;
+        if (m2) cc = *s2;
+        if (m3) d = *s3;
+        *d0 = a;
+        if (m1) *d1 = b;
+        if (m2) *d2 = cc;
+        if (m3) *d3 = d;
+    }
+}
+
 // Plain device copy of a known byte count: the reference reading for scaling memory counters
 // (FETCH_SIZE / WRITE_SIZE per dispatch) to bytes.
 __global__ __launch_bounds__(256) void k_copy_calib(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16) {
@@ -217,6 +252,23 @@ int launch_stage(const SlotTable* t, int list, const uint8_t* store, size_t stor
     MOE_LAUNCH(TK_STAGE, k_stage, dim3(ctas, MOE_MAX_PREFETCH), dim3(256), 0, s, t, list, store, store_stride,
                pool, pool_stride, bytes);
     HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+int launch_stage_pairs(const int32_t* eids, const int32_t* slots, int n, const StageSet& S, hipStream_t s) {
+    if (S.n <= 0 || S.n > MOE_NUM_TENSORS) { moe_set_error("stage_pairs: %d tensors", S.n); return -1; }
+    for (int i0 = 0; i0 < n; i0 += kStagePairsMax) {
+        StagePairs P;
+        P.n = n - i0 < kStagePairsMax ? n - i0 : kStagePairsMax;
+        for (int i = 0; i < P.n; ++i) {
+            P.eid[i] = eids[i0 + i];
+            P.slot[i] = slots[i0 + i];
+        }
+        // ~32 blocks over the launch's copies keep the link busy (each block has 16 KB in flight)
+        const int ctas = P.n >= 32 ? 1 : (32 + P.n - 1) / P.n;
+        MOE_LAUNCH(TK_STAGE, k_stage_pairs, dim3(ctas, P.n), dim3(256), 0, s, P, S);
+        HIP_TRY(hipGetLastError());
+    }
     return 0;
 }
 
