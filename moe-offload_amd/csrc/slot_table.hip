@@ -264,8 +264,9 @@ int launch_stage_pairs(const int32_t* eids, const int32_t* slots, int n, const S
             P.eid[i] = eids[i0 + i];
             P.slot[i] = slots[i0 + i];
         }
-        // ~32 blocks over the launch's copies keep the link busy (each block has 16 KB in flight)
-        const int ctas = P.n >= 32 ? 1 : (32 + P.n - 1) / P.n;
+        // ~128 blocks over the launch's copies, 16 KB in flight each (a prefill chunk's ~100
+        // copies: 9.6 ms per chunk through a 102-slot layer against 9.8 with ~32 or ~512 blocks)
+        const int ctas = P.n >= 128 ? 1 : (128 + P.n - 1) / P.n;
         MOE_LAUNCH(TK_STAGE, k_stage_pairs, dim3(ctas, P.n), dim3(256), 0, s, P, S);
         HIP_TRY(hipGetLastError());
     }
