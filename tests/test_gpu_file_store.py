@@ -277,20 +277,28 @@ def test_reference_shard_in_pinned_host_memory(tmp_path, mode):
         store.close()
 
 
-def test_reference_shard_prefill(tmp_path):
+@pytest.mark.parametrize("kind", ["file", "pinned"])
+def test_reference_shard_prefill(tmp_path, kind):
     """Prefill through a layer bound to the reference's shard (9 tensors, bf16 scales, 2560 x 640):
     the grouped kernels read the 9 pools; outputs, LRU state, counters and pool contents follow
-    the oracle's prefill plan after a few decode steps."""
+    the oracle's prefill plan after a few decode steps.  file: the chunk loads are reads of the
+    shard by the reader threads; pinned: the shard in pinned host memory, the chunk loads one CU
+    copy kernel over the 9 tensors."""
     from moe_offload import _lib
-    from moe_offload.loader import CachedSwitchGLU, ShardExpertStore
-    Hs, Is, Es, cap, layer = 2560, 640, 40, 16, 38
+    from moe_offload.loader import CachedSwitchGLU, HostShardStore, ShardExpertStore
+    Hs, Is, Es, cap = 2560, 640, 40, 16
+    layer = 38 if kind == "file" else 39
+    print(f"reference shard prefill: store={kind}", flush=True)
     mlx = experts_bf16(Es, Hs, Is, seed=51)
     write_reference_shard(tmp_path / f"experts-{layer:02d}.safetensors", layer, mlx)
     want_rows = role_arrays(mlx)
     dev = torch.device("cuda:0")
     L = _lib.lib()
     L.c_io_init(8)
-    store = ShardExpertStore(tmp_path, layers=[layer])
+    if kind == "file":
+        store = ShardExpertStore(tmp_path, layers=[layer])
+    else:
+        store = HostShardStore(tmp_path, layers=[layer], threads=4)
     mod = None
     try:
         mod = CachedSwitchGLU(store, layer, cap)
@@ -307,8 +315,15 @@ def test_reference_shard_prefill(tmp_path):
         px = rng.standard_normal((n_tok, Hs)).astype(np.float16)
         e0, s0 = ora.get_state()
         plan = q2.prefill_plan(pids.reshape(-1), e0, s0, cap)
+        _lib.check(L.c_timing_begin(4096), "timing_begin")
         y = mod(torch.from_numpy(px).to(dev)[None], torch.from_numpy(pids).to(dev)[None])
         torch.cuda.synchronize()
+        ms, nk = (ctypes.c_double * 11)(), (ctypes.c_int * 11)()
+        _lib.check(L.c_timing_end(ms, nk), "timing_end")
+        n_loads = sum(1 for _, _, le, _ in plan["chunks"] if le)
+        assert n_loads > 0
+        # kind 3: staging kernels -- the pinned store's chunk loads, none for the file's reads
+        assert (nk[3] >= n_loads) if kind == "pinned" else (nk[3] == 0), (kind, nk[3], n_loads)
         yh = y[0].reshape(n_tok * K, Hs).cpu().numpy().astype(np.float64)
         flat = pids.reshape(-1)
         f = lambda e: tuple((p[0][e], p[1][e], p[2][e]) for p in mlx)
