@@ -649,15 +649,21 @@ def decode_kernel_loops(st, rounds=4, repeats=3):
                                  st.ids[l].data_ptr(), st.scores[l].data_ptr(), c.top_k, c.hidden, c.inter, c.group,
                                  st.xs[l].data_ptr(), st.hs[l].data_ptr(), 0, s), "down")
 
-    kernels = [("k_router (logits)", router, rt_b), ("k_q2_gate_up_routed", gate_up, gu_b),
-               ("k_q2_down", down, dn_b)]
+    import torch
+    kernels = [("k_router (logits)", router, rt_b, "router"), ("k_q2_gate_up_routed", gate_up, gu_b, "gate_up"),
+               ("k_q2_down", down, dn_b, "down")]
     out = {}
     n = rounds * c.n_layers
-    for name, fn, nbytes in kernels:
+    for name, fn, nbytes, kind in kernels:
         per = graph_loop_us(fn, n, repeats)
         us = sorted(per)[len(per) // 2]
+        # each launch's own span: start/stop events stamped at the kernel's begin and end, the
+        # same launches issued eagerly (what a profiler's per-dispatch duration measures)
+        stream = torch.cuda.current_stream().cuda_stream
+        d_us = timed_kernels(lambda i: fn(i, stream), n, 1)[kind]["avg_us"]
         out[name] = {"us": round(us, 3), "loops": [round(v, 3) for v in per], "bytes_per_launch": nbytes,
                      "gb_s": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                     "dispatch_us": round(d_us, 3), "dispatch_frac": round(nbytes / d_us / 1e3 / HBM_PEAK_GBS, 4),
                      "launches": n, "traffic": KERNEL_TRAFFIC.get(name, (None,))[0]}
     return out
 
@@ -1073,7 +1079,8 @@ def main():
         measured_in = (f"resident decode (all experts in HBM): {dec[rk]['launches']} launches back to back over the "
                        f"{cfg.n_layers} layers with the decode's own per-layer inputs, bracketed by HIP events on the "
                        "launch stream; median of 3 such runs (every kernel of the decode: resident."
-                       "decode_kernels_back_to_back)")
+                       "decode_kernels_back_to_back, whose dispatch_us is the same launches issued one by one, each "
+                       "timed by start/stop events stamped at the kernel's own begin and end)")
     else:
         rk, r_bytes, r_us = "k_q2_gate_up", gu_bytes, gu_avg * 1e6
         measured_in = "isolated k_q2_gate_up loop (resident.gemv_back_to_back_us)"
@@ -1106,6 +1113,7 @@ def main():
                      "traffic_source": traffic[1] if traffic else None,
                      "kernel": rk, "measured_in": measured_in,
                      "bytes_per_launch": r_bytes, "avg_launch_us": round(r_us, 3),
+                     "dispatch_us": dec[rk]["dispatch_us"] if dec else None,
                      "launch_floor_us": round(floor_us, 3),
                      "frac_of_launch_floor": round(floor_us / r_us, 4)},
         "cache": {"effective_hit_rate": round((tot1[0] - tot0[0] + tot1[1] - tot0[1]) / req, 4),
