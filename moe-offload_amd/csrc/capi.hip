@@ -785,7 +785,23 @@ void c_layer_load_sync(int layer, const int32_t* eids, const int32_t* slots, int
     if (is_prefill) L.tab.stats[ST_PRE_BYTES] += (uint64_t)n * L.tab.expert_bytes;
     slot_host::count_runs(&L.tab, eids, n);
     if (push_table(L)) return;
-    if (issue_copies(layer, L, eids, slots, n, false, true)) return;
+    // Copied one after the other, the last pair naming a slot decides what it holds; the copies
+    // here run concurrently, so only that pair is copied.
+    std::vector<int32_t> ce, cs;
+    ce.reserve(n);
+    cs.reserve(n);
+    uint64_t seen[MOE_NUM_EXPERTS / 64] = {};
+    for (int i = n - 1; i >= 0; --i) {
+        uint64_t& w = seen[slots[i] >> 6];
+        const uint64_t bit = 1ull << (slots[i] & 63);
+        if (w & bit) continue;
+        w |= bit;
+        ce.push_back(eids[i]);
+        cs.push_back(slots[i]);
+    }
+    std::reverse(ce.begin(), ce.end());
+    std::reverse(cs.begin(), cs.end());
+    if (issue_copies(layer, L, ce.data(), cs.data(), (int)ce.size(), false, true)) return;
     if (drain_copies(L)) return;
     wait_copies_gpu(L, g_compute);
 }

@@ -268,6 +268,45 @@ def test_staging_fills_slots_with_the_right_experts(L, mode):
         L.c_host_free(ptr)
 
 
+def test_load_sync_copies(L):
+    """c_layer_load_sync from a pinned store (CU copy kernel, 128 pairs per launch): 300 pairs in
+    one call land in their slots; a slot named twice in one call holds the later pair's expert,
+    as when the copies run one after the other (expert_io.c:710-724)."""
+    from moe_offload import q2format
+    blob = q2format.expert_bytes(256, 128)
+    n_exp, cap, layer = 512, 300, 63
+    ptr = L.c_host_alloc(n_exp * blob)
+    assert ptr
+    try:
+        store = np.ctypeslib.as_array(ctypes.cast(ptr, ctypes.POINTER(ctypes.c_uint8)), shape=(n_exp, blob))
+        store[:] = np.random.default_rng(5).integers(0, 256, size=store.shape, dtype=np.uint8)
+        store_dev = torch.from_numpy(store.copy()).to("cuda")
+        pool = torch.zeros((cap, blob), dtype=torch.uint8, device="cuda")
+        slots = torch.zeros(16, dtype=torch.int32, device="cuda")
+        _init_layer(L, layer, cap, store_ptr=ptr, blob=blob, pool_ptr=pool.data_ptr(), slot_ptr=slots.data_ptr())
+        rng = np.random.default_rng(6)
+        eids = rng.choice(n_exp, size=cap, replace=False).astype(np.int32)
+        sl = rng.permutation(cap).astype(np.int32)
+        c32 = ctypes.c_int32 * cap
+        L.c_layer_load_sync(layer, c32(*eids.tolist()), c32(*sl.tolist()), cap, 1)
+        _check(L)
+        torch.cuda.synchronize()
+        assert torch.equal(pool[torch.from_numpy(sl.astype(np.int64)).to("cuda")],
+                           store_dev[torch.from_numpy(eids.astype(np.int64)).to("cuda")])
+        # slot 5 named twice (expert 7, then 9), slot 6 once
+        pairs_e, pairs_s = [7, 11, 9], [5, 6, 5]
+        c3 = ctypes.c_int32 * 3
+        L.c_layer_load_sync(layer, c3(*pairs_e), c3(*pairs_s), 3, 1)
+        _check(L)
+        torch.cuda.synchronize()
+        assert torch.equal(pool[5], store_dev[9]) and torch.equal(pool[6], store_dev[11])
+    finally:
+        torch.cuda.synchronize()
+        L.c_sync_copies()
+        L.c_layer_init(layer, -1, 16, None, None, None, 0)
+        L.c_host_free(ptr)
+
+
 def test_host_staging_small_pool_victims_of_inflight_prefetch(L):
     """Host-driven staging at the 16-slot floor with prefetch cap 8: a demand miss then takes a
     slot that the prefetch just before it is still filling, and the two copies must land in
