@@ -303,7 +303,11 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
     pool = random_blobs(n_exp, hidden, inter, 64, gen, dev)
     ids, scores = synth.prefill_routing(n_tok, k, n_exp)
     x = torch.randn((n_tok, hidden), device=dev, generator=gen).half()
-    row_tok, row_out, seg, slot = [torch.from_numpy(a).to(dev) for a in prefill.resident_plan(ids, k)]
+    plan = prefill.resident_plan(ids, k)
+    row_tok, row_out, seg, slot = [torch.from_numpy(a).to(dev) for a in plan]
+    # gate/up over one-tile segments (an expert's 16-row tiles as neighbouring blocks), down over the
+    # expert segments (its whole-K form keeps a segment's weights in registers across tiles)
+    seg_t, slot_t = [torch.from_numpy(a).to(dev) for a in prefill.tile_segments(plan[2], plan[3])]
     sc = torch.from_numpy(scores).to(dev)
     m = ids.size
     h_ws = torch.empty((m, inter), dtype=torch.float16, device=dev)
@@ -311,11 +315,11 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
     out = torch.empty((n_tok, hidden), dtype=torch.float32, device=dev)
 
     def chunk(_i):
-        ops.q2_grouped_switch_glu(x, row_tok, seg, pool, hidden, inter, row_out=row_out, n_out_rows=m,
-                                  seg_slot=slot, h_ws=h_ws, out=y)
+        ops.q2_grouped_gate_up(x, row_tok, seg_t, pool, hidden, inter, seg_slot=slot_t, h_out=h_ws)
+        ops.q2_grouped_down(h_ws, seg, pool, hidden, inter, row_out=row_out, n_out_rows=m, seg_slot=slot, out=y)
         ops.pair_combine(y, sc, out=out)
 
-    for i in range(3):
+    for i in range(50):                  # ~10 ms of chunks first: the clocks settle under load
         chunk(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -336,7 +340,7 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
         e1.record(s)
         e1.synchronize()
         return e0.elapsed_time(e1) * 1e-3 / iters
-    gu = bracketed(lambda: ops.q2_grouped_gate_up(x, row_tok, seg, pool, hidden, inter, seg_slot=slot, h_out=h_ws))
+    gu = bracketed(lambda: ops.q2_grouped_gate_up(x, row_tok, seg_t, pool, hidden, inter, seg_slot=slot_t, h_out=h_ws))
     dn = bracketed(lambda: ops.q2_grouped_down(h_ws, seg, pool, hidden, inter, row_out=row_out, n_out_rows=m,
                                                seg_slot=slot, out=y))
     cb = bracketed(lambda: ops.pair_combine(y, sc, out=out))
@@ -352,7 +356,8 @@ def prefill_pass(hidden=2048, inter=512, n_exp=512, k=10, n_tok=512, iters=20, c
     res = {
         "workload": f"{n_tok}-token prefill chunk through one layer, top-{k} of {n_exp} (long-tailed: "
                     f"max {int(counts.max())} rows/expert, {n_used} experts touched), hidden {hidden}, inter {inter}, "
-                    f"Q2 g64, all experts resident in HBM",
+                    f"Q2 g64, all experts resident in HBM; gate/up over {int(seg_t.numel()) - 1} one-tile segments, "
+                    f"down over the {n_used} expert segments",
         "ms_per_chunk": round(wall * 1e3, 4),
         "tok_s": round(n_tok / wall, 1),
         "kernels_us": {"grouped_gate_up": round(gu * 1e6, 2), "grouped_down": round(dn * 1e6, 2),

@@ -144,6 +144,31 @@ def cached_prefill(module, x: torch.Tensor, indices: torch.Tensor) -> torch.Tens
     return y.reshape(*indices.shape, H)
 
 
+def tile_segments(seg_start: np.ndarray, seg_slot: np.ndarray, rows: int = 16):
+    """The same sorted rows cut into segments of at most `rows` rows, each keeping its expert's slot.
+
+    The grouped gate/up kernel gives every (segment, 128-row slice) one block that takes the
+    segment's 16-row M tiles one after the other; an expert of several tiles given as several
+    one-tile segments runs as neighbouring blocks on one XCD instead, which read its weights
+    together (from L2 after the first) rather than one block re-reading them per tile.  Outputs
+    are bit-identical (each tile is multiplied the same way).  Empty segments are dropped.
+    Returns int32 (seg_start', seg_slot').
+    """
+    seg_start = np.asarray(seg_start, dtype=np.int64)
+    seg_slot = np.asarray(seg_slot, dtype=np.int64)
+    counts = np.diff(seg_start)
+    if counts.size != seg_slot.size:
+        raise ValueError("seg_start must have one more entry than seg_slot")
+    if np.any(counts < 0) or rows <= 0:
+        raise ValueError("segments must be ascending and rows positive")
+    pieces = (counts + rows - 1) // rows
+    n = int(pieces.sum())
+    first_piece = np.cumsum(pieces) - pieces
+    within = np.arange(n) - np.repeat(first_piece, pieces)
+    starts = np.repeat(seg_start[:-1], pieces) + rows * within
+    return (np.append(starts, seg_start[-1]).astype(np.int32), np.repeat(seg_slot, pieces).astype(np.int32))
+
+
 def resident_plan(ids: np.ndarray, k: int):
     """Row plan for a pool holding every expert at slot = expert id (the pinned layer 0).
 

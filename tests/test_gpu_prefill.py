@@ -70,6 +70,13 @@ def test_grouped_prefill_chunk_matches_oracle(dev, experts):
     chosen = [longest] + singles + [int(e) for e in rng.choice(seg_slot, 20, replace=False)]
     _check_experts(yh, ids, xs, mlx, chosen, K)
 
+    # gate/up over one-tile segments (the same rows, each keeping its expert's slot): bit-identical h
+    h_e = ops.q2_grouped_gate_up(t(xs), t(row_tok), t(seg_start), pool, H, I, seg_slot=t(seg_slot))
+    seg_t, slot_t = prefill.tile_segments(seg_start, seg_slot)
+    assert slot_t.size == int(np.sum((counts + 15) // 16))
+    h_t = ops.q2_grouped_gate_up(t(xs), t(row_tok), t(seg_t), pool, H, I, seg_slot=t(slot_t))
+    assert torch.equal(h_e, h_t)
+
     comb = ops.pair_combine(y, t(scores)).cpu().numpy()
     want = (yh.reshape(512, K, H).astype(np.float32) * scores.astype(np.float32)[..., None]).astype(np.float64)
     want = want.sum(axis=1)

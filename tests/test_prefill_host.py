@@ -5,6 +5,7 @@ checks every piece against oracle.prefill_plan on random LRU states, capacities 
 multisets, including the empty prefill.  No GPU needed.
 """
 import numpy as np
+import pytest
 
 from moe_offload import prefill
 from oracle import q2
@@ -50,3 +51,29 @@ def test_resident_plan_rows():
     assert seg.tolist() == [0, 2, 5, 6]
     assert row_out.tolist() == [1, 2, 0, 4, 5, 3]          # stable within an expert
     assert row_tok.tolist() == [0, 1, 0, 2, 2, 1]
+
+
+def test_tile_segments_known_answer():
+    # [0,5) slot 3; an empty segment (dropped); [5,40) slot 9 -> 16 + 16 + 3 rows; [40,48) slot 2
+    seg, slot = prefill.tile_segments(np.array([0, 5, 5, 40, 48]), np.array([3, 7, 9, 2]))
+    assert seg.tolist() == [0, 5, 21, 37, 40, 48]
+    assert slot.tolist() == [3, 9, 9, 9, 2]
+    assert seg.dtype == np.int32 and slot.dtype == np.int32
+
+
+def test_tile_segments_cover_the_same_rows():
+    rng = np.random.default_rng(4)
+    counts = rng.integers(0, 70, size=200)
+    seg = np.append(0, np.cumsum(counts))
+    slot = rng.permutation(512)[:200]
+    s2, t2 = prefill.tile_segments(seg, slot, rows=16)
+    c2 = np.diff(s2)
+    assert c2.min() >= 1 and c2.max() <= 16 and s2[0] == 0 and s2[-1] == seg[-1]
+    # every row keeps its expert's slot
+    want = np.repeat(slot, counts)
+    got = np.repeat(t2, c2)
+    assert np.array_equal(want, got)
+    # a segment splits into ceil(rows / 16) pieces
+    assert t2.size == int(np.sum((counts + 15) // 16))
+    with pytest.raises(ValueError):
+        prefill.tile_segments(np.array([0, 4]), np.array([1, 2]))
