@@ -41,7 +41,8 @@ class CbStackConfig:
     eps: float = 1e-6
     seed: int = 0
     layer_base: int = 0
-    stage_ctas: int = 2
+    stage_ctas: int = 8          # staging blocks per 2.4 MB expert (118.1 tok/s at the 4 GiB cache against
+                                 # 115.0 with 2, 117.5 with 4, 117.4 with 16)
     resident: bool = False
     d_scale: float = 0.01
 
