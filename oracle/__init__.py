@@ -1,8 +1,8 @@
 """CPU oracle for the routed-expert decode path -- TEST INFRASTRUCTURE ONLY.
 
 Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import
-anything from this package, and only as the checker (or the timed CPU baseline), never as the
-thing measured or shipped.  The product path (`moe-offload_amd/`) never imports it and fails
+anything from this package, and only as the reference the results are compared with (or the timed
+CPU baseline), never as the thing measured or shipped.  The product path (`moe-offload_amd/`) never imports it and fails
 loudly when its HIP library is missing.
 
 Contents

@@ -1,5 +1,5 @@
-"""CPU restatement of the 2-bit codebook expert path (TEST INFRASTRUCTURE ONLY: the checker for
-the HIP codebook kernels; never imported by the product).
+"""CPU restatement of the 2-bit codebook expert path (TEST INFRASTRUCTURE ONLY: what the tests
+compare the HIP codebook kernels with; never imported by the product).
 
 Restated behaviour.  The reference runs its Nemotron model (README.md:37: IQ2_XXS GGUF, 240
 experts, top-9; non-gated up -> squared ReLU -> down) only inside llama.cpp's Metal backend,

@@ -1,7 +1,7 @@
 /*
  * lru.c -- plain-C restatement of the per-layer expert slot LRU of the reference's
- * `mlx-qwen38/expert_io.c` (TEST INFRASTRUCTURE ONLY: the checker for the HIP library's
- * host and device LRU tables; never linked into the product).
+ * `mlx-qwen38/expert_io.c` (TEST INFRASTRUCTURE ONLY: what the tests compare the HIP
+ * library's host and device LRU tables with; never linked into the product).
  *
  * Restated behaviour (file:line of `mlx-qwen38/expert_io.c`):
  *   reset             450-468  all maps -1, free stack [cap-1 .. 0] so pops yield 0,1,2,..

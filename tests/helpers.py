@@ -1,4 +1,4 @@
-"""Shared helpers for the GPU parity tests (inputs are seeded; the oracle is the checker)."""
+"""Shared helpers for the GPU parity tests (inputs are seeded; results are compared with the oracle)."""
 from __future__ import annotations
 
 import numpy as np

@@ -1,6 +1,6 @@
 """Pins two oracle/host functions that no golden vector covers.
 
-* `oracle.q2.rmsnorm`, the checker of every GPU RMSNorm (router prologue, stack glue, codebook
+* `oracle.q2.rmsnorm`, the reference for every GPU RMSNorm (router prologue, stack glue, codebook
   stack): against torch's own `rms_norm` and against closed forms chosen so that a plausible
   mistake fails one of them (eps outside the square root, a missing weight, a sum instead of a
   mean).  A planted mistake must fail.
