@@ -147,11 +147,13 @@ def cached_prefill(module, x: torch.Tensor, indices: torch.Tensor) -> torch.Tens
 def tile_segments(seg_start: np.ndarray, seg_slot: np.ndarray, rows: int = 16):
     """The same sorted rows cut into segments of at most `rows` rows, each keeping its expert's slot.
 
-    The grouped gate/up kernel gives every (segment, 128-row slice) one block that takes the
-    segment's 16-row M tiles one after the other; an expert of several tiles given as several
-    one-tile segments runs as neighbouring blocks on one XCD instead, which read its weights
-    together (from L2 after the first) rather than one block re-reading them per tile.  Outputs
-    are bit-identical (each tile is multiplied the same way).  Empty segments are dropped.
+    For the blob pool's gate/up at hidden 2048 (the whole-K form): that kernel gives every
+    (segment, 128-row slice) one block that takes the segment's 16-row M tiles one after the
+    other; an expert of several tiles given as several one-tile segments runs as neighbouring
+    blocks on one XCD instead, which read its weights together (from L2 after the first) rather
+    than one block re-reading them per tile.  Outputs are bit-identical (each tile is multiplied
+    the same way).  The chunked kernels (down, other shapes) multiply two tiles per weight pass
+    and are faster over the expert segments.  Empty segments are dropped.
     Returns int32 (seg_start', seg_slot').
     """
     seg_start = np.asarray(seg_start, dtype=np.int64)
