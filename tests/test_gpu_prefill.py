@@ -191,11 +191,14 @@ def test_cached_layer_prefill(dev, experts, n_tok):
         store.close()
 
 
-@pytest.mark.parametrize("hidden,inter", [(384, 192), (1024, 320), (128, 768), (2560, 64)])
+@pytest.mark.parametrize("hidden,inter", [(384, 192), (1024, 320), (128, 768), (2560, 64), (2048, 576), (384, 512),
+                                          (2048, 512)])
 def test_grouped_gate_up_and_down_odd_contractions(dev, hidden, inter):
     """Contraction lengths off the 256-wide chunk grid (K = 384, 192, 320, 128, 64) take the
     per-chunk scale/bias loads; multiples of 256 from 512 up (1024, 768, 2560) take the
-    four-chunk blocks; both against the fp64 oracle."""
+    four-chunk blocks; gate/up at K = 2048 and down at K = 512 take the whole-K forms, here also
+    with a last slice only partly in range (inter 576: half of a 128-row gate/up slice; hidden
+    384: half of a 256-row down slice); all against the fp64 oracle."""
     from moe_offload import ops, q2format, synth
     n_exp, rows_per = 6, [1, 17, 40, 3, 64, 9]
     gate, up, down = synth.q2_experts(n_exp, hidden, inter, seed=hidden + inter, scale_std=0.05)
