@@ -816,6 +816,46 @@ def tensor_form_pass(hidden=2560, inter=640, n_exp=512, k=10, layers=8, draws=6,
                      ("norm_in_router_selection_in_gate_up", layer_norm_in_router)):
         per = graph_loop_us(fn, 2 * n_r, repeats)
         out["layer_us"][name] = round(sorted(per)[len(per) // 2], 3)
+
+    # prefill in this format: a 512-token chunk (the long-tailed top-k routing of the blob prefill
+    # pass) through one layer with every expert resident, the grouped SwitchGLU over the 9 pools
+    # (expert segments) and the weighted combine; 30 chunks first while the clocks settle
+    from moe_offload import prefill, synth
+    n_tok = 512
+    p_ids, p_sc = synth.prefill_routing(n_tok, k, n_exp)
+    plan = [torch.from_numpy(a).to(dev) for a in prefill.resident_plan(p_ids, k)]
+    p_x = torch.randn((n_tok, hidden), device=dev, generator=g).half()
+    p_sc_d = torch.from_numpy(p_sc).to(dev)
+    m = p_ids.size
+    p_h = torch.empty((m, inter), dtype=torch.float16, device=dev)
+    p_y = torch.empty((m, hidden), dtype=torch.float16, device=dev)
+    p_out = torch.empty((n_tok, hidden), dtype=torch.float32, device=dev)
+    n_seg = int(plan[3].numel())
+
+    def prefill_chunk():
+        s = torch.cuda.current_stream().cuda_stream
+        _lib.check(L.moe_q2t_grouped_switch_glu(p_x.data_ptr(), n_tok, plan[0].data_ptr(), plan[1].data_ptr(), m, m,
+                                                plan[2].data_ptr(), plan[3].data_ptr(), n_seg, ptrs[0], nbytes, 1,
+                                                n_exp, hidden, inter, 64, p_h.data_ptr(), p_y.data_ptr(), s),
+                   "q2t_grouped_switch_glu")
+        _lib.check(L.moe_pair_combine(p_y.data_ptr(), p_sc_d.data_ptr(), None, n_tok, k, hidden, p_out.data_ptr(), s),
+                   "pair_combine")
+
+    for _ in range(30):
+        prefill_chunk()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        prefill_chunk()
+    e1.record()
+    e1.synchronize()
+    p_us = e0.elapsed_time(e1) * 1e3 / 20
+    p_bytes = n_seg * expert
+    out["prefill_chunk"] = {"tokens": n_tok, "experts_touched": n_seg, "us": round(p_us, 1),
+                            "tok_s": round(n_tok / p_us * 1e6, 1), "expert_bytes": p_bytes,
+                            "hbm_gb_s": round(p_bytes / p_us / 1e3, 1),
+                            "hbm_frac": round(p_bytes / p_us / 1e3 / HBM_PEAK_GBS, 4)}
     del sets, rcodes, rs, rb
     torch.cuda.empty_cache()
     return out
