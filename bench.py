@@ -1158,7 +1158,6 @@ def main():
                      "traffic_source": traffic[1] if traffic else None,
                      "kernel": rk, "measured_in": measured_in,
                      "bytes_per_launch": r_bytes, "avg_launch_us": round(r_us, 3),
-                     "dispatch_us": dec[rk]["dispatch_us"] if dec else None,
                      "launch_floor_us": round(floor_us, 3),
                      "frac_of_launch_floor": round(floor_us / r_us, 4)},
         "cache": {"effective_hit_rate": round((tot1[0] - tot0[0] + tot1[1] - tot0[1]) / req, 4),
