@@ -77,3 +77,8 @@ def test_tile_segments_cover_the_same_rows():
     assert t2.size == int(np.sum((counts + 15) // 16))
     with pytest.raises(ValueError):
         prefill.tile_segments(np.array([0, 4]), np.array([1, 2]))
+    # no segments, and segments that are all empty
+    s0, t0 = prefill.tile_segments(np.array([0]), np.array([], np.int32))
+    assert s0.tolist() == [0] and t0.size == 0
+    s1, t1 = prefill.tile_segments(np.array([3, 3, 3]), np.array([1, 2]))
+    assert s1.tolist() == [3] and t1.size == 0
